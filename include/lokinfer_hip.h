@@ -1,0 +1,97 @@
+/* lokinfer MI355X (gfx950) backend: the C-ABI boundary.
+ *
+ * Two layers, both plain C: pointers, sizes, a hipStream_t passed as void*, an int status (0 = ok).
+ *
+ * 1. The kernel registry. It replaces the reference's KernelEntry / KernelArgs / findKernel ABI
+ *    (lariaus/lokinfer include/lokinfer/runtime/kernel.h:24-74, src/runtime/registry.cpp:39-77) for the GPU
+ *    kernel names of its compiled path. lk_run_kernel takes the reference's argument convention
+ *    (kernel.h:3-11): ptrs = operands then outs (device pointers), ints = every operand's dims, every out's
+ *    dims, then int attrs in attribute-name order, floats = float attrs in attribute-name order. The
+ *    reference's Executable::Impl::execute (src/runtime/executable.cpp:582-653) is the caller it replaces.
+ *
+ * 2. Typed launchers (lk_hip_*), one per kernel family. The registry entries are thin decoders over these.
+ *    Each launcher cites the reference kernel it replaces. All enqueue on `stream` and never synchronise.
+ *
+ * Workspace: kernels that merge partial results across workgroups (gemv, decode attention) take a
+ * caller-owned device workspace whose first 64 KiB are ticket counters. The owner zero-fills it once; every
+ * kernel leaves the counters at zero. Calls that share one workspace must be ordered (one stream).
+ */
+#ifndef LOKINFER_HIP_H
+#define LOKINFER_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lk_kernel lk_kernel;
+
+/* ---- registry (reference: registerBuiltinKernels / findKernel / registeredKernels, kernel.h:68-72) ---- */
+int lk_init(void);
+int lk_num_kernels(void);
+const char* lk_kernel_name_at(int i); /* sorted */
+const lk_kernel* lk_find_kernel(const char* name);
+int lk_kernel_is_gpu(const lk_kernel* k);
+int lk_kernel_arity(const lk_kernel* k, int* num_operands, int* num_outs);
+/* Reference: KernelEntry::run(ExecCtx&, const KernelArgs&) (kernel.h:56-66). Nonzero on error; the message
+ * (the kernel's ExecCtx::error, prefixed with its name) is in lk_last_error(). */
+int lk_run_kernel(const lk_kernel* k, void* const* ptrs, uint32_t num_ptrs, const int64_t* ints, uint32_t num_ints,
+                  const double* floats, uint32_t num_floats, void* workspace, uint64_t workspace_bytes,
+                  void* stream);
+const char* lk_last_error(void);
+
+/* ---- GEMM / conv (reference: gemm_f32_gpu_mps mps.mm:41-84; gemm_bias[_relu]_f32_gpu kokoro_lc.cpp:460-581;
+ *      gemm_steel* kokoro_lc.cpp:391-409; conv1d_lc[_res]_f32_gpu kokoro_lc.cpp:81-109) ---- */
+/* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu */
+int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
+                    int64_t n, int64_t k, int nt, int act, float scale, void* stream);
+/* channel-last conv1d: x [L, Ci] (Ci % 16 == 0), w [Co, K, Ci] -> out [Lo, Co] = (conv(pre(x)) + b + res) * scale;
+ * pre = optional affine [3, Ci] (mean, scale, beta) then snake(alpha) (pre 1) / leaky(slope) (pre 2) */
+int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
+                         int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
+                         const float* affine, const float* alpha, int pre, float slope, void* stream);
+
+/* ---- GEMV (reference: gemv4*_f32_gpu transformer_gpu.cpp:233-251; gemv_rows / gemv1_bias kokoro_lc.cpp:227-267) */
+int64_t lk_hip_gemv_workspace_bytes(int64_t n, int64_t k);
+int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,
+                    int64_t k, int act, void* workspace, int64_t workspace_bytes, void* stream);
+int lk_hip_rowdot_f32(const float* mat, const float* vec, const float* bias, int bias_per_row, float* out,
+                      int64_t rows, int64_t k, int nvec, int64_t ldo, void* stream);
+
+/* ---- transformer (reference: kokoro_tok.metal:25-204, 465-876; transformer_gpu.cpp:72-222) ---- */
+int lk_hip_layernorm_f32(const float* a, const float* bias, const float* r, const float* gamma, const float* beta,
+                         float* sum, float* out, int64_t rows, int64_t cols, float eps, int mode, void* stream);
+int lk_hip_bias_gelu_f32(const float* x, const float* bias, float* out, int64_t rows, int64_t cols, void* stream);
+int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, int64_t t, int heads, int causal,
+                             void* stream);
+int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap);
+int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
+                                float* out, int64_t cap, int heads, int64_t max_keys, int keys_per_split,
+                                int write_kv, void* workspace, int64_t workspace_bytes, void* stream);
+int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
+                        void* stream);
+
+/* ---- Kokoro frame-rate, channel-last (reference: kokoro_lc.metal:143-398) ---- */
+int lk_hip_channel_stats_lc_f32(const float* x, float* stats, int64_t l, int64_t c, void* stream);
+int lk_hip_adain_affine_lc_f32(const float* stats, const float* gb, float* affine, int64_t l, int64_t c,
+                               int64_t creal, float eps, void* stream);
+int lk_hip_act_lc_f32(const float* x, const float* affine, const float* alpha, float* out, int64_t l, int64_t c,
+                      int act, float slope, void* stream);
+int lk_hip_convt_gather_lc_f32(const float* y, const float* bias, const float* add, float* out, int64_t lin,
+                               int64_t lout, int64_t co, int k, int stride, int pad, int reflect_left, void* stream);
+int lk_hip_dwconvt_lc_f32(const float* x, const float* w, const float* bias, float* out, int64_t lin, int64_t lout,
+                          int64_t c, int k, int stride, int pad, void* stream);
+int lk_hip_upsample2_lc_f32(const float* x, float* out, int64_t l, int64_t c, void* stream);
+int lk_hip_concat_pad_lc_f32(const float* a, const float* b, float* out, int64_t l, int64_t ca, int64_t cb,
+                             int64_t cout, void* stream);
+int lk_hip_transpose_f32(const float* x, float* out, int64_t r, int64_t c, int64_t ldx, void* stream);
+int lk_hip_elementwise_f32(const float* a, const float* b, const float* c, float* out, int64_t n, int op, float s,
+                           void* stream);
+int lk_hip_istft_lc_f32(const float* x, float* out, int64_t l, int64_t cpad, int nfft, int hop, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOKINFER_HIP_H */

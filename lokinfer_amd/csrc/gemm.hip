@@ -1,0 +1,346 @@
+// f32 GEMM family on CDNA4 matrix cores (v_mfma_f32_32x32x2f32), LDS-staged and double-buffered, with the
+// epilogues the reference fuses (bias, ReLU, gelu_tanh, residual, output scale) and two operand loaders:
+//   A: row-major [M, lda]              or channel-last implicit im2col of a conv1d input x [L, Ci]
+//      (optionally with a per-channel affine + Snake / leaky prologue applied while staging)
+//   B: row-major [K, ldb] ("NN")       or row-major B^T [N, ldb] ("NT": conv weights [Co, K*Ci], tied LM heads)
+//
+// Reference kernels this family replaces (lariaus/lokinfer):
+//   gemm_f32_gpu_mps / gemm_nt_f32_gpu_mps      kernels/gpu/mps.mm:41-84
+//   gemm_bias[_relu]_f32_gpu                    kernels/gpu/kokoro_lc.cpp:460-581, gemm.metal:82-341
+//   gemm_steel*_f32_gpu, gemm_nt_steel_f32_gpu  kernels/gpu/kokoro_lc.cpp:391-409, gemm_steel.metal:81-133
+//   conv1d_lc_f32_gpu / conv1d_lc_res_f32_gpu   kernels/gpu/kokoro_lc.cpp:81-109, kokoro_lc.metal:62-128
+//   gemv4*_f32_gpu                              kernels/gpu/transformer_gpu.cpp:233-251, kokoro_tok.metal:878-924
+//   gemv_rows_f32_gpu, gemv1_bias_f32_gpu       kernels/gpu/kokoro_lc.cpp:227-267, vision.metal:266-284
+//
+// Design (gfx950): 256-thread workgroups = 4 wave64s in a 2x2 layout; each wave owns a (BM/2)x(BN/2) block of
+// 32x32 MFMA tiles and accumulates over K in steps of 2. Per 16-deep K tile both operands are staged in LDS
+// k-major ([16][BM], [16][BN]) so that a wave's MFMA operand fetch is 32 consecutive floats per k row.
+#include "common.h"
+
+namespace lkd {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+enum : int { PRE_NONE = 0, PRE_SNAKE = 1, PRE_LEAKY = 2 };
+enum : int { A_ROWMAJOR = 0, A_CONV = 1 };
+enum : int { B_NN = 0, B_NT = 1 };
+
+struct GemmParams {
+  const float* a;
+  const float* b;
+  const float* bias;  // [N] or null
+  const float* res;   // [M, ldr] or null
+  float* c;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc, ldr;
+  int act;
+  float scale;
+  // conv loader (A_CONV): x = a [L, Ci]; row t reads x[t * stride - pad + kk * dil]
+  int64_t convL, convCi;
+  int convStride, convPad, convDil;
+  // optional prologue on the conv input: v = (x - af[c]) * af[C + c] + af[2C + c]; snake(alpha) / leaky(slope)
+  const float* affine;
+  const float* alpha;
+  int pre;
+  float slope;
+};
+
+constexpr int BK = 16;
+constexpr int NT = 256;
+
+__device__ __forceinline__ float preAct(const GemmParams& p, float v, int c) {
+  if (p.affine) {
+    const int64_t C = p.convCi;
+    v = (v - p.affine[c]) * p.affine[C + c] + p.affine[2 * C + c];
+  }
+  if (p.pre == PRE_SNAKE) {
+    const float a = p.alpha[c];
+    const float s = sinf(a * v);
+    v = v + (1.0f / a) * (s * s);
+  } else if (p.pre == PRE_LEAKY) {
+    v = v >= 0.0f ? v : v * p.slope;
+  }
+  return v;
+}
+
+// 4 consecutive elements of A along k for row `row`, k0..k0+3 (zero outside the matrix).
+template <int AM>
+__device__ __forceinline__ float4 loadA4(const GemmParams& p, int64_t row, int64_t k0) {
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (row >= p.m) return r;
+  if constexpr (AM == A_ROWMAJOR) {
+    const float* src = p.a + row * p.lda + k0;
+    if (k0 + 3 < p.k && ((p.lda & 3) == 0)) {
+      r = *reinterpret_cast<const float4*>(src);
+    } else {
+      if (k0 < p.k) r.x = src[0];
+      if (k0 + 1 < p.k) r.y = src[1];
+      if (k0 + 2 < p.k) r.z = src[2];
+      if (k0 + 3 < p.k) r.w = src[3];
+    }
+  } else {
+    // k = kk * Ci + ci, Ci % 16 == 0: a 16-deep K tile never straddles two taps.
+    if (k0 >= p.k) return r;
+    const int64_t kk = k0 / p.convCi, ci = k0 - kk * p.convCi;
+    const int64_t t = row * p.convStride - p.convPad + kk * p.convDil;
+    if (t < 0 || t >= p.convL) return r;
+    r = *reinterpret_cast<const float4*>(p.a + t * p.convCi + ci);
+    if (p.pre != PRE_NONE || p.affine) {
+      r.x = preAct(p, r.x, static_cast<int>(ci));
+      r.y = preAct(p, r.y, static_cast<int>(ci + 1));
+      r.z = preAct(p, r.z, static_cast<int>(ci + 2));
+      r.w = preAct(p, r.w, static_cast<int>(ci + 3));
+    }
+  }
+  return r;
+}
+
+// NN: 4 consecutive elements of B along n for row k (zero outside).
+__device__ __forceinline__ float4 loadBnn4(const GemmParams& p, int64_t k, int64_t n0) {
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (k >= p.k) return r;
+  const float* src = p.b + k * p.ldb + n0;
+  if (n0 + 3 < p.n && ((p.ldb & 3) == 0)) {
+    r = *reinterpret_cast<const float4*>(src);
+  } else {
+    if (n0 < p.n) r.x = src[0];
+    if (n0 + 1 < p.n) r.y = src[1];
+    if (n0 + 2 < p.n) r.z = src[2];
+    if (n0 + 3 < p.n) r.w = src[3];
+  }
+  return r;
+}
+
+// NT: 4 consecutive elements of B^T along k for column n (zero outside).
+__device__ __forceinline__ float4 loadBnt4(const GemmParams& p, int64_t n, int64_t k0) {
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n >= p.n) return r;
+  const float* src = p.b + n * p.ldb + k0;
+  if (k0 + 3 < p.k && ((p.ldb & 3) == 0)) {
+    r = *reinterpret_cast<const float4*>(src);
+  } else {
+    if (k0 < p.k) r.x = src[0];
+    if (k0 + 1 < p.k) r.y = src[1];
+    if (k0 + 2 < p.k) r.z = src[2];
+    if (k0 + 3 < p.k) r.w = src[3];
+  }
+  return r;
+}
+
+__device__ __forceinline__ float epilogue(const GemmParams& p, float v, int64_t row, int64_t col) {
+  if (p.bias) v += p.bias[col];
+  if (p.act == ACT_RELU) v = fmaxf(v, 0.0f);
+  else if (p.act == ACT_GELU) v = geluTanh(v);
+  if (p.res) v += p.res[row * p.ldr + col];
+  return v * p.scale;
+}
+
+template <int BM, int BN, int AM, int BMODE>
+__global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
+  constexpr int WTM = BM / 2, WTN = BN / 2;    // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
+  constexpr int PADA = 4, PADB = 4;
+  constexpr int LDA_S = BM + PADA, LDB_S = BN + PADB;
+  constexpr int A4 = BM * BK / 4 / NT;  // float4 loads per thread (A tile)
+  constexpr int B4 = BN * BK / 4 / NT;
+  static_assert(A4 >= 1 && B4 >= 1, "tile too small for 256 threads");
+
+  __shared__ float As[2][BK][LDA_S];
+  __shared__ float Bs[2][BK][LDB_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  float4 ra[A4], rb[B4];
+  auto gload = [&](int64_t kt) {
+    const int64_t k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int idx = tid + i * NT;
+      const int row = idx >> 2, kq = (idx & 3) * 4;
+      ra[i] = loadA4<AM>(p, m0 + row, k0 + kq);
+    }
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      if constexpr (BMODE == B_NN) {
+        const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
+        rb[i] = loadBnn4(p, k0 + kr, n0 + nq);
+      } else {
+        const int col = idx >> 2, kq = (idx & 3) * 4;
+        rb[i] = loadBnt4(p, n0 + col, k0 + kq);
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int idx = tid + i * NT;
+      const int row = idx >> 2, kq = (idx & 3) * 4;
+      As[buf][kq + 0][row] = ra[i].x;
+      As[buf][kq + 1][row] = ra[i].y;
+      As[buf][kq + 2][row] = ra[i].z;
+      As[buf][kq + 3][row] = ra[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      if constexpr (BMODE == B_NN) {
+        const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
+        *reinterpret_cast<float4*>(&Bs[buf][kr][nq]) = rb[i];
+      } else {
+        const int col = idx >> 2, kq = (idx & 3) * 4;
+        Bs[buf][kq + 0][col] = rb[i].x;
+        Bs[buf][kq + 1][col] = rb[i].y;
+        Bs[buf][kq + 2][col] = rb[i].z;
+        Bs[buf][kq + 3][col] = rb[i].w;
+      }
+    }
+  };
+
+  const int64_t nk = (p.k + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = static_cast<int>(kt & 1);
+    if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 2) {
+      float av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[i] = As[buf][ks + lk][wm * WTM + i * 32 + lrow];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = Bs[buf][ks + lk][wn * WTN + j * 32 + lrow];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // D[i][j] of a 32x32x2 MFMA: j = lane % 32, i = 8 * (r / 4) + 4 * (lane / 32) + r % 4 for accumulator r.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (row < p.m) p.c[row * p.ldc + col] = epilogue(p, acc[i][j][r], row, col);
+      }
+    }
+}
+
+}  // namespace lkd
+
+namespace lkh {
+
+using lkd::GemmParams;
+
+// Tile choice: 128x128 when it still yields a few hundred workgroups, else 64x64 (small M, e.g. ALBERT at
+// T = 59 or the MNIST layers).
+template <int AM, int BMODE>
+static void launchGemm(const GemmParams& p, hipStream_t s) {
+  const int64_t big = static_cast<int64_t>(ceilDiv(p.m, 128)) * ceilDiv(p.n, 128);
+  if (big >= 512) {
+    dim3 grid(ceilDiv(p.n, 128), ceilDiv(p.m, 128));
+    hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+  } else {
+    dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
+    hipLaunchKernelGGL((lkd::gemmMfmaKernel<64, 64, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+  }
+}
+
+static GemmParams baseParams() {
+  GemmParams p{};
+  p.scale = 1.0f;
+  p.convStride = 1;
+  p.convDil = 1;
+  return p;
+}
+
+}  // namespace lkh
+
+// ---- typed C-ABI launchers ---------------------------------------------------------------------------------
+extern "C" {
+
+// out[M, N] = act(A[M, K] . B + bias) + res, then * scale. nt: B is given as B^T [N, K].
+int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
+                    int64_t n, int64_t k, int nt, int act, float scale, void* stream) {
+  if (m <= 0 || n <= 0 || k <= 0) return m >= 0 && n >= 0 && k >= 0 ? 0 : 1;
+  lkd::GemmParams p = lkh::baseParams();
+  p.a = a;
+  p.b = b;
+  p.bias = bias;
+  p.res = res;
+  p.c = out;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.lda = k;
+  p.ldb = nt ? k : n;
+  p.ldc = n;
+  p.ldr = n;
+  p.act = act;
+  p.scale = scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s);
+  else lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NN>(p, s);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Channel-last conv1d as an implicit GEMM: x [L, Ci] (Ci % 16 == 0), w [Co, K, Ci], bias [Co] (or null),
+// res [Lo, Co] (or null) -> out [Lo, Co] = (conv(pre(x)) + bias + res) * scale; pre = optional affine [3, Ci]
+// then snake(alpha [Ci]) (pre = 1) or leaky(slope) (pre = 2); zero padding applies after pre.
+int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
+                         int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
+                         const float* affine, const float* alpha, int pre, float slope, void* stream) {
+  if (ci % 16 != 0 || stride < 1 || dilation < 1 || padding < 0) return 1;
+  const int64_t lo = (l + 2 * padding - static_cast<int64_t>(dilation) * (kw - 1) - 1) / stride + 1;
+  if (lo <= 0 || co <= 0) return lo == 0 ? 0 : 1;
+  lkd::GemmParams p = lkh::baseParams();
+  p.a = x;
+  p.b = w;
+  p.bias = bias;
+  p.res = res;
+  p.c = out;
+  p.m = lo;
+  p.n = co;
+  p.k = kw * ci;
+  p.lda = ci;
+  p.ldb = kw * ci;
+  p.ldc = co;
+  p.ldr = co;
+  p.scale = scale;
+  p.convL = l;
+  p.convCi = ci;
+  p.convStride = stride;
+  p.convPad = padding;
+  p.convDil = dilation;
+  p.affine = affine;
+  p.alpha = alpha;
+  p.pre = pre;
+  p.slope = slope;
+  lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, static_cast<hipStream_t>(stream));
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"

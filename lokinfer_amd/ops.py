@@ -1,0 +1,457 @@
+"""`ops.*_gpu`: the reference's GPU kernel ops (python/lokinfer/ops/{gemm,transformer,kokoro_gpu,elementwise,
+device}.py in lariaus/lokinfer) with the same names, operand order, attribute names and shape rules, executed
+on the MI355X kernels through the C-ABI registry.
+
+Each op checks its operands (OpError, like the reference's `check`), allocates its outputs on the device and
+launches the kernel on the current stream. Attributes are passed in attribute-name order: ints/bools as ints,
+Python floats as floats (the reference ABI, include/lokinfer/runtime/kernel.h:3-11).
+
+Ops that are not in the reference are marked "(MI355X backend)" in their docstring.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import trace as _trace
+from .runtime import GpuContext
+from .tensor import Tensor, f32, i64
+
+STAT_CHUNK = 128
+
+
+class OpError(ValueError):
+    pass
+
+
+def check(cond: bool, msg: str = "invalid operands") -> None:
+    if not cond:
+        raise OpError(msg)
+
+
+def _gpu(*xs: Tensor) -> None:
+    for x in xs:
+        if not isinstance(x, Tensor):
+            raise TypeError(f"expected lk.Tensor, got {type(x).__name__}")
+        if x.device != "gpu":
+            raise OpError("GPU kernel operands must be on the GPU (use ops.to_gpu)")
+
+
+def _f32(*xs: Tensor, rank: int | None = None) -> None:
+    for x in xs:
+        check(x.dtype == f32, f"expected f32, got {x.dtype.name}")
+        if rank is not None:
+            check(x.ndim == rank, f"expected rank {rank}, got shape {list(x.shape)}")
+
+
+def _launch(name: str, operands: list[Tensor], out_shapes: list[tuple], attrs: dict | None = None,
+           out_dtypes: list | None = None, outs: list[Tensor] | None = None):
+    """Allocates outputs (unless given) and runs registry kernel `name` with the reference argument layout."""
+    _gpu(*operands)
+    ctx = GpuContext.shared()
+    if outs is None:
+        out_dtypes = out_dtypes or [f32] * len(out_shapes)
+        outs = [Tensor(torch.empty(s, dtype=d.torch, device=ctx.device)) for s, d in zip(out_shapes, out_dtypes)]
+    ints: list[int] = []
+    for x in list(operands) + list(outs):
+        ints.extend(int(d) for d in x.shape)
+    floats: list[float] = []
+    for k in sorted(attrs or {}):
+        v = attrs[k]
+        if isinstance(v, bool) or isinstance(v, int):
+            ints.append(int(v))
+        elif isinstance(v, float):
+            floats.append(v)
+        elif isinstance(v, (list, tuple)):
+            ints.extend(int(e) for e in v)
+        else:
+            raise OpError(f"attribute {k}: unsupported type {type(v).__name__}")
+    ptrs = [x.data_ptr() for x in list(operands) + list(outs)]
+    ctx.run(name, ptrs, ints, floats)
+    _trace.record(name, operands, outs, ints, floats)
+    if not outs:
+        return None
+    return outs[0] if len(outs) == 1 else tuple(outs)
+
+
+# ---- device sync (reference ops/device.py:13-25; on discrete HBM these are real copies) ----------------------
+
+def to_gpu(x: Tensor) -> Tensor:
+    out = Tensor(x.t.to(GpuContext.shared().device, non_blocking=False))
+    _trace.record_copy(x, out)
+    return out
+
+
+def to_cpu(x: Tensor) -> Tensor:
+    return Tensor(x.t.to("cpu"))
+
+
+def reshape(x: Tensor, shape) -> Tensor:
+    """Zero-cost view with a new shape (same element count)."""
+    return Tensor(x.t.view(*[int(s) for s in shape]))
+
+
+def view(x: Tensor, shape, offset: int = 0) -> Tensor:
+    """Zero-cost view of `shape` starting `offset` elements into x (reference models/kokoro/model.py:109-114)."""
+    n = 1
+    for s in shape:
+        n *= int(s)
+    flat = x.t.reshape(-1)
+    check(offset + n <= flat.numel(), "view out of range")
+    return Tensor(flat[offset:offset + n].view(*[int(s) for s in shape]))
+
+
+# ---- GEMM / GEMV --------------------------------------------------------------------------------------------
+
+def _gemm_shapes(a, b, nt=False):
+    _f32(a, b, rank=2)
+    if nt:
+        check(a.shape[1] == b.shape[1], f"gemm_nt: a f32[M, K], b f32[N, K]: {a.shape}, {b.shape}")
+        return (a.shape[0], b.shape[0])
+    check(a.shape[1] == b.shape[0], f"gemm: a f32[M, K], b f32[K, N]: {a.shape}, {b.shape}")
+    return (a.shape[0], b.shape[1])
+
+
+def gemm_f32_gpu_mps(a, b):
+    """a f32[M, K] @ b f32[K, N] -> f32[M, N] (reference ops/gemm.py:32-35)."""
+    return _launch("gemm_f32_gpu_mps", [a, b], [_gemm_shapes(a, b)])
+
+
+def gemm_f32_gpu(a, b):
+    return _launch("gemm_f32_gpu", [a, b], [_gemm_shapes(a, b)])
+
+
+def gemm_nt_f32_gpu_mps(a, b):
+    """a f32[M, K] @ b^T (b f32[N, K]) -> f32[M, N] (reference ops/transformer.py:45-48)."""
+    return _launch("gemm_nt_f32_gpu_mps", [a, b], [_gemm_shapes(a, b, nt=True)])
+
+
+def _bias_ok(bias, n):
+    _f32(bias, rank=1)
+    check(bias.shape[0] == n, "bias must be f32[N]")
+
+
+def gemm_bias_f32_gpu(a, b, bias):
+    s = _gemm_shapes(a, b)
+    _bias_ok(bias, s[1])
+    return _launch("gemm_bias_f32_gpu", [a, b, bias], [s])
+
+
+def gemm_bias_relu_f32_gpu(a, b, bias):
+    s = _gemm_shapes(a, b)
+    _bias_ok(bias, s[1])
+    return _launch("gemm_bias_relu_f32_gpu", [a, b, bias], [s])
+
+
+def gemm_steel_f32_gpu(a, b, bias=None, act="none", residual=None):
+    """act(a @ b + bias) [+ residual] (reference ops/transformer.py:166-180)."""
+    s = _gemm_shapes(a, b)
+    if bias is None:
+        check(act == "none" and residual is None, "act / residual need a bias")
+        return _launch("gemm_steel_f32_gpu", [a, b], [s])
+    _bias_ok(bias, s[1])
+    if residual is not None:
+        check(act == "none" and tuple(residual.shape) == s, "residual must be f32[M, N], act none")
+        return _launch("gemm_steel_bias_res_f32_gpu", [a, b, bias, residual], [s])
+    name = {"none": "gemm_steel_bias_f32_gpu", "gelu": "gemm_steel_bias_gelu_f32_gpu",
+            "relu": "gemm_steel_bias_relu_f32_gpu"}[act]
+    return _launch(name, [a, b, bias], [s])
+
+
+def gemm_nt_steel_f32_gpu(a, b):
+    return _launch("gemm_nt_steel_f32_gpu", [a, b], [_gemm_shapes(a, b, nt=True)])
+
+
+def _gemv_shapes(x, w, bias=None):
+    _f32(x, w, rank=2)
+    check(x.shape[0] == 1 and x.shape[1] == w.shape[0], f"x must be f32[1, K] and w f32[K, N]: {x.shape}, {w.shape}")
+    if bias is not None:
+        _bias_ok(bias, w.shape[1])
+    return (1, w.shape[1])
+
+
+def gemv4_f32_gpu(x, w, bias=None, act="none", residual=None, cw=0):
+    """x f32[1, K] @ w f32[K, N] (+ bias) (gelu) (+ residual) -> f32[1, N] (reference ops/transformer.py:371-382).
+    cw (Metal column width) is accepted and ignored: the CDNA4 kernel picks its own K split."""
+    check(cw in (0, 2, 4, 8, 16), "cw must be 0 (auto), 2, 4, 8 or 16")
+    s = _gemv_shapes(x, w, bias)
+    check(w.shape[1] % 4 == 0, "N must be a multiple of 4")
+    if bias is None:
+        check(act == "none" and residual is None, "act / residual need a bias")
+        return _launch("gemv4_f32_gpu", [x, w], [s], dict(cw=cw))
+    if residual is not None:
+        check(tuple(residual.shape) == s, "residual must be f32[1, N]")
+        return _launch("gemv4_bias_res_f32_gpu", [x, w, bias, residual], [s], dict(cw=cw))
+    name = "gemv4_bias_gelu_f32_gpu" if act == "gelu" else "gemv4_bias_f32_gpu"
+    return _launch(name, [x, w, bias], [s], dict(cw=cw))
+
+
+def gemv_f32_gpu(x, w, bias=None, act="none"):
+    s = _gemv_shapes(x, w, bias)
+    if bias is None:
+        check(act == "none", "act needs a bias")
+        return _launch("gemv_f32_gpu", [x, w], [s])
+    return _launch("gemv_bias_gelu_f32_gpu" if act == "gelu" else "gemv_bias_f32_gpu", [x, w, bias], [s])
+
+
+def gemv_rows_f32_gpu(x, w):
+    """x f32[1, K] . rows of w f32[N, K] -> f32[1, N] (tied LM head; reference ops/transformer.py:209-215)."""
+    _f32(x, w, rank=2)
+    check(x.shape[0] == 1 and x.shape[1] == w.shape[1], "x must be f32[1, K] and w f32[N, K]")
+    return _launch("gemv_rows_f32_gpu", [x, w], [(1, w.shape[0])])
+
+
+def gemv1_bias_f32_gpu(x, w, b):
+    """x f32[R, K] @ w f32[K, 1] + b f32[1] -> f32[R, 1] (reference gemv1_bias, kokoro_lc.cpp:257-267)."""
+    _f32(x, w, rank=2)
+    check(w.shape == (x.shape[1], 1) and tuple(b.shape) == (1,), "w must be f32[K, 1], b f32[1]")
+    return _launch("gemv1_bias_f32_gpu", [x, w, b], [(x.shape[0], 1)])
+
+
+# ---- conv1d (channel-last) ----------------------------------------------------------------------------------
+
+def _conv_lc_shape(x, w, b, padding, dilation, stride):
+    _f32(x, rank=2)
+    _f32(w, rank=3)
+    _f32(b, rank=1)
+    check(w.shape[2] == x.shape[1], f"w must be [Co, K, Ci]: x {x.shape}, w {w.shape}")
+    check(b.shape[0] == w.shape[0], "bias must be f32[Co]")
+    check(x.shape[1] % 16 == 0, "Ci must be a multiple of 16")
+    check(stride >= 1 and dilation >= 1 and padding >= 0, "invalid conv attrs")
+    lo = (x.shape[0] + 2 * padding - dilation * (w.shape[1] - 1) - 1) // stride + 1
+    check(lo >= 1, "empty conv output")
+    return (lo, w.shape[0])
+
+
+def conv1d_lc_f32_gpu(x, w, b, residual=None, out_scale=1.0, padding=0, dilation=1, stride=1):
+    """(conv1d(x, w) + b [+ residual]) * out_scale, channel-last: x f32[L, Ci], w f32[Co, K, Ci] -> f32[Lo, Co]
+    (reference ops/kokoro_gpu.py:20-54). stride > 1 is an MI355X-backend extension (the reference keeps strided
+    convs on the CPU)."""
+    s = _conv_lc_shape(x, w, b, padding, dilation, stride)
+    attrs = dict(padding=int(padding), dilation=int(dilation), stride=int(stride))
+    if residual is None:
+        check(out_scale == 1.0, "out_scale needs a residual")
+        return _launch("conv1d_lc_f32_gpu", [x, w, b], [s], attrs)
+    check(tuple(residual.shape) == s, "residual shape mismatch")
+    return _launch("conv1d_lc_res_f32_gpu", [x, w, b, residual], [s], dict(attrs, oscale=float(out_scale)))
+
+
+def conv1d_act_lc_f32_gpu(x, w, b, affine, alpha=None, act="snake", slope=0.0, residual=None, out_scale=1.0,
+                          padding=0, dilation=1, stride=1):
+    """(MI355X backend) conv1d_lc over act(affine(x)) with the prologue fused into the implicit-GEMM operand
+    staging: v = (x - af[0]) * af[1] + af[2] per channel, then snake(alpha) / leaky(slope) / none; the conv's zero
+    padding applies after the activation. Replaces the reference's snake_affine_lc + conv1d_lc pair and its
+    Winograd transform prologue (winograd.metal:37-91)."""
+    s = _conv_lc_shape(x, w, b, padding, dilation, stride)
+    _f32(affine, rank=2)
+    check(affine.shape == (3, x.shape[1]), "affine must be f32[3, Ci]")
+    code = {"none": 0, "snake": 1, "leaky": 2}[act]
+    if alpha is None:
+        check(code != 1, "snake needs alpha")
+        alpha = b  # unused operand slot
+    check(alpha.shape[0] == x.shape[1] or code != 1, "alpha must be f32[Ci]")
+    attrs = dict(act=code, dilation=int(dilation), oscale=float(out_scale), padding=int(padding), slope=float(slope),
+                 stride=int(stride))
+    if residual is None:
+        check(out_scale == 1.0, "out_scale needs a residual")
+        return _launch("conv1d_act_lc_f32_gpu", [x, w, b, affine, alpha], [s], attrs)
+    check(tuple(residual.shape) == s, "residual shape mismatch")
+    return _launch("conv1d_act_lc_res_f32_gpu", [x, w, b, affine, alpha, residual], [s], attrs)
+
+
+# ---- transformer --------------------------------------------------------------------------------------------
+
+def layernorm_f32_gpu(x, gamma, beta, eps=1e-5):
+    _f32(x, rank=2)
+    check(x.shape[1] <= 2048 and gamma.shape == (x.shape[1],) and beta.shape == (x.shape[1],), "layernorm: bad shapes")
+    return _launch("layernorm_f32_gpu", [x, gamma, beta], [x.shape], dict(eps=float(eps)))
+
+
+def _abln_check(a, bias, r, gamma, beta):
+    _f32(a, r, rank=2)
+    check(tuple(a.shape) == tuple(r.shape), "residual shape mismatch")
+    check(a.shape[1] <= 2048, "C must be <= 2048")
+    check(all(tuple(v.shape) == (a.shape[1],) for v in (bias, gamma, beta)), "bias/gamma/beta must be f32[C]")
+
+
+def add_bias_layernorm_f32_gpu(a, bias, r, gamma, beta, eps=1e-12):
+    """LayerNorm(a + bias + r) * gamma + beta (reference ops/kokoro_gpu.py:273-295)."""
+    _abln_check(a, bias, r, gamma, beta)
+    return _launch("add_bias_layernorm_f32_gpu", [a, bias, r, gamma, beta], [a.shape], dict(eps=float(eps)))
+
+
+def add_bias_layernorm2_f32_gpu(a, bias, r, gamma, beta, eps=1e-5):
+    """(s, LN(s)) with s = a + bias + r (reference ops/transformer.py:51-64)."""
+    _abln_check(a, bias, r, gamma, beta)
+    return _launch("add_bias_layernorm2_f32_gpu", [a, bias, r, gamma, beta], [a.shape, a.shape], dict(eps=float(eps)))
+
+
+def bias_gelu_f32_gpu(x, bias):
+    _f32(x, rank=2)
+    _bias_ok(bias, x.shape[1])
+    return _launch("bias_gelu_f32_gpu", [x, bias], [x.shape])
+
+
+def _attn_shape(qkv, bias, heads):
+    _f32(qkv, rank=2)
+    check(qkv.shape[1] == 3 * 64 * heads, "qkv must be f32[T, 3D] with head_dim = 64")
+    check(tuple(bias.shape) == (qkv.shape[1],), "bias must be f32[3D]")
+    return (qkv.shape[0], qkv.shape[1] // 3)
+
+
+def attention_qkv_f32_gpu(qkv, bias, heads, causal=False):
+    s = _attn_shape(qkv, bias, heads)
+    return _launch("attention_qkv_causal_f32_gpu" if causal else "attention_qkv_f32_gpu", [qkv, bias], [s],
+                  dict(heads=int(heads)))
+
+
+def attention_qkv_sg_f32_gpu(qkv, bias, heads, causal=False, nsg=4):
+    """Flash SDPA over fused QKV + bias (reference ops/transformer.py:297-307); nsg is a Metal launch shape and is
+    accepted for ABI compatibility."""
+    s = _attn_shape(qkv, bias, heads)
+    return _launch("attention_qkv_sg_causal_f32_gpu" if causal else "attention_qkv_sg_f32_gpu", [qkv, bias], [s],
+                  dict(heads=int(heads), nsg=int(nsg)))
+
+
+def _decode_check(qkv, kc, vc, pos, bias, heads):
+    _f32(qkv, kc, vc, rank=2)
+    d = kc.shape[1]
+    check(qkv.shape == (1, 3 * d) and vc.shape == kc.shape and d == 64 * heads, "decode attention: bad shapes")
+    check(pos.dtype == i64 and tuple(pos.shape) == (1,), "pos must be i64[1]")
+    check(tuple(bias.shape) == (3 * d,), "bias must be f32[3D]")
+    _gpu(pos)
+    return (1, d)
+
+
+def attention_decode_split_f32_gpu(qkv, kcache, vcache, pos, bias, heads, splits=0, nsg=0, single=1):
+    """Writes k, v (+ bias) at row pos of the caches (in place) and attends one query over rows 0..pos
+    (reference ops/transformer.py:323-337). pos is a device i64[1]; the caller guarantees pos < cache rows."""
+    s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
+    return _launch("attention_decode_split_f32_gpu", [qkv, kcache, vcache, pos, bias], [s],
+                  dict(heads=int(heads), nsg=int(nsg), single=int(single), splits=int(splits)))
+
+
+def attention_decode_kvw_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
+    s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
+    return _launch("attention_decode_kvw_f32_gpu", [qkv, kcache, vcache, pos, bias], [s], dict(heads=int(heads)))
+
+
+def attention_decode_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
+    s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
+    return _launch("attention_decode_f32_gpu", [qkv, kcache, vcache, pos, bias], [s], dict(heads=int(heads)))
+
+
+def kv_write_f32_gpu(kcache, vcache, qkv, pos, bias):
+    _decode_check(qkv, kcache, vcache, pos, bias, kcache.shape[1] // 64)
+    return _launch("kv_write_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[])
+
+
+# ---- Kokoro frame-rate (channel-last) -------------------------------------------------------------------------
+
+def channel_stats_lc_f32_gpu(x):
+    """Per-(128-row chunk, channel) (mean, M2) of x f32[L, C] -> f32[ceil(L / 128), C, 2]."""
+    _f32(x, rank=2)
+    return _launch("channel_stats_lc_f32_gpu", [x], [(-(-x.shape[0] // STAT_CHUNK), x.shape[1], 2)])
+
+
+def adain_affine_lc_f32_gpu(stats, gb, length, eps=1e-5):
+    """AdaIN affine f32[3, C] = (mean, (1 + g) / std, b) from channel_stats_lc over `length` rows; channels past
+    len(gb) / 2 get (0, 0, 0) (reference ops/kokoro_gpu.py:104-118)."""
+    _f32(stats, rank=3)
+    _f32(gb, rank=1)
+    c = stats.shape[1]
+    check(gb.shape[0] % 2 == 0 and gb.shape[0] // 2 <= c, "gb must be f32[2 Creal] with Creal <= C")
+    check(stats.shape[0] == -(-int(length) // STAT_CHUNK), "stats chunks don't match length")
+    return _launch("adain_affine_lc_f32_gpu", [stats, gb], [(3, c)], dict(eps=float(eps), length=int(length)))
+
+
+def snake_affine_lc_f32_gpu(x, affine, alpha):
+    _f32(x, affine, rank=2)
+    check(affine.shape == (3, x.shape[1]) and alpha.shape == (x.shape[1],), "affine f32[3, C], alpha f32[C]")
+    return _launch("snake_affine_lc_f32_gpu", [x, affine, alpha], [x.shape])
+
+
+def leaky_lc_f32_gpu(x, slope, affine=None):
+    _f32(x, rank=2)
+    if affine is None:
+        return _launch("leaky_lc_f32_gpu", [x], [x.shape], dict(slope=float(slope)))
+    check(affine.shape == (3, x.shape[1]), "affine must be f32[3, C]")
+    return _launch("leaky_affine_lc_f32_gpu", [x, affine], [x.shape], dict(slope=float(slope)))
+
+
+def convt_gather_lc_f32_gpu(y, b, kernel, stride, padding, add=None, reflect_left=False):
+    """ConvTranspose1d overlap-add of y = x @ W[Ci, K*Co] (f32[Lin, K*Co]) + b [+ add] -> f32[Lout, Co]
+    (reference ops/kokoro_gpu.py:151-160; `kernel` is the kernel size)."""
+    k = int(kernel)
+    _f32(y, rank=2)
+    co = b.shape[0]
+    check(y.shape[1] == k * co, "y must be f32[Lin, K * Co]")
+    rl = 1 if reflect_left else 0
+    lout = (y.shape[0] - 1) * stride - 2 * padding + k + rl
+    check(lout >= (2 if rl else 1), "empty convT output")
+    attrs = dict(kernel=k, padding=int(padding), reflect_left=rl, stride=int(stride))
+    if add is None:
+        return _launch("convt_gather_lc_f32_gpu", [y, b], [(lout, co)], attrs)
+    check(tuple(add.shape) == (lout, co), "add shape mismatch")
+    return _launch("convt_gather_add_lc_f32_gpu", [y, b, add], [(lout, co)], attrs)
+
+
+
+def dwconvt_lc_f32_gpu(x, w, b, stride=2, padding=1):
+    _f32(x, w, rank=2)
+    check(w.shape[0] == x.shape[1] and b.shape == (x.shape[1],), "w must be f32[C, K], b f32[C]")
+    lout = (x.shape[0] - 1) * stride - 2 * padding + w.shape[1] + (stride - 1)
+    return _launch("dwconvt_lc_f32_gpu", [x, w, b], [(lout, x.shape[1])], dict(padding=int(padding), stride=int(stride)))
+
+
+def upsample2_lc_f32_gpu(x):
+    _f32(x, rank=2)
+    return _launch("upsample2_lc_f32_gpu", [x], [(2 * x.shape[0], x.shape[1])])
+
+
+def concat_pad_lc_f32_gpu(a, b=None, cout=None):
+    _f32(a, rank=2)
+    cb = 0 if b is None else b.shape[1]
+    total = a.shape[1] + cb
+    cout = -(-total // 16) * 16 if cout is None else int(cout)
+    check(cout >= total, "cout smaller than the concatenation")
+    if b is None:
+        return _launch("pad_cols_lc_f32_gpu", [a], [(a.shape[0], cout)], dict(cout=cout))
+    check(a.shape[0] == b.shape[0], "row counts differ")
+    return _launch("concat_pad_lc_f32_gpu", [a, b], [(a.shape[0], cout)], dict(cout=cout))
+
+
+def lc_to_cf_f32_gpu(x, channels):
+    _f32(x, rank=2)
+    check(x.shape[1] >= channels, "channels exceeds the padded width")
+    return _launch("lc_to_cf_f32_gpu", [x], [(int(channels), x.shape[0])], dict(channels=int(channels)))
+
+
+def transpose_f32_gpu(x):
+    _f32(x, rank=2)
+    return _launch("transpose_f32_gpu", [x], [(x.shape[1], x.shape[0])])
+
+
+def add_f32_gpu(a, b):
+    _f32(a, b)
+    check(tuple(a.shape) == tuple(b.shape), "shape mismatch")
+    return _launch("add_f32_gpu", [a, b], [a.shape])
+
+
+def mul_f32_gpu(a, b):
+    _f32(a, b)
+    check(tuple(a.shape) == tuple(b.shape), "shape mismatch")
+    return _launch("mul_f32_gpu", [a, b], [a.shape])
+
+
+def add3_scale_f32_gpu(a, b, c, scale):
+    _f32(a, b, c)
+    check(tuple(a.shape) == tuple(b.shape) == tuple(c.shape), "add3 shape mismatch")
+    return _launch("add3_scale_f32_gpu", [a, b, c], [a.shape], dict(scale=float(scale)))
+
+
+def istft_logits_lc_f32_gpu(x, n_fft=20, hop=5):
+    """torch.istft(exp(m) e^{i sin(p)}, periodic hann, center) from channel-last logits x f32[L, Cpad] -> f32[hop (L - 1)]
+    (reference ops/kokoro_gpu.py:183-195)."""
+    _f32(x, rank=2)
+    check(n_fft >= 2 and n_fft % 2 == 0 and hop >= 1 and x.shape[1] >= n_fft + 2 and x.shape[0] >= 2, "bad iSTFT")
+    return _launch("istft_logits_lc_f32_gpu", [x], [(hop * (x.shape[0] - 1),)], dict(hop=int(hop), n_fft=int(n_fft)))

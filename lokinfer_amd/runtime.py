@@ -1,0 +1,60 @@
+"""HIP execution context: one stream (torch's current stream on the device), one zero-initialised device
+workspace for kernels that merge partial results, and the launch path into the C-ABI registry.
+
+Replaces the reference's GpuContext (src/runtime/gpu_internal.h:53-290): Metal command buffers, arg tables and
+the params ring become plain HIP launches on one stream; errors come back as a status + message and are raised
+as LokinferError, the binding-level exception the reference raises from Status (python/ext/module.cpp:29-31).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from ._lib import LokinferError, lib
+
+WORKSPACE_BYTES = 64 << 20
+
+
+class GpuContext:
+    _shared: "GpuContext | None" = None
+
+    def __init__(self):
+        if not torch.cuda.is_available():
+            raise LokinferError("no HIP device available (the lokinfer GPU kernels need an MI355X / gfx950)")
+        self.device = torch.device("cuda", torch.cuda.current_device())
+        # First 64 KiB: ticket counters (must start at zero; kernels restore them), rest: partials.
+        self.workspace = torch.zeros(WORKSPACE_BYTES // 4, dtype=torch.float32, device=self.device)
+        self.lib = lib()
+        self._handles: dict[str, int] = {}
+
+    @classmethod
+    def shared(cls) -> "GpuContext":
+        if cls._shared is None:
+            cls._shared = GpuContext()
+        return cls._shared
+
+    def handle(self, name: str) -> int:
+        h = self._handles.get(name)
+        if h is None:
+            h = self.lib.lk_find_kernel(name.encode())
+            if not h:
+                raise LokinferError(f"unknown kernel '{name}'")
+            self._handles[name] = h
+        return h
+
+    def run(self, name: str, ptrs, ints, floats) -> None:
+        L = self.lib
+        n_p, n_i, n_f = len(ptrs), len(ints), len(floats)
+        pa = (C.c_void_p * max(1, n_p))(*ptrs)
+        ia = (C.c_int64 * max(1, n_i))(*ints)
+        fa = (C.c_double * max(1, n_f))(*floats)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        rc = L.lk_run_kernel(self.handle(name), pa, n_p, ia, n_i, fa, n_f, self.workspace.data_ptr(),
+                             self.workspace.numel() * 4, stream)
+        if rc != 0:
+            raise LokinferError(L.lk_last_error().decode())
+
+
+def synchronize() -> None:
+    torch.cuda.synchronize()

@@ -1,0 +1,167 @@
+"""Pins the CPU oracle (oracle/) against independent references: torch.nn.functional library routines, closed
+forms, brute-force loops and exact-arithmetic cases, chosen so that a dropped term, a wrong index or a
+transposed operand in the oracle fails one of them (reference tests: tests/kernels/test_kokoro_gpu.py,
+test_transformer_fused.py, test_gemm_bias_gpu.py in lariaus/lokinfer)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kernels as K
+from oracle import mnist
+
+rng = np.random.default_rng(0)
+
+
+def T(a):
+    return torch.from_numpy(np.asarray(a, np.float64))
+
+
+def test_gemm_against_torch_and_exact_integers():
+    a, b, bias, r = rng.standard_normal((7, 5)), rng.standard_normal((5, 3)), rng.standard_normal(3), rng.standard_normal((7, 3))
+    np.testing.assert_allclose(K.gemm(a, b, bias, "relu"), F.relu(T(a) @ T(b) + T(bias)).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(K.gemm(a, b.T.copy(), nt=True), (T(a) @ T(b)).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(K.gemm(a, b, bias, "gelu", r, 0.5),
+                               ((F.gelu(T(a) @ T(b) + T(bias), approximate="tanh") + T(r)) * 0.5).numpy(), rtol=1e-12)
+    ai, bi = np.arange(6.0).reshape(2, 3), np.arange(6.0).reshape(3, 2)
+    assert K.gemm(ai, bi).tolist() == [[10.0, 13.0], [28.0, 40.0]]
+
+
+def test_mnist_c_oracle_is_the_fma_chain():
+    a = rng.standard_normal((3, 37)).astype(np.float32)
+    b = rng.standard_normal((37, 5)).astype(np.float32)
+    bias = rng.standard_normal(5).astype(np.float32)
+    got = mnist.gemm_bias_act(a, b, bias, relu=True)
+    # brute force: the same fma chain in Python (math.fma is exactly rounded in double; emulate float32 fma by
+    # exact double product + sum rounded once, which is exact for float32 operands).
+    want = np.empty((3, 5), np.float32)
+    for i in range(3):
+        for j in range(5):
+            c = np.float32(0)
+            for p in range(37):
+                c = np.float32(float(a[i, p]) * float(b[p, j]) + float(c))
+            c = np.float32(c + bias[j])
+            want[i, j] = max(c, np.float32(0))
+    assert np.array_equal(got, want)
+    # and against float64 within float32 accumulation error
+    np.testing.assert_allclose(got, np.maximum(a.astype(np.float64) @ b + bias, 0), rtol=1e-5, atol=1e-5)
+
+
+def test_mnist_plumbing_inputs_are_lk_randn():
+    x, (w1, b1, w2, b2) = mnist.mlp_inputs()
+    assert x.shape == (1, 784) and w1.shape == (784, 128) and w2.shape == (128, 10)
+    assert np.array_equal(x, np.random.default_rng(mnist.SEEDS["x"]).standard_normal((1, 784)).astype(np.float32))
+    out = mnist.mlp_forward(x, (w1, b1, w2, b2))
+    ref = np.maximum(x.astype(np.float64) @ w1 + b1, 0) @ w2 + b2
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_layernorm_matches_torch():
+    x, g, b = rng.standard_normal((4, 33)), rng.standard_normal(33), rng.standard_normal(33)
+    np.testing.assert_allclose(K.layernorm(x, g, b, 1e-5), F.layer_norm(T(x), (33,), T(g), T(b), 1e-5).numpy(),
+                               rtol=1e-10, atol=1e-12)
+    s, ln = K.add_bias_layernorm2(x, g, x, g, b, 1e-12)
+    np.testing.assert_allclose(s, 2 * x + g)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_qkv_matches_sdpa(causal):
+    t, heads = 9, 2
+    qkv, bias = rng.standard_normal((t, 3 * 64 * heads)), rng.standard_normal(3 * 64 * heads)
+    x = T(qkv) + T(bias)
+    q, k, v = x.split(64 * heads, 1)
+    f = lambda z: z.view(t, heads, 64).transpose(0, 1)  # noqa: E731
+    ref = F.scaled_dot_product_attention(f(q), f(k), f(v), is_causal=causal).transpose(0, 1).reshape(t, -1)
+    np.testing.assert_allclose(K.attention_qkv(qkv, bias, heads, causal), ref.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_attention_qkv_drops_k_bias_exactly_in_math():
+    # softmax is invariant to the k-bias (q . bk is constant across keys): the reference drops it.
+    qkv, bias = rng.standard_normal((5, 192)), rng.standard_normal(192)
+    b2 = bias.copy()
+    b2[64:128] = 0
+    np.testing.assert_allclose(K.attention_qkv(qkv, bias, 1), K.attention_qkv(qkv, b2, 1), rtol=1e-10)
+
+
+def test_attention_decode_equals_full_causal_row():
+    heads, t = 2, 6
+    d = 64 * heads
+    qkv, bias = rng.standard_normal((t, 3 * d)), rng.standard_normal(3 * d)
+    full = K.attention_qkv(qkv, bias, heads, causal=True)
+    kc, vc = np.zeros((8, d)), np.zeros((8, d))
+    for p in range(t):
+        out, kc, vc = K.attention_decode(qkv[p:p + 1], kc, vc, p, bias, heads)
+        np.testing.assert_allclose(out[0], full[p], rtol=1e-10, atol=1e-12)
+
+
+def test_channel_stats_and_adain_affine_closed_form():
+    x = rng.standard_normal((300, 6)) * 3 + 1
+    st = K.channel_stats_lc(x)
+    assert st.shape == (3, 6, 2)
+    np.testing.assert_allclose(st[2, :, 0], x[256:].mean(0))
+    np.testing.assert_allclose(st[0, :, 1], ((x[:128] - x[:128].mean(0)) ** 2).sum(0))
+    gb = rng.standard_normal(8)  # Creal = 4 of C = 6
+    af = K.adain_affine_lc(st, gb, 300)
+    mean, var = x.mean(0), x.var(0)
+    np.testing.assert_allclose(af[0, :4], mean[:4], rtol=1e-12)
+    np.testing.assert_allclose(af[1, :4], (1 + gb[:4]) / np.sqrt(var[:4] + 1e-5), rtol=1e-12)
+    np.testing.assert_allclose(af[2, :4], gb[4:], rtol=1e-12)
+    assert np.all(af[:, 4:] == 0)
+    # AdaIN(x) = (1 + g) * instance_norm(x) + b
+    y = K.affine_act(x[:, :4], af[:, :4])
+    ref = (1 + T(gb[:4])) * F.instance_norm(T(x[:, :4]).T[None], eps=1e-5)[0].T + T(gb[4:])
+    np.testing.assert_allclose(y, ref.numpy(), rtol=1e-9, atol=1e-10)
+
+
+def test_snake_and_leaky():
+    x, a = rng.standard_normal((5, 3)), np.array([0.5, 1.0, 2.0])
+    np.testing.assert_allclose(K.affine_act(x, alpha=a, act="snake"), x + np.sin(a * x) ** 2 / a)
+    np.testing.assert_allclose(K.affine_act(x, act="leaky", slope=0.2), F.leaky_relu(T(x), 0.2).numpy())
+
+
+@pytest.mark.parametrize("k,pad,dil,stride", [(3, 1, 1, 1), (7, 9, 3, 1), (11, 25, 5, 1), (1, 0, 1, 1), (12, 3, 1, 6)])
+def test_conv1d_lc_matches_torch(k, pad, dil, stride):
+    x, w, b = rng.standard_normal((40, 16)), rng.standard_normal((8, 16, k)), rng.standard_normal(8)
+    ref = F.conv1d(T(x).T[None], T(w), T(b), stride=stride, padding=pad, dilation=dil)[0].T
+    got = K.conv1d_lc(x, w.transpose(0, 2, 1), b, padding=pad, dilation=dil, stride=stride)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("k,s,reflect", [(20, 10, False), (12, 6, True), (4, 2, False)])
+def test_convt_gather_matches_conv_transpose(k, s, reflect):
+    ci, co, lin = 5, 3, 9
+    x, w, b = rng.standard_normal((lin, ci)), rng.standard_normal((ci, co, k)), rng.standard_normal(co)
+    y = x @ w.transpose(0, 2, 1).reshape(ci, k * co)  # the GEMM half: [Lin, K*Co]
+    p = (k - s) // 2
+    ref = F.conv_transpose1d(T(x).T[None], T(w), T(b), stride=s, padding=p)
+    if reflect:
+        ref = F.pad(ref, (1, 0), mode="reflect")
+    np.testing.assert_allclose(K.convt_gather_lc(y, b, k, s, p, reflect_left=reflect), ref[0].T.numpy(), rtol=1e-10,
+                               atol=1e-10)
+
+
+def test_dwconvt_matches_grouped_conv_transpose():
+    c, lin = 4, 7
+    x, w, b = rng.standard_normal((lin, c)), rng.standard_normal((c, 1, 3)), rng.standard_normal(c)
+    ref = F.conv_transpose1d(T(x).T[None], T(w), T(b), stride=2, padding=1, output_padding=1, groups=c)[0].T
+    np.testing.assert_allclose(K.dwconvt_lc(x, w[:, 0, :], b), ref.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_istft_matches_torch_istft():
+    l, n_fft, hop = 30, 20, 5
+    bins = n_fft // 2 + 1
+    x = rng.standard_normal((l, 2 * bins + 3)) * 0.5
+    spec = torch.exp(T(x[:, :bins])) * torch.exp(1j * torch.sin(T(x[:, bins:2 * bins])))
+    ref = torch.istft(spec.T, n_fft, hop, window=torch.hann_window(n_fft, periodic=True, dtype=torch.float64),
+                      center=True)
+    got = K.istft_logits(x, n_fft, hop)
+    assert got.shape == ref.shape == (hop * (l - 1),)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-9, atol=1e-10)
+
+
+def test_gelu_tanh_closed_form_points():
+    assert K.gelu_tanh(0.0) == 0.0
+    v = 1.5
+    assert math.isclose(float(K.gelu_tanh(v)), 0.5 * v * (1 + math.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3))))
