@@ -90,6 +90,12 @@ int lk_hip_elementwise_f32(const float* a, const float* b, const float* c, float
                            void* stream);
 int lk_hip_istft_lc_f32(const float* x, float* out, int64_t l, int64_t cpad, int nfft, int hop, void* stream);
 
+/* ---- token-rate front end on the device (reference: host kernels embedding_f32_cpu kernels/cpu/kokoro_norm.cpp,
+ *      GPT-2 argmax in Python models/gpt2.py:348-359) ---- */
+int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* table2, const int64_t* ids2, float* out,
+                         int64_t n, int64_t d, int64_t rows, int64_t rows2, void* stream);
+int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

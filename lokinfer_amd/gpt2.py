@@ -1,0 +1,92 @@
+"""GPT-2 124M decode step on the MI355X kernels: the graph of the reference's `build_decode(sd, device="gpu")`
+(models/gpt2.py:161-249 in lariaus/lokinfer), GPU-resident end to end.
+
+Per step (inputs tok i64[1], pos i64[1], both on the device):
+  h = wte[tok] + wpe[pos];  ln = LN_1(h)
+  per layer: qkv = gemv4(ln, c_attn.W) -> attention_decode_split (writes k, v + bias at row pos of the layer's
+             persistent [1024, 768] caches, attends over rows 0..pos) -> gemv4(., c_proj.W) ->
+             (h, ln) = add_bias_layernorm2(., c_proj.b, h, LN_2) -> gemv4_bias_gelu(ln, c_fc) -> gemv4(., mlp.c_proj.W)
+             -> (h, ln) = add_bias_layernorm2(., mlp.c_proj.b, h, next LN_1 or ln_f)
+  logits = ln . wte^T (tied LM head, gemm_nt);  next = argmax(logits) on the device
+The reference does the two embedding lookups on the CPU and the argmax in Python; here they are device kernels
+so a step is one captured HIP graph.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+from .compiler import compile as lk_compile
+from .tensor import Tensor, from_numpy
+
+N_LAYER, D, HEADS, N_POS, VOCAB, FFN = 12, 768, 12, 1024, 50257, 3072
+LN_EPS = 1e-5
+
+
+def param_shapes() -> dict[str, tuple]:
+    """HF GPT2LMHeadModel parameter names and shapes (Conv1D weights are [in, out])."""
+    s = {"transformer.wte.weight": (VOCAB, D), "transformer.wpe.weight": (N_POS, D),
+         "transformer.ln_f.weight": (D,), "transformer.ln_f.bias": (D,)}
+    for i in range(N_LAYER):
+        L = f"transformer.h.{i}."
+        s.update({L + "ln_1.weight": (D,), L + "ln_1.bias": (D,), L + "attn.c_attn.weight": (D, 3 * D),
+                  L + "attn.c_attn.bias": (3 * D,), L + "attn.c_proj.weight": (D, D), L + "attn.c_proj.bias": (D,),
+                  L + "ln_2.weight": (D,), L + "ln_2.bias": (D,), L + "mlp.c_fc.weight": (D, FFN),
+                  L + "mlp.c_fc.bias": (FFN,), L + "mlp.c_proj.weight": (FFN, D), L + "mlp.c_proj.bias": (D,)})
+    return s
+
+
+def random_weights(seed: int = 2024) -> dict[str, np.ndarray]:
+    """Random-init state dict: every parameter ~ N(0, 0.02) (numpy default_rng(seed + index) over the sorted
+    names), LayerNorm weights 1 + N(0, 0.02) so that every term of the LN is exercised."""
+    sd = {}
+    for i, (k, shape) in enumerate(sorted(param_shapes().items())):
+        a = np.random.default_rng(seed + i).standard_normal(shape).astype(np.float32) * np.float32(0.02)
+        if k.endswith(("ln_1.weight", "ln_2.weight", "ln_f.weight")):
+            a = a + np.float32(1.0)
+        sd[k] = a.astype(np.float32)
+    return sd
+
+
+class Gpt2Decoder:
+    """Weights uploaded once; 12 persistent K/V caches f32[1024, 768] on the device (the reference's
+    lk.persistent_buffer caches, models/gpt2.py:186-188)."""
+
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True):
+        self.w = {k: from_numpy(v, device="gpu", copy=True) for k, v in sd.items()}
+        dev = self.w["transformer.wte.weight"].t.device
+        self.caches = [(Tensor(torch.zeros(N_POS, D, device=dev)), Tensor(torch.zeros(N_POS, D, device=dev)))
+                       for _ in range(N_LAYER)]
+        self.step_model = lk_compile(self._step, graph=graph)
+
+    def _step(self, tok: Tensor, pos: Tensor):
+        w = self.w
+        P = "transformer."
+        h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos)
+        ln = ops.layernorm_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"], eps=LN_EPS)
+        for i, (kc, vc) in enumerate(self.caches):
+            L = f"{P}h.{i}."
+            nxt = f"{P}h.{i + 1}.ln_1." if i + 1 < N_LAYER else P + "ln_f."
+            qkv = ops.gemv4_f32_gpu(ln, w[L + "attn.c_attn.weight"])
+            att = ops.attention_decode_split_f32_gpu(qkv, kc, vc, pos, w[L + "attn.c_attn.bias"], heads=HEADS)
+            o = ops.gemv4_f32_gpu(att, w[L + "attn.c_proj.weight"])
+            h, ln = ops.add_bias_layernorm2_f32_gpu(o, w[L + "attn.c_proj.bias"], h, w[L + "ln_2.weight"],
+                                                    w[L + "ln_2.bias"], eps=LN_EPS)
+            f = ops.gemv4_f32_gpu(ln, w[L + "mlp.c_fc.weight"], w[L + "mlp.c_fc.bias"], act="gelu")
+            o = ops.gemv4_f32_gpu(f, w[L + "mlp.c_proj.weight"])
+            h, ln = ops.add_bias_layernorm2_f32_gpu(o, w[L + "mlp.c_proj.bias"], h, w[nxt + "weight"], w[nxt + "bias"],
+                                                    eps=LN_EPS)
+        logits = ops.gemm_nt_f32_gpu_mps(ln, w[P + "wte.weight"])
+        return logits, ops.argmax_f32_gpu(logits)
+
+    def step(self, tok: Tensor, pos: Tensor):
+        """One decode step; returns (logits f32[1, 50257], argmax i64[1]) as the graph's output buffers
+        (overwritten by the next step)."""
+        return self.step_model.run_inplace(tok, pos)
+
+    def prefill(self, ids: np.ndarray) -> None:
+        """Fills the caches by stepping the prompt tokens at positions 0..len-1."""
+        dev = self.w["transformer.wte.weight"].t.device
+        for p, t in enumerate(np.asarray(ids, np.int64)):
+            self.step(Tensor(torch.tensor([int(t)], device=dev)), Tensor(torch.tensor([p], device=dev)))

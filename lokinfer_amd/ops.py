@@ -455,3 +455,27 @@ def istft_logits_lc_f32_gpu(x, n_fft=20, hop=5):
     _f32(x, rank=2)
     check(n_fft >= 2 and n_fft % 2 == 0 and hop >= 1 and x.shape[1] >= n_fft + 2 and x.shape[0] >= 2, "bad iSTFT")
     return _launch("istft_logits_lc_f32_gpu", [x], [(hop * (x.shape[0] - 1),)], dict(hop=int(hop), n_fft=int(n_fft)))
+
+
+# ---- token-rate front end (MI355X backend: the reference runs these on the host) ------------------------------
+
+def embedding_f32_gpu(table, ids):
+    """(MI355X backend) rows of table f32[V, D] at ids i64[N] -> f32[N, D]; an out-of-range id gives a NaN row
+    (the reference's embedding_f32_cpu reports an error instead; a device kernel cannot)."""
+    _f32(table, rank=2)
+    check(ids.dtype == i64 and ids.ndim == 1, "ids must be i64[N]")
+    return _launch("embedding_f32_gpu", [table, ids], [(ids.shape[0], table.shape[1])], out_dtypes=[f32])
+
+
+def embedding2_add_f32_gpu(table, ids, table2, ids2):
+    """(MI355X backend) table[ids] + table2[ids2] (GPT-2 token + position embedding) -> f32[N, D]."""
+    _f32(table, table2, rank=2)
+    check(table.shape[1] == table2.shape[1] and ids.shape == ids2.shape and ids.dtype == i64 == ids2.dtype,
+          "embedding2_add: shape mismatch")
+    return _launch("embedding2_add_f32_gpu", [table, ids, table2, ids2], [(ids.shape[0], table.shape[1])])
+
+
+def argmax_f32_gpu(x):
+    """(MI355X backend) first index of the row maximum of x f32[R, N] -> i64[R] (greedy decoding on device)."""
+    _f32(x, rank=2)
+    return _launch("argmax_f32_gpu", [x], [(x.shape[0],)], out_dtypes=[i64])
