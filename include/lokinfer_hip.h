@@ -12,9 +12,9 @@
  * 2. Typed launchers (lk_hip_*), one per kernel family. The registry entries are thin decoders over these.
  *    Each launcher cites the reference kernel it replaces. All enqueue on `stream` and never synchronise.
  *
- * Workspace: kernels that merge partial results across workgroups (gemv, decode attention) take a
- * caller-owned device workspace whose first 64 KiB are ticket counters. The owner zero-fills it once; every
- * kernel leaves the counters at zero. Calls that share one workspace must be ordered (one stream).
+ * Workspace: kernels that merge partial results across workgroups (split-key decode attention) take a
+ * caller-owned device workspace for the partials and merge them in a second launch on the same stream.
+ * Calls that share one workspace must be ordered (one stream).
  */
 #ifndef LOKINFER_HIP_H
 #define LOKINFER_HIP_H
@@ -53,9 +53,8 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
                          const float* affine, const float* alpha, int pre, float slope, void* stream);
 
 /* ---- GEMV (reference: gemv4*_f32_gpu transformer_gpu.cpp:233-251; gemv_rows / gemv1_bias kokoro_lc.cpp:227-267) */
-int64_t lk_hip_gemv_workspace_bytes(int64_t n, int64_t k);
 int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,
-                    int64_t k, int act, void* workspace, int64_t workspace_bytes, void* stream);
+                    int64_t k, int act, void* stream);
 int lk_hip_rowdot_f32(const float* mat, const float* vec, const float* bias, int bias_per_row, float* out,
                       int64_t rows, int64_t k, int nvec, int64_t ldo, void* stream);
 
@@ -65,10 +64,11 @@ int lk_hip_layernorm_f32(const float* a, const float* bias, const float* r, cons
 int lk_hip_bias_gelu_f32(const float* x, const float* bias, float* out, int64_t rows, int64_t cols, void* stream);
 int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, int64_t t, int heads, int causal,
                              void* stream);
+/* split-key decode attention (64-key chunks + merge launch); pos is a device i64[1] */
 int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap);
 int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
-                                float* out, int64_t cap, int heads, int64_t max_keys, int keys_per_split,
-                                int write_kv, void* workspace, int64_t workspace_bytes, void* stream);
+                                float* out, int64_t cap, int heads, int64_t max_keys, int write_kv, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
                         void* stream);
 
@@ -94,7 +94,8 @@ int lk_hip_istft_lc_f32(const float* x, float* out, int64_t l, int64_t cpad, int
  *      GPT-2 argmax in Python models/gpt2.py:348-359) ---- */
 int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* table2, const int64_t* ids2, float* out,
                          int64_t n, int64_t d, int64_t rows, int64_t rows2, void* stream);
-int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* stream);
+int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

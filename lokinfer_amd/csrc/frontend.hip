@@ -25,19 +25,26 @@ __global__ void embeddingKernel(const float* __restrict__ table, const int64_t* 
   }
 }
 
-// One workgroup per row: (value, index) max with ties to the lower index (numpy / torch argmax semantics).
-__global__ __launch_bounds__(256) void argmaxKernel(const float* __restrict__ x, int64_t* __restrict__ out,
-                                                   int64_t n) {
+// Two launches: workgroup (c, r) reduces chunk c of row r to (value, index) with ties to the lower index
+// (numpy / torch argmax semantics) into the workspace; then one workgroup per row reduces the chunks in order.
+// mode 0: x is the row data (chunked); mode 1: x is the [rows][chunks] partial values, idx the partial indices.
+__global__ __launch_bounds__(256) void argmaxKernel(const float* __restrict__ x, const int64_t* __restrict__ idxIn,
+                                                   float* __restrict__ pv, int64_t* __restrict__ pi,
+                                                   int64_t* __restrict__ out, int64_t n, int64_t chunk) {
   __shared__ float sv[4];
   __shared__ int64_t si[4];
-  const float* row = x + static_cast<int64_t>(blockIdx.x) * n;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t c1 = min<int64_t>(n, c0 + chunk);
+  const float* row = x + static_cast<int64_t>(blockIdx.y) * n;
+  const int64_t* irow = idxIn ? idxIn + static_cast<int64_t>(blockIdx.y) * n : nullptr;
   float best = -INFINITY;
-  int64_t bi = n;
-  for (int64_t i = threadIdx.x; i < n; i += 256) {
+  int64_t bi = INT64_MAX;
+  for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
     const float v = row[i];
-    if (v > best || (bi == n && !(v < best))) {  // first element (also -inf / NaN rows) seeds the index
+    const int64_t gi = irow ? irow[i] : i;
+    if (v > best || (!(v < best) && gi < bi)) {
       best = v;
-      bi = i;
+      bi = gi;
     }
   }
 #pragma unroll
@@ -61,7 +68,12 @@ __global__ __launch_bounds__(256) void argmaxKernel(const float* __restrict__ x,
         best = sv[w];
         bi = si[w];
       }
-    out[blockIdx.x] = bi < n ? bi : 0;
+    if (out) {
+      out[blockIdx.y] = bi == INT64_MAX ? 0 : bi;
+    } else {
+      pv[static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = best;
+      pi[static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = bi;
+    }
   }
 }
 
@@ -80,10 +92,23 @@ int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* ta
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* stream) {
+int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
+                      int64_t workspaceBytes, void* stream) {
   if (rows <= 0 || n <= 0) return 1;
-  hipLaunchKernelGGL(lkd::argmaxKernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, out, n);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t chunk = 2048;
+  const int64_t chunks = (n + chunk - 1) / chunk;
+  if (chunks == 1 || !workspace || workspaceBytes < rows * chunks * 16) {
+    hipLaunchKernelGGL(lkd::argmaxKernel, dim3(1, static_cast<unsigned>(rows)), dim3(256), 0, s, x, nullptr, nullptr,
+                       nullptr, out, n, n);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+  }
+  float* pv = static_cast<float*>(workspace);
+  int64_t* pi = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + ((rows * chunks * 4 + 255) / 256) * 256);
+  hipLaunchKernelGGL(lkd::argmaxKernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), dim3(256), 0,
+                     s, x, nullptr, pv, pi, nullptr, n, chunk);
+  hipLaunchKernelGGL(lkd::argmaxKernel, dim3(1, static_cast<unsigned>(rows)), dim3(256), 0, s, pv, pi, nullptr,
+                     nullptr, out, chunks, chunks);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -112,7 +137,8 @@ void runEmbedding2(ExecCtx& ctx, const KernelArgs& a) {
 
 // argmax_f32_gpu(x[R, N]) -> i64[R]
 void runArgmax(ExecCtx& ctx, const KernelArgs& a) {
-  if (lk_hip_argmax_f32(P<float>(a, 0), P<int64_t>(a, 1), a.ints[0], a.ints[1], ctx.stream))
+  if (lk_hip_argmax_f32(P<float>(a, 0), P<int64_t>(a, 1), a.ints[0], a.ints[1], ctx.workspace,
+                        static_cast<int64_t>(ctx.workspaceBytes), ctx.stream))
     ctx.error = "argmax: launch failed";
 }
 

@@ -6,10 +6,11 @@
 //                     for the GPT-2 LM head, gemv_rows_f32_gpu kokoro_lc.cpp:227-254, gemv1_bias_f32_gpu
 //                     kokoro_lc.cpp:257-267 / vision.metal:266-284)
 //
-// gemv: each 256-thread workgroup owns 64 columns (16 lanes x float4) and a K-chunk (16 row slots); the K
-// split makes enough workgroups to keep HBM busy at N = 768. Partials land in the caller's workspace and the
-// last workgroup of a column group (atomic ticket) sums them in fixed split order, so results are
-// deterministic and the op stays one launch. The ticket counters are restored to 0 by that last workgroup.
+// gemv: one 1024-thread workgroup (16 waves) owns a 16-column slab of W over the whole K: 4 lanes x float4
+// cover the 16 columns (64 contiguous bytes of a row) and the 256 row slots stride K, so every thread has
+// K / 256 independent loads in flight. The 256 partial sums per column are reduced in LDS in a fixed order:
+// no cross-workgroup communication, deterministic results, one launch. N / 16 workgroups (48 at N = 768,
+// 192 at N = 3072) each stream K x 64 B.
 #include "common.h"
 
 #include <algorithm>
@@ -23,60 +24,64 @@ __device__ __forceinline__ float4 ntLoad4(const float* p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
+constexpr int kGemvCols = 16;
+constexpr int kGemvThreads = 1024;
+constexpr int kGemvSlots = kGemvThreads / (kGemvCols / 4);  // 256
+
 struct GemvParams {
   const float* x;
   const float* w;
   const float* bias;
   const float* res;
   float* out;
-  float* partial;       // [splits, N]
-  unsigned* tickets;    // [ceil(N / 64)], zero between calls
   int64_t n, k;
-  int splits;
-  int64_t kChunk;
   int act;  // 0 none, 2 gelu_tanh
 };
 
-__global__ __launch_bounds__(256) void gemvKernel(GemvParams p) {
-  __shared__ float4 red[16][17];
-  __shared__ bool last;
+__global__ __launch_bounds__(kGemvThreads) void gemvKernel(GemvParams p) {
+  __shared__ float4 red[kGemvSlots][kGemvCols / 4];
   const int tid = threadIdx.x;
-  const int cl = tid & 15, slot = tid >> 4;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + cl * 4;
-  const int s = blockIdx.y;
-  const int64_t kb = s * p.kChunk, ke = min(p.k, kb + p.kChunk);
+  const int cl = tid & 3, slot = tid >> 2;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * kGemvCols + cl * 4;
   const bool vec = (p.n & 3) == 0 && col + 3 < p.n;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t k = kb + slot; k < ke; k += 16) {
-    const float xv = p.x[k];
-    const float* wr = p.w + k * p.n + col;
-    float4 wv;
-    if (vec) {
-      wv = ntLoad4(wr);
-    } else {
-      wv.x = col < p.n ? wr[0] : 0.f;
-      wv.y = col + 1 < p.n ? wr[1] : 0.f;
-      wv.z = col + 2 < p.n ? wr[2] : 0.f;
-      wv.w = col + 3 < p.n ? wr[3] : 0.f;
+  if (col < p.n) {
+#pragma unroll 4
+    for (int64_t k = slot; k < p.k; k += kGemvSlots) {
+      const float xv = p.x[k];
+      const float* wr = p.w + k * p.n + col;
+      float4 wv;
+      if (vec) {
+        wv = ntLoad4(wr);
+      } else {
+        wv.x = wr[0];
+        wv.y = col + 1 < p.n ? wr[1] : 0.f;
+        wv.z = col + 2 < p.n ? wr[2] : 0.f;
+        wv.w = col + 3 < p.n ? wr[3] : 0.f;
+      }
+      acc.x += xv * wv.x;
+      acc.y += xv * wv.y;
+      acc.z += xv * wv.z;
+      acc.w += xv * wv.w;
     }
-    acc.x += xv * wv.x;
-    acc.y += xv * wv.y;
-    acc.z += xv * wv.z;
-    acc.w += xv * wv.w;
   }
   red[slot][cl] = acc;
   __syncthreads();
-  float4 tot = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (slot == 0) {
-    for (int j = 0; j < 16; ++j) {
-      const float4 v = red[j][cl];
-      tot.x += v.x;
-      tot.y += v.y;
-      tot.z += v.z;
-      tot.w += v.w;
+  // Tree over the 256 slots: 8 halvings, each step adds slot s + half into s.
+  for (int half = kGemvSlots / 2; half > 0; half >>= 1) {
+    if (slot < half) {
+      const float4 o = red[slot + half][cl];
+      float4 v = red[slot][cl];
+      v.x += o.x;
+      v.y += o.y;
+      v.z += o.z;
+      v.w += o.w;
+      red[slot][cl] = v;
     }
+    __syncthreads();
   }
-  auto finish = [&](float4 v) {
+  if (slot == 0) {
+    const float4 v = red[0][cl];
     const float vv[4] = {v.x, v.y, v.z, v.w};
     for (int q = 0; q < 4; ++q) {
       const int64_t c = col + q;
@@ -87,38 +92,7 @@ __global__ __launch_bounds__(256) void gemvKernel(GemvParams p) {
       if (p.res) o += p.res[c];
       p.out[c] = o;
     }
-  };
-  if (p.splits == 1) {
-    if (slot == 0) finish(tot);
-    return;
   }
-  if (slot == 0) {
-    const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
-    for (int q = 0; q < 4; ++q)
-      if (col + q < p.n) p.partial[static_cast<int64_t>(s) * p.n + col + q] = tv[q];
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned t = atomicAdd(&p.tickets[blockIdx.x], 1u);
-    last = (t == static_cast<unsigned>(p.splits - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (slot == 0) {
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < p.splits; ++j) {
-      const float* pr = p.partial + static_cast<int64_t>(j) * p.n + col;
-      // Device-coherent reads: the partials were written by other workgroups (possibly other XCDs).
-      sum.x += col < p.n ? __hip_atomic_load(pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      sum.y += col + 1 < p.n ? __hip_atomic_load(pr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      sum.z += col + 2 < p.n ? __hip_atomic_load(pr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      sum.w += col + 3 < p.n ? __hip_atomic_load(pr + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
-    finish(sum);
-  }
-  if (tid == 0) p.tickets[blockIdx.x] = 0u;
 }
 
 // One wave per matrix row: out[m * ldo + r] = sum_k vec[m, k] mat[r, k] (+ bias). K % 4 == 0 (float4 loads).
@@ -132,9 +106,9 @@ __global__ __launch_bounds__(256) void rowdotKernel(const float* __restrict__ ma
     float acc[MV];
 #pragma unroll
     for (int m = 0; m < MV; ++m) acc[m] = 0.f;
-    const float4* mr = reinterpret_cast<const float4*>(mat + r * k);
+    const float* mr = mat + r * k;
     for (int64_t q = lane; q < k / 4; q += 64) {
-      const float4 a = ntLoad4(reinterpret_cast<const float*>(mr + q));
+      const float4 a = ntLoad4(mr + 4 * q);
 #pragma unroll
       for (int m = 0; m < MV; ++m) {
         const float4 v = reinterpret_cast<const float4*>(vec + m * k)[q];
@@ -156,15 +130,9 @@ __global__ __launch_bounds__(256) void rowdotKernel(const float* __restrict__ ma
 
 extern "C" {
 
-// Workspace bytes gemv needs: tickets (64 KiB, zero-initialised once by the owner) + partials.
-int64_t lk_hip_gemv_workspace_bytes(int64_t n, int64_t k) {
-  (void)k;
-  return 65536 + 64 * n * static_cast<int64_t>(sizeof(float));
-}
-
 int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,
-                    int64_t k, int act, void* workspace, int64_t workspaceBytes, void* stream) {
-  if (n <= 0) return n == 0 ? 0 : 1;
+                    int64_t k, int act, void* stream) {
+  if (n <= 0 || k < 0) return n == 0 ? 0 : 1;
   lkd::GemvParams p{};
   p.x = x;
   p.w = w;
@@ -174,19 +142,8 @@ int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const flo
   p.n = n;
   p.k = k;
   p.act = act;
-  const int64_t colGroups = (n + 63) / 64;
-  // Aim for ~1024 workgroups; each split covers at least 32 rows.
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>((1024 + colGroups - 1) / colGroups, (k + 31) / 32));
-  splits = std::min<int64_t>(splits, 64);
-  if (splits > 1 && (workspace == nullptr || colGroups > 16384 ||
-                     workspaceBytes < 65536 + splits * n * static_cast<int64_t>(sizeof(float))))
-    splits = 1;
-  p.splits = static_cast<int>(splits);
-  p.kChunk = (k + splits - 1) / splits;
-  p.tickets = static_cast<unsigned*>(workspace);
-  p.partial = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + 65536) : nullptr;
-  dim3 grid(static_cast<unsigned>(colGroups), static_cast<unsigned>(splits));
-  hipLaunchKernelGGL(lkd::gemvKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  const unsigned blocks = lkh::ceilDiv(n, lkd::kGemvCols);
+  hipLaunchKernelGGL(lkd::gemvKernel, dim3(blocks), dim3(lkd::kGemvThreads), 0, static_cast<hipStream_t>(stream), p);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

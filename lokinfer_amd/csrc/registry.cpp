@@ -104,8 +104,7 @@ void runGemv(ExecCtx& ctx, const KernelArgs& a) {
   int idx = 2;
   const float* bias = BIAS ? P<float>(a, idx++) : nullptr;
   const float* res = RES ? P<float>(a, idx++) : nullptr;
-  status(ctx, lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), bias, res, P<float>(a, idx), n, k, ACT, ctx.workspace,
-                              static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
+  status(ctx, lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), bias, res, P<float>(a, idx), n, k, ACT, ctx.stream),
          "gemv: launch failed");
 }
 
@@ -264,11 +263,11 @@ void runAttnDecode(ExecCtx& ctx, const KernelArgs& a) {
     splitsAttr = static_cast<int>(it.next());
   }
   LK_REQUIRE(ctx, d3 == 3 * d && d == 64 * heads, "attention_decode: head_dim must be 64, qkv f32[1, 3D]");
-  // splits attr (reference: number of key splits, 0 = auto) -> keys per split.
-  int kps = 0;
-  if (splitsAttr > 0) kps = static_cast<int>((cap + splitsAttr - 1) / splitsAttr);
+  // The splits attr (reference: Metal key-split count, 0 = auto) has no meaning here: the CDNA4 kernel always
+  // uses 64-key chunks (one wave each) and a merge launch.
+  (void)splitsAttr;
   const int rc = lk_hip_attention_decode_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
-                                             P<float>(a, 4), P<float>(a, 5), cap, heads, cap, kps, WRITE ? 1 : 0,
+                                             P<float>(a, 4), P<float>(a, 5), cap, heads, cap, WRITE ? 1 : 0,
                                              ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream);
   status(ctx, rc, rc == 3 ? "attention_decode: workspace too small" : "attention_decode: launch failed");
 }

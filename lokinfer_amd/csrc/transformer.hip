@@ -5,9 +5,7 @@
 //   lk_hip_bias_gelu_f32         gelu_tanh(x + bias)            (bias_gelu_f32_gpu, kokoro_tok.metal:25-34)
 //   lk_hip_attention_qkv_f32     SDPA over a fused QKV [T, 3D]  (attention_qkv[_sg][_causal]_f32_gpu,
 //                                transformer_gpu.cpp:72-86, kokoro_tok.metal:465-601)
-//   lk_hip_attention_decode_f32  fused KV write + one-query attention over rows 0..pos, split over keys with an
-//                                in-kernel combine (attention_decode_split_f32_gpu, transformer_gpu.cpp:122-222,
-//                                kokoro_tok.metal:637-876)
+//   lk_hip_kv_write_f32          k, v (+ bias) into row pos of the caches (kv_write_f32_gpu, kokoro_lc.cpp:826-872)
 //
 // Rows are reduced by a whole workgroup with wave64 shuffles; statistics use the reference's two-pass form
 // (mean, then the centred sum of squares) with the biased variance.
@@ -114,118 +112,6 @@ __global__ __launch_bounds__(64) void attnQkvKernel(const float* __restrict__ qk
   for (int d = 0; d < HD; ++d) o[d] = acc[d] * inv + bias[2 * D + h * HD + d];
 }
 
-// Decode attention, one wave per (head, key split): lane j scores key kb + j against q (q = (q + bq) / 8),
-// then p = exp(s - m_split), acc[d] = sum p v[d] with lane = d. Row `pos` comes from qkv + bias (and the block
-// owning it writes it to both caches). Partials (m, l, acc[64]) go to the workspace; the last split of a head
-// (atomic ticket) merges them in split order.
-struct DecodeParams {
-  const float* qkv;
-  float* kc;
-  float* vc;
-  const int64_t* pos;
-  const float* bias;
-  float* out;
-  float* partial;     // [heads, splits, 66]
-  unsigned* tickets;  // [heads]
-  int64_t cap;
-  int heads;
-  int keysPerSplit;
-  int splits;
-  int writeKv;
-};
-
-__global__ __launch_bounds__(64) void decodeAttnKernel(DecodeParams p) {
-  constexpr int HD = 64;
-  __shared__ bool last;
-  const int h = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
-  const int64_t D = static_cast<int64_t>(p.heads) * HD;
-  const int64_t pos = *p.pos;
-  if (pos < 0 || pos >= p.cap) {  // out-of-range position: no cache write, NaN output (every block exits here)
-    if (s == 0) p.out[h * HD + lane] = __builtin_nanf("");
-    return;
-  }
-  const int64_t kb = static_cast<int64_t>(s) * p.keysPerSplit;
-  const int64_t ke = min<int64_t>(pos + 1, kb + p.keysPerSplit);
-  const float* qrow = p.qkv + h * HD;
-  // New key / value row (bias added), lane = dim.
-  const float knew = p.qkv[D + h * HD + lane] + p.bias[D + h * HD + lane];
-  const float vnew = p.qkv[2 * D + h * HD + lane] + p.bias[2 * D + h * HD + lane];
-  if (p.writeKv && pos >= kb && pos < kb + p.keysPerSplit) {
-    p.kc[pos * D + h * HD + lane] = knew;
-    p.vc[pos * D + h * HD + lane] = vnew;
-  }
-  float q[HD];
-#pragma unroll
-  for (int d = 0; d < HD; ++d) q[d] = (qrow[d] + p.bias[h * HD + d]) * 0.125f;
-  // Score of the new key (row pos), computed by the whole wave: lane d holds q[d] and k_new[d].
-  const float snew = waveSum((qrow[lane] + p.bias[h * HD + lane]) * 0.125f * knew);
-  float m = -INFINITY, l = 0.0f, acc = 0.0f;
-  for (int64_t c0 = kb; c0 < ke; c0 += 64) {
-    const int64_t j = c0 + lane;
-    float sc = -INFINITY;
-    if (j < ke) {
-      float dot = snew;
-      if (j != pos) {
-        dot = 0.0f;
-        const float4* kr = reinterpret_cast<const float4*>(p.kc + j * D + h * HD);
-#pragma unroll
-        for (int d4 = 0; d4 < HD / 4; ++d4) {
-          const float4 kv = kr[d4];
-          dot += q[4 * d4] * kv.x + q[4 * d4 + 1] * kv.y + q[4 * d4 + 2] * kv.z + q[4 * d4 + 3] * kv.w;
-        }
-      }
-      sc = dot;
-    }
-    const float cm = waveMax(sc);
-    const float mn = fmaxf(m, cm);
-    const float pj = j < ke ? expf(sc - mn) : 0.0f;
-    const float corr = expf(m - mn);
-    l = l * corr + waveSum(pj);
-    acc *= corr;
-    const int nk = static_cast<int>(min<int64_t>(64, ke - c0));
-    for (int jj = 0; jj < nk; ++jj) {
-      const float pw = __shfl(pj, jj, 64);
-      const int64_t row = c0 + jj;
-      const float vv = row == pos ? vnew : p.vc[row * D + h * HD + lane];
-      acc += pw * vv;
-    }
-    m = mn;
-  }
-  if (p.splits == 1) {
-    p.out[h * HD + lane] = acc / l;
-    return;
-  }
-  float* part = p.partial + (static_cast<int64_t>(h) * p.splits + s) * (HD + 2);
-  part[2 + lane] = acc;
-  if (lane == 0) {
-    part[0] = m;
-    part[1] = l;
-  }
-  __threadfence();
-  __syncthreads();
-  if (lane == 0) last = atomicAdd(&p.tickets[h], 1u) == static_cast<unsigned>(p.splits - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  float M = -INFINITY;
-  for (int i = 0; i < p.splits; ++i) {
-    const float* pi = p.partial + (static_cast<int64_t>(h) * p.splits + i) * (HD + 2);
-    M = fmaxf(M, __hip_atomic_load(pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  }
-  float L = 0.0f, A = 0.0f;
-  for (int i = 0; i < p.splits; ++i) {
-    const float* pi = p.partial + (static_cast<int64_t>(h) * p.splits + i) * (HD + 2);
-    const float mi = __hip_atomic_load(pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float li = __hip_atomic_load(pi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float ai = __hip_atomic_load(pi + 2 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float w = li > 0.0f ? expf(mi - M) : 0.0f;
-    L += li * w;
-    A += ai * w;
-  }
-  p.out[h * HD + lane] = A / L;
-  if (lane == 0) p.tickets[h] = 0u;
-}
-
 __global__ void kvWriteKernel(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias,
                               int64_t d) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -263,44 +149,6 @@ int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, in
   dim3 grid(lkh::ceilDiv(t, 64), static_cast<unsigned>(heads));
   hipLaunchKernelGGL(lkd::attnQkvKernel, grid, dim3(64), 0, static_cast<hipStream_t>(stream), qkv, bias, out, t,
                      heads, causal);
-  return hipGetLastError() == hipSuccess ? 0 : 2;
-}
-
-int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap) {
-  const int64_t splits = (cap + 31) / 32;
-  return 65536 + static_cast<int64_t>(heads) * splits * 66 * 4;
-}
-
-// qkv [1, 3D] (before bias), kc / vc [cap, D] (rows 0..pos-1 valid; row pos written when writeKv), pos device
-// i64[1], bias [3D] -> out [1, D]. keysPerSplit 0 = auto. The caller guarantees pos < cap (checked on the host
-// by the registry entry, which reads nothing from the device; the kernel clamps nothing).
-int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
-                                float* out, int64_t cap, int heads, int64_t maxKeys, int keysPerSplit, int writeKv,
-                                void* workspace, int64_t workspaceBytes, void* stream) {
-  if (keysPerSplit <= 0) keysPerSplit = 32;
-  lkd::DecodeParams p{};
-  p.qkv = qkv;
-  p.kc = kc;
-  p.vc = vc;
-  p.pos = pos;
-  p.bias = bias;
-  p.out = out;
-  p.cap = cap;
-  p.heads = heads;
-  p.keysPerSplit = keysPerSplit;
-  p.writeKv = writeKv;
-  // maxKeys bounds pos + 1 for the grid; splits beyond the live keys exit after contributing l = 0.
-  int64_t splits = (maxKeys + keysPerSplit - 1) / keysPerSplit;
-  if (splits < 1) splits = 1;
-  if (splits > 1) {
-    const int64_t need = 65536 + static_cast<int64_t>(heads) * splits * 66 * 4;
-    if (!workspace || workspaceBytes < need) return 3;
-  }
-  p.splits = static_cast<int>(splits);
-  p.tickets = static_cast<unsigned*>(workspace);
-  p.partial = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + 65536) : nullptr;
-  dim3 grid(static_cast<unsigned>(heads), static_cast<unsigned>(splits));
-  hipLaunchKernelGGL(lkd::decodeAttnKernel, grid, dim3(64), 0, static_cast<hipStream_t>(stream), p);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
