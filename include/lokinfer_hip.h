@@ -97,6 +97,29 @@ int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* ta
 int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
+/* ---- Kokoro token-rate sequence kernels (reference host kernels: lstm_bidir[_t]_f32_cpu ops/kokoro.py:88-116,
+ *      repeat_interleave_f32_cpu kokoro_misc.cpp:253-265, adalayernorm_f32_cpu kokoro_norm.cpp:10-62,
+ *      concat_cols / broadcast_rows ops/kokoro.py:141-173) ---- */
+/* x [T, I], w_ih [8H, I], w_hh_t [H, 8H] (W_hh^T), b [8H] = b_ih + b_hh -> out [T, 2H]; workspace >= T * 8H floats */
+int lk_hip_lstm_bidir_f32(const float* x, const float* w_ih, const float* w_hh_t, const float* b, float* out,
+                          int64_t t, int64_t in, int64_t h, void* workspace, int64_t workspace_bytes, void* stream);
+int lk_hip_repeat_interleave_f32(const float* x, const int64_t* dur, float* out, int64_t t, int64_t c, int64_t frames,
+                                 void* stream);
+int lk_hip_adalayernorm_f32(const float* x, const float* gb, float* out, int64_t r, int64_t c, float eps,
+                            void* stream);
+int lk_hip_concat_bcast_f32(const float* x, const float* v, float* out, int64_t r, int64_t c1, int64_t c2,
+                            void* stream);
+
+/* ---- Kokoro signal path (reference host kernels: harmonic_source_f32_cpu kokoro_signal.cpp:89-192,
+ *      stft_magphase_f32_cpu kokoro_signal.cpp:196-273, decoder F0_conv / N_conv conv1d_f32_cpu) ---- */
+/* f0 [n], noise [300 n, 9], w [9], b [1] -> out [300 n]; workspace >= 9 n floats */
+int lk_hip_harmonic_source_f32(const float* f0, const float* noise, const float* w, const float* b, float* out,
+                               int64_t n, void* workspace, int64_t workspace_bytes, void* stream);
+/* x [S] -> out [S / hop + 1, ldo]: magnitude in columns 0..K-1, phase in K..2K-1 (K = nfft / 2 + 1), rest 0 */
+int lk_hip_stft_magphase_lc_f32(const float* x, float* out, int64_t s, int nfft, int hop, int64_t ldo, void* stream);
+int lk_hip_conv1d_1ch_f32(const float* x, const float* w, const float* b, float* out, int64_t l, int k, int stride,
+                          int pad, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,8 @@ void registerGemmKernels();
 void registerTransformerKernels();
 void registerKokoroKernels();
 void registerFrontendKernels();
+void registerSequenceKernels();
+void registerSignalKernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 

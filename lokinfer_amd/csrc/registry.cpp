@@ -465,6 +465,8 @@ static void registerAll() {
     registerTransformerKernels();
     registerKokoroKernels();
     registerFrontendKernels();
+    registerSequenceKernels();
+    registerSignalKernels();
     std::sort(names().begin(), names().end());
   });
 }

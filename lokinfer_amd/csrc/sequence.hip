@@ -1,0 +1,235 @@
+// Kokoro token-rate sequence kernels on the GPU (the reference runs these on the host CPU inside its GPU graph):
+//
+//   lk_hip_lstm_bidir_f32      1-layer bidirectional nn.LSTM (gates i, f, g, o; b = b_ih + b_hh)
+//                              (reference lstm_bidir_f32_cpu / lstm_bidir_t_f32_cpu, ops/kokoro.py:88-116,
+//                              kernels/cpu/kokoro_lstm.cpp)
+//   lk_hip_repeat_interleave_f32  x.repeat_interleave(dur, 0) (repeat_interleave_f32_cpu, kokoro_misc.cpp:253-265)
+//   lk_hip_adalayernorm_f32    (1 + g) * LN_noaffine(x) + b (adalayernorm_f32_cpu, kokoro_norm.cpp:10-62)
+//   lk_hip_concat_bcast_f32    [x | v] per row (concat_cols + broadcast_rows, ops/kokoro.py:141-173)
+//
+// LSTM design: the input projection of every step, G = x W_ih^T + b for both directions, is one MFMA GEMM; the
+// recurrence then runs as one 4H-thread workgroup per direction. Thread i owns gate row i and reads column i
+// of W_hh^T (layout [H, 8H], the reference's lstm_bidir_t weight) for k = 0..H-1, so a wave's 64 loads of one k
+// are 256 contiguous bytes; h(t-1) is broadcast from LDS. After a barrier, threads j < H apply the cell update
+// in the reference order (c = f c + i g, h = o tanh(c)). Both directions run concurrently on two CUs.
+#include "common.h"
+#include "lokinfer_hip.h"
+
+#include <algorithm>
+
+namespace lkd {
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// g: [T, 8H] gate pre-activations (forward gates in columns 0..4H, backward 4H..8H); whhT: [H, 8H];
+// out: [T, 2H] = [h_fwd | h_bwd]. blockIdx.x = direction, blockDim.x = 4H.
+__global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __restrict__ g,
+                                                            const float* __restrict__ whhT, float* __restrict__ out,
+                                                            int64_t t, int h) {
+  __shared__ float hs[256];
+  __shared__ float gs[1024];
+  const int dir = blockIdx.x, i = threadIdx.x;
+  const int g4 = 4 * h, ld = 8 * h;
+  float c = 0.0f;
+  if (i < h) hs[i] = 0.0f;
+  __syncthreads();
+  const float* wcol = whhT + dir * g4 + i;
+  for (int64_t step = 0; step < t; ++step) {
+    const int64_t tt = dir == 0 ? step : t - 1 - step;
+    float acc = g[tt * ld + dir * g4 + i];
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int k = 0;
+    for (; k + 4 <= h; k += 4) {
+      a0 += wcol[(k + 0) * ld] * hs[k + 0];
+      a1 += wcol[(k + 1) * ld] * hs[k + 1];
+      a2 += wcol[(k + 2) * ld] * hs[k + 2];
+      a3 += wcol[(k + 3) * ld] * hs[k + 3];
+    }
+    for (; k < h; ++k) a0 += wcol[k * ld] * hs[k];
+    acc += (a0 + a1) + (a2 + a3);
+    gs[i] = acc;
+    __syncthreads();
+    if (i < h) {
+      const float ig = sigmoidf(gs[i]), fg = sigmoidf(gs[h + i]);
+      const float gg = tanhf(gs[2 * h + i]), og = sigmoidf(gs[3 * h + i]);
+      c = fg * c + ig * gg;
+      const float hv = og * tanhf(c);
+      hs[i] = hv;
+      out[tt * 2 * h + dir * h + i] = hv;
+    }
+    __syncthreads();
+  }
+}
+
+// Each workgroup scans dur (T <= 8192) into LDS, then gathers its rows: row f copies x[token(f)], token(f) =
+// the first i with cum[i] > f.
+__global__ __launch_bounds__(256) void repeatInterleaveKernel(const float* __restrict__ x,
+                                                             const int64_t* __restrict__ dur, float* __restrict__ out,
+                                                             int64_t t, int64_t c, int64_t frames) {
+  __shared__ int64_t cum[8192];
+  __shared__ int64_t part[256];
+  const int tid = threadIdx.x;
+  const int64_t per = (t + 255) / 256;
+  int64_t s = 0;
+  for (int64_t i = tid * per; i < min<int64_t>(t, (tid + 1) * per); ++i) s += dur[i] > 0 ? dur[i] : 0;
+  part[tid] = s;
+  __syncthreads();
+  if (tid == 0)
+    for (int j = 1; j < 256; ++j) part[j] += part[j - 1];
+  __syncthreads();
+  int64_t run = tid == 0 ? 0 : part[tid - 1];
+  for (int64_t i = tid * per; i < min<int64_t>(t, (tid + 1) * per); ++i) {
+    run += dur[i] > 0 ? dur[i] : 0;
+    cum[i] = run;
+  }
+  __syncthreads();
+  const int64_t rowsPerBlock = (frames + gridDim.x - 1) / gridDim.x;
+  const int64_t r0 = blockIdx.x * rowsPerBlock, r1 = min<int64_t>(frames, r0 + rowsPerBlock);
+  for (int64_t f = r0; f < r1; ++f) {
+    int64_t lo = 0, hi = t;  // first i with cum[i] > f
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (cum[mid] > f) hi = mid;
+      else lo = mid + 1;
+    }
+    const bool ok = lo < t;
+    for (int64_t j = tid; j < c; j += 256) out[f * c + j] = ok ? x[lo * c + j] : __builtin_nanf("");
+  }
+}
+
+__device__ __forceinline__ float blockSum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = waveSum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  return scratch[0] + scratch[1] + scratch[2] + scratch[3];
+}
+
+// (1 + gb[c]) * (x - mean) / sqrt(var + eps) + gb[C + c]; one 256-thread workgroup per row, C <= 2048.
+__global__ __launch_bounds__(256) void adaLayerNormKernel(const float* __restrict__ x, const float* __restrict__ gb,
+                                                         float* __restrict__ out, int64_t c, float eps) {
+  __shared__ float scratch[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * c;
+  float v[8];
+  float s = 0.0f;
+  int n = 0;
+  for (int64_t j = threadIdx.x; j < c; j += 256, ++n) {
+    v[n] = x[base + j];
+    s += v[n];
+  }
+  const float mean = blockSum(s, scratch) / static_cast<float>(c);
+  float q = 0.0f;
+  for (int i = 0; i < n; ++i) q += (v[i] - mean) * (v[i] - mean);
+  const float rstd = 1.0f / sqrtf(blockSum(q, scratch) / static_cast<float>(c) + eps);
+  n = 0;
+  for (int64_t j = threadIdx.x; j < c; j += 256, ++n)
+    out[base + j] = (1.0f + gb[j]) * ((v[n] - mean) * rstd) + gb[c + j];
+}
+
+__global__ void concatBcastKernel(const float* __restrict__ x, const float* __restrict__ v, float* __restrict__ out,
+                                  int64_t r, int64_t c1, int64_t c2) {
+  const int64_t cw = c1 + c2, n = r * cw;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = i / cw, col = i - row * cw;
+    out[i] = col < c1 ? x[row * c1 + col] : v[col - c1];
+  }
+}
+
+}  // namespace lkd
+
+extern "C" {
+
+// x [T, I], w_ih [8H, I], w_hh_t [H, 8H], b [8H] -> out [T, 2H]; gates workspace: T * 8H floats.
+int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, const float* b, float* out, int64_t t,
+                          int64_t in, int64_t h, void* workspace, int64_t workspaceBytes, void* stream) {
+  if (h < 1 || h > 256 || t < 1) return 1;
+  if (!workspace || workspaceBytes < t * 8 * h * 4) return 3;
+  float* g = static_cast<float*>(workspace);
+  int rc = lk_hip_gemm_f32(x, wih, b, nullptr, g, t, 8 * h, in, 1, 0, 1.0f, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0,
+                     static_cast<hipStream_t>(stream), g, whhT, out, t, static_cast<int>(h));
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_repeat_interleave_f32(const float* x, const int64_t* dur, float* out, int64_t t, int64_t c, int64_t frames,
+                                 void* stream) {
+  if (t < 1 || t > 8192 || frames < 0) return 1;
+  if (frames == 0) return 0;
+  const int64_t blocks = std::min<int64_t>(frames, 1024);
+  hipLaunchKernelGGL(lkd::repeatInterleaveKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, dur, out, t, c, frames);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_adalayernorm_f32(const float* x, const float* gb, float* out, int64_t r, int64_t c, float eps,
+                            void* stream) {
+  if (c < 1 || c > 2048 || r < 1) return 1;
+  hipLaunchKernelGGL(lkd::adaLayerNormKernel, dim3(static_cast<unsigned>(r)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, gb, out, c, eps);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_concat_bcast_f32(const float* x, const float* v, float* out, int64_t r, int64_t c1, int64_t c2,
+                            void* stream) {
+  const int64_t n = r * (c1 + c2);
+  if (n <= 0) return n == 0 ? 0 : 1;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(lkd::concatBcastKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, v, out, r, c1, c2);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"
+
+namespace lkh {
+
+namespace {
+
+// lstm_bidir_t_f32_gpu(x[T, I], w_ih[8H, I], w_hh_t[H, 8H], b[8H]) -> [T, 2H]
+void runLstm(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t t = a.ints[0], in = a.ints[1];
+  const int64_t h = a.ints[4];
+  LK_REQUIRE(ctx, a.ints[2] == 8 * h && a.ints[3] == in && a.ints[5] == 8 * h && a.ints[6] == 8 * h,
+             "lstm_bidir_t: expected w_ih [8H, I], w_hh_t [H, 8H], b [8H]");
+  const int rc = lk_hip_lstm_bidir_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<float>(a, 3), P<float>(a, 4),
+                                       t, in, h, ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream);
+  if (rc) ctx.error = rc == 3 ? "lstm_bidir_t: workspace too small for the gate pre-activations" : "lstm: failed";
+}
+
+// repeat_interleave_f32_gpu(x[T, C], dur i64[T]; frames) -> [frames, C]
+void runRepeatInterleave(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t t = a.ints[0], c = a.ints[1], frames = a.ints[3];
+  if (lk_hip_repeat_interleave_f32(P<float>(a, 0), P<int64_t>(a, 1), P<float>(a, 2), t, c, frames, ctx.stream))
+    ctx.error = "repeat_interleave: T must be in 1..8192";
+}
+
+// adalayernorm_f32_gpu(x[R, C], gb[2C]; eps) -> [R, C]
+void runAdaLn(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t r = a.ints[0], c = a.ints[1];
+  LK_REQUIRE(ctx, a.ints[2] == 2 * c, "adalayernorm: gb must be f32[2C]");
+  if (lk_hip_adalayernorm_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), r, c,
+                              static_cast<float>(a.numFloats ? a.floats[0] : 1e-5), ctx.stream))
+    ctx.error = "adalayernorm: C must be <= 2048";
+}
+
+// concat_bcast_f32_gpu(x[R, C1], v[C2]) -> [R, C1 + C2]
+void runConcatBcast(ExecCtx& ctx, const KernelArgs& a) {
+  if (lk_hip_concat_bcast_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), a.ints[0], a.ints[1], a.ints[2],
+                              ctx.stream))
+    ctx.error = "concat_bcast: failed";
+}
+
+}  // namespace
+
+void registerSequenceKernels() {
+  const Device G = Device::Gpu;
+  registerKernel({"lstm_bidir_t_f32_gpu", G, runLstm, 4, 1});
+  registerKernel({"repeat_interleave_f32_gpu", G, runRepeatInterleave, 2, 1});
+  registerKernel({"adalayernorm_f32_gpu", G, runAdaLn, 2, 1});
+  registerKernel({"concat_bcast_f32_gpu", G, runConcatBcast, 2, 1});
+}
+
+}  // namespace lkh

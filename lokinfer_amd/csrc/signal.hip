@@ -1,0 +1,224 @@
+// Kokoro signal path on the GPU (the reference runs these as host CPU kernels, kernels/cpu/kokoro_signal.cpp):
+//
+//   lk_hip_harmonic_source_f32  hn-NSF source (SineGen, 9 harmonics) with explicit noise
+//                               (harmonic_source_f32_cpu, kokoro_signal.cpp:89-192)
+//   lk_hip_stft_magphase_lc_f32 STFT -> magnitude | phase, channel-last and zero-padded to a multiple of 16
+//                               columns for the implicit-GEMM conv that consumes it
+//                               (stft_magphase_f32_cpu, kokoro_signal.cpp:196-273)
+//   lk_hip_conv1d_1ch_f32       single-channel strided conv1d (the decoder's F0_conv / N_conv, which the
+//                               reference runs as conv1d_f32_cpu, models/kokoro/model.py:704-705)
+//
+// The harmonic source keeps the reference's f32 op order, which is PyTorch's: per frame j and harmonic h the
+// phase increment rad = remainder(f0 (h + 1) / 24000, 1) is accumulated in double and rounded to f32, then
+// ((phase * 2) * pi) * 300; the x300 linear upsample uses src = fma(1/300, i + 0.5, -0.5) and
+// fma(t0, l0, t1 * l1); the merge is y += v * w[h] in harmonic order, then tanh(y + b). With the same F0 input
+// the f32 phases are bit-identical to the CPU restatement, which matters because they reach ~1e6 rad.
+#include "common.h"
+
+#include <algorithm>
+
+// Every fused multiply-add in this file is an explicit __builtin_fmaf; nothing else may be contracted.
+#pragma clang fp contract(off)
+
+namespace lkd {
+
+constexpr int kHarm = 9;
+
+__device__ __forceinline__ float torchRemainder1(float a) {
+  float m = fmodf(a, 1.0f);
+  if (m != 0.0f && m < 0.0f) m += 1.0f;
+  return m;
+}
+
+// One wave per harmonic: wave-level inclusive scans of 64 frames in double plus a running carry (the sums of
+// f32 increments in [0, 1) over <= 2^16 frames are exact in double, so the scan order does not change them).
+// p300[j, h] = ((f32(acc) * 2) * pi) * 300.
+__global__ __launch_bounds__(64 * kHarm) void harmonicPhaseKernel(const float* __restrict__ f0,
+                                                                 float* __restrict__ p300, int64_t n) {
+  const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double carry = 0.0;
+  const float hf = static_cast<float>(h + 1);
+  for (int64_t j0 = 0; j0 < n; j0 += 64) {
+    const int64_t j = j0 + lane;
+    double v = 0.0;
+    if (j < n) {
+      const float fn = f0[j] * hf;
+      v = static_cast<double>(torchRemainder1(fn / 24000.0f));
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const double u = __shfl_up(v, o, 64);
+      if (lane >= o) v += u;
+    }
+    const double acc = carry + v;
+    if (j < n) {
+      const float phase = (static_cast<float>(acc) * 2.0f) * 3.14159265358979323846f;
+      p300[j * kHarm + h] = phase * 300.0f;
+    }
+    carry += __shfl(v, 63, 64);
+  }
+}
+
+__global__ void harmonicSourceKernel(const float* __restrict__ f0, const float* __restrict__ p300,
+                                     const float* __restrict__ noise, const float* __restrict__ w,
+                                     const float* __restrict__ b, float* __restrict__ out, int64_t n) {
+  const int64_t s = n * 300;
+  const float scale = static_cast<float>(1.0 / 300.0);
+  const float ampV = 0.003f, ampU = (1.0f * 0.1f) / 3.0f;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < s;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float real = __builtin_fmaf(scale, static_cast<float>(i) + 0.5f, -0.5f);
+    real = fmaxf(real, 0.0f);
+    int64_t i0 = static_cast<int64_t>(floorf(real));
+    if (i0 > n - 1) i0 = n - 1;
+    const float l1 = fminf(fmaxf(real - static_cast<float>(i0), 0.0f), 1.0f);
+    const float l0 = 1.0f - l1;
+    const int64_t i1 = i0 < n - 1 ? i0 + 1 : i0;
+    const bool voiced = f0[i / 300] > 10.0f;
+    const float uv = voiced ? 1.0f : 0.0f, amp = voiced ? ampV : ampU;
+    float y = 0.0f;
+#pragma unroll
+    for (int h = 0; h < kHarm; ++h) {
+      const float t0 = p300[i0 * kHarm + h], t1 = p300[i1 * kHarm + h];
+      const float phase = __builtin_fmaf(t0, l0, t1 * l1);
+      const float sine = sinf(phase) * 0.1f;
+      const float v = sine * uv + amp * noise[i * kHarm + h];
+      y = y + v * w[h];
+    }
+    out[i] = tanhf(y + b[0]);
+  }
+}
+
+// One thread per frame: reflect-padded frame (center = True), windowed DFT by a table built like the
+// reference's (double cos / sin, rounded to f32), accumulation over m in order, im = 0 at DC / Nyquist.
+constexpr int kStftMaxN = 64;
+__global__ __launch_bounds__(256) void stftKernel(const float* __restrict__ x, float* __restrict__ out, int64_t s,
+                                                 int64_t frames, int nfft, int hop, int64_t ldo) {
+  __shared__ float tabRe[33 * kStftMaxN], tabIm[33 * kStftMaxN];
+  const int bins = nfft / 2 + 1, pad = nfft / 2;
+  for (int i = threadIdx.x; i < bins * nfft; i += blockDim.x) {
+    const int k = i / nfft, m = i % nfft;
+    const float win = static_cast<float>(0.5 - 0.5 * cos(2.0 * M_PI * static_cast<double>(m) / nfft));
+    const double ang = 2.0 * M_PI * static_cast<double>((k * m) % nfft) / static_cast<double>(nfft);
+    tabRe[i] = static_cast<float>(win * cos(ang));
+    tabIm[i] = static_cast<float>(-win * sin(ang));
+  }
+  __syncthreads();
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= frames) return;
+  float fr[kStftMaxN];
+  for (int m = 0; m < nfft; ++m) {
+    int64_t q = t * hop + m - pad;
+    if (q < 0) q = -q;
+    if (q >= s) q = 2 * (s - 1) - q;
+    fr[m] = x[q];
+  }
+  float* o = out + t * ldo;
+  for (int k = 0; k < bins; ++k) {
+    float re = 0.0f, im = 0.0f;
+    for (int m = 0; m < nfft; ++m) {
+      re += tabRe[k * nfft + m] * fr[m];
+      im += tabIm[k * nfft + m] * fr[m];
+    }
+    if (k == 0 || 2 * k == nfft) im = 0.0f;
+    o[k] = sqrtf(re * re + im * im);
+    o[bins + k] = atan2f(im, re);
+  }
+  for (int64_t c = 2 * bins; c < ldo; ++c) o[c] = 0.0f;
+}
+
+__global__ void conv1chKernel(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
+                              float* __restrict__ out, int64_t l, int64_t lo, int k, int stride, int pad) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= lo) return;
+  float acc = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    const int64_t src = i * stride - pad + kk;
+    if (src >= 0 && src < l) acc += x[src] * w[kk];
+  }
+  out[i] = acc + b[0];
+}
+
+}  // namespace lkd
+
+extern "C" {
+
+// f0 [n], noise [300 n, 9], w [9], b [1] -> out [300 n]; workspace >= n * 9 floats (the phase table).
+int lk_hip_harmonic_source_f32(const float* f0, const float* noise, const float* w, const float* b, float* out,
+                               int64_t n, void* workspace, int64_t workspaceBytes, void* stream) {
+  if (n < 1) return 1;
+  if (!workspace || workspaceBytes < n * lkd::kHarm * 4) return 3;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* p300 = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(lkd::harmonicPhaseKernel, dim3(1), dim3(64 * lkd::kHarm), 0, st, f0, p300, n);
+  const int64_t s = n * 300;
+  const int64_t blocks = std::min<int64_t>((s + 255) / 256, 65536);
+  hipLaunchKernelGGL(lkd::harmonicSourceKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, f0, p300,
+                     noise, w, b, out, n);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// x [S] -> out [frames, ldo], frames = S / hop + 1, columns 0..K-1 magnitude, K..2K-1 phase, rest 0.
+int lk_hip_stft_magphase_lc_f32(const float* x, float* out, int64_t s, int nfft, int hop, int64_t ldo, void* stream) {
+  if (nfft < 2 || nfft % 2 || nfft > lkd::kStftMaxN || hop < 1 || s <= nfft / 2 || ldo < nfft + 2) return 1;
+  const int64_t frames = s / hop + 1;
+  hipLaunchKernelGGL(lkd::stftKernel, dim3(lkh::ceilDiv(frames, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, out, s, frames, nfft, hop, ldo);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_conv1d_1ch_f32(const float* x, const float* w, const float* b, float* out, int64_t l, int k, int stride,
+                          int pad, void* stream) {
+  const int64_t lo = (l + 2 * pad - k) / stride + 1;
+  if (lo < 1 || stride < 1) return 1;
+  hipLaunchKernelGGL(lkd::conv1chKernel, dim3(lkh::ceilDiv(lo, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, w, b, out, l, lo, k, stride, pad);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"
+
+namespace lkh {
+
+namespace {
+
+// harmonic_source_f32_gpu(f0[n], noise[300 n, 9], w[9], b[1]) -> [300 n]
+void runHarmonic(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t n = a.ints[0];
+  LK_REQUIRE(ctx, a.ints[1] == 300 * n && a.ints[2] == 9 && a.ints[3] == 9 && a.ints[4] == 1,
+             "harmonic_source: expected f0 [n], noise [300 n, 9], w [9], b [1]");
+  const int rc = lk_hip_harmonic_source_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<float>(a, 3),
+                                            P<float>(a, 4), n, ctx.workspace,
+                                            static_cast<int64_t>(ctx.workspaceBytes), ctx.stream);
+  if (rc) ctx.error = rc == 3 ? "harmonic_source: workspace too small" : "harmonic_source: failed";
+}
+
+// stft_magphase_lc_f32_gpu(x[S]; hop, n_fft) -> [S / hop + 1, Cpad]
+void runStft(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t s = a.ints[0], ldo = a.ints[2];
+  const int hop = static_cast<int>(a.ints[3]), nfft = static_cast<int>(a.ints[4]);
+  LK_REQUIRE(ctx, a.ints[1] == s / hop + 1, "stft_magphase_lc: bad output rows");
+  if (lk_hip_stft_magphase_lc_f32(P<float>(a, 0), P<float>(a, 1), s, nfft, hop, ldo, ctx.stream))
+    ctx.error = "stft_magphase_lc: invalid configuration";
+}
+
+// conv1d_1ch_f32_gpu(x[L], w[K], b[1]; padding, stride) -> [Lo]
+void runConv1ch(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t l = a.ints[0];
+  const int k = static_cast<int>(a.ints[1]);
+  const int pad = static_cast<int>(a.ints[4]), stride = static_cast<int>(a.ints[5]);
+  if (lk_hip_conv1d_1ch_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<float>(a, 3), l, k, stride, pad,
+                            ctx.stream))
+    ctx.error = "conv1d_1ch: invalid configuration";
+}
+
+}  // namespace
+
+void registerSignalKernels() {
+  const Device G = Device::Gpu;
+  registerKernel({"harmonic_source_f32_gpu", G, runHarmonic, 4, 1});
+  registerKernel({"stft_magphase_lc_f32_gpu", G, runStft, 1, 1});
+  registerKernel({"conv1d_1ch_f32_gpu", G, runConv1ch, 3, 1});
+}
+
+}  // namespace lkh

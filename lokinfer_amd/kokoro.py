@@ -1,0 +1,308 @@
+"""Kokoro-82M forward on the MI355X kernels, GPU-resident end to end: the graph of the reference's
+`build(sd, gpu=True, forced_durations=True, explicit_noise=True)` (models/kokoro/model.py:619-785 in
+lariaus/lokinfer) with every stage on the device.
+
+Inputs: ids i64[T] (pad id 0 at both ends), ref_s f32[256], dur i64[T] (forced durations), noise f32[600 F, 9]
+(the SineGen noise; F = sum(dur) frames). Output: audio f32[600 F].
+
+Stages (channel-last [L, C] at frame rate, [T, C] at token rate):
+  ALBERT x12 (shared weights): MFMA GEMMs + flash attention + fused add/bias/LayerNorm   (model.py:583-610)
+  bert_encoder, DurationEncoder (3 BiLSTM + AdaLayerNorm), repeat_interleave by dur     (model.py:649-680)
+  shared BiLSTM -> F0 / N curves (3 AdainResBlk1d each + one-column projection)          (model.py:387-401)
+  TextEncoder (3 x conv k5 + LN + leaky, BiLSTM) -> asr                                   (model.py:591-603)
+  Decoder: F0_conv / N_conv, encode + 4 decode AdainResBlk1d                             (model.py:369-380)
+  Generator: harmonic source + STFT, noise convs, 2 x (noise_res, convT, 3 resblocks), conv_post, iSTFT
+                                                                                          (model.py:479-508)
+Where the reference keeps work on the host CPU (LSTMs, embeddings, alignment, harmonic source, STFT, strided and
+single-channel convs, the ALBERT embeddings) this backend runs device kernels, so a forward is one captured HIP
+graph with no host round trips. Every conv is one implicit-GEMM MFMA kernel with the AdaIN affine and Snake /
+leaky activation fused into its operand staging (the reference fuses them into its Winograd input transform).
+
+The durations predictor (predictor.lstm + duration_proj) is not computed: with forced durations its output is
+unused, and the reference's dead-code pass removes it from the compiled graph as well.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import ops
+from .compiler import compile as lk_compile
+from .tensor import Tensor, from_numpy
+
+SQRT1_2 = 1.0 / math.sqrt(2.0)
+
+
+def _pad16(n: int) -> int:
+    return -(-n // 16) * 16
+
+
+def _w_lc(a: np.ndarray, ci_pad: int | None = None) -> np.ndarray:
+    """torch conv weight [Co, Ci, K] -> channel-last [Co, K, Ci_pad] (zero input channels past Ci)."""
+    co, ci, k = a.shape
+    cp = ci_pad or _pad16(ci)
+    out = np.zeros((co, k, cp), np.float32)
+    out[:, :, :ci] = a.transpose(0, 2, 1)
+    return out
+
+
+def _w_convt(a: np.ndarray) -> np.ndarray:
+    """ConvTranspose1d weight [Ci, Co, K] -> [Ci, K * Co] (GEMM, then the overlap-add gather)."""
+    ci, co, k = a.shape
+    return np.ascontiguousarray(a.transpose(0, 2, 1).reshape(ci, k * co))
+
+
+def _vec_pad(a: np.ndarray, n: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    out[: a.shape[0]] = a
+    return out
+
+
+class KokoroGpu:
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True):
+        self.sd = sd
+        self._g: dict[str, Tensor] = {}
+        self._per_t: dict[tuple, Tensor] = {}
+        self.banks = {root: self._bank(root) for root in ("predictor", "decoder")}
+        self.model = lk_compile(self._forward, graph=graph)
+
+    # ---- weights (uploaded once) ------------------------------------------------------------------------
+    def g(self, key: str, fn=None) -> Tensor:
+        k = key if fn is None else f"{key}#{fn.__name__}"
+        t = self._g.get(k)
+        if t is None:
+            a = self.sd[key] if fn is None else fn(self.sd[key])
+            t = from_numpy(np.ascontiguousarray(a, dtype=np.float32), device="gpu", copy=True)
+            self._g[k] = t
+        return t
+
+    def const(self, key: str, make) -> Tensor:
+        t = self._g.get(key)
+        if t is None:
+            t = from_numpy(np.ascontiguousarray(make(), dtype=np.float32), device="gpu", copy=True)
+            self._g[key] = t
+        return t
+
+    def _bank(self, root: str):
+        """All `<root>.*.fc` style projections as one [128, total] weight (one GEMV per style vector), with each
+        fc's (offset, width) (reference W.style_bank, model.py:67-81)."""
+        names = sorted(k[: -len(".weight")] for k in self.sd if k.startswith(root + ".") and k.endswith(".fc.weight"))
+        wt = np.concatenate([self.sd[n + ".weight"].T for n in names], axis=1)
+        b = np.concatenate([self.sd[n + ".bias"] for n in names])
+        offs, o = {}, 0
+        for n in names:
+            offs[n] = (o, self.sd[n + ".bias"].shape[0])
+            o += offs[n][1]
+        return (from_numpy(np.ascontiguousarray(wt), device="gpu", copy=True),
+                from_numpy(np.ascontiguousarray(b), device="gpu", copy=True), offs)
+
+    def lstm_w(self, p: str):
+        key = p + "#lstm"
+        if key not in self._g:
+            sd = self.sd
+            w_ih = np.concatenate([sd[p + ".weight_ih_l0"], sd[p + ".weight_ih_l0_reverse"]])
+            w_hh_t = np.concatenate([sd[p + ".weight_hh_l0"], sd[p + ".weight_hh_l0_reverse"]]).T
+            b = np.concatenate([sd[p + ".bias_ih_l0"] + sd[p + ".bias_hh_l0"],
+                                sd[p + ".bias_ih_l0_reverse"] + sd[p + ".bias_hh_l0_reverse"]])
+            self._g[key] = tuple(from_numpy(np.ascontiguousarray(a, np.float32), device="gpu", copy=True)
+                                 for a in (w_ih, w_hh_t, b))
+        return self._g[key]
+
+    def per_t(self, kind: str, n: int, make) -> Tensor:
+        """Shape-dependent constants (positions 0..T-1, zero rows), built on the eager warm-up call so that the
+        captured graph only reads them."""
+        key = (kind, n)
+        t = self._per_t.get(key)
+        if t is None:
+            t = make()
+            self._per_t[key] = t
+        return t
+
+    # ---- building blocks ------------------------------------------------------------------------------------
+    def style(self, bank, prefix: str) -> Tensor:
+        vec, offs = bank
+        off, n = offs[prefix]
+        return ops.view(vec, [n], off)
+
+    def affine(self, x: Tensor, bank, prefix: str, stats: Tensor | None = None) -> Tensor:
+        st = ops.channel_stats_lc_f32_gpu(x) if stats is None else stats
+        return ops.adain_affine_lc_f32_gpu(st, self.style(bank, prefix), length=x.shape[0])
+
+    def resblk(self, x: Tensor, bank, p: str, cin: int, cout: int, upsample: bool) -> Tensor:
+        """AdainResBlk1d, channel-last x f32[L, pad16(cin)] (padding channels stay 0)."""
+        af = self.affine(x, bank, p + ".norm1.fc")
+        cp = _pad16(cin)
+        if upsample:
+            h = ops.leaky_lc_f32_gpu(x, 0.2, affine=af)
+            h = ops.dwconvt_lc_f32_gpu(h, self.const(p + "#pool_w", lambda: _pool_pad(self.sd[p + ".pool.weight"], cp)),
+                                       self.const(p + "#pool_b", lambda: _vec_pad(self.sd[p + ".pool.bias"], cp)))
+            h = ops.conv1d_lc_f32_gpu(h, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), padding=1)
+        else:
+            h = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), af,
+                                          act="leaky", slope=0.2, padding=1)
+        af2 = self.affine(h, bank, p + ".norm2.fc")
+        sc = ops.upsample2_lc_f32_gpu(x) if upsample else x
+        if p + ".conv1x1.weight" in self.sd:
+            sc = ops.conv1d_lc_f32_gpu(sc, self.g(p + ".conv1x1.weight", _w_lc),
+                                       self.const(f"zeros#{cout}", lambda: np.zeros(cout)))
+        return ops.conv1d_act_lc_f32_gpu(h, self.g(p + ".conv2.weight", _w_lc), self.g(p + ".conv2.bias"), af2,
+                                         act="leaky", slope=0.2, padding=1, residual=sc, out_scale=SQRT1_2)
+
+    def resblock1(self, x: Tensor, bank, p: str, k: int, x_stats: Tensor | None = None) -> Tensor:
+        """AdaINResBlock1 (Snake), dilations 1, 3, 5; every conv has AdaIN affine + Snake fused in its staging."""
+        st = ops.channel_stats_lc_f32_gpu(x) if x_stats is None else x_stats
+        for j, d in enumerate((1, 3, 5)):
+            af = self.affine(x, bank, f"{p}.adain1.{j}.fc", st)
+            h = ops.conv1d_act_lc_f32_gpu(x, self.g(f"{p}.convs1.{j}.weight", _w_lc), self.g(f"{p}.convs1.{j}.bias"),
+                                          af, self.g(f"{p}.alpha1.{j}", _flat), act="snake",
+                                          padding=d * (k - 1) // 2, dilation=d)
+            af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc")
+            x = ops.conv1d_act_lc_f32_gpu(h, self.g(f"{p}.convs2.{j}.weight", _w_lc), self.g(f"{p}.convs2.{j}.bias"),
+                                          af2, self.g(f"{p}.alpha2.{j}", _flat), act="snake", padding=(k - 1) // 2,
+                                          residual=x)
+            if j < 2:
+                st = ops.channel_stats_lc_f32_gpu(x)
+        return x
+
+    def lstm(self, x: Tensor, p: str) -> Tensor:
+        return ops.lstm_bidir_t_f32_gpu(x, *self.lstm_w(p))
+
+    # ---- stages ---------------------------------------------------------------------------------------------
+    def albert(self, ids: Tensor) -> Tensor:
+        t = ids.shape[0]
+        E = "bert.embeddings."
+        pos = self.per_t("pos", t, lambda: from_numpy(np.arange(t, dtype=np.int64), device="gpu", copy=True))
+        zeros = self.per_t("zeros128", t, lambda: from_numpy(np.zeros((t, 128), np.float32), device="gpu", copy=True))
+        e = ops.embedding2_add_f32_gpu(self.g(E + "word_embeddings.weight"), ids, self.g(E + "position_embeddings.weight"),
+                                       pos)
+        e = ops.add_bias_layernorm_f32_gpu(e, self.const("tt_row0", lambda: self.sd[E + "token_type_embeddings.weight"][0]),
+                                           zeros, self.g(E + "LayerNorm.weight"), self.g(E + "LayerNorm.bias"), eps=1e-12)
+        M = "bert.encoder.embedding_hidden_mapping_in"
+        h = ops.gemm_bias_f32_gpu(e, self.g(M + ".weight", _t), self.g(M + ".bias"))
+        L = "bert.encoder.albert_layer_groups.0.albert_layers.0."
+        wqkv = self.const("albert#wqkv", lambda: np.concatenate(
+            [self.sd[L + f"attention.{n}.weight"].T for n in ("query", "key", "value")], axis=1))
+        bqkv = self.const("albert#bqkv", lambda: np.concatenate(
+            [self.sd[L + f"attention.{n}.bias"] for n in ("query", "key", "value")]))
+        for _ in range(12):
+            a = ops.attention_qkv_sg_f32_gpu(ops.gemm_f32_gpu_mps(h, wqkv), bqkv, heads=12)
+            a = ops.gemm_f32_gpu_mps(a, self.g(L + "attention.dense.weight", _t))
+            h = ops.add_bias_layernorm_f32_gpu(a, self.g(L + "attention.dense.bias"), h,
+                                               self.g(L + "attention.LayerNorm.weight"),
+                                               self.g(L + "attention.LayerNorm.bias"), eps=1e-12)
+            f = ops.gemm_steel_f32_gpu(h, self.g(L + "ffn.weight", _t), self.g(L + "ffn.bias"), act="gelu")
+            f = ops.gemm_f32_gpu_mps(f, self.g(L + "ffn_output.weight", _t))
+            h = ops.add_bias_layernorm_f32_gpu(f, self.g(L + "ffn_output.bias"), h,
+                                               self.g(L + "full_layer_layer_norm.weight"),
+                                               self.g(L + "full_layer_layer_norm.bias"), eps=1e-12)
+        return h
+
+    def text_encoder(self, ids: Tensor) -> Tensor:
+        x = ops.embedding_f32_gpu(self.g("text_encoder.embedding.weight"), ids)  # [T, 512]
+        for i in range(3):
+            x = ops.conv1d_lc_f32_gpu(x, self.g(f"text_encoder.cnn.{i}.0.weight", _w_lc),
+                                      self.g(f"text_encoder.cnn.{i}.0.bias"), padding=2)
+            x = ops.layernorm_f32_gpu(x, self.g(f"text_encoder.cnn.{i}.1.gamma"), self.g(f"text_encoder.cnn.{i}.1.beta"),
+                                      eps=1e-5)
+            x = ops.leaky_lc_f32_gpu(x, 0.2)
+        return self.lstm(x, "text_encoder.lstm")  # [T, 512]
+
+    def _forward(self, ids: Tensor, ref_s: Tensor, dur: Tensor, noise: Tensor):
+        frames = noise.shape[0] // 600
+        s_d, s_p = ops.view(ref_s, [1, 128], 0), ops.view(ref_s, [1, 128], 128)
+        bank_p = (ops.gemv4_f32_gpu(s_p, self.banks["predictor"][0], self.banks["predictor"][1]),
+                  self.banks["predictor"][2])
+        bank_d = (ops.gemv4_f32_gpu(s_d, self.banks["decoder"][0], self.banks["decoder"][1]), self.banks["decoder"][2])
+        sp_vec = ops.view(s_p, [128])
+        # text side
+        bert = self.albert(ids)
+        d_en = ops.gemm_bias_f32_gpu(bert, self.g("bert_encoder.weight", _t), self.g("bert_encoder.bias"))
+        x = ops.concat_bcast_f32_gpu(d_en, sp_vec)
+        for i in range(3):
+            x = self.lstm(x, f"predictor.text_encoder.lstms.{2 * i}")
+            x = ops.adalayernorm_f32_gpu(x, self.style(bank_p, f"predictor.text_encoder.lstms.{2 * i + 1}.fc"))
+            x = ops.concat_bcast_f32_gpu(x, sp_vec)
+        en = ops.repeat_interleave_f32_gpu(x, dur, frames)  # [F, 640]
+        sh = self.lstm(en, "predictor.shared")  # [F, 512]
+        curves = []
+        for name in ("F0", "N"):
+            y = self.resblk(sh, bank_p, f"predictor.{name}.0", 512, 512, False)
+            y = self.resblk(y, bank_p, f"predictor.{name}.1", 512, 256, True)
+            y = self.resblk(y, bank_p, f"predictor.{name}.2", 256, 256, False)
+            y = ops.gemv1_bias_f32_gpu(y, self.g(f"predictor.{name}_proj.weight", _col),
+                                       self.g(f"predictor.{name}_proj.bias"))
+            curves.append(ops.reshape(y, [2 * frames]))
+        f0, n_curve = curves
+        t_en = self.text_encoder(ids)
+        asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
+        # decoder
+        fn_cf = Tensor(torch.empty((2, frames), dtype=torch.float32, device=asr.t.device))
+        ops.conv1d_1ch_f32_gpu(f0, self.g("decoder.F0_conv.weight", _flat), self.g("decoder.F0_conv.bias"), stride=2,
+                               padding=1, out=ops.view(fn_cf, [frames], 0))
+        ops.conv1d_1ch_f32_gpu(n_curve, self.g("decoder.N_conv.weight", _flat), self.g("decoder.N_conv.bias"),
+                               stride=2, padding=1, out=ops.view(fn_cf, [frames], frames))
+        fn_lc = ops.transpose_f32_gpu(fn_cf)  # [F, 2]
+        asr_res = ops.conv1d_lc_f32_gpu(asr, self.g("decoder.asr_res.0.weight", _w_lc), self.g("decoder.asr_res.0.bias"))
+        extra = ops.concat_pad_lc_f32_gpu(asr_res, fn_lc, cout=66)  # [F, 66]
+        x = self.resblk(ops.concat_pad_lc_f32_gpu(asr, fn_lc), bank_d, "decoder.encode", 514, 1024, False)
+        for i in range(4):
+            x = self.resblk(ops.concat_pad_lc_f32_gpu(x, extra), bank_d, f"decoder.decode.{i}", 1090,
+                            1024 if i < 3 else 512, i == 3)
+        # generator
+        G = "decoder.generator."
+        har_src = ops.harmonic_source_f32_gpu(f0, noise, self.g(G + "m_source.l_linear.weight", _flat),
+                                              self.g(G + "m_source.l_linear.bias"))
+        har = ops.stft_magphase_lc_f32_gpu(har_src, 20, 5, cpad=32)  # [120 F + 1, 32]
+        for i, (k_up, u, k_noise) in enumerate(((20, 10, 7), (12, 6, 11))):
+            xs = ops.conv1d_lc_f32_gpu(har, self.g(G + f"noise_convs.{i}.weight", _w_lc_32),
+                                       self.g(G + f"noise_convs.{i}.bias"),
+                                       **({"stride": 6, "padding": 3} if i == 0 else {}))
+            xs = self.resblock1(xs, bank_d, f"{G}noise_res.{i}", k_noise)
+            x = ops.leaky_lc_f32_gpu(x, 0.1)
+            y = ops.gemm_f32_gpu_mps(x, self.g(G + f"ups.{i}.weight", _w_convt))  # [Lin, K * Co]
+            x = ops.convt_gather_lc_f32_gpu(y, self.g(G + f"ups.{i}.bias"), k_up, u, (k_up - u) // 2, add=xs,
+                                            reflect_left=(i == 1))
+            xst = ops.channel_stats_lc_f32_gpu(x)  # shared by the three resblocks' first AdaIN
+            rb = [self.resblock1(x, bank_d, f"{G}resblocks.{3 * i + j}", kk, xst) for j, kk in enumerate((3, 7, 11))]
+            x = ops.add3_scale_f32_gpu(rb[0], rb[1], rb[2], 1.0 / 3.0)
+        ident = self.const("identity_affine128", lambda: np.stack([np.zeros(128), np.ones(128), np.zeros(128)]))
+        post = ops.conv1d_act_lc_f32_gpu(x, self.g(G + "conv_post.weight", _w_lc), self.g(G + "conv_post.bias"), ident,
+                                         act="leaky", slope=0.01, padding=3)  # [120 F + 1, 22]
+        audio = ops.istft_logits_lc_f32_gpu(post, n_fft=20, hop=5)
+        return audio, f0, n_curve, post
+
+    # ---- host API ----------------------------------------------------------------------------------------------
+    def forward(self, ids, ref_s, dur, noise, inplace: bool = False):
+        """One forward from host or device tensors; checks sum(dur) == F on the host (the reference's
+        repeat_interleave reports a mismatch, kokoro_misc.cpp:253-260). Returns (audio, f0, n, post)."""
+        dur_h = np.asarray(dur.numpy() if isinstance(dur, Tensor) else dur, np.int64)
+        noise_rows = (noise.shape if isinstance(noise, Tensor) else np.shape(noise))[0]
+        if noise_rows % 600 or int(dur_h.sum()) != noise_rows // 600 or (dur_h < 0).any():
+            raise ValueError(f"durations sum to {int(dur_h.sum())} frames but the noise holds {noise_rows / 600} frames")
+        args = [a if isinstance(a, Tensor) else from_numpy(np.ascontiguousarray(a), device="gpu", copy=True)
+                for a in (ids, ref_s, dur, noise)]
+        return self.model.run_inplace(*args) if inplace else self.model(*args)
+
+
+def _t(a):
+    return np.ascontiguousarray(a.T)
+
+
+def _flat(a):
+    return np.ascontiguousarray(a.reshape(-1))
+
+
+def _col(a):  # [1, C, 1] projection -> [C, 1]
+    return np.ascontiguousarray(a.reshape(-1, 1))
+
+
+def _w_lc_32(a):  # noise convs: Ci = 22 padded to 32
+    return _w_lc(a, 32)
+
+
+def _pool_pad(a, cp):  # depthwise convT weight [C, 1, K] -> [Cpad, K]
+    out = np.zeros((cp, a.shape[2]), np.float32)
+    out[: a.shape[0]] = a[:, 0, :]
+    return out

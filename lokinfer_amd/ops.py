@@ -479,3 +479,71 @@ def argmax_f32_gpu(x):
     """(MI355X backend) first index of the row maximum of x f32[R, N] -> i64[R] (greedy decoding on device)."""
     _f32(x, rank=2)
     return _launch("argmax_f32_gpu", [x], [(x.shape[0],)], out_dtypes=[i64])
+
+
+# ---- Kokoro token-rate sequence + signal kernels (MI355X backend: the reference runs these on the host) ------
+
+def lstm_bidir_t_f32_gpu(x, w_ih, w_hh_t, b):
+    """1-layer bidirectional nn.LSTM (gates i, f, g, o): x f32[T, I], w_ih f32[8H, I] (rows 0..4H forward),
+    w_hh_t = W_hh^T f32[H, 8H], b = b_ih + b_hh f32[8H] -> f32[T, 2H] = [h_fwd | h_bwd]
+    (reference lstm_bidir_t_f32_cpu, ops/kokoro.py:107-116)."""
+    _f32(x, w_ih, w_hh_t, rank=2)
+    h = w_hh_t.shape[0]
+    check(w_ih.shape == (8 * h, x.shape[1]) and w_hh_t.shape[1] == 8 * h and tuple(b.shape) == (8 * h,),
+          "expected w_ih [8H, I], w_hh_t [H, 8H], b [8H]")
+    check(h <= 256, "H must be <= 256")
+    return _launch("lstm_bidir_t_f32_gpu", [x, w_ih, w_hh_t, b], [(x.shape[0], 2 * h)])
+
+
+def repeat_interleave_f32_gpu(x, dur, frames):
+    """x.repeat_interleave(dur, 0) -> f32[frames, C]; dur is a device i64[T]. `frames` must equal sum(dur): the
+    caller checks it on the host (reference repeat_interleave_f32_cpu reports a mismatch as an error)."""
+    _f32(x, rank=2)
+    check(dur.dtype == i64 and tuple(dur.shape) == (x.shape[0],), "dur must be i64[T]")
+    check(x.shape[0] <= 8192, "T must be <= 8192")
+    return _launch("repeat_interleave_f32_gpu", [x, dur], [(int(frames), x.shape[1])], dict(frames=int(frames)))
+
+
+def adalayernorm_f32_gpu(x, gb, eps=1e-5):
+    """(1 + gb[:C]) * LN_noaffine(x) + gb[C:] over x f32[R, C] (reference adalayernorm_f32_cpu, ops/kokoro.py:69)."""
+    _f32(x, rank=2)
+    check(tuple(gb.shape) == (2 * x.shape[1],) and x.shape[1] <= 2048, "gb must be f32[2C], C <= 2048")
+    return _launch("adalayernorm_f32_gpu", [x, gb], [x.shape], dict(eps=float(eps)))
+
+
+def concat_bcast_f32_gpu(x, v):
+    """[x | v] per row: concat_cols(x, broadcast_rows(v)) for x f32[R, C1], v f32[C2] -> f32[R, C1 + C2]."""
+    _f32(x, rank=2)
+    _f32(v, rank=1)
+    return _launch("concat_bcast_f32_gpu", [x, v], [(x.shape[0], x.shape[1] + v.shape[0])])
+
+
+def harmonic_source_f32_gpu(f0, noise, w, b):
+    """hn-NSF harmonic source with explicit SineGen noise: f0 f32[n], noise f32[300 n, 9], l_linear w f32[9],
+    b f32[1] -> f32[300 n] (reference harmonic_source_f32_cpu, kernels/cpu/kokoro_signal.cpp:89-192)."""
+    _f32(f0, w, b, rank=1)
+    n = f0.shape[0]
+    check(noise.shape == (300 * n, 9) and w.shape == (9,) and b.shape == (1,), "bad harmonic source operands")
+    return _launch("harmonic_source_f32_gpu", [f0, noise, w, b], [(300 * n,)])
+
+
+def stft_magphase_lc_f32_gpu(x, n_fft=20, hop=5, cpad=32):
+    """torch.stft (periodic Hann, center, reflect) -> channel-last f32[S / hop + 1, cpad]: magnitude in columns
+    0..K-1, phase in K..2K-1 (K = n_fft / 2 + 1), zero padding after (reference stft_magphase_f32_cpu, which
+    returns the channel-first [2K, frames])."""
+    _f32(x, rank=1)
+    check(cpad >= n_fft + 2 and x.shape[0] > n_fft // 2, "bad STFT configuration")
+    return _launch("stft_magphase_lc_f32_gpu", [x], [(x.shape[0] // hop + 1, int(cpad))],
+                   dict(hop=int(hop), n_fft=int(n_fft)))
+
+
+def conv1d_1ch_f32_gpu(x, w, b, stride=1, padding=0, out=None):
+    """Single-channel conv1d: x f32[L], w f32[K], b f32[1] -> f32[Lo] (the decoder's F0_conv / N_conv); `out`
+    optionally names a preallocated f32[Lo] destination (e.g. a row of a [2, Lo] buffer)."""
+    _f32(x, w, b, rank=1)
+    lo = (x.shape[0] + 2 * padding - w.shape[0]) // stride + 1
+    check(lo >= 1, "empty conv output")
+    if out is not None:
+        check(out.dtype == f32 and tuple(out.shape) == (lo,), "out must be f32[Lo]")
+    return _launch("conv1d_1ch_f32_gpu", [x, w, b], [(lo,)], dict(padding=int(padding), stride=int(stride)),
+                   outs=None if out is None else [out])

@@ -1,0 +1,99 @@
+"""GPU parity of the Kokoro front-end / signal kernels (the host kernels of the reference's GPU graph, run on the
+device here) against the oracle: torch nn.LSTM / F.layer_norm / torch.stft in float64 and the f32 restatement
+of the harmonic source (oracle/kokoro.py, reference kernels/cpu/kokoro_signal.cpp:89-192)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kokoro as OK
+
+pytestmark = pytest.mark.gpu
+
+rng = np.random.default_rng(99)
+
+
+def G(lk, a, dt=np.float32):
+    return lk.from_numpy(np.ascontiguousarray(a, dt), device="gpu", copy=True)
+
+
+def close(got, ref, tol):
+    got = got.numpy() if hasattr(got, "numpy") else np.asarray(got)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    err = np.abs(got.astype(np.float64) - ref).max()
+    scale = max(1.0, np.abs(ref).max())
+    assert err <= tol * scale, f"max err {err:.3e} > {tol:.1e} * {scale:.3e}"
+
+
+@pytest.mark.parametrize("t,i", [(1, 640), (59, 640), (300, 512), (2435, 640)])
+def test_lstm_bidir(gpu, t, i):
+    lk = gpu
+    h = 256
+    x = rng.standard_normal((t, i)).astype(np.float32)
+    sd = {}
+    for sfx in ("", "_reverse"):
+        sd[f"l.weight_ih_l0{sfx}"] = (rng.standard_normal((4 * h, i)) / np.sqrt(i)).astype(np.float32)
+        sd[f"l.weight_hh_l0{sfx}"] = (rng.standard_normal((4 * h, h)) / np.sqrt(h)).astype(np.float32)
+        sd[f"l.bias_ih_l0{sfx}"] = (rng.standard_normal(4 * h) * 0.1).astype(np.float32)
+        sd[f"l.bias_hh_l0{sfx}"] = (rng.standard_normal(4 * h) * 0.1).astype(np.float32)
+    ref = OK.Oracle(sd, torch.float64).lstm(torch.from_numpy(x).double(), "l").numpy()
+    w_ih = np.concatenate([sd["l.weight_ih_l0"], sd["l.weight_ih_l0_reverse"]])
+    w_hh_t = np.concatenate([sd["l.weight_hh_l0"], sd["l.weight_hh_l0_reverse"]]).T
+    b = np.concatenate([sd["l.bias_ih_l0"] + sd["l.bias_hh_l0"], sd["l.bias_ih_l0_reverse"] + sd["l.bias_hh_l0_reverse"]])
+    got = lk.ops.lstm_bidir_t_f32_gpu(G(lk, x), G(lk, w_ih), G(lk, w_hh_t), G(lk, b))
+    close(got, ref, 1e-4)
+
+
+def test_repeat_interleave_adaln_concat(gpu):
+    lk = gpu
+    t, c = 59, 640
+    x = rng.standard_normal((t, c)).astype(np.float32)
+    dur = rng.integers(0, 9, t).astype(np.int64)
+    frames = int(dur.sum())
+    got = lk.ops.repeat_interleave_f32_gpu(G(lk, x), G(lk, dur, np.int64), frames).numpy()
+    assert np.array_equal(got, np.repeat(x, dur, 0))
+    gb = rng.standard_normal(2 * 512).astype(np.float32)
+    y = rng.standard_normal((t, 512)).astype(np.float32)
+    ref = (1 + gb[:512]) * F.layer_norm(torch.from_numpy(y).double(), (512,), eps=1e-5).numpy() + gb[512:]
+    close(lk.ops.adalayernorm_f32_gpu(G(lk, y), G(lk, gb)), ref, 2e-5)
+    v = rng.standard_normal(128).astype(np.float32)
+    out = lk.ops.concat_bcast_f32_gpu(G(lk, y), G(lk, v)).numpy()
+    assert np.array_equal(out, np.concatenate([y, np.broadcast_to(v, (t, 128))], 1))
+
+
+@pytest.mark.parametrize("voiced", [True, False])
+def test_harmonic_source_matches_f32_restatement(gpu, voiced):
+    lk = gpu
+    n = 574
+    f0 = (150 + 20 * rng.standard_normal(n) if voiced else rng.standard_normal(n)).astype(np.float32)
+    f0[:7] = 0.0  # unvoiced frames inside a voiced curve
+    noise = rng.standard_normal((300 * n, 9)).astype(np.float32)
+    w, b = (rng.standard_normal(9) / 3).astype(np.float32), np.array([0.05], np.float32)
+    ref = OK.harmonic_source(f0, noise, w, b)
+    got = lk.ops.harmonic_source_f32_gpu(G(lk, f0), G(lk, noise), G(lk, w), G(lk, b)).numpy()
+    err = np.abs(got.astype(np.float64) - ref).max()
+    assert err <= 2e-6, err  # same f32 phases: only sin / tanh ulps differ
+
+
+@pytest.mark.parametrize("s", [3000, 172200])
+def test_stft_magphase(gpu, s):
+    lk = gpu
+    x = np.tanh(rng.standard_normal(s) * 0.3).astype(np.float32)
+    got = lk.ops.stft_magphase_lc_f32_gpu(G(lk, x)).numpy()
+    z = torch.stft(torch.from_numpy(x).double(), 20, 5, 20, window=torch.hann_window(20, periodic=True,
+                   dtype=torch.float64), center=True, pad_mode="reflect", return_complex=True)
+    mag, ph = z.abs().numpy().T, torch.angle(z).numpy().T
+    assert got.shape == (s // 5 + 1, 32) and not got[:, 22:].any()
+    close(got[:, :11], mag, 2e-6)
+    d = np.angle(np.exp(1j * (got[:, 11:22] - ph)))  # wrap-aware phase difference
+    big = mag > 1e-3
+    assert np.abs(d[big]).max() < 1e-3
+
+
+def test_conv1d_1ch(gpu):
+    lk = gpu
+    x, w, b = rng.standard_normal(574).astype(np.float32), rng.standard_normal(3).astype(np.float32), np.float32([0.3])
+    ref = F.conv1d(torch.from_numpy(x).double()[None, None], torch.from_numpy(w).double()[None, None],
+                   torch.from_numpy(b).double(), stride=2, padding=1)[0, 0].numpy()
+    close(lk.ops.conv1d_1ch_f32_gpu(G(lk, x), G(lk, w), G(lk, b), stride=2, padding=1), ref, 1e-6)
