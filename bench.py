@@ -99,30 +99,149 @@ def cpu_gpt2(sd, ids, nxt, budget_s: float = 15.0) -> dict:
                                       f"same seeded weights), median"}
 
 
+# ---- Kokoro-82M forward ----------------------------------------------------------------------------------------
+
+def kokoro_conv_flops(tokens: int, frames: int) -> float:
+    """Algorithmic (direct-convolution) FLOPs of one forward's convs + GEMMs, from the module shapes."""
+    from lokinfer_amd import kokoro_weights as KW
+
+    f, t = frames, tokens
+    l0, l1 = 20 * f, 120 * f + 1
+    mac = 0
+    # ALBERT (12 layers) + bert_encoder
+    mac += t * 128 * 768 + 12 * (t * 768 * 2304 + 2 * t * t * 768 + t * 768 * 768 + 2 * t * 768 * 2048) + t * 768 * 512
+    # LSTM input projections (gate GEMMs) + recurrences: 3 duration-encoder + text encoder over T, shared over F
+    mac += 3 * t * (640 * 2048 + 256 * 2048) + t * (512 * 2048 + 256 * 2048) + f * (640 * 2048 + 256 * 2048)
+    # F0 / N: blocks 0 (512->512 @F), 1 (512->256 @2F + 1x1), 2 (256->256 @2F)
+    mac += 2 * (2 * f * 512 * 512 * 3 + 2 * f * (512 * 256 * 3 + 256 * 256 * 3 + 512 * 256) + 2 * 2 * f * 256 * 256 * 3)
+    # text encoder convs
+    mac += 3 * t * 512 * 512 * 5
+    # decoder: encode (514->1024 + 1x1), 3 decode (1090->1024 + 1x1), decode.3 (1090->512 @2F, 1x1), asr_res
+    mac += f * (514 * 1024 * 3 + 1024 * 1024 * 3 + 514 * 1024) + 3 * f * (1090 * 1024 * 3 + 1024 * 1024 * 3 + 1090 * 1024)
+    mac += 2 * f * (1090 * 512 * 3 + 512 * 512 * 3 + 1090 * 512) + f * 512 * 64
+    # generator: noise convs, noise_res, ups (GEMM), resblocks, conv_post
+    mac += l0 * 22 * 256 * 12 + l1 * 22 * 128
+    mac += 6 * l0 * 256 * 256 * 7 + 6 * l1 * 128 * 128 * 11
+    mac += 2 * f * 512 * 20 * 256 + l0 * 256 * 12 * 128
+    mac += 6 * l0 * 256 * 256 * (3 + 7 + 11) + 6 * l1 * 128 * 128 * (3 + 7 + 11)
+    mac += l1 * 128 * 22 * 7
+    del KW
+    return 2.0 * mac
+
+
+def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
+    import lokinfer_amd as lk
+    from lokinfer_amd import kokoro_weights as KW
+    from lokinfer_amd.kokoro import KokoroGpu
+
+    sd = KW.random_weights()
+    ids, ref_s, dur, noise = KW.inputs(tokens)
+    frames = int(dur.sum())
+    m = KokoroGpu(sd)
+    args = [lk.from_numpy(a, device="gpu", copy=True) for a in (ids, ref_s, dur, noise)]
+    for _ in range(max(warmup, 1)):
+        m.forward(*args, inplace=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.forward(*args, inplace=True)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    per = event_times(lambda: m.model.run_inplace(*args), steps)
+    return {"median_ms": statistics.median(per), "wall_ms_per_step": wall, "frames": frames,
+            "flops": kokoro_conv_flops(tokens, frames), "sd": sd, "inputs": (ids, ref_s, dur, noise)}
+
+
+def roofline_conv() -> dict:
+    """The dominant kernel of the Kokoro forward: the implicit-GEMM conv with the AdaIN + Snake prologue, at the
+    generator's stage-1 resblock shape (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11, d = 5)."""
+    import lokinfer_amd as lk
+
+    rng = np.random.default_rng(0)
+    l, c, k, d = 292201, 128, 11, 5
+    G = lambda a: lk.from_numpy(np.ascontiguousarray(a, np.float32), device="gpu", copy=True)  # noqa: E731
+    x, w, b = G(rng.standard_normal((l, c))), G(rng.standard_normal((c, k, c)) / 40), G(rng.standard_normal(c))
+    af = G(np.stack([np.zeros(c), np.ones(c), np.zeros(c)]))
+    alpha = G(np.ones(c))
+    fn = lambda: lk.ops.conv1d_act_lc_f32_gpu(x, w, b, af, alpha, act="snake", padding=d * (k - 1) // 2, dilation=d)  # noqa: E731
+    fn()
+    ms = statistics.mean(event_times(fn, 20))
+    flops = 2.0 * l * c * c * k
+    return {"kernel": "gemmMfmaKernel<128,128,A_CONV,B_NT> (conv1d_act_lc_f32_gpu, snake prologue)", "bound": "mfma",
+            "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS, "traffic": None, "avg_launch_ms": ms,
+            "flops_per_launch": flops}
+
+
+def cpu_kokoro(sd, inputs, budget_s: float = 30.0) -> dict:
+    from oracle.kokoro import Oracle
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    o = Oracle(sd)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < 3):
+        t0 = time.perf_counter()
+        o.forward(*inputs)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return {"value": statistics.median(times), "unit": "ms", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} full forward(s) of the same {len(inputs[0])}-token config (PyTorch f32 CPU "
+                      f"restatement of the Kokoro-82M graph, same weights and inputs), median"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="gpt2")
+    ap.add_argument("--workload", default="all", choices=["all", "kokoro487", "kokoro59", "gpt2"])
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this backend has no multi-GPU path (every box has one GPU)",
               file=sys.stderr)
         sys.exit(2)
-    r = bench_gpt2(a.steps, a.warmup, cpu=not a.no_cpu)
+    wl = a.workload
+    if wl == "gpt2":
+        r = bench_gpt2(a.steps, a.warmup, cpu=not a.no_cpu)
+        line = {
+            "metric": "median Kokoro-82M f32 forward ms @59 & 487 tok; GPT-2 decode ms/token",
+            "value": round(r["median_ms"], 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": round(r["wall_ms_per_step"], 4), "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded random-init weights and token ids)",
+            "config": {"workload": "gpt2-124m decode 1 token @ 512 cached, batch 1", "model": "gpt2-124m",
+                       "global_batch": 1, "seq_len": 513, "parallelism": "none"},
+            "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+            "roofline_kernel": r["roofline"]["kernel"], "cpu_baseline": r.get("cpu_baseline"),
+        }
+        print(json.dumps(line))
+        return
+    tokens = 59 if wl == "kokoro59" else 487
+    r = bench_kokoro(tokens, a.steps, a.warmup)
+    extra = {}
+    if wl == "all":
+        r59 = bench_kokoro(59, a.steps, a.warmup)
+        g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=False)
+        extra = {"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
+                 "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_lm_head_roofline": g["roofline"]}
+    roof = roofline_conv()
+    cpu = None if a.no_cpu else cpu_kokoro(r["sd"], r["inputs"])
     line = {
         "metric": "median Kokoro-82M f32 forward ms @59 & 487 tok; GPT-2 decode ms/token",
-        "value": round(r["median_ms"], 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(r["wall_ms_per_step"], 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded random-init weights and token ids)",
-        "config": {"workload": "gpt2-124m decode 1 token @ 512 cached, batch 1", "model": "gpt2-124m",
-                   "global_batch": 1, "seq_len": 513, "parallelism": "none"},
-        "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "roofline_kernel": r["roofline"]["kernel"], "roofline_avg_launch_ms": r["roofline"]["avg_launch_ms"],
-        "cpu_baseline": r.get("cpu_baseline"),
+        "value": round(r["median_ms"], 3), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(r["wall_ms_per_step"], 3), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded random-init Kokoro-82M-shaped weights, ids, style, durations 2..8, noise)",
+        "config": {"workload": f"kokoro-82m forward, {tokens} tokens, {r['frames']} frames "
+                               f"({600 * r['frames']} samples), forced durations", "model": "kokoro-82m",
+                   "global_batch": 1, "seq_len": tokens, "parallelism": "none"},
+        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline_kernel": roof["kernel"], "roofline_avg_launch_ms": roof["avg_launch_ms"],
+        "forward_algorithmic_tflops": round(r["flops"] / (r["median_ms"] * 1e-3) / 1e12, 2),
+        "cpu_baseline": cpu,
     }
+    line.update(extra)
     print(json.dumps(line))
 
 

@@ -120,7 +120,10 @@ __global__ __launch_bounds__(256) void stftKernel(const float* __restrict__ x, f
       re += tabRe[k * nfft + m] * fr[m];
       im += tabIm[k * nfft + m] * fr[m];
     }
-    if (k == 0 || 2 * k == nfft) im = 0.0f;
+    // Real-input DFT: the DC and Nyquist bins are exactly real. So is every bin of frame 0: with center = True
+    // and reflect padding that frame is even about its centre (as is the periodic Hann window), and its exact
+    // imaginary parts are 0 rather than rounding noise whose sign would flip the phase between +pi and -pi.
+    if (k == 0 || 2 * k == nfft || t == 0) im = 0.0f;
     o[k] = sqrtf(re * re + im * im);
     o[bins + k] = atan2f(im, re);
   }

@@ -67,6 +67,11 @@ class KokoroGpu:
         self._per_t: dict[tuple, Tensor] = {}
         self.banks = {root: self._bank(root) for root in ("predictor", "decoder")}
         self.model = lk_compile(self._forward, graph=graph)
+        self.debug: dict | None = None  # set to {} to keep named intermediates (eager runs only)
+
+    def _keep(self, name: str, t: Tensor) -> None:
+        if self.debug is not None:
+            self.debug[name] = t
 
     # ---- weights (uploaded once) ------------------------------------------------------------------------
     def g(self, key: str, fn=None) -> Tensor:
@@ -250,23 +255,30 @@ class KokoroGpu:
         for i in range(4):
             x = self.resblk(ops.concat_pad_lc_f32_gpu(x, extra), bank_d, f"decoder.decode.{i}", 1090,
                             1024 if i < 3 else 512, i == 3)
+        self._keep("dec", x)
         # generator
         G = "decoder.generator."
         har_src = ops.harmonic_source_f32_gpu(f0, noise, self.g(G + "m_source.l_linear.weight", _flat),
                                               self.g(G + "m_source.l_linear.bias"))
         har = ops.stft_magphase_lc_f32_gpu(har_src, 20, 5, cpad=32)  # [120 F + 1, 32]
+        self._keep("har_source", har_src)
+        self._keep("har", har)
         for i, (k_up, u, k_noise) in enumerate(((20, 10, 7), (12, 6, 11))):
             xs = ops.conv1d_lc_f32_gpu(har, self.g(G + f"noise_convs.{i}.weight", _w_lc_32),
                                        self.g(G + f"noise_convs.{i}.bias"),
                                        **({"stride": 6, "padding": 3} if i == 0 else {}))
+            self._keep(f"xs{i}_conv", xs)
             xs = self.resblock1(xs, bank_d, f"{G}noise_res.{i}", k_noise)
+            self._keep(f"xs{i}", xs)
             x = ops.leaky_lc_f32_gpu(x, 0.1)
             y = ops.gemm_f32_gpu_mps(x, self.g(G + f"ups.{i}.weight", _w_convt))  # [Lin, K * Co]
             x = ops.convt_gather_lc_f32_gpu(y, self.g(G + f"ups.{i}.bias"), k_up, u, (k_up - u) // 2, add=xs,
                                             reflect_left=(i == 1))
             xst = ops.channel_stats_lc_f32_gpu(x)  # shared by the three resblocks' first AdaIN
             rb = [self.resblock1(x, bank_d, f"{G}resblocks.{3 * i + j}", kk, xst) for j, kk in enumerate((3, 7, 11))]
+            self._keep(f"ups{i}", x)
             x = ops.add3_scale_f32_gpu(rb[0], rb[1], rb[2], 1.0 / 3.0)
+            self._keep(f"stage{i}", x)
         ident = self.const("identity_affine128", lambda: np.stack([np.zeros(128), np.ones(128), np.zeros(128)]))
         post = ops.conv1d_act_lc_f32_gpu(x, self.g(G + "conv_post.weight", _w_lc), self.g(G + "conv_post.bias"), ident,
                                          act="leaky", slope=0.01, padding=3)  # [120 F + 1, 22]

@@ -158,22 +158,33 @@ class Oracle:
         center, reflect) -> [22, frames]."""
         win = torch.hann_window(20, periodic=True, dtype=self.dt)
         z = torch.stft(x, 20, 5, 20, window=win, center=True, pad_mode="reflect", return_complex=True)
+        # Frame 0 is even about its centre (reflect padding, periodic Hann), so its spectrum is exactly real; the
+        # FFT's rounding-noise imaginary parts would make its phase +pi or -pi at random. Use the exact value.
+        z[:, 0] = torch.complex(z[:, 0].real, torch.zeros_like(z[:, 0].real))
         return torch.cat([z.abs(), torch.angle(z)], 0)
 
-    def generator(self, x, har, s_d):
+    def generator(self, x, har, s_d, keep=None):
         G = "decoder.generator."
         rb = None
         for i, (k_up, u, k_noise) in enumerate(((20, 10, 7), (12, 6, 11))):
             x = F.leaky_relu(x, 0.1)
             xs = self.conv(har, G + f"noise_convs.{i}", **({"stride": 6, "padding": 3} if i == 0 else {}))
+            if keep is not None:
+                keep[f"xs{i}_conv"] = xs
             xs = self.resblock1(xs, s_d, f"{G}noise_res.{i}", k_noise)
+            if keep is not None:
+                keep[f"xs{i}"] = xs
             x = F.conv_transpose1d(x[None], self.w[G + f"ups.{i}.weight"], self.w[G + f"ups.{i}.bias"], stride=u,
                                    padding=(k_up - u) // 2)[0]
             if i == 1:
                 x = F.pad(x[None], (1, 0), mode="reflect")[0]
             x = x + xs
+            if keep is not None:
+                keep[f"ups{i}"] = x
             rb = [self.resblock1(x, s_d, f"{G}resblocks.{3 * i + j}", kk) for j, kk in enumerate((3, 7, 11))]
             x = (rb[0] + rb[1] + rb[2]) / 3
+            if keep is not None:
+                keep[f"stage{i}"] = x
         x = F.leaky_relu(x, 0.01)
         return self.conv(x, G + "conv_post", padding=3)  # [22, L1]
 
@@ -202,7 +213,7 @@ class Oracle:
         f0_src = f0 if f0_override is None else torch.as_tensor(f0_override).to(self.dt)
         st["har_source"] = har_source = self.harmonic_source(f0_src, noise)
         st["har"] = har = self.stft(har_source)
-        st["post"] = post = self.generator(x, har, s_d)
+        st["post"] = post = self.generator(x, har, s_d, keep=st if stages else None)
         st["audio"] = self.istft(post)
         return st if stages else st["audio"]
 
