@@ -81,11 +81,13 @@ __global__ void harmonicSourceKernel(const float* __restrict__ f0, const float* 
     for (int h = 0; h < kHarm; ++h) {
       const float t0 = p300[i0 * kHarm + h], t1 = p300[i1 * kHarm + h];
       const float phase = __builtin_fmaf(t0, l0, t1 * l1);
-      const float sine = sinf(phase) * 0.1f;
+      // sin and tanh in double, rounded once to f32: correctly rounded (up to ties ~2^-29 apart), so the source
+      // is reproducible bit for bit by any implementation that rounds the same exact values.
+      const float sine = static_cast<float>(sin(static_cast<double>(phase))) * 0.1f;
       const float v = sine * uv + amp * noise[i * kHarm + h];
       y = y + v * w[h];
     }
-    out[i] = tanhf(y + b[0]);
+    out[i] = static_cast<float>(tanh(static_cast<double>(y + b[0])));
   }
 }
 
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(256) void stftKernel(const float* __restrict__ x, f
     // and reflect padding that frame is even about its centre (as is the periodic Hann window), and its exact
     // imaginary parts are 0 rather than rounding noise whose sign would flip the phase between +pi and -pi.
     if (k == 0 || 2 * k == nfft || t == 0) im = 0.0f;
-    o[k] = sqrtf(re * re + im * im);
+    o[k] = sqrtf(__builtin_fmaf(re, re, im * im));
     o[bins + k] = atan2f(im, re);
   }
   for (int64_t c = 2 * bins; c < ldo; ++c) o[c] = 0.0f;

@@ -154,6 +154,10 @@ class Oracle:
         return torch.from_numpy(harmonic_source(f0.detach().numpy().astype(np.float32), noise.numpy(), w, b)).to(self.dt)
 
     def stft(self, x):
+        """TorchSTFT.transform as the reference computes it in f32 (stft_magphase, below) -> [22, frames]."""
+        return torch.from_numpy(stft_magphase(x.detach().numpy().astype(np.float32))).to(self.dt)
+
+    def stft_torch(self, x):
         """TorchSTFT.transform: magnitude and phase (angle) of torch.stft(n_fft 20, hop 5, periodic Hann,
         center, reflect) -> [22, frames]."""
         win = torch.hann_window(20, periodic=True, dtype=self.dt)
@@ -265,3 +269,37 @@ def harmonic_source(f0: np.ndarray, noise: np.ndarray, w: np.ndarray, b: np.ndar
     for h in range(9):
         y = (y + (v[:, h] * f32(w[h])).astype(f32)).astype(f32)
     return np.tanh((y + f32(b[0])).astype(np.float64)).astype(f32)
+
+
+def stft_magphase(x: np.ndarray, n_fft: int = 20, hop: int = 5) -> np.ndarray:
+    """(|X|, angle X) of the center = True, reflect-padded, periodic-Hann STFT of f32 x -> f32[2K, frames]
+    (reference stft_magphase_f32, kernels/cpu/kokoro_signal.cpp:196-273): the windowed DFT table is built in
+    double and rounded to f32, each bin accumulates re += tab[m] * frame[m] over m in order in f32, the DC and
+    Nyquist bins (and every bin of the even-symmetric frame 0) are exactly real, |X| = sqrt(fma(re, re, im^2))."""
+    f32 = np.float32
+    x = x.astype(f32)
+    s = x.shape[0]
+    bins, pad = n_fft // 2 + 1, n_fft // 2
+    frames = s // hop + 1
+    m = np.arange(n_fft)
+    win = (0.5 - 0.5 * np.cos(2.0 * np.pi * m / n_fft)).astype(f32)
+    q = np.arange(frames)[:, None] * hop + m[None, :] - pad
+    q = np.abs(q)
+    q = np.where(q >= s, 2 * (s - 1) - q, q)
+    fr = x[q]  # [frames, n_fft]
+    out = np.zeros((2 * bins, frames), f32)
+    for k in range(bins):
+        ang = 2.0 * np.pi * ((k * m) % n_fft) / n_fft
+        tre = (win.astype(np.float64) * np.cos(ang)).astype(f32)
+        tim = (-win.astype(np.float64) * np.sin(ang)).astype(f32)
+        re = np.zeros(frames, f32)
+        im = np.zeros(frames, f32)
+        for j in range(n_fft):
+            re = (re + (tre[j] * fr[:, j]).astype(f32)).astype(f32)
+            im = (im + (tim[j] * fr[:, j]).astype(f32)).astype(f32)
+        if k == 0 or 2 * k == n_fft:
+            im[:] = 0
+        im[0] = 0
+        out[k] = np.sqrt(_fma32(re, re, (im * im).astype(f32)))
+        out[bins + k] = np.arctan2(im.astype(np.float64), re.astype(np.float64)).astype(f32)
+    return out
