@@ -61,6 +61,101 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
   }
 }
 
+// Persistent LSTM recurrence: 8 workgroups per direction, each owning 32 hidden units (their 4 x 32 gate rows of
+// W_hh, 128 KiB, resident in LDS for the whole sequence). Per step a workgroup computes its 128 gate rows
+// against h(t-1) from LDS, applies the cell update to its 32 units, and publishes h(t) as 64-bit words
+// {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256 values of h(t)
+// by polling those words until the tag matches. No fences, no counters: the tag orders each value on its own,
+// and a writer cannot run two steps ahead of any reader (it needs that reader's h of the step in between).
+// The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
+// kLstmSpinLimit polls the workgroup stops, writes NaN and records the failure, so a missing peer (e.g. not
+// co-resident) ends the kernel instead of hanging it.
+constexpr int kLstmWgs = 8;          // workgroups per direction
+constexpr int kLstmUnits = 32;       // hidden units per workgroup (H = 256)
+constexpr int kLstmRows = 4 * kLstmUnits;
+constexpr int kLstmThreads = 256;
+constexpr long long kLstmSpinLimit = 1LL << 22;
+
+__global__ void lstmClearKernel(unsigned long long* xbuf, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) xbuf[i] = 0ull;
+}
+
+__global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float* __restrict__ g,
+                                                                    const float* __restrict__ whhT,
+                                                                    float* __restrict__ out,
+                                                                    unsigned long long* xbuf, int* failed,
+                                                                    int64_t t) {
+  constexpr int H = 256;
+  extern __shared__ float lds[];
+  float* w = lds;                      // [H k][128 rows]
+  float* hs = w + H * kLstmRows;       // [H]
+  float* part = hs + H;                // [2][128]
+  const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
+  const int tid = threadIdx.x;
+  const int ld = 8 * H;
+  // rows r = gate * 32 + j  <->  gate row gate * H + 32 b + j of this direction
+  for (int i = tid; i < H * kLstmRows; i += kLstmThreads) {
+    const int k = i / kLstmRows, r = i % kLstmRows;
+    const int row = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
+    w[i] = whhT[static_cast<int64_t>(k) * ld + dir * 4 * H + row];
+  }
+  for (int i = tid; i < H; i += kLstmThreads) hs[i] = 0.0f;
+  __syncthreads();
+  const int r = tid % kLstmRows, half = tid / kLstmRows;  // two threads per gate row, 128 k each
+  const int growRow = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
+  unsigned long long* xb = xbuf + dir * H;
+  float c = 0.0f;
+  bool ok = true;
+  for (int64_t step = 0; step < t; ++step) {
+    const int64_t tt = dir == 0 ? step : t - 1 - step;
+    float a0 = 0.0f, a1 = 0.0f;
+    const float* wr = w + half * 128 * kLstmRows + r;
+    const float* hh = hs + half * 128;
+#pragma unroll 8
+    for (int k = 0; k < 128; k += 2) {
+      a0 += wr[k * kLstmRows] * hh[k];
+      a1 += wr[(k + 1) * kLstmRows] * hh[k + 1];
+    }
+    part[half * kLstmRows + r] = a0 + a1;
+    __syncthreads();
+    const unsigned tag = static_cast<unsigned>(step + 1);
+    if (tid < kLstmUnits) {
+      const int u = tid;
+      float gv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rr = q * kLstmUnits + u;
+        gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + u] + (part[rr] + part[kLstmRows + rr]);
+      }
+      const float ig = sigmoidf(gv[0]), fg = sigmoidf(gv[1]), gg = tanhf(gv[2]), og = sigmoidf(gv[3]);
+      c = fg * c + ig * gg;
+      const float hv = ok ? og * tanhf(c) : __builtin_nanf("");
+      out[tt * 2 * H + dir * H + b * kLstmUnits + u] = hv;
+      const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
+      __hip_atomic_store(xb + b * kLstmUnits + u, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    (void)growRow;
+    // gather h(t): thread k polls word k
+    {
+      const int k = tid;
+      unsigned long long word = 0ull;
+      long long spins = 0;
+      while (ok) {
+        word = __hip_atomic_load(xb + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<unsigned>(word >> 32) == tag) break;
+        if (++spins > kLstmSpinLimit) {
+          ok = false;
+          atomicExch(failed, 1);
+        }
+      }
+      hs[k] = ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
+    }
+    // A workgroup that timed out keeps stepping (so all of its waves reach the end) but stops waiting.
+    ok = __syncthreads_and(ok);
+  }
+}
+
 // Each workgroup scans dur (T <= 8192) into LDS, then gathers its rows: row f copies x[token(f)], token(f) =
 // the first i with cum[i] > f.
 __global__ __launch_bounds__(256) void repeatInterleaveKernel(const float* __restrict__ x,
@@ -149,8 +244,27 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   float* g = static_cast<float*>(workspace);
   int rc = lk_hip_gemm_f32(x, wih, b, nullptr, g, t, 8 * h, in, 1, 0, 1.0f, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0,
-                     static_cast<hipStream_t>(stream), g, whhT, out, t, static_cast<int>(h));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;
+  const int64_t xBytes = 2 * 256 * 8 + 256;
+  if (h == 256 && workspaceBytes >= gBytes + xBytes) {
+    auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
+    int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 2 * 256 * 8);
+    const size_t lds = (256 * lkd::kLstmRows + 256 + 2 * lkd::kLstmRows) * sizeof(float);
+    static bool attrSet = false;
+    if (!attrSet) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(lkd::lstmPersistentKernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+        return 2;
+      attrSet = true;
+    }
+    hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(2), dim3(256), 0, s, xbuf, 2 * 256);
+    hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), lds, s, g, whhT,
+                       out, xbuf, failed, t);
+  } else {
+    hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0, s, g, whhT, out,
+                       t, static_cast<int>(h));
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
