@@ -249,6 +249,146 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
     }
 }
 
+// Stride-1 channel-last conv with the taps innermost. For each 16-channel input chunk a workgroup stages the
+// halo rows its 128 output rows need (BM + (K-1) dil rows x 16 channels) once, with the affine + Snake / leaky
+// prologue applied once per element, k-major in LDS; then every tap kk is a 16-deep MFMA step whose A operand
+// is the same halo shifted by kk * dil rows and whose B operand is w[:, kk, chunk] ([16][BN] in LDS). Compared
+// with the flat im2col loop this reads each input element from L2 once per chunk instead of K times and
+// evaluates the prologue once instead of K times. Steps = chunks x taps, double-buffered: B per step, the halo
+// per chunk (prefetched into registers during the last tap of the previous chunk).
+constexpr int kMaxHalo = 256;
+
+template <int BM, int BN>
+__global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int halo) {
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int LDH = kMaxHalo + 4, LDB_S = BN + 4;
+  constexpr int B4 = BN * BK / 4 / NT;
+  constexpr int H4 = kMaxHalo * BK / 4 / NT;  // halo float4 slots per thread (4 at 256 rows)
+
+  __shared__ float Hs[2][BK][LDH];
+  __shared__ float Bs[2][BK][LDB_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const int64_t ci = p.convCi;
+  const int chunks = static_cast<int>(ci / BK);
+  const int steps = chunks * taps;
+  const int64_t rowBase = m0 - p.convPad;  // input row of halo row 0
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  float4 rh[H4], rb[B4];
+  auto loadHalo = [&](int chunk) {
+    const int64_t c0 = static_cast<int64_t>(chunk) * BK;
+#pragma unroll
+    for (int i = 0; i < H4; ++i) {
+      const int idx = tid + i * NT;
+      const int hr = idx >> 2, cq = (idx & 3) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int64_t t = rowBase + hr;
+      if (hr < halo && t >= 0 && t < p.convL) {
+        v = *reinterpret_cast<const float4*>(p.a + t * ci + c0 + cq);
+        if (p.pre != PRE_NONE || p.affine) {
+          v.x = preAct(p, v.x, static_cast<int>(c0 + cq));
+          v.y = preAct(p, v.y, static_cast<int>(c0 + cq + 1));
+          v.z = preAct(p, v.z, static_cast<int>(c0 + cq + 2));
+          v.w = preAct(p, v.w, static_cast<int>(c0 + cq + 3));
+        }
+      }
+      rh[i] = v;
+    }
+  };
+  auto storeHalo = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < H4; ++i) {
+      const int idx = tid + i * NT;
+      const int hr = idx >> 2, cq = (idx & 3) * 4;
+      if (hr < halo) {
+        Hs[buf][cq + 0][hr] = rh[i].x;
+        Hs[buf][cq + 1][hr] = rh[i].y;
+        Hs[buf][cq + 2][hr] = rh[i].z;
+        Hs[buf][cq + 3][hr] = rh[i].w;
+      }
+    }
+  };
+  // B for step s = chunk * taps + kk: w[co][kk][chunk * 16 .. +15] (w is [Co, K, Ci] row-major = ldb K * Ci)
+  auto loadB = [&](int s) {
+    const int chunk = s / taps, kk = s - chunk * taps;
+    const int64_t k0 = static_cast<int64_t>(kk) * ci + static_cast<int64_t>(chunk) * BK;
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      const int col = idx >> 2, kq = (idx & 3) * 4;
+      rb[i] = loadBnt4(p, n0 + col, k0 + kq);
+    }
+  };
+  auto storeB = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      const int col = idx >> 2, kq = (idx & 3) * 4;
+      Bs[buf][kq + 0][col] = rb[i].x;
+      Bs[buf][kq + 1][col] = rb[i].y;
+      Bs[buf][kq + 2][col] = rb[i].z;
+      Bs[buf][kq + 3][col] = rb[i].w;
+    }
+  };
+
+  loadHalo(0);
+  storeHalo(0);
+  loadB(0);
+  storeB(0);
+  __syncthreads();
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int s = 0; s < steps; ++s) {
+    const int chunk = s / taps, kk = s - chunk * taps;
+    const int hbuf = chunk & 1, bbuf = s & 1;
+    const bool more = s + 1 < steps;
+    const bool newChunk = more && kk == taps - 1;
+    if (more) loadB(s + 1);
+    if (newChunk) loadHalo(chunk + 1);
+    const int shift = kk * p.convDil;
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 2) {
+      float av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[i] = Hs[hbuf][ks + lk][wm * WTM + i * 32 + lrow + shift];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = Bs[bbuf][ks + lk][wn * WTN + j * 32 + lrow];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) storeB(bbuf ^ 1);
+    if (newChunk) storeHalo(hbuf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (row < p.m) p.c[row * p.ldc + col] = epilogue(p, acc[i][j][r], row, col);
+      }
+    }
+}
+
 }  // namespace lkd
 
 namespace lkh {
@@ -339,6 +479,14 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
   p.alpha = alpha;
   p.pre = pre;
   p.slope = slope;
+  const int64_t halo = 128 + static_cast<int64_t>(dilation) * (kw - 1);
+  const int64_t tiles = static_cast<int64_t>(lkh::ceilDiv(lo, 128)) * lkh::ceilDiv(co, 128);
+  if (stride == 1 && halo <= lkd::kMaxHalo && tiles >= 256) {
+    dim3 grid(lkh::ceilDiv(co, 128), lkh::ceilDiv(lo, 128));
+    hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, static_cast<hipStream_t>(stream), p,
+                       static_cast<int>(kw), static_cast<int>(halo));
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+  }
   lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }

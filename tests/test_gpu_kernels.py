@@ -248,3 +248,28 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(g1, e1) and np.array_equal(g2, e2)
         e1b = lk.ops.gemm_bias_relu_f32_gpu(A, B, BI).numpy()  # eager work between replays
         assert np.array_equal(e1b, e1)
+
+
+@pytest.mark.parametrize("l,c,co,k,d,act", [(40001, 128, 128, 11, 5, "snake"), (33000, 128, 128, 3, 1, "snake"),
+                                            (20000, 256, 256, 7, 3, "snake"), (30000, 128, 128, 7, 1, "leaky"),
+                                            (32768, 512, 256, 3, 1, "none")])
+def test_conv_tap_kernel_large(gpu, l, c, co, k, d, act):
+    """Large-L convs take the taps-innermost halo kernel; check it against the oracle on a row sample."""
+    lk = gpu
+    x, w, b = rng.standard_normal((l, c)), rng.standard_normal((co, k, c)) / np.sqrt(k * c), rng.standard_normal(co)
+    af = np.stack([rng.standard_normal(c) * 0.1, np.abs(rng.standard_normal(c)) + 0.5, rng.standard_normal(c) * 0.1])
+    alpha = np.abs(rng.standard_normal(c)) + 0.2
+    res = rng.standard_normal((l, co))
+    pad = d * (k - 1) // 2
+    got = lk.ops.conv1d_act_lc_f32_gpu(G(lk, x), G(lk, w), G(lk, b), G(lk, af), G(lk, alpha), act=act, slope=0.2,
+                                       residual=G(lk, res), out_scale=0.5, padding=pad, dilation=d).numpy()
+    rows = np.r_[0:300, l // 2 - 150:l // 2 + 150, l - 300:l]
+    lo_in, hi_in = max(0, rows.min() - pad), rows.max() + pad + 1
+    for seg in (slice(0, 300), slice(l // 2 - 150, l // 2 + 150), slice(l - 300, l)):
+        s0, s1 = seg.start, seg.stop
+        i0, i1 = max(0, s0 - pad), min(l, s1 + pad)
+        h = K.affine_act(x[i0:i1], af, alpha, act, 0.2)
+        full = K.conv1d_lc(np.pad(h, ((pad - (s0 - i0), pad - (i1 - s1)), (0, 0))), w, b, padding=0, dilation=d)
+        ref = (full + res[s0:s1]) * 0.5
+        close(got[s0:s1], ref, 1e-4)
+    del lo_in, hi_in
