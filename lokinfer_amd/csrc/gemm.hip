@@ -481,10 +481,17 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
   p.slope = slope;
   const int64_t halo = 128 + static_cast<int64_t>(dilation) * (kw - 1);
   const int64_t tiles = static_cast<int64_t>(lkh::ceilDiv(lo, 128)) * lkh::ceilDiv(co, 128);
-  if (stride == 1 && halo <= lkd::kMaxHalo && tiles >= 256) {
-    dim3 grid(lkh::ceilDiv(co, 128), lkh::ceilDiv(lo, 128));
-    hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, static_cast<hipStream_t>(stream), p,
-                       static_cast<int>(kw), static_cast<int>(halo));
+  if (stride == 1 && halo <= lkd::kMaxHalo) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (tiles >= 256) {
+      dim3 grid(lkh::ceilDiv(co, 128), lkh::ceilDiv(lo, 128));
+      hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
+                         static_cast<int>(halo));
+    } else {  // few output tiles (decoder / F0-N at frame rate): 64 x 64 tiles fill more of the 256 CUs
+      dim3 grid(lkh::ceilDiv(co, 64), lkh::ceilDiv(lo, 64));
+      hipLaunchKernelGGL((lkd::convTapKernel<64, 64>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
+                         static_cast<int>(halo - 64));
+    }
     return hipGetLastError() == hipSuccess ? 0 : 2;
   }
   lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, static_cast<hipStream_t>(stream));

@@ -112,6 +112,101 @@ __global__ __launch_bounds__(64) void attnQkvKernel(const float* __restrict__ qk
   for (int d = 0; d < HD; ++d) o[d] = acc[d] * inv + bias[2 * D + h * HD + d];
 }
 
+// Flash attention on f32 MFMA (32x32x2), head_dim 64. A workgroup = 4 waves = 128 queries of one head; each wave
+// owns 32 queries and walks the keys in 32-key tiles shared through LDS:
+//   S = Q K^T   32 MFMAs over the 64 dims (Q pre-scaled by 1/8 and + q-bias, held in 32 registers per lane)
+//   online softmax per query row on the accumulator layout (a row's 32 keys sit in 32 lanes of one half-wave)
+//   O += P V    P goes through LDS to the A-operand layout; 2 x 16 MFMAs for the 64 output dims
+// The k-bias cancels in softmax and is dropped; the v-bias is added once at the end.
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void attnMfmaKernel(const float* __restrict__ qkv, const float* __restrict__ bias,
+                                                      float* __restrict__ out, int64_t t, int heads, int causal) {
+  constexpr int HD = 64, KT = 32, LDK = HD + 1, LDV = HD + 4, LDP = KT + 1;
+  __shared__ float ks[KT][LDK];
+  __shared__ float vs[KT][LDV];
+  __shared__ float ps[4][32][LDP];
+  const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t D = static_cast<int64_t>(heads) * HD, ld = 3 * D;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * 128 + wave * 32;
+  const int lr = lane & 31, lh = lane >> 5;
+  // Q operand: lane holds Q[q0 + lr][2 s + lh] for s = 0..31
+  float qa[32];
+  {
+    const int64_t qi = min<int64_t>(q0 + lr, t - 1);
+    const float* qr = qkv + qi * ld + h * HD;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) qa[s] = (qr[2 * s + lh] + bias[h * HD + 2 * s + lh]) * 0.125f;
+  }
+  v16f_t o0, o1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
+  float mrow[16], lrow[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    mrow[r] = -INFINITY;
+    lrow[r] = 0.0f;
+  }
+  const int64_t blockQmax = min<int64_t>(t, static_cast<int64_t>(blockIdx.x) * 128 + 128);
+  const int64_t kEnd = causal ? blockQmax : t;
+  for (int64_t k0 = 0; k0 < kEnd; k0 += KT) {
+    __syncthreads();
+    for (int i = tid; i < KT * HD; i += 256) {
+      const int kr = i / HD, d = i % HD;
+      const int64_t j = k0 + kr;
+      ks[kr][d] = j < t ? qkv[j * ld + D + h * HD + d] : 0.0f;
+      vs[kr][d] = j < t ? qkv[j * ld + 2 * D + h * HD + d] : 0.0f;
+    }
+    __syncthreads();
+    // S tile: rows = queries, cols = keys
+    v16f_t sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[s], ks[lr][2 * s + lh], sacc, 0, 0, 0);
+    // online softmax: register r holds row 8 (r / 4) + 4 lh + r % 4, column (key) lr
+    const int64_t key = k0 + lr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t qrow = q0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      float sv = sacc[r];
+      if (key >= t || (causal && key > qrow)) sv = -INFINITY;
+      float mx = sv;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float mn = fmaxf(mrow[r], mx);
+      const float p = mn == -INFINITY ? 0.0f : expf(sv - mn);
+      const float corr = mn == -INFINITY ? 1.0f : expf(mrow[r] - mn);
+      float ps_ = p;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) ps_ += __shfl_xor(ps_, o, 64);
+      lrow[r] = lrow[r] * corr + ps_;
+      mrow[r] = mn;
+      o0[r] *= corr;
+      o1[r] *= corr;
+      ps[wave][8 * (r >> 2) + 4 * lh + (r & 3)][lr] = p;
+    }
+    __syncthreads();
+    // O += P V: A = P[q = lr][key = 2 s + lh], B = V[key][dim]
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float pa = ps[wave][lr][2 * s + lh];
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa, vs[2 * s + lh][lr], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa, vs[2 * s + lh][32 + lr], o1, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t qrow = q0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+    if (qrow < t) {
+      const float inv = 1.0f / lrow[r];
+      float* o = out + qrow * D + h * HD;
+      o[lr] = o0[r] * inv + bias[2 * D + h * HD + lr];
+      o[32 + lr] = o1[r] * inv + bias[2 * D + h * HD + 32 + lr];
+    }
+  }
+}
+
 __global__ void kvWriteKernel(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias,
                               int64_t d) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -146,8 +241,8 @@ int lk_hip_bias_gelu_f32(const float* x, const float* bias, float* out, int64_t 
 int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, int64_t t, int heads, int causal,
                              void* stream) {
   if (t <= 0) return t == 0 ? 0 : 1;
-  dim3 grid(lkh::ceilDiv(t, 64), static_cast<unsigned>(heads));
-  hipLaunchKernelGGL(lkd::attnQkvKernel, grid, dim3(64), 0, static_cast<hipStream_t>(stream), qkv, bias, out, t,
+  dim3 grid(lkh::ceilDiv(t, 128), static_cast<unsigned>(heads));
+  hipLaunchKernelGGL(lkd::attnMfmaKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), qkv, bias, out, t,
                      heads, causal);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
