@@ -152,25 +152,51 @@ def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
             "flops": kokoro_conv_flops(tokens, frames), "sd": sd, "inputs": (ids, ref_s, dur, noise)}
 
 
-def roofline_conv() -> dict:
+ROOFLINE_SHAPE = (292201, 128, 11, 5)  # L = 120 F + 1 at 487 tokens, C = 128, K = 11, dilation 5
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv_tap_snake_k11_L292201_traffic.txt")
+
+
+def measured_traffic() -> float | None:
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel of known size), or None when it has not been measured."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def roofline_conv(launches: int = 20, calibrate: bool = False) -> dict:
     """The dominant kernel of the Kokoro forward: the implicit-GEMM conv with the AdaIN + Snake prologue, at the
-    generator's stage-1 resblock shape (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11, d = 5)."""
+    generator's stage-1 resblock shape (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11, d = 5).
+    Algorithmic work per launch: 2 L C_in C_out K FLOPs. With calibrate, also launches add_f32_gpu over
+    2^26 floats (reads 512 MiB, writes 256 MiB) as the reference kernel for the --pmc byte counters."""
     import lokinfer_amd as lk
 
     rng = np.random.default_rng(0)
-    l, c, k, d = 292201, 128, 11, 5
+    l, c, k, d = ROOFLINE_SHAPE
     G = lambda a: lk.from_numpy(np.ascontiguousarray(a, np.float32), device="gpu", copy=True)  # noqa: E731
     x, w, b = G(rng.standard_normal((l, c))), G(rng.standard_normal((c, k, c)) / 40), G(rng.standard_normal(c))
     af = G(np.stack([np.zeros(c), np.ones(c), np.zeros(c)]))
     alpha = G(np.ones(c))
     fn = lambda: lk.ops.conv1d_act_lc_f32_gpu(x, w, b, af, alpha, act="snake", padding=d * (k - 1) // 2, dilation=d)  # noqa: E731
     fn()
-    ms = statistics.mean(event_times(fn, 20))
+    ms = statistics.mean(event_times(fn, launches))
+    if calibrate:
+        n = 1 << 26
+        p = lk.Tensor(torch.ones(n, device="cuda"))
+        q = lk.Tensor(torch.ones(n, device="cuda"))
+        for _ in range(5):
+            lk.ops.add_f32_gpu(p, q)
+        torch.cuda.synchronize()
     flops = 2.0 * l * c * c * k
-    return {"kernel": "gemmMfmaKernel<128,128,A_CONV,B_NT> (conv1d_act_lc_f32_gpu, snake prologue)", "bound": "mfma",
-            "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS, "traffic": None, "avg_launch_ms": ms,
-            "flops_per_launch": flops}
+    return {"kernel": "convTapKernel<128,128> (conv1d_act_lc_f32_gpu, AdaIN affine + Snake prologue)",
+            "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
+            "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops}
 
 
 def cpu_kokoro(sd, inputs, budget_s: float = 30.0) -> dict:
@@ -196,7 +222,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all", choices=["all", "kokoro487", "kokoro59", "gpt2"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="launch only the roofline kernel (and the copy-calibration kernel), for rocprofv3 runs")
     a = ap.parse_args()
+    if a.roofline_only:
+        r = roofline_conv(launches=a.steps, calibrate=True)
+        print(json.dumps({k: v for k, v in r.items()}))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this backend has no multi-GPU path (every box has one GPU)",
               file=sys.stderr)
