@@ -1,5 +1,5 @@
 """Benchmark of the reference's headline metric on one MI355X:
-"median Kokoro-82M f32 forward ms @59 & 487 tok; GPT-2 decode ms/token" (BASELINE.json).
+"median Kokoro-82M f32 forward ms @59 & 487 tok; GPT-2 decode ms/token".
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gpt2|kokoro487|kokoro59|all]
 

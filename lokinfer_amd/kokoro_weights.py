@@ -1,4 +1,4 @@
-"""Kokoro-82M-shaped parameters and synthetic inputs (BASELINE configs 3 and 4).
+"""Kokoro-82M-shaped parameters and synthetic inputs (the 59- and 487-token benchmark forwards).
 
 Parameter names and shapes follow the Kokoro-82M (StyleTTS2 + iSTFTNet) state dict as the reference's graph
 builder reads it (models/kokoro/model.py in lariaus/lokinfer; module shapes bench/research/kokoro/

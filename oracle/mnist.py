@@ -48,7 +48,7 @@ def gemm_bias_act(a, b, bias, relu: bool) -> np.ndarray:
     return out
 
 
-# Plumbing config (BASELINE.json configs[0]): x[1, 784] ~ N(0, 1); Linear 784->128 + ReLU; Linear 128->10.
+# Plumbing config: x[1, 784] ~ N(0, 1); Linear 784->128 + ReLU; Linear 128->10.
 # Weights / biases lk.randn(seed) / sqrt(fan_in), i.e. numpy default_rng(seed).standard_normal.
 SEEDS = dict(x=1000, w1=1001, b1=1002, w2=1003, b2=1004)
 

@@ -1,4 +1,4 @@
-"""GPT-2 124M decode on the GPU vs the transformers oracle: caches filled by stepping 512
+"""GPT-2 124M decode on the GPU vs the transformers oracle (the decode benchmark config): caches filled by stepping 512
 seeded prompt tokens, then the seeded next token at pos 512. Logits within max rel err 1e-4 of the f32 oracle;
 greedy argmax bit-exact."""
 import numpy as np

@@ -1,7 +1,7 @@
-"""Kokoro-82M-shaped forward on the GPU vs the PyTorch f32 oracle (BASELINE configs 3 / 4 semantics, reference
+"""Kokoro-82M-shaped forward on the GPU vs the PyTorch f32 oracle (the 59/487-token benchmark configs, reference
 models/kokoro/model.py:619-785), stage by stage.
 
-Tolerances (BASELINE north_star): token-rate / curve outputs max rel err <= 1e-4, waveform <= 1e-3 with equal
+Tolerances: token-rate / curve outputs max rel err <= 1e-4, waveform <= 1e-3 with equal
 frame counts. The waveform is compared with the oracle's harmonic source fed the GPU's F0 curve: the source
 phase is a running sum over every frame that reaches ~1e6 rad, so an f32 F0 difference of 1e-7 relative moves
 late samples by ~0.1 rad; the F0 curve itself is checked separately, and with identical F0 the source is
