@@ -16,6 +16,7 @@
 // 32x32 MFMA tiles and accumulates over K in steps of 2. Per 16-deep K tile both operands are staged in LDS
 // k-major ([16][BM], [16][BN]) so that a wave's MFMA operand fetch is 32 consecutive floats per k row.
 #include "common.h"
+#include "lokinfer_hip.h"
 
 namespace lkd {
 
@@ -44,6 +45,8 @@ struct GemmParams {
   const float* alpha;
   int pre;
   float slope;
+  // optional per-(128-row chunk, channel) (mean, M2) of the output, [ceil(M / 128), N, 2] (conv tap kernel)
+  float* stats;
 };
 
 constexpr int BK = 16;
@@ -259,7 +262,8 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
 constexpr int kMaxHalo = 256;
 
 template <int BM, int BN>
-__global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int halo) {
+// At most 168 VGPRs: three waves per SIMD (12 per CU) keep the MFMA pipe fed through the barriers.
+__global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, int halo) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int LDH = kMaxHalo + 4, LDB_S = BN + 4;
@@ -288,36 +292,67 @@ __global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int 
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   float4 rh[H4], rb[B4];
+  // A thread always stages the same 4 channels of a chunk (idx & 3 == tid & 3), so the prologue's per-channel
+  // parameters are loaded once per chunk, not once per element.
+  const bool hasPre = p.pre != PRE_NONE || p.affine;
+  // Raw halo loads only: the prologue runs at LDS-store time, so its parameters are not live across the MFMAs.
   auto loadHalo = [&](int chunk) {
     const int64_t c0 = static_cast<int64_t>(chunk) * BK;
+    const int cq = (tid & 3) * 4;
 #pragma unroll
     for (int i = 0; i < H4; ++i) {
       const int idx = tid + i * NT;
-      const int hr = idx >> 2, cq = (idx & 3) * 4;
+      const int hr = idx >> 2;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       const int64_t t = rowBase + hr;
-      if (hr < halo && t >= 0 && t < p.convL) {
-        v = *reinterpret_cast<const float4*>(p.a + t * ci + c0 + cq);
-        if (p.pre != PRE_NONE || p.affine) {
-          v.x = preAct(p, v.x, static_cast<int>(c0 + cq));
-          v.y = preAct(p, v.y, static_cast<int>(c0 + cq + 1));
-          v.z = preAct(p, v.z, static_cast<int>(c0 + cq + 2));
-          v.w = preAct(p, v.w, static_cast<int>(c0 + cq + 3));
-        }
-      }
+      if (hr < halo && t >= 0 && t < p.convL) v = *reinterpret_cast<const float4*>(p.a + t * ci + c0 + cq);
       rh[i] = v;
     }
   };
-  auto storeHalo = [&](int buf) {
+  auto storeHalo = [&](int buf, int chunk) {
+    const int64_t c0 = static_cast<int64_t>(chunk) * BK;
+    const int cq = (tid & 3) * 4;
+    float mu[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f}, be[4] = {0.f, 0.f, 0.f, 0.f};
+    float al[4] = {1.f, 1.f, 1.f, 1.f}, ial[4] = {1.f, 1.f, 1.f, 1.f};
+    if (hasPre) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t c = c0 + cq + q;
+        if (p.affine) {
+          mu[q] = p.affine[c];
+          sc[q] = p.affine[ci + c];
+          be[q] = p.affine[2 * ci + c];
+        }
+        if (p.pre == PRE_SNAKE) {
+          al[q] = p.alpha[c];
+          ial[q] = 1.0f / al[q];
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < H4; ++i) {
       const int idx = tid + i * NT;
-      const int hr = idx >> 2, cq = (idx & 3) * 4;
+      const int hr = idx >> 2;
       if (hr < halo) {
-        Hs[buf][cq + 0][hr] = rh[i].x;
-        Hs[buf][cq + 1][hr] = rh[i].y;
-        Hs[buf][cq + 2][hr] = rh[i].z;
-        Hs[buf][cq + 3][hr] = rh[i].w;
+        float e[4] = {rh[i].x, rh[i].y, rh[i].z, rh[i].w};
+        const int64_t t = rowBase + hr;
+        if (hasPre && t >= 0 && t < p.convL) {  // zero padding stays zero: it is applied after the prologue
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float u = p.affine ? (e[q] - mu[q]) * sc[q] + be[q] : e[q];
+            if (p.pre == PRE_SNAKE) {
+              const float s = sinf(al[q] * u);
+              u = u + ial[q] * (s * s);
+            } else if (p.pre == PRE_LEAKY) {
+              u = u >= 0.0f ? u : u * p.slope;
+            }
+            e[q] = u;
+          }
+        }
+        Hs[buf][cq + 0][hr] = e[0];
+        Hs[buf][cq + 1][hr] = e[1];
+        Hs[buf][cq + 2][hr] = e[2];
+        Hs[buf][cq + 3][hr] = e[3];
       }
     }
   };
@@ -345,7 +380,7 @@ __global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int 
   };
 
   loadHalo(0);
-  storeHalo(0);
+  storeHalo(0, 0);
   loadB(0);
   storeB(0);
   __syncthreads();
@@ -371,7 +406,7 @@ __global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int 
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
     if (more) storeB(bbuf ^ 1);
-    if (newChunk) storeHalo(hbuf ^ 1);
+    if (newChunk) storeHalo(hbuf ^ 1, chunk + 1);
     __syncthreads();
   }
 
@@ -380,13 +415,74 @@ __global__ __launch_bounds__(NT) void convTapKernel(GemmParams p, int taps, int 
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = n0 + wn * WTN + j * 32 + lrow;
-      if (col >= p.n) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        if (row < p.m) p.c[row * p.ldc + col] = epilogue(p, acc[i][j][r], row, col);
+        if (row < p.m && col < p.n) {
+          const float v = epilogue(p, acc[i][j][r], row, col);
+          p.c[row * p.ldc + col] = v;
+          acc[i][j][r] = v;
+        }
       }
     }
+  if (BM == 128 && p.stats) {
+    // Per-(128-row chunk, channel) (mean, M2) of the stored output, two passes over the registers: this tile is
+    // exactly chunk blockIdx.y. A column's 128 rows sit in (wm, i, lane half, r); reduce r and i in registers,
+    // the two lane halves with a shuffle, and the two wm waves through LDS.
+    float* red = &Hs[0][0][0];  // reuse the staging LDS (free after the last barrier)
+    const int n = static_cast<int>(min<int64_t>(BM, p.m - m0));
+    float colSum[TN], colM2[TN], mean[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rloc = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (rloc < n) s += acc[i][j][r];
+        }
+      colSum[j] = s + __shfl_xor(s, 32, 64);
+    }
+    if (lk == 0)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) red[wm * BN + wn * WTN + j * 32 + lrow] = colSum[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = wn * WTN + j * 32 + lrow;
+      mean[j] = (red[c] + red[BN + c]) / static_cast<float>(n);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rloc = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          const float d = acc[i][j][r] - mean[j];
+          if (rloc < n) s += d * d;
+        }
+      colM2[j] = s + __shfl_xor(s, 32, 64);
+    }
+    if (lk == 0)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) red[wm * BN + wn * WTN + j * 32 + lrow] = colM2[j];
+    __syncthreads();
+    if (wm == 0 && lk == 0)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int c = wn * WTN + j * 32 + lrow;
+        const int64_t col = n0 + c;
+        if (col < p.n) {
+          float* st = p.stats + (static_cast<int64_t>(blockIdx.y) * p.n + col) * 2;
+          st[0] = mean[j];
+          st[1] = red[c] + red[BN + c];
+        }
+      }
+  }
 }
 
 }  // namespace lkd
@@ -452,7 +548,7 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
 // then snake(alpha [Ci]) (pre = 1) or leaky(slope) (pre = 2); zero padding applies after pre.
 int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
                          int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
-                         const float* affine, const float* alpha, int pre, float slope, void* stream) {
+                         const float* affine, const float* alpha, int pre, float slope, float* stats, void* stream) {
   if (ci % 16 != 0 || stride < 1 || dilation < 1 || padding < 0) return 1;
   const int64_t lo = (l + 2 * padding - static_cast<int64_t>(dilation) * (kw - 1) - 1) / stride + 1;
   if (lo <= 0 || co <= 0) return lo == 0 ? 0 : 1;
@@ -479,11 +575,14 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
   p.alpha = alpha;
   p.pre = pre;
   p.slope = slope;
+  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t halo = 128 + static_cast<int64_t>(dilation) * (kw - 1);
   const int64_t tiles = static_cast<int64_t>(lkh::ceilDiv(lo, 128)) * lkh::ceilDiv(co, 128);
+  bool statsDone = false;
   if (stride == 1 && halo <= lkd::kMaxHalo) {
-    hipStream_t s = static_cast<hipStream_t>(stream);
     if (tiles >= 256) {
+      p.stats = stats;  // the 128-row tiles are exactly the statistics chunks
+      statsDone = stats != nullptr;
       dim3 grid(lkh::ceilDiv(co, 128), lkh::ceilDiv(lo, 128));
       hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
                          static_cast<int>(halo));
@@ -492,10 +591,12 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
       hipLaunchKernelGGL((lkd::convTapKernel<64, 64>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
                          static_cast<int>(halo - 64));
     }
-    return hipGetLastError() == hipSuccess ? 0 : 2;
+  } else {
+    lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, s);
   }
-  lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, static_cast<hipStream_t>(stream));
-  return hipGetLastError() == hipSuccess ? 0 : 2;
+  if (hipGetLastError() != hipSuccess) return 2;
+  if (stats && !statsDone) return lk_hip_channel_stats_lc_f32(out, stats, lo, co, stream);
+  return 0;
 }
 
 }  // extern "C"

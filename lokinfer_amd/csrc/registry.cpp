@@ -144,13 +144,14 @@ void runConvLc(ExecCtx& ctx, const KernelArgs& a) {
   const float* res = RES ? P<float>(a, 3) : nullptr;
   float* out = P<float>(a, RES ? 4 : 3);
   status(ctx, lk_hip_conv1d_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), res, out, l, ci, co, kw, str, pad,
-                                   dil, scale, nullptr, nullptr, 0, 0.0f, ctx.stream),
+                                   dil, scale, nullptr, nullptr, 0, 0.0f, nullptr, ctx.stream),
          "conv1d_lc: invalid configuration");
 }
 
-// conv1d_act_lc (this backend's fused prologue conv): x[L, Ci], w[Co, K, Ci], b[Co], affine[3, Ci], alpha[Ci],
-// [res[Lo, Co]]; ints attrs: act (0 affine only, 1 snake, 2 leaky), dilation, padding, stride; floats: oscale, slope
-template <bool RES>
+// conv1d_act_lc[_res][_stats] (this backend's fused prologue conv): x[L, Ci], w[Co, K, Ci], b[Co], affine[3, Ci],
+// alpha[Ci], [res[Lo, Co]] -> out[Lo, Co] [, stats[ceil(Lo / 128), Co, 2]]; ints attrs: act (0 affine only,
+// 1 snake, 2 leaky), dilation, padding, stride; floats: oscale, slope
+template <bool RES, bool STATS>
 void runConvActLc(ExecCtx& ctx, const KernelArgs& a) {
   Ints it(a);
   const int64_t l = it.next(), ci = it.next();
@@ -158,15 +159,21 @@ void runConvActLc(ExecCtx& ctx, const KernelArgs& a) {
   LK_REQUIRE(ctx, it.next() == ci, "conv1d_act_lc: w must be f32[Co, K, Ci]");
   it.skip(1 + 2 + 1);  // b, affine, alpha
   if (RES) it.skip(2);
-  it.skip(2);
+  const int64_t lo = it.next();
+  it.skip(1);
+  if (STATS) {
+    LK_REQUIRE(ctx, it.next() == (lo + 127) / 128 && it.next() == co && it.next() == 2,
+               "conv1d_act_lc_stats: stats must be f32[ceil(Lo / 128), Co, 2]");
+  }
   const int act = static_cast<int>(it.next());
   const int dil = static_cast<int>(it.next()), pad = static_cast<int>(it.next()), str = static_cast<int>(it.next());
   const float scale = F(a, 0, 1.0f), slope = F(a, 1, 0.0f);
   LK_REQUIRE(ctx, ci % 16 == 0, "conv1d_act_lc: Ci must be a multiple of 16");
   const float* res = RES ? P<float>(a, 5) : nullptr;
   float* out = P<float>(a, RES ? 6 : 5);
+  float* stats = STATS ? P<float>(a, RES ? 7 : 6) : nullptr;
   status(ctx, lk_hip_conv1d_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), res, out, l, ci, co, kw, str, pad,
-                                   dil, scale, P<float>(a, 3), P<float>(a, 4), act, slope, ctx.stream),
+                                   dil, scale, P<float>(a, 3), P<float>(a, 4), act, slope, stats, ctx.stream),
          "conv1d_act_lc: invalid configuration");
 }
 
@@ -196,8 +203,10 @@ void registerGemmKernels() {
   registerKernel({"gemv1_bias_f32_gpu", G, runGemv1Bias, 3, 1});
   registerKernel({"conv1d_lc_f32_gpu", G, runConvLc<false>, 3, 1});
   registerKernel({"conv1d_lc_res_f32_gpu", G, runConvLc<true>, 4, 1});
-  registerKernel({"conv1d_act_lc_f32_gpu", G, runConvActLc<false>, 5, 1});
-  registerKernel({"conv1d_act_lc_res_f32_gpu", G, runConvActLc<true>, 6, 1});
+  registerKernel({"conv1d_act_lc_f32_gpu", G, runConvActLc<false, false>, 5, 1});
+  registerKernel({"conv1d_act_lc_res_f32_gpu", G, runConvActLc<true, false>, 6, 1});
+  registerKernel({"conv1d_act_lc_stats_f32_gpu", G, runConvActLc<false, true>, 5, 2});
+  registerKernel({"conv1d_act_lc_res_stats_f32_gpu", G, runConvActLc<true, true>, 6, 2});
 }
 
 // ---- transformer ------------------------------------------------------------------------------------------

@@ -143,11 +143,13 @@ class KokoroGpu:
             h = ops.leaky_lc_f32_gpu(x, 0.2, affine=af)
             h = ops.dwconvt_lc_f32_gpu(h, self.const(p + "#pool_w", lambda: _pool_pad(self.sd[p + ".pool.weight"], cp)),
                                        self.const(p + "#pool_b", lambda: _vec_pad(self.sd[p + ".pool.bias"], cp)))
-            h = ops.conv1d_lc_f32_gpu(h, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), padding=1)
+            ident = self.const(f"identity_affine{cp}", lambda: np.stack([np.zeros(cp), np.ones(cp), np.zeros(cp)]))
+            h, hst = ops.conv1d_act_lc_f32_gpu(h, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), ident,
+                                               act="none", padding=1, stats=True)
         else:
-            h = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), af,
-                                          act="leaky", slope=0.2, padding=1)
-        af2 = self.affine(h, bank, p + ".norm2.fc")
+            h, hst = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), af,
+                                               act="leaky", slope=0.2, padding=1, stats=True)
+        af2 = self.affine(h, bank, p + ".norm2.fc", hst)
         sc = ops.upsample2_lc_f32_gpu(x) if upsample else x
         if p + ".conv1x1.weight" in self.sd:
             sc = ops.conv1d_lc_f32_gpu(sc, self.g(p + ".conv1x1.weight", _w_lc),
@@ -160,15 +162,14 @@ class KokoroGpu:
         st = ops.channel_stats_lc_f32_gpu(x) if x_stats is None else x_stats
         for j, d in enumerate((1, 3, 5)):
             af = self.affine(x, bank, f"{p}.adain1.{j}.fc", st)
-            h = ops.conv1d_act_lc_f32_gpu(x, self.g(f"{p}.convs1.{j}.weight", _w_lc), self.g(f"{p}.convs1.{j}.bias"),
-                                          af, self.g(f"{p}.alpha1.{j}", _flat), act="snake",
-                                          padding=d * (k - 1) // 2, dilation=d)
-            af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc")
-            x = ops.conv1d_act_lc_f32_gpu(h, self.g(f"{p}.convs2.{j}.weight", _w_lc), self.g(f"{p}.convs2.{j}.bias"),
+            h, hst = ops.conv1d_act_lc_f32_gpu(x, self.g(f"{p}.convs1.{j}.weight", _w_lc),
+                                               self.g(f"{p}.convs1.{j}.bias"), af, self.g(f"{p}.alpha1.{j}", _flat),
+                                               act="snake", padding=d * (k - 1) // 2, dilation=d, stats=True)
+            af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc", hst)
+            y = ops.conv1d_act_lc_f32_gpu(h, self.g(f"{p}.convs2.{j}.weight", _w_lc), self.g(f"{p}.convs2.{j}.bias"),
                                           af2, self.g(f"{p}.alpha2.{j}", _flat), act="snake", padding=(k - 1) // 2,
-                                          residual=x)
-            if j < 2:
-                st = ops.channel_stats_lc_f32_gpu(x)
+                                          residual=x, stats=j < 2)
+            x, st = y if j < 2 else (y, None)
         return x
 
     def lstm(self, x: Tensor, p: str) -> Tensor:

@@ -236,7 +236,7 @@ def conv1d_lc_f32_gpu(x, w, b, residual=None, out_scale=1.0, padding=0, dilation
 
 
 def conv1d_act_lc_f32_gpu(x, w, b, affine, alpha=None, act="snake", slope=0.0, residual=None, out_scale=1.0,
-                          padding=0, dilation=1, stride=1):
+                          padding=0, dilation=1, stride=1, stats=False):
     """(MI355X backend) conv1d_lc over act(affine(x)) with the prologue fused into the implicit-GEMM operand
     staging: v = (x - af[0]) * af[1] + af[2] per channel, then snake(alpha) / leaky(slope) / none; the conv's zero
     padding applies after the activation. Replaces the reference's snake_affine_lc + conv1d_lc pair and its
@@ -251,11 +251,15 @@ def conv1d_act_lc_f32_gpu(x, w, b, affine, alpha=None, act="snake", slope=0.0, r
     check(alpha.shape[0] == x.shape[1] or code != 1, "alpha must be f32[Ci]")
     attrs = dict(act=code, dilation=int(dilation), oscale=float(out_scale), padding=int(padding), slope=float(slope),
                  stride=int(stride))
+    # stats=True also returns the output's per-(128-row chunk, channel) (mean, M2), the channel_stats_lc layout,
+    # computed in the conv's epilogue
+    shapes = [s, (-(-s[0] // STAT_CHUNK), s[1], 2)] if stats else [s]
+    sfx = "_stats" if stats else ""
     if residual is None:
         check(out_scale == 1.0, "out_scale needs a residual")
-        return _launch("conv1d_act_lc_f32_gpu", [x, w, b, affine, alpha], [s], attrs)
+        return _launch(f"conv1d_act_lc{sfx}_f32_gpu", [x, w, b, affine, alpha], shapes, attrs)
     check(tuple(residual.shape) == s, "residual shape mismatch")
-    return _launch("conv1d_act_lc_res_f32_gpu", [x, w, b, affine, alpha, residual], [s], attrs)
+    return _launch(f"conv1d_act_lc_res{sfx}_f32_gpu", [x, w, b, affine, alpha, residual], shapes, attrs)
 
 
 # ---- transformer --------------------------------------------------------------------------------------------
