@@ -30,6 +30,7 @@ import torch
 
 from . import ops
 from .compiler import compile as lk_compile
+from .runtime import GpuContext
 from .tensor import Tensor, from_numpy
 
 SQRT1_2 = 1.0 / math.sqrt(2.0)
@@ -66,6 +67,8 @@ class KokoroGpu:
         self._g: dict[str, Tensor] = {}
         self._per_t: dict[tuple, Tensor] = {}
         self.banks = {root: self._bank(root) for root in ("predictor", "decoder")}
+        # side streams for the graph's concurrent branches (default priority)
+        self.streams = [torch.cuda.Stream(), torch.cuda.Stream()]
         self.model = lk_compile(self._forward, graph=graph)
         self.debug: dict | None = None  # set to {} to keep named intermediates (eager runs only)
 
@@ -222,7 +225,12 @@ class KokoroGpu:
                   self.banks["predictor"][2])
         bank_d = (ops.gemv4_f32_gpu(s_d, self.banks["decoder"][0], self.banks["decoder"][1]), self.banks["decoder"][2])
         sp_vec = ops.view(s_p, [128])
-        # text side
+        ctx = GpuContext.shared()
+        # The TextEncoder (-> asr) depends only on the ids: it runs as a concurrent branch of the graph, next to
+        # ALBERT and the duration encoder (the reference overlaps it with GPU work the same way, model.py:682-699).
+        with ctx.branch(self.streams[0], 1):
+            t_en = self.text_encoder(ids)
+            asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
         bert = self.albert(ids)
         d_en = ops.gemm_bias_f32_gpu(bert, self.g("bert_encoder.weight", _t), self.g("bert_encoder.bias"))
         x = ops.concat_bcast_f32_gpu(d_en, sp_vec)
@@ -232,17 +240,21 @@ class KokoroGpu:
             x = ops.concat_bcast_f32_gpu(x, sp_vec)
         en = ops.repeat_interleave_f32_gpu(x, dur, frames)  # [F, 640]
         sh = self.lstm(en, "predictor.shared")  # [F, 512]
-        curves = []
-        for name in ("F0", "N"):
+
+        def curve(name: str) -> Tensor:
             y = self.resblk(sh, bank_p, f"predictor.{name}.0", 512, 512, False)
             y = self.resblk(y, bank_p, f"predictor.{name}.1", 512, 256, True)
             y = self.resblk(y, bank_p, f"predictor.{name}.2", 256, 256, False)
             y = ops.gemv1_bias_f32_gpu(y, self.g(f"predictor.{name}_proj.weight", _col),
                                        self.g(f"predictor.{name}_proj.bias"))
-            curves.append(ops.reshape(y, [2 * frames]))
-        f0, n_curve = curves
-        t_en = self.text_encoder(ids)
-        asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
+            return ops.reshape(y, [2 * frames])
+
+        # F0 and N are independent frame-rate conv stacks of a few hundred tiles each: run them side by side.
+        with ctx.branch(self.streams[1], 2):
+            n_curve = curve("N")
+        f0 = curve("F0")
+        ctx.join(self.streams[1])
+        ctx.join(self.streams[0])
         # decoder
         fn_cf = Tensor(torch.empty((2, frames), dtype=torch.float32, device=asr.t.device))
         ops.conv1d_1ch_f32_gpu(f0, self.g("decoder.F0_conv.weight", _flat), self.g("decoder.F0_conv.bias"), stride=2,

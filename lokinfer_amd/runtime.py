@@ -27,6 +27,44 @@ class GpuContext:
         self.workspace = torch.zeros(WORKSPACE_BYTES // 4, dtype=torch.float32, device=self.device)
         self.lib = lib()
         self._handles: dict[str, int] = {}
+        self._ws_by_slot: dict[int, torch.Tensor] = {0: self.workspace}
+        self.slot = 0
+
+    def workspace_for(self, slot: int) -> torch.Tensor:
+        """Workspace of a branch slot. Kernels on one stream are ordered and share slot 0; a branch that runs
+        concurrently on another stream (see `branch`) uses its own slot. A new slot is allocated on first use,
+        which happens on a model's eager warm-up run, before any graph capture."""
+        ws = self._ws_by_slot.get(slot)
+        if ws is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise LokinferError("no workspace for this branch yet: run the function once outside capture")
+            ws = torch.zeros(WORKSPACE_BYTES // 4, dtype=torch.float32, device=self.device)
+            self._ws_by_slot[slot] = ws
+        return ws
+
+    def branch(self, stream: "torch.cuda.Stream", slot: int):
+        """Context manager: run the enclosed launches on `stream` (which first waits for the current stream)
+        with workspace slot `slot`. Join with `join(stream)` before consuming the branch's outputs."""
+        ctx = self
+
+        class _Branch:
+            def __enter__(self):
+                stream.wait_stream(torch.cuda.current_stream(ctx.device))
+                self._prev = ctx.slot
+                self._sc = torch.cuda.stream(stream)
+                self._sc.__enter__()
+                ctx.slot = slot
+                return stream
+
+            def __exit__(self, *exc):
+                ctx.slot = self._prev
+                self._sc.__exit__(*exc)
+                return False
+
+        return _Branch()
+
+    def join(self, stream: "torch.cuda.Stream") -> None:
+        torch.cuda.current_stream(self.device).wait_stream(stream)
 
     @classmethod
     def shared(cls) -> "GpuContext":
@@ -50,8 +88,8 @@ class GpuContext:
         ia = (C.c_int64 * max(1, n_i))(*ints)
         fa = (C.c_double * max(1, n_f))(*floats)
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        rc = L.lk_run_kernel(self.handle(name), pa, n_p, ia, n_i, fa, n_f, self.workspace.data_ptr(),
-                             self.workspace.numel() * 4, stream)
+        ws = self.workspace_for(self.slot)
+        rc = L.lk_run_kernel(self.handle(name), pa, n_p, ia, n_i, fa, n_f, ws.data_ptr(), ws.numel() * 4, stream)
         if rc != 0:
             raise LokinferError(L.lk_last_error().decode())
 
