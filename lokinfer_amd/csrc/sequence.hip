@@ -61,18 +61,19 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
   }
 }
 
-// Persistent LSTM recurrence: 8 workgroups per direction, each owning 32 hidden units (their 4 x 32 gate rows of
-// W_hh, 128 KiB, resident in LDS for the whole sequence). Per step a workgroup computes its 128 gate rows
-// against h(t-1) from LDS, applies the cell update to its 32 units, and publishes h(t) as 64-bit words
+// Persistent LSTM recurrence: 16 workgroups per direction, each owning 16 hidden units (their 4 x 16 gate rows of
+// W_hh, 65 KiB, resident in LDS for the whole sequence). Per step a workgroup computes its 64 gate rows
+// against h(t-1) from LDS, applies the cell update to its 16 units, and publishes h(t) as 64-bit words
 // {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256 values of h(t)
 // by polling those words until the tag matches. No fences, no counters: the tag orders each value on its own,
 // and a writer cannot run two steps ahead of any reader (it needs that reader's h of the step in between).
 // The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
 // kLstmSpinLimit polls the workgroup stops, writes NaN and records the failure, so a missing peer (e.g. not
 // co-resident) ends the kernel instead of hanging it.
-constexpr int kLstmWgs = 8;          // workgroups per direction
-constexpr int kLstmUnits = 32;       // hidden units per workgroup (H = 256)
+constexpr int kLstmWgs = 16;         // workgroups per direction
+constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
 constexpr int kLstmRows = 4 * kLstmUnits;
+constexpr int kLstmLdk = 256 + 4;    // LDS row stride of the W_hh slice (float4 reads without bank conflicts)
 constexpr int kLstmThreads = 256;
 constexpr long long kLstmSpinLimit = 1LL << 22;
 
@@ -88,36 +89,41 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
                                                                     int64_t t) {
   constexpr int H = 256;
   extern __shared__ float lds[];
-  float* w = lds;                      // [H k][128 rows]
-  float* hs = w + H * kLstmRows;       // [H]
-  float* part = hs + H;                // [2][128]
+  float* w = lds;                            // [rows][kLstmLdk]: row r's 256 weights contiguous (+4 pad)
+  float* hs = w + kLstmRows * kLstmLdk;      // [H]
+  float* part = hs + H;                      // [rows]
   const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
   const int tid = threadIdx.x;
   const int ld = 8 * H;
-  // rows r = gate * 32 + j  <->  gate row gate * H + 32 b + j of this direction
+  // rows r = gate * U + j  <->  gate row gate * H + U b + j of this direction (U = units per workgroup)
   for (int i = tid; i < H * kLstmRows; i += kLstmThreads) {
     const int k = i / kLstmRows, r = i % kLstmRows;
     const int row = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
-    w[i] = whhT[static_cast<int64_t>(k) * ld + dir * 4 * H + row];
+    w[r * kLstmLdk + k] = whhT[static_cast<int64_t>(k) * ld + dir * 4 * H + row];
   }
   for (int i = tid; i < H; i += kLstmThreads) hs[i] = 0.0f;
   __syncthreads();
-  const int r = tid % kLstmRows, half = tid / kLstmRows;  // two threads per gate row, 128 k each
-  const int growRow = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
+  // Four threads per gate row (adjacent lanes), 64 k each, read as float4 from LDS; the rows' 4 partial sums
+  // are combined with two lane shuffles.
+  const int r = tid >> 2, q4 = tid & 3;
   unsigned long long* xb = xbuf + dir * H;
   float c = 0.0f;
   bool ok = true;
   for (int64_t step = 0; step < t; ++step) {
     const int64_t tt = dir == 0 ? step : t - 1 - step;
     float a0 = 0.0f, a1 = 0.0f;
-    const float* wr = w + half * 128 * kLstmRows + r;
-    const float* hh = hs + half * 128;
-#pragma unroll 8
-    for (int k = 0; k < 128; k += 2) {
-      a0 += wr[k * kLstmRows] * hh[k];
-      a1 += wr[(k + 1) * kLstmRows] * hh[k + 1];
+    const float4* wr = reinterpret_cast<const float4*>(w + r * kLstmLdk + q4 * 64);
+    const float4* hh = reinterpret_cast<const float4*>(hs + q4 * 64);
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+      const float4 w0 = wr[k], h0 = hh[k], w1 = wr[k + 1], h1 = hh[k + 1];
+      a0 += w0.x * h0.x + w0.y * h0.y + w0.z * h0.z + w0.w * h0.w;
+      a1 += w1.x * h1.x + w1.y * h1.y + w1.z * h1.z + w1.w * h1.w;
     }
-    part[half * kLstmRows + r] = a0 + a1;
+    float acc = a0 + a1;
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (q4 == 0) part[r] = acc;
     __syncthreads();
     const unsigned tag = static_cast<unsigned>(step + 1);
     if (tid < kLstmUnits) {
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int rr = q * kLstmUnits + u;
-        gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + u] + (part[rr] + part[kLstmRows + rr]);
+        gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + u] + part[rr];
       }
       const float ig = sigmoidf(gv[0]), fg = sigmoidf(gv[1]), gg = tanhf(gv[2]), og = sigmoidf(gv[3]);
       c = fg * c + ig * gg;
@@ -135,7 +141,6 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
       __hip_atomic_store(xb + b * kLstmUnits + u, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    (void)growRow;
     // gather h(t): thread k polls word k
     {
       const int k = tid;
@@ -250,7 +255,7 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (h == 256 && workspaceBytes >= gBytes + xBytes) {
     auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
     int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 2 * 256 * 8);
-    const size_t lds = (256 * lkd::kLstmRows + 256 + 2 * lkd::kLstmRows) * sizeof(float);
+    const size_t lds = (lkd::kLstmRows * lkd::kLstmLdk + 256 + lkd::kLstmRows) * sizeof(float);
     static bool attrSet = false;
     if (!attrSet) {
       if (hipFuncSetAttribute(reinterpret_cast<const void*>(lkd::lstmPersistentKernel),
