@@ -148,6 +148,11 @@ def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     per = event_times(lambda: m.model.run_inplace(*args), steps)
+    # A persistent kernel that stops on its bounded wait writes NaN; a timed run with such a launch is void.
+    outs = m.model.run_inplace(*args)
+    for o in (outs if isinstance(outs, tuple) else (outs,)):
+        if not bool(torch.isfinite(o.t).all()):
+            raise RuntimeError("kokoro forward produced non-finite outputs; timing discarded")
     return {"median_ms": statistics.median(per), "wall_ms_per_step": wall, "frames": frames,
             "flops": kokoro_conv_flops(tokens, frames), "sd": sd, "inputs": (ids, ref_s, dur, noise)}
 

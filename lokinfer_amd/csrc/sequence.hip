@@ -65,8 +65,11 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 // W_hh, 65 KiB, resident in LDS for the whole sequence). Per step a workgroup computes its 64 gate rows
 // against h(t-1) from LDS, applies the cell update to its 16 units, and publishes h(t) as 64-bit words
 // {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256 values of h(t)
-// by polling those words until the tag matches. No fences, no counters: the tag orders each value on its own,
-// and a writer cannot run two steps ahead of any reader (it needs that reader's h of the step in between).
+// by polling those words until the tag matches. No fences, no counters: the tag orders each value on its own.
+// The words are double-buffered by step parity: a writer can be one step ahead of a reader (it only needs the
+// reader's h of the current step, which the reader publishes before it gathers), so with a single buffer its
+// step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
+// replaces the step s-1 word, and every reader is past step s-1 once the writer holds all h(s).
 // The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
 // kLstmSpinLimit polls the workgroup stops, writes NaN and records the failure, so a missing peer (e.g. not
 // co-resident) ends the kernel instead of hanging it.
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
   // Four threads per gate row (adjacent lanes), 64 k each, read as float4 from LDS; the rows' 4 partial sums
   // are combined with two lane shuffles.
   const int r = tid >> 2, q4 = tid & 3;
-  unsigned long long* xb = xbuf + dir * H;
+  unsigned long long* xdir = xbuf + dir * 2 * H;  // [parity][H]
   float c = 0.0f;
   bool ok = true;
   for (int64_t step = 0; step < t; ++step) {
@@ -126,6 +129,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
     if (q4 == 0) part[r] = acc;
     __syncthreads();
     const unsigned tag = static_cast<unsigned>(step + 1);
+    unsigned long long* xb = xdir + (step & 1) * H;
     if (tid < kLstmUnits) {
       const int u = tid;
       float gv[4];
@@ -251,10 +255,10 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;
-  const int64_t xBytes = 2 * 256 * 8 + 256;
+  const int64_t xBytes = 4 * 256 * 8 + 256;  // [direction][parity][256] words + failure flag
   if (h == 256 && workspaceBytes >= gBytes + xBytes) {
     auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
-    int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 2 * 256 * 8);
+    int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 4 * 256 * 8);
     const size_t lds = (lkd::kLstmRows * lkd::kLstmLdk + 256 + lkd::kLstmRows) * sizeof(float);
     static bool attrSet = false;
     if (!attrSet) {
@@ -263,7 +267,7 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
         return 2;
       attrSet = true;
     }
-    hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(2), dim3(256), 0, s, xbuf, 2 * 256);
+    hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(4), dim3(256), 0, s, xbuf, 4 * 256);
     hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), lds, s, g, whhT,
                        out, xbuf, failed, t);
   } else {

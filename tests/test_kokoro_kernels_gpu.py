@@ -45,6 +45,35 @@ def test_lstm_bidir(gpu, t, i):
     close(got, ref, 1e-4)
 
 
+def test_lstm_bidir_repeated_launches(gpu):
+    """Back-to-back launches with alternating lengths, the second one concurrent with work on another stream:
+    every result is finite and identical to the first (the cross-workgroup exchange words are reused by every
+    launch and by every step of one launch)."""
+    lk = gpu
+    h, i = 256, 512
+    w_ih = (rng.standard_normal((8 * h, i)) / np.sqrt(i)).astype(np.float32)
+    w_hh_t = (rng.standard_normal((h, 8 * h)) / np.sqrt(h)).astype(np.float32)
+    b = (rng.standard_normal(8 * h) * 0.1).astype(np.float32)
+    xs = {t: rng.standard_normal((t, i)).astype(np.float32) for t in (2, 59, 300)}
+    args = {t: (G(lk, x), G(lk, w_ih), G(lk, w_hh_t), G(lk, b)) for t, x in xs.items()}
+    first = {t: lk.ops.lstm_bidir_t_f32_gpu(*a).numpy() for t, a in args.items()}
+    for t, r in first.items():
+        assert np.isfinite(r).all(), t
+    side = torch.cuda.Stream()
+    big = torch.randn(2048, 2048, device="cuda")
+    for n in range(60):
+        t = (2, 59, 300)[n % 3]
+        if n % 2:
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(4):
+                    big = big @ big * 1e-3
+        got = lk.ops.lstm_bidir_t_f32_gpu(*args[t]).numpy()
+        assert np.array_equal(got, first[t]), f"launch {n} (T={t}) differs"
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+
 def test_repeat_interleave_adaln_concat(gpu):
     lk = gpu
     t, c = 59, 640
