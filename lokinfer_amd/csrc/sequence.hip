@@ -61,11 +61,13 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
   }
 }
 
-// Persistent LSTM recurrence: 16 workgroups per direction, each owning 16 hidden units (their 4 x 16 gate rows of
-// W_hh, 65 KiB, resident in LDS for the whole sequence). Per step a workgroup computes its 64 gate rows
-// against h(t-1) from LDS, applies the cell update to its 16 units, and publishes h(t) as 64-bit words
-// {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256 values of h(t)
-// by polling those words until the tag matches. No fences, no counters: the tag orders each value on its own.
+// Persistent LSTM recurrence: 16 workgroups per direction, each owning 16 hidden units, i.e. 64 gate rows of
+// W_hh held in registers for the whole sequence (four threads per row, 64 weights each). Per step a workgroup
+// computes its 64 gate rows against h(t-1) from LDS, applies the cell update to its 16 units, and publishes h(t)
+// as 64-bit words {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256
+// values of h(t) by polling those words until the tag matches. No fences, no counters: the tag orders each value
+// on its own. The gate pre-activations of the next step are loaded while the workgroup polls, so the step's
+// critical path is the LDS dot products, the cell update and one exchange.
 // The words are double-buffered by step parity: a writer can be one step ahead of a reader (it only needs the
 // reader's h of the current step, which the reader publishes before it gathers), so with a single buffer its
 // step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
@@ -76,7 +78,6 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 constexpr int kLstmWgs = 16;         // workgroups per direction
 constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
 constexpr int kLstmRows = 4 * kLstmUnits;
-constexpr int kLstmLdk = 256 + 4;    // LDS row stride of the W_hh slice (float4 reads without bank conflicts)
 constexpr int kLstmThreads = 256;
 constexpr long long kLstmSpinLimit = 1LL << 22;
 
@@ -91,37 +92,40 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
                                                                     unsigned long long* xbuf, int* failed,
                                                                     int64_t t) {
   constexpr int H = 256;
-  extern __shared__ float lds[];
-  float* w = lds;                            // [rows][kLstmLdk]: row r's 256 weights contiguous (+4 pad)
-  float* hs = w + kLstmRows * kLstmLdk;      // [H]
-  float* part = hs + H;                      // [rows]
+  __shared__ float4 hs4[H / 4];
+  __shared__ float part[kLstmRows];
   const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
   const int tid = threadIdx.x;
   const int ld = 8 * H;
-  // rows r = gate * U + j  <->  gate row gate * H + U b + j of this direction (U = units per workgroup)
-  for (int i = tid; i < H * kLstmRows; i += kLstmThreads) {
-    const int k = i / kLstmRows, r = i % kLstmRows;
-    const int row = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
-    w[r * kLstmLdk + k] = whhT[static_cast<int64_t>(k) * ld + dir * 4 * H + row];
-  }
-  for (int i = tid; i < H; i += kLstmThreads) hs[i] = 0.0f;
-  __syncthreads();
-  // Four threads per gate row (adjacent lanes), 64 k each, read as float4 from LDS; the rows' 4 partial sums
-  // are combined with two lane shuffles.
+  // Thread (r, q4): gate row r = gate * U + j  <->  row gate * H + U b + j of this direction, k = 64 q4 .. +63.
   const int r = tid >> 2, q4 = tid & 3;
+  const int row = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
+  float4 wreg[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float* src = whhT + static_cast<int64_t>(q4 * 64 + 4 * j) * ld + dir * 4 * H + row;
+    wreg[j] = make_float4(src[0], src[ld], src[2 * ld], src[3 * ld]);
+  }
+  if (tid < H / 4) hs4[tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   unsigned long long* xdir = xbuf + dir * 2 * H;  // [parity][H]
   float c = 0.0f;
   bool ok = true;
+  // gate pre-activations of the current step (threads < U)
+  float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (tid < kLstmUnits) {
+    const int64_t tt = dir == 0 ? 0 : t - 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + tid];
+  }
+  __syncthreads();
   for (int64_t step = 0; step < t; ++step) {
     const int64_t tt = dir == 0 ? step : t - 1 - step;
     float a0 = 0.0f, a1 = 0.0f;
-    const float4* wr = reinterpret_cast<const float4*>(w + r * kLstmLdk + q4 * 64);
-    const float4* hh = reinterpret_cast<const float4*>(hs + q4 * 64);
 #pragma unroll
     for (int k = 0; k < 16; k += 2) {
-      const float4 w0 = wr[k], h0 = hh[k], w1 = wr[k + 1], h1 = hh[k + 1];
-      a0 += w0.x * h0.x + w0.y * h0.y + w0.z * h0.z + w0.w * h0.w;
-      a1 += w1.x * h1.x + w1.y * h1.y + w1.z * h1.z + w1.w * h1.w;
+      const float4 h0 = hs4[q4 * 16 + k], h1 = hs4[q4 * 16 + k + 1];
+      a0 += wreg[k].x * h0.x + wreg[k].y * h0.y + wreg[k].z * h0.z + wreg[k].w * h0.w;
+      a1 += wreg[k + 1].x * h1.x + wreg[k + 1].y * h1.y + wreg[k + 1].z * h1.z + wreg[k + 1].w * h1.w;
     }
     float acc = a0 + a1;
     acc += __shfl_xor(acc, 1, 64);
@@ -132,18 +136,20 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
     unsigned long long* xb = xdir + (step & 1) * H;
     if (tid < kLstmUnits) {
       const int u = tid;
-      float gv[4];
+      float x4[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rr = q * kLstmUnits + u;
-        gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + u] + part[rr];
-      }
-      const float ig = sigmoidf(gv[0]), fg = sigmoidf(gv[1]), gg = tanhf(gv[2]), og = sigmoidf(gv[3]);
+      for (int q = 0; q < 4; ++q) x4[q] = gv[q] + part[q * kLstmUnits + u];
+      const float ig = sigmoidf(x4[0]), fg = sigmoidf(x4[1]), gg = tanhf(x4[2]), og = sigmoidf(x4[3]);
       c = fg * c + ig * gg;
       const float hv = ok ? og * tanhf(c) : __builtin_nanf("");
-      out[tt * 2 * H + dir * H + b * kLstmUnits + u] = hv;
       const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
       __hip_atomic_store(xb + b * kLstmUnits + u, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      out[tt * 2 * H + dir * H + b * kLstmUnits + u] = hv;
+      if (step + 1 < t) {
+        const int64_t tn = dir == 0 ? step + 1 : t - 2 - step;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gv[q] = g[tn * ld + dir * 4 * H + q * H + b * kLstmUnits + u];
+      }
     }
     // gather h(t): thread k polls word k
     {
@@ -158,7 +164,8 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
           atomicExch(failed, 1);
         }
       }
-      hs[k] = ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
+      reinterpret_cast<float*>(hs4)[k] =
+          ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
     // A workgroup that timed out keeps stepping (so all of its waves reach the end) but stops waiting.
     ok = __syncthreads_and(ok);
@@ -259,16 +266,8 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (h == 256 && workspaceBytes >= gBytes + xBytes) {
     auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
     int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 4 * 256 * 8);
-    const size_t lds = (lkd::kLstmRows * lkd::kLstmLdk + 256 + lkd::kLstmRows) * sizeof(float);
-    static bool attrSet = false;
-    if (!attrSet) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(lkd::lstmPersistentKernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-        return 2;
-      attrSet = true;
-    }
     hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(4), dim3(256), 0, s, xbuf, 4 * 256);
-    hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), lds, s, g, whhT,
+    hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), 0, s, g, whhT,
                        out, xbuf, failed, t);
   } else {
     hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0, s, g, whhT, out,
