@@ -62,23 +62,24 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 }
 
 // Persistent LSTM recurrence: 16 workgroups per direction, each owning 16 hidden units, i.e. 64 gate rows of
-// W_hh held in registers for the whole sequence (four threads per row, 64 weights each). Per step a workgroup
-// computes its 64 gate rows against h(t-1) from LDS, applies the cell update to its 16 units, and publishes h(t)
-// as 64-bit words {tag = step + 1, value} with agent-scope atomic stores; every workgroup then gathers the 256
-// values of h(t) by polling those words until the tag matches. No fences, no counters: the tag orders each value
-// on its own. The gate pre-activations of the next step are loaded while the workgroup polls, so the step's
-// critical path is the LDS dot products, the cell update and one exchange.
+// W_hh held in registers for the whole sequence. Wave w of a workgroup owns k = 64 w .. 64 w + 63 and lane r
+// the gate row r = gate * 16 + unit, so a lane keeps 64 weights and the wave needs only the 64 values of h(t-1)
+// that its own lanes polled: they pass through a wave-private LDS slice (no workgroup barrier before the dot
+// products). The four waves' partial sums meet at one barrier; then wave 0 applies one activation per lane (its
+// gate row), combines the four gates of each unit with lane shuffles, updates the cell and publishes h(t) as
+// 64-bit words {tag = step + 1, value} with agent-scope atomic stores. Every wave then polls its 64 words of h(t)
+// until the tags match. No fences, no counters: the tag orders each value on its own. The gate pre-activations
+// of the next step are loaded while wave 0 polls.
 // The words are double-buffered by step parity: a writer can be one step ahead of a reader (it only needs the
 // reader's h of the current step, which the reader publishes before it gathers), so with a single buffer its
 // step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
 // replaces the step s-1 word, and every reader is past step s-1 once the writer holds all h(s).
 // The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
-// kLstmSpinLimit polls the workgroup stops, writes NaN and records the failure, so a missing peer (e.g. not
+// kLstmSpinLimit polls the lane stops, writes NaN and records the failure, so a missing peer (e.g. not
 // co-resident) ends the kernel instead of hanging it.
 constexpr int kLstmWgs = 16;         // workgroups per direction
 constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
-constexpr int kLstmRows = 4 * kLstmUnits;
-constexpr int kLstmThreads = 256;
+constexpr int kLstmThreads = 256;    // 4 waves x 64 k
 constexpr long long kLstmSpinLimit = 1LL << 22;
 
 __global__ void lstmClearKernel(unsigned long long* xbuf, int n) {
@@ -92,83 +93,68 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
                                                                     unsigned long long* xbuf, int* failed,
                                                                     int64_t t) {
   constexpr int H = 256;
-  __shared__ float4 hs4[H / 4];
-  __shared__ float part[kLstmRows];
+  __shared__ float4 hsw[4][16];   // wave w: h(t-1)[64 w .. 64 w + 63]
+  __shared__ float part[4][64];   // wave w's partial dot product of each gate row
   const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
-  const int tid = threadIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ld = 8 * H;
-  // Thread (r, q4): gate row r = gate * U + j  <->  row gate * H + U b + j of this direction, k = 64 q4 .. +63.
-  const int r = tid >> 2, q4 = tid & 3;
-  const int row = (r / kLstmUnits) * H + b * kLstmUnits + (r % kLstmUnits);
-  float4 wreg[16];
+  const int gate = lane >> 4, unit = lane & 15;
+  const int64_t col = dir * 4 * H + gate * H + b * kLstmUnits + unit;  // this lane's gate row in g / W_hh^T
+  float w[64];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float* src = whhT + static_cast<int64_t>(q4 * 64 + 4 * j) * ld + dir * 4 * H + row;
-    wreg[j] = make_float4(src[0], src[ld], src[2 * ld], src[3 * ld]);
-  }
-  if (tid < H / 4) hs4[tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int i = 0; i < 64; ++i) w[i] = whhT[static_cast<int64_t>(64 * wave + i) * ld + col];
+  reinterpret_cast<float*>(hsw[wave])[lane] = 0.0f;
   unsigned long long* xdir = xbuf + dir * 2 * H;  // [parity][H]
   float c = 0.0f;
   bool ok = true;
-  // gate pre-activations of the current step (threads < U)
-  float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (tid < kLstmUnits) {
-    const int64_t tt = dir == 0 ? 0 : t - 1;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) gv[q] = g[tt * ld + dir * 4 * H + q * H + b * kLstmUnits + tid];
-  }
-  __syncthreads();
+  float gv = 0.0f;  // wave 0: this lane's gate pre-activation for the current step
+  if (wave == 0) gv = g[(dir == 0 ? 0 : t - 1) * ld + col];
   for (int64_t step = 0; step < t; ++step) {
     const int64_t tt = dir == 0 ? step : t - 1 - step;
-    float a0 = 0.0f, a1 = 0.0f;
+    __builtin_amdgcn_wave_barrier();
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; k += 2) {
-      const float4 h0 = hs4[q4 * 16 + k], h1 = hs4[q4 * 16 + k + 1];
-      a0 += wreg[k].x * h0.x + wreg[k].y * h0.y + wreg[k].z * h0.z + wreg[k].w * h0.w;
-      a1 += wreg[k + 1].x * h1.x + wreg[k + 1].y * h1.y + wreg[k + 1].z * h1.z + wreg[k + 1].w * h1.w;
+    for (int i = 0; i < 16; ++i) {
+      const float4 h = hsw[wave][i];
+      a0 = fmaf(w[4 * i], h.x, a0);
+      a1 = fmaf(w[4 * i + 1], h.y, a1);
+      a2 = fmaf(w[4 * i + 2], h.z, a2);
+      a3 = fmaf(w[4 * i + 3], h.w, a3);
     }
-    float acc = a0 + a1;
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
-    if (q4 == 0) part[r] = acc;
-    __syncthreads();
+    part[wave][lane] = (a0 + a1) + (a2 + a3);
+    ok = __syncthreads_and(ok);
     const unsigned tag = static_cast<unsigned>(step + 1);
     unsigned long long* xb = xdir + (step & 1) * H;
-    if (tid < kLstmUnits) {
-      const int u = tid;
-      float x4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) x4[q] = gv[q] + part[q * kLstmUnits + u];
-      const float ig = sigmoidf(x4[0]), fg = sigmoidf(x4[1]), gg = tanhf(x4[2]), og = sigmoidf(x4[3]);
-      c = fg * c + ig * gg;
-      const float hv = ok ? og * tanhf(c) : __builtin_nanf("");
-      const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
-      __hip_atomic_store(xb + b * kLstmUnits + u, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[tt * 2 * H + dir * H + b * kLstmUnits + u] = hv;
-      if (step + 1 < t) {
-        const int64_t tn = dir == 0 ? step + 1 : t - 2 - step;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) gv[q] = g[tn * ld + dir * 4 * H + q * H + b * kLstmUnits + u];
+    if (wave == 0) {
+      const float x = gv + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+      const float act = gate == 2 ? tanhf(x) : sigmoidf(x);
+      const float ig = __shfl(act, unit, 64), fg = __shfl(act, 16 + unit, 64);
+      const float gg = __shfl(act, 32 + unit, 64), og = __shfl(act, 48 + unit, 64);
+      if (lane < kLstmUnits) {
+        c = fg * c + ig * gg;
+        const float hv = ok ? og * tanhf(c) : __builtin_nanf("");
+        const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
+        __hip_atomic_store(xb + b * kLstmUnits + lane, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        out[tt * 2 * H + dir * H + b * kLstmUnits + lane] = hv;
       }
+      if (step + 1 < t) gv = g[(dir == 0 ? step + 1 : t - 2 - step) * ld + col];
     }
-    // gather h(t): thread k polls word k
+    // gather this wave's 64 values of h(t): lane polls word 64 w + lane
     {
-      const int k = tid;
       unsigned long long word = 0ull;
       long long spins = 0;
       while (ok) {
-        word = __hip_atomic_load(xb + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        word = __hip_atomic_load(xb + 64 * wave + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (static_cast<unsigned>(word >> 32) == tag) break;
         if (++spins > kLstmSpinLimit) {
           ok = false;
           atomicExch(failed, 1);
         }
       }
-      reinterpret_cast<float*>(hs4)[k] =
+      // A lane that timed out keeps stepping (so every wave reaches the end) but stops waiting.
+      reinterpret_cast<float*>(hsw[wave])[lane] =
           ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
-    // A workgroup that timed out keeps stepping (so all of its waves reach the end) but stops waiting.
-    ok = __syncthreads_and(ok);
   }
 }
 
