@@ -21,6 +21,14 @@ namespace lkd {
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal (each within 1 ulp; absolute error of a few
+// 1e-8); saturates to 0 / 1 for large |x|. tanh(x) = 2 sigmoid(2x) - 1 to the same absolute error, so one
+// branch-free sequence serves every gate of an LSTM cell.
+__device__ __forceinline__ float sigmoidHw(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
+__device__ __forceinline__ float tanhHw(float x) { return fmaf(2.0f, sigmoidHw(2.0f * x), -1.0f); }
+
 // g: [T, 8H] gate pre-activations (forward gates in columns 0..4H, backward 4H..8H); whhT: [H, 8H];
 // out: [T, 2H] = [h_fwd | h_bwd]. blockIdx.x = direction, blockDim.x = 4H.
 __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __restrict__ g,
@@ -75,7 +83,7 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 // step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
 // replaces the step s-1 word, and every reader is past step s-1 once the writer holds all h(s).
 // The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
-// kLstmSpinLimit polls the lane stops, writes NaN and records the failure, so a missing peer (e.g. not
+// kLstmSpinLimit polls the lane stops, writes NaN (which every later h inherits) and records the failure, so a missing peer (e.g. not
 // co-resident) ends the kernel instead of hanging it.
 constexpr int kLstmWgs = 16;         // workgroups per direction
 constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
@@ -112,27 +120,33 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
   for (int64_t step = 0; step < t; ++step) {
     const int64_t tt = dir == 0 ? step : t - 1 - step;
     __builtin_amdgcn_wave_barrier();
+    // all 16 broadcast reads in flight before the first product
+    float4 hv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) hv[i] = hsw[wave][i];
+    __builtin_amdgcn_sched_barrier(0);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float4 h = hsw[wave][i];
+      const float4 h = hv[i];
       a0 = fmaf(w[4 * i], h.x, a0);
       a1 = fmaf(w[4 * i + 1], h.y, a1);
       a2 = fmaf(w[4 * i + 2], h.z, a2);
       a3 = fmaf(w[4 * i + 3], h.w, a3);
     }
     part[wave][lane] = (a0 + a1) + (a2 + a3);
-    ok = __syncthreads_and(ok);
+    __syncthreads();
     const unsigned tag = static_cast<unsigned>(step + 1);
     unsigned long long* xb = xdir + (step & 1) * H;
     if (wave == 0) {
       const float x = gv + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
-      const float act = gate == 2 ? tanhf(x) : sigmoidf(x);
+      const float sg = sigmoidHw(gate == 2 ? 2.0f * x : x);
+      const float act = gate == 2 ? fmaf(2.0f, sg, -1.0f) : sg;
       const float ig = __shfl(act, unit, 64), fg = __shfl(act, 16 + unit, 64);
       const float gg = __shfl(act, 32 + unit, 64), og = __shfl(act, 48 + unit, 64);
       if (lane < kLstmUnits) {
         c = fg * c + ig * gg;
-        const float hv = ok ? og * tanhf(c) : __builtin_nanf("");
+        const float hv = ok ? og * tanhHw(c) : __builtin_nanf("");
         const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
         __hip_atomic_store(xb + b * kLstmUnits + lane, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         out[tt * 2 * H + dir * H + b * kLstmUnits + lane] = hv;
@@ -151,7 +165,8 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
           atomicExch(failed, 1);
         }
       }
-      // A lane that timed out keeps stepping (so every wave reaches the end) but stops waiting.
+      // A lane that timed out keeps stepping (so every wave reaches the end) but stops waiting; its NaN
+      // reaches every gate row through the next step's dot products.
       reinterpret_cast<float*>(hsw[wave])[lane] =
           ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
