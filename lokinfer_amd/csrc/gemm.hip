@@ -21,6 +21,7 @@
 namespace lkd {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
 enum : int { PRE_NONE = 0, PRE_SNAKE = 1, PRE_LEAKY = 2 };
@@ -253,25 +254,37 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
 }
 
 // Stride-1 channel-last conv with the taps innermost. For each 16-channel input chunk a workgroup stages the
-// halo rows its 128 output rows need (BM + (K-1) dil rows x 16 channels) once, with the affine + Snake / leaky
-// prologue applied once per element, k-major in LDS; then every tap kk is a 16-deep MFMA step whose A operand
-// is the same halo shifted by kk * dil rows and whose B operand is w[:, kk, chunk] ([16][BN] in LDS). Compared
-// with the flat im2col loop this reads each input element from L2 once per chunk instead of K times and
-// evaluates the prologue once instead of K times. Steps = chunks x taps, double-buffered: B per step, the halo
-// per chunk (prefetched into registers during the last tap of the previous chunk).
-constexpr int kMaxHalo = 256;
+// halo rows its BM output rows need (BM + (K-1) dil rows x 16 channels) once, with the affine + Snake / leaky
+// prologue applied once per element; then every tap kk is a 16-deep MFMA step whose A operand is the same halo
+// shifted by kk * dil rows and whose B operand is w[n0 .., kk, chunk] (16 contiguous floats per output channel
+// in the [Co, K, Ci] weight). Compared with the flat im2col loop this reads each input element from L2 once per
+// chunk instead of K times and evaluates the prologue once instead of K times. Steps = chunks x taps,
+// double-buffered: B per step, the halo per chunk (prefetched into registers during the chunk's last tap).
+//
+// LDS layout: both operands row-major with their 16 channels contiguous ([row][16], row stride 20 floats), so a
+// global float4 lands in LDS as one float4 (no transposition) and 16 consecutive rows of 16-byte reads cover all
+// 64 banks once. The 16 channels of a chunk are fed to the MFMAs in the order ch(g, q, half) = 8 g + 4 half + q
+// (MFMA step 4 g + q, lane half = lane / 32): a lane's 8 operand values of one tap are then two 16-byte reads
+// per 32-row block, for A and B alike; the k order inside a chunk does not change the sum's terms.
+constexpr int kLdRow = 20;  // floats per staged row (16 channels + 4 pad)
+
+template <int BM>
+struct TapCfg {
+  static constexpr int maxHalo = BM == 128 ? 192 : 128;  // rows of halo the LDS holds (BM + (K-1) dil <= this)
+};
 
 template <int BM, int BN>
 // At most 168 VGPRs: three waves per SIMD (12 per CU) keep the MFMA pipe fed through the barriers.
 __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, int halo) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int LDH = kMaxHalo + 4, LDB_S = BN + 4;
+  constexpr int MAXH = TapCfg<BM>::maxHalo;
   constexpr int B4 = BN * BK / 4 / NT;
-  constexpr int H4 = kMaxHalo * BK / 4 / NT;  // halo float4 slots per thread (4 at 256 rows)
+  constexpr int H4 = MAXH * BK / 4 / NT;  // halo 4-float slots per thread
+  static_assert(B4 >= 1 && H4 >= 1 && (MAXH * BK / 4) % NT == 0, "staging slots");
 
-  __shared__ float Hs[2][BK][LDH];
-  __shared__ float Bs[2][BK][LDB_S];
+  __shared__ v4f Hs[2][MAXH * kLdRow / 4];
+  __shared__ v4f Bs[2][BN * kLdRow / 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -282,6 +295,8 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   const int chunks = static_cast<int>(ci / BK);
   const int steps = chunks * taps;
   const int64_t rowBase = m0 - p.convPad;  // input row of halo row 0
+  const int cq = (tid & 3) * 4;            // the 4 channels of a chunk this thread stages (same for every slot)
+  const int lastRow = static_cast<int>(p.convL - 1);
 
   v16f acc[TM][TN];
 #pragma unroll
@@ -291,91 +306,78 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  float4 rh[H4], rb[B4];
-  // A thread always stages the same 4 channels of a chunk (idx & 3 == tid & 3), so the prologue's per-channel
-  // parameters are loaded once per chunk, not once per element.
+  v4f rh[H4], rb[B4];
   const bool hasPre = p.pre != PRE_NONE || p.affine;
-  // Raw halo loads only: the prologue runs at LDS-store time, so its parameters are not live across the MFMAs.
+  // Raw halo loads from clamped rows (always in bounds, no branches); rows outside [0, L) become zero padding
+  // at store time, after the prologue.
   auto loadHalo = [&](int chunk) {
-    const int64_t c0 = static_cast<int64_t>(chunk) * BK;
-    const int cq = (tid & 3) * 4;
+    const float* src = p.a + static_cast<int64_t>(chunk) * BK + cq;
 #pragma unroll
     for (int i = 0; i < H4; ++i) {
-      const int idx = tid + i * NT;
-      const int hr = idx >> 2;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      const int64_t t = rowBase + hr;
-      if (hr < halo && t >= 0 && t < p.convL) v = *reinterpret_cast<const float4*>(p.a + t * ci + c0 + cq);
-      rh[i] = v;
+      const int hr = (tid + i * NT) >> 2;
+      const int64_t t = min<int64_t>(max<int64_t>(rowBase + hr, 0), lastRow);
+      if (hr < halo) rh[i] = *reinterpret_cast<const v4f*>(src + t * ci);
     }
   };
   auto storeHalo = [&](int buf, int chunk) {
-    const int64_t c0 = static_cast<int64_t>(chunk) * BK;
-    const int cq = (tid & 3) * 4;
+    const int64_t c0 = static_cast<int64_t>(chunk) * BK + cq;
     float mu[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f}, be[4] = {0.f, 0.f, 0.f, 0.f};
     float al[4] = {1.f, 1.f, 1.f, 1.f}, ial[4] = {1.f, 1.f, 1.f, 1.f};
     if (hasPre) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t c = c0 + cq + q;
         if (p.affine) {
-          mu[q] = p.affine[c];
-          sc[q] = p.affine[ci + c];
-          be[q] = p.affine[2 * ci + c];
+          mu[q] = p.affine[c0 + q];
+          sc[q] = p.affine[ci + c0 + q];
+          be[q] = p.affine[2 * ci + c0 + q];
         }
         if (p.pre == PRE_SNAKE) {
-          al[q] = p.alpha[c];
+          al[q] = p.alpha[c0 + q];
           ial[q] = 1.0f / al[q];
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < H4; ++i) {
-      const int idx = tid + i * NT;
-      const int hr = idx >> 2;
-      if (hr < halo) {
-        float e[4] = {rh[i].x, rh[i].y, rh[i].z, rh[i].w};
-        const int64_t t = rowBase + hr;
-        if (hasPre && t >= 0 && t < p.convL) {  // zero padding stays zero: it is applied after the prologue
+      const int hr = (tid + i * NT) >> 2;
+      if (hr >= halo) continue;  // slots past this conv's halo are never read
+      const int64_t t = rowBase + hr;
+      float e[4] = {rh[i].x, rh[i].y, rh[i].z, rh[i].w};
+      if (hasPre) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float u = p.affine ? (e[q] - mu[q]) * sc[q] + be[q] : e[q];
-            if (p.pre == PRE_SNAKE) {
-              const float s = sinf(al[q] * u);
-              u = u + ial[q] * (s * s);
-            } else if (p.pre == PRE_LEAKY) {
-              u = u >= 0.0f ? u : u * p.slope;
-            }
-            e[q] = u;
+        for (int q = 0; q < 4; ++q) {
+          float u = p.affine ? (e[q] - mu[q]) * sc[q] + be[q] : e[q];
+          if (p.pre == PRE_SNAKE) {
+            const float sn = sinf(al[q] * u);
+            u = u + ial[q] * (sn * sn);
+          } else if (p.pre == PRE_LEAKY) {
+            u = u >= 0.0f ? u : u * p.slope;
           }
+          e[q] = u;
         }
-        Hs[buf][cq + 0][hr] = e[0];
-        Hs[buf][cq + 1][hr] = e[1];
-        Hs[buf][cq + 2][hr] = e[2];
-        Hs[buf][cq + 3][hr] = e[3];
       }
+      const bool inside = t >= 0 && t <= lastRow;  // zero padding is applied after the prologue
+      Hs[buf][hr * (kLdRow / 4) + (cq >> 2)] =
+          inside ? v4f{e[0], e[1], e[2], e[3]} : v4f{0.f, 0.f, 0.f, 0.f};
     }
   };
-  // B for step s = chunk * taps + kk: w[co][kk][chunk * 16 .. +15] (w is [Co, K, Ci] row-major = ldb K * Ci)
+  // B for step s = chunk * taps + kk: w[co][kk][chunk * 16 .. +15] (w is [Co, K, Ci] row-major = ldb K * Ci);
+  // columns past N read the last valid row (never stored).
   auto loadB = [&](int s) {
     const int chunk = s / taps, kk = s - chunk * taps;
-    const int64_t k0 = static_cast<int64_t>(kk) * ci + static_cast<int64_t>(chunk) * BK;
+    const float* src = p.b + static_cast<int64_t>(kk) * ci + static_cast<int64_t>(chunk) * BK + cq;
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
-      const int idx = tid + i * NT;
-      const int col = idx >> 2, kq = (idx & 3) * 4;
-      rb[i] = loadBnt4(p, n0 + col, k0 + kq);
+      const int col = (tid + i * NT) >> 2;
+      const int64_t n = min<int64_t>(n0 + col, p.n - 1);
+      rb[i] = *reinterpret_cast<const v4f*>(src + n * p.ldb);
     }
   };
   auto storeB = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
-      const int idx = tid + i * NT;
-      const int col = idx >> 2, kq = (idx & 3) * 4;
-      Bs[buf][kq + 0][col] = rb[i].x;
-      Bs[buf][kq + 1][col] = rb[i].y;
-      Bs[buf][kq + 2][col] = rb[i].z;
-      Bs[buf][kq + 3][col] = rb[i].w;
+      const int col = (tid + i * NT) >> 2;
+      Bs[buf][col * (kLdRow / 4) + (cq >> 2)] = rb[i];
     }
   };
 
@@ -385,25 +387,33 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   storeB(0);
   __syncthreads();
   const int lrow = lane & 31, lk = lane >> 5;
+  const int aRow = wm * WTM + lrow, bRow = wn * WTN + lrow;
   for (int s = 0; s < steps; ++s) {
     const int chunk = s / taps, kk = s - chunk * taps;
     const int hbuf = chunk & 1, bbuf = s & 1;
     const bool more = s + 1 < steps;
     const bool newChunk = more && kk == taps - 1;
+    const int shift = kk * p.convDil;
+    // this step's operand fragments first, then the next step's global prefetch (consumed after the MFMAs)
+    v4f af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[g][i] = Hs[hbuf][(aRow + i * 32 + shift) * (kLdRow / 4) + 2 * g + lk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[g][j] = Bs[bbuf][(bRow + j * 32) * (kLdRow / 4) + 2 * g + lk];
+    }
     if (more) loadB(s + 1);
     if (newChunk) loadHalo(chunk + 1);
-    const int shift = kk * p.convDil;
 #pragma unroll
-    for (int ks = 0; ks < BK; ks += 2) {
-      float av[TM], bv[TN];
+    for (int g = 0; g < 2; ++g) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) av[i] = Hs[hbuf][ks + lk][wm * WTM + i * 32 + lrow + shift];
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[bbuf][ks + lk][wn * WTN + j * 32 + lrow];
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][i][q], bf[g][j][q], acc[i][j], 0, 0, 0);
     }
     if (more) storeB(bbuf ^ 1);
     if (newChunk) storeHalo(hbuf ^ 1, chunk + 1);
@@ -429,7 +439,7 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
     // Per-(128-row chunk, channel) (mean, M2) of the stored output, two passes over the registers: this tile is
     // exactly chunk blockIdx.y. A column's 128 rows sit in (wm, i, lane half, r); reduce r and i in registers,
     // the two lane halves with a shuffle, and the two wm waves through LDS.
-    float* red = &Hs[0][0][0];  // reuse the staging LDS (free after the last barrier)
+    float* red = reinterpret_cast<float*>(&Hs[0][0]);  // reuse the staging LDS (free after the last barrier)
     const int n = static_cast<int>(min<int64_t>(BM, p.m - m0));
     float colSum[TN], colM2[TN], mean[TN];
 #pragma unroll
@@ -576,20 +586,21 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
   p.pre = pre;
   p.slope = slope;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t halo = 128 + static_cast<int64_t>(dilation) * (kw - 1);
+  const int64_t reach = static_cast<int64_t>(dilation) * (kw - 1);  // halo rows beyond the output tile
   const int64_t tiles = static_cast<int64_t>(lkh::ceilDiv(lo, 128)) * lkh::ceilDiv(co, 128);
+  const bool big = tiles >= 256 && 128 + reach <= lkd::TapCfg<128>::maxHalo;
   bool statsDone = false;
-  if (stride == 1 && halo <= lkd::kMaxHalo) {
-    if (tiles >= 256) {
+  if (stride == 1 && (big || 64 + reach <= lkd::TapCfg<64>::maxHalo)) {
+    if (big) {
       p.stats = stats;  // the 128-row tiles are exactly the statistics chunks
       statsDone = stats != nullptr;
       dim3 grid(lkh::ceilDiv(co, 128), lkh::ceilDiv(lo, 128));
       hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
-                         static_cast<int>(halo));
+                         static_cast<int>(128 + reach));
     } else {  // few output tiles (decoder / F0-N at frame rate): 64 x 64 tiles fill more of the 256 CUs
       dim3 grid(lkh::ceilDiv(co, 64), lkh::ceilDiv(lo, 64));
       hipLaunchKernelGGL((lkd::convTapKernel<64, 64>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
-                         static_cast<int>(halo - 64));
+                         static_cast<int>(64 + reach));
     }
   } else {
     lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, s);
