@@ -60,8 +60,7 @@ __device__ __forceinline__ float preAct(const GemmParams& p, float v, int c) {
   }
   if (p.pre == PRE_SNAKE) {
     const float a = p.alpha[c];
-    const float s = sinf(a * v);
-    v = v + (1.0f / a) * (s * s);
+    v = v + (1.0f / a) * snakeSinSq(a * v);
   } else if (p.pre == PRE_LEAKY) {
     v = v >= 0.0f ? v : v * p.slope;
   }
@@ -348,8 +347,7 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
         for (int q = 0; q < 4; ++q) {
           float u = p.affine ? (e[q] - mu[q]) * sc[q] + be[q] : e[q];
           if (p.pre == PRE_SNAKE) {
-            const float sn = sinf(al[q] * u);
-            u = u + ial[q] * (sn * sn);
+            u = u + ial[q] * snakeSinSq(al[q] * u);
           } else if (p.pre == PRE_LEAKY) {
             u = u >= 0.0f ? u : u * p.slope;
           }

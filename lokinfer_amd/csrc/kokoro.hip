@@ -100,8 +100,7 @@ __global__ void actKernel(const float* __restrict__ x, const float* __restrict__
     if (af) v = (v - af[ch]) * af[c + ch] + af[2 * c + ch];
     if (act == 1) {
       const float a = alpha[ch];
-      const float s = sinf(a * v);
-      v = v + (1.0f / a) * (s * s);
+      v = v + (1.0f / a) * snakeSinSq(a * v);
     } else if (act == 2) {
       v = v >= 0.0f ? v : v * slope;
     }

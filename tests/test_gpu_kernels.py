@@ -158,6 +158,23 @@ def test_stats_affine_act(gpu, l, c):
     close(lk.ops.leaky_lc_f32_gpu(X, 0.1), K.affine_act(x, act="leaky", slope=0.1), 1e-6)
 
 
+def test_snake_wide_range(gpu):
+    """Snake x + sin(a x)^2 / a over |a x| up to ~1e3: the kernel's pi-periodic reduction + hardware sine stays
+    within 1e-6 of sin^2 evaluated in float64 at the same float32 product a x (plus the output's own rounding)."""
+    lk = gpu
+    l, c = 4096, 64
+    x = np.concatenate([rng.uniform(-4, 4, (l // 2, c)), rng.uniform(-400, 400, (l // 2, c))]).astype(np.float32)
+    alpha = rng.uniform(0.1, 3.0, c).astype(np.float32)
+    af = np.stack([np.zeros(c), np.ones(c), np.zeros(c)]).astype(np.float32)  # identity affine
+    got = lk.ops.snake_affine_lc_f32_gpu(G(lk, x), G(lk, af), G(lk, alpha)).numpy().astype(np.float64)
+    y32 = (alpha[None, :] * x).astype(np.float32).astype(np.float64)
+    inv = (np.float32(1) / alpha).astype(np.float64)
+    ref = x.astype(np.float64) + inv[None, :] * np.sin(y32) ** 2
+    err = np.abs(got - ref)
+    tol = 1e-6 * np.maximum(1.0, inv[None, :]) + 2.0 ** -22 * np.abs(ref)
+    assert (err <= tol).all(), f"max excess {np.max(err - tol):.3e}"
+
+
 @pytest.mark.parametrize("l,ci,co,k,pad,dil", [(295, 528, 1024, 3, 1, 1), (600, 256, 256, 7, 9, 3), (1000, 128, 128, 11, 25, 5),
                                                (70, 1104, 512, 1, 0, 1), (33, 16, 64, 3, 1, 1), (5000, 128, 128, 3, 1, 1)])
 def test_conv1d_lc(gpu, l, ci, co, k, pad, dil):
