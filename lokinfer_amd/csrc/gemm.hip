@@ -131,12 +131,55 @@ __device__ __forceinline__ float4 loadBnt4(const GemmParams& p, int64_t n, int64
   return r;
 }
 
-__device__ __forceinline__ float epilogue(const GemmParams& p, float v, int64_t row, int64_t col) {
-  if (p.bias) v += p.bias[col];
-  if (p.act == ACT_RELU) v = fmaxf(v, 0.0f);
-  else if (p.act == ACT_GELU) v = geluTanh(v);
-  if (p.res) v += p.res[row * p.ldr + col];
-  return v * p.scale;
+// Writes a wave's TM x TN block of 32x32 accumulators: c = (act(acc + bias) + res) * scale for the elements
+// inside the matrix, leaving the stored values in acc. Done in phases (per-column bias, then every residual load,
+// then every store) so that no global load sits between two stores: the compiler cannot prove that the output
+// does not alias bias or res, and would otherwise wait out a load latency per element. Loads use clamped
+// indices; elements outside the matrix are computed but not stored.
+// D[i][j] of a 32x32x2 MFMA: j = lane % 32, i = 8 * (r / 4) + 4 * (lane / 32) + r % 4 for accumulator r.
+template <int TM, int TN>
+__device__ __forceinline__ void storeTile(const GemmParams& p, v16f (&acc)[TM][TN], int64_t rowBase,
+                                          int64_t colBase, int lrow, int lk) {
+  const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
+  float bcol[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bcol[j] = p.bias ? p.bias[min<int64_t>(colBase + j * 32 + lrow, lastCol)] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = acc[i][j][r] + bcol[j];
+        if (p.act == ACT_RELU) v = fmaxf(v, 0.0f);
+        else if (p.act == ACT_GELU) v = geluTanh(v);
+        acc[i][j][r] = v;
+      }
+  if (p.res) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col = min<int64_t>(colBase + j * 32 + lrow, lastCol);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = min<int64_t>(rowBase + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3), lastRow);
+          acc[i][j][r] += p.res[row * p.ldr + col];
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = colBase + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = rowBase + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        acc[i][j][r] *= p.scale;
+        if (row <= lastRow && col <= lastCol) p.c[row * p.ldc + col] = acc[i][j][r];
+      }
+    }
 }
 
 template <int BM, int BN, int AM, int BMODE>
@@ -237,19 +280,7 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
     __syncthreads();
   }
 
-  // D[i][j] of a 32x32x2 MFMA: j = lane % 32, i = 8 * (r / 4) + 4 * (lane / 32) + r % 4 for accumulator r.
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
-      if (col >= p.n) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        if (row < p.m) p.c[row * p.ldc + col] = epilogue(p, acc[i][j][r], row, col);
-      }
-    }
+  storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
 }
 
 // Stride-1 channel-last conv with the taps innermost. For each 16-channel input chunk a workgroup stages the
@@ -318,24 +349,25 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
       if (hr < halo) rh[i] = *reinterpret_cast<const v4f*>(src + t * ci);
     }
   };
-  auto storeHalo = [&](int buf, int chunk) {
+  // The prologue's per-channel parameters of a chunk (this thread's 4 channels): four 16-byte loads issued
+  // together when the chunk's halo is stored (registers are not held across the MFMAs for them).
+  v4f pmu = {0.f, 0.f, 0.f, 0.f}, psc = {1.f, 1.f, 1.f, 1.f}, pbe = {0.f, 0.f, 0.f, 0.f};
+  v4f pal = {1.f, 1.f, 1.f, 1.f};
+  auto loadParams = [&](int chunk) {
     const int64_t c0 = static_cast<int64_t>(chunk) * BK + cq;
-    float mu[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f}, be[4] = {0.f, 0.f, 0.f, 0.f};
-    float al[4] = {1.f, 1.f, 1.f, 1.f}, ial[4] = {1.f, 1.f, 1.f, 1.f};
-    if (hasPre) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (p.affine) {
-          mu[q] = p.affine[c0 + q];
-          sc[q] = p.affine[ci + c0 + q];
-          be[q] = p.affine[2 * ci + c0 + q];
-        }
-        if (p.pre == PRE_SNAKE) {
-          al[q] = p.alpha[c0 + q];
-          ial[q] = 1.0f / al[q];
-        }
-      }
+    if (p.affine) {
+      pmu = *reinterpret_cast<const v4f*>(p.affine + c0);
+      psc = *reinterpret_cast<const v4f*>(p.affine + ci + c0);
+      pbe = *reinterpret_cast<const v4f*>(p.affine + 2 * ci + c0);
     }
+    if (p.pre == PRE_SNAKE) pal = *reinterpret_cast<const v4f*>(p.alpha + c0);
+  };
+  auto storeHalo = [&](int buf, int chunk) {
+    if (hasPre) loadParams(chunk);
+    float mu[4] = {pmu.x, pmu.y, pmu.z, pmu.w}, sc[4] = {psc.x, psc.y, psc.z, psc.w};
+    float be[4] = {pbe.x, pbe.y, pbe.z, pbe.w}, al[4] = {pal.x, pal.y, pal.z, pal.w}, ial[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ial[q] = 1.0f / al[q];
 #pragma unroll
     for (int i = 0; i < H4; ++i) {
       const int hr = (tid + i * NT) >> 2;
@@ -403,6 +435,8 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
     }
     if (more) loadB(s + 1);
     if (newChunk) loadHalo(chunk + 1);
+    // raised issue priority while this wave has MFMAs to issue (other waves' staging work yields to it)
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
 #pragma unroll
@@ -413,26 +447,13 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][i][q], bf[g][j][q], acc[i][j], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (more) storeB(bbuf ^ 1);
     if (newChunk) storeHalo(hbuf ^ 1, chunk + 1);
     __syncthreads();
   }
 
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        if (row < p.m && col < p.n) {
-          const float v = epilogue(p, acc[i][j][r], row, col);
-          p.c[row * p.ldc + col] = v;
-          acc[i][j][r] = v;
-        }
-      }
-    }
+  storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
   if (BM == 128 && p.stats) {
     // Per-(128-row chunk, channel) (mean, M2) of the stored output, two passes over the registers: this tile is
     // exactly chunk blockIdx.y. A column's 128 rows sit in (wm, i, lane half, r); reduce r and i in registers,
