@@ -60,150 +60,147 @@ __global__ void biasGeluKernel(const float* x, const float* bias, float* out, in
   if (i < n) out[i] = geluTanh(x[i] + bias[i % cols]);
 }
 
-// Flash attention over a fused QKV projection, head_dim 64. One wave per (head, 64-query tile), one query per
-// lane: q (+ q-bias, * 1/8) in registers, 64-key K/V tiles staged in LDS, online softmax in base e. The k-bias
-// cancels in softmax and is dropped; the v-bias is added once at the end (softmax weights sum to 1), as in the
-// reference kernel.
-__global__ __launch_bounds__(64) void attnQkvKernel(const float* __restrict__ qkv, const float* __restrict__ bias,
-                                                    float* __restrict__ out, int64_t t, int heads, int causal) {
-  constexpr int HD = 64, KT = 64;
-  __shared__ float ks[KT][HD + 1];
-  __shared__ float vs[KT][HD];
-  const int h = blockIdx.y, lane = threadIdx.x;
-  const int64_t D = static_cast<int64_t>(heads) * HD, ld = 3 * D;
-  const int64_t qi = static_cast<int64_t>(blockIdx.x) * 64 + lane;
-  const bool active = qi < t;
-  float q[HD], acc[HD];
-  const float* qr = qkv + (active ? qi : 0) * ld + h * HD;
-#pragma unroll
-  for (int d = 0; d < HD; ++d) {
-    q[d] = (qr[d] + bias[h * HD + d]) * 0.125f;
-    acc[d] = 0.0f;
-  }
-  float m = -INFINITY, l = 0.0f;
-  const int64_t kEnd = causal ? min<int64_t>(t, static_cast<int64_t>(blockIdx.x) * 64 + 64) : t;
-  for (int64_t k0 = 0; k0 < kEnd; k0 += KT) {
-    __syncthreads();
-    for (int i = lane; i < KT * HD; i += 64) {
-      const int kr = i / HD, d = i % HD;
-      const int64_t j = k0 + kr;
-      ks[kr][d] = j < t ? qkv[j * ld + D + h * HD + d] : 0.0f;
-      vs[kr][d] = j < t ? qkv[j * ld + 2 * D + h * HD + d] : 0.0f;
-    }
-    __syncthreads();
-    const int nk = static_cast<int>(min<int64_t>(KT, kEnd - k0));
-    for (int j = 0; j < nk; ++j) {
-      if (causal && k0 + j > qi) break;
-      float sc = 0.0f;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) sc += q[d] * ks[j][d];
-      const float mn = fmaxf(m, sc);
-      const float corr = expf(m - mn), p = expf(sc - mn);
-      l = l * corr + p;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) acc[d] = acc[d] * corr + p * vs[j][d];
-      m = mn;
-    }
-  }
-  if (!active) return;
-  const float inv = 1.0f / l;
-  float* o = out + qi * D + h * HD;
-#pragma unroll
-  for (int d = 0; d < HD; ++d) o[d] = acc[d] * inv + bias[2 * D + h * HD + d];
-}
-
-// Flash attention on f32 MFMA (32x32x2), head_dim 64. A workgroup = 4 waves = 128 queries of one head; each wave
-// owns 32 queries and walks the keys in 32-key tiles shared through LDS:
-//   S = Q K^T   32 MFMAs over the 64 dims (Q pre-scaled by 1/8 and + q-bias, held in 32 registers per lane)
-//   online softmax per query row on the accumulator layout (a row's 32 keys sit in 32 lanes of one half-wave)
-//   O += P V    P goes through LDS to the A-operand layout; 2 x 16 MFMAs for the 64 output dims
-// The k-bias cancels in softmax and is dropped; the v-bias is added once at the end.
+// Flash attention on f32 MFMA (32x32x2) over a fused QKV projection, head_dim 64, in the transposed form: a wave
+// computes S^T = K Q^T for 32 queries x 32 keys, so each lane's accumulator column is ONE query (16 of its 32 keys
+// in this lane, the other 16 in lane ^ 32):
+//   * the online-softmax max / sum of a query is 15 in-lane operations and one shuffle;
+//   * P^T sits in registers exactly as the B operand of O^T = V^T P^T: MFMA step s, lane half h reads key
+//     8 (s / 4) + 4 h + s % 4, which is accumulator register s of that lane; P never goes through LDS.
+// The 64 dims are consumed in the order 32 h + s (lane half h, step s), so a lane's share of a Q or K row is 32
+// contiguous floats (eight 16-byte loads, straight into registers, no LDS); V^T is read as 32-float rows per
+// key. Q is pre-scaled by log2(e) / 8 (+ q-bias) so that softmax uses exp2. The k-bias cancels in softmax and is
+// dropped; the v-bias is added once at the end (softmax weights sum to 1), as in the reference kernel.
+// A workgroup = 4 waves = one head's 32-query block; wave w takes key tiles w, w + 4, ... (prefetched one tile
+// ahead into registers) and the four partial (max, sum, O) states merge through LDS at the end. Grid =
+// ceil(T / 32) x heads.
 typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void attnMfmaKernel(const float* __restrict__ qkv, const float* __restrict__ bias,
                                                       float* __restrict__ out, int64_t t, int heads, int causal) {
-  constexpr int HD = 64, KT = 32, LDK = HD + 1, LDV = HD + 4, LDP = KT + 1;
-  __shared__ float ks[KT][LDK];
-  __shared__ float vs[KT][LDV];
-  __shared__ float ps[4][32][LDP];
+  constexpr int HD = 64, KT = 32;
+  __shared__ float mS[4][32], lS[4][32];
+  __shared__ float oS[4][32][HD + 1];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t D = static_cast<int64_t>(heads) * HD, ld = 3 * D;
-  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * 128 + wave * 32;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * 32;
   const int lr = lane & 31, lh = lane >> 5;
-  // Q operand: lane holds Q[q0 + lr][2 s + lh] for s = 0..31
-  float qa[32];
+  const int64_t qi = q0 + lr;  // this lane's query (accumulator column)
+  // B operand of S^T: Q[q][32 lh + s] * log2(e) / 8
+  float qb[32];
   {
-    const int64_t qi = min<int64_t>(q0 + lr, t - 1);
-    const float* qr = qkv + qi * ld + h * HD;
+    const float* qr = qkv + min<int64_t>(qi, t - 1) * ld + h * HD + 32 * lh;
+    const float* br = bias + h * HD + 32 * lh;
+    constexpr float kScale = 0.125f * 1.44269504088896341f;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) qa[s] = (qr[2 * s + lh] + bias[h * HD + 2 * s + lh]) * 0.125f;
+    for (int v = 0; v < 8; ++v) {
+      const v4f_t x = *reinterpret_cast<const v4f_t*>(qr + 4 * v), bb = *reinterpret_cast<const v4f_t*>(br + 4 * v);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qb[4 * v + c] = (x[c] + bb[c]) * kScale;
+    }
   }
+  const int64_t kEnd = causal ? min<int64_t>(t, q0 + 32) : t;
+  const int tiles = static_cast<int>((kEnd + KT - 1) / KT);
+  // A operands of one key tile: K[k0 + lr][32 lh + s] (32 floats) and V[k0 + key(s, lh)][32 b + lr] (2 x 16)
+  v4f_t kr[8];
+  float vr[32];
+  auto loadTile = [&](int tile) {
+    const int64_t k0 = static_cast<int64_t>(tile) * KT;
+    const float* kp = qkv + min<int64_t>(k0 + lr, t - 1) * ld + D + h * HD + 32 * lh;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) kr[v] = *reinterpret_cast<const v4f_t*>(kp + 4 * v);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int64_t key = min<int64_t>(k0 + 8 * (s >> 2) + 4 * lh + (s & 3), t - 1);
+      const float* vp = qkv + key * ld + 2 * D + h * HD + lr;
+      vr[s] = vp[0];
+      vr[16 + s] = vp[32];
+    }
+  };
   v16f_t o0, o1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
-  float mrow[16], lrow[16];
+  float m = -INFINITY, l = 0.0f;
+  if (wave < tiles) loadTile(wave);
+  for (int tile = wave; tile < tiles; tile += 4) {
+    const int64_t k0 = static_cast<int64_t>(tile) * KT;
+    float ka[32], va[32];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    mrow[r] = -INFINITY;
-    lrow[r] = 0.0f;
-  }
-  const int64_t blockQmax = min<int64_t>(t, static_cast<int64_t>(blockIdx.x) * 128 + 128);
-  const int64_t kEnd = causal ? blockQmax : t;
-  for (int64_t k0 = 0; k0 < kEnd; k0 += KT) {
-    __syncthreads();
-    for (int i = tid; i < KT * HD; i += 256) {
-      const int kr = i / HD, d = i % HD;
-      const int64_t j = k0 + kr;
-      ks[kr][d] = j < t ? qkv[j * ld + D + h * HD + d] : 0.0f;
-      vs[kr][d] = j < t ? qkv[j * ld + 2 * D + h * HD + d] : 0.0f;
-    }
-    __syncthreads();
-    // S tile: rows = queries, cols = keys
+    for (int v = 0; v < 8; ++v)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ka[4 * v + c] = kr[v][c];
+#pragma unroll
+    for (int s = 0; s < 32; ++s) va[s] = vr[s];
+    if (tile + 4 < tiles) loadTile(tile + 4);
     v16f_t sacc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[s], ks[lr][2 * s + lh], sacc, 0, 0, 0);
-    // online softmax: register r holds row 8 (r / 4) + 4 lh + r % 4, column (key) lr
-    const int64_t key = k0 + lr;
+    for (int s = 0; s < 32; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], qb[s], sacc, 0, 0, 0);
+    // accumulator r: key k0 + 8 (r / 4) + 4 lh + r % 4, query qi
+    float mt = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int64_t qrow = q0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-      float sv = sacc[r];
-      if (key >= t || (causal && key > qrow)) sv = -INFINITY;
-      float mx = sv;
+      const int64_t key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      if (key >= t || (causal && key > qi)) sacc[r] = -INFINITY;
+      mt = fmaxf(mt, sacc[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);  // finite: every tile holds a key <= qi (causal) or < t
+    const float corr = __builtin_amdgcn_exp2f(m - mn);
+    float ls = 0.0f;
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-      const float mn = fmaxf(mrow[r], mx);
-      const float p = mn == -INFINITY ? 0.0f : expf(sv - mn);
-      const float corr = mn == -INFINITY ? 1.0f : expf(mrow[r] - mn);
-      float ps_ = p;
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = __builtin_amdgcn_exp2f(sacc[r] - mn);
+      ls += sacc[r];
+    }
+    ls += __shfl_xor(ls, 32, 64);
+    l = l * corr + ls;
+    m = mn;
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) ps_ += __shfl_xor(ps_, o, 64);
-      lrow[r] = lrow[r] * corr + ps_;
-      mrow[r] = mn;
+    for (int r = 0; r < 16; ++r) {
       o0[r] *= corr;
       o1[r] *= corr;
-      ps[wave][8 * (r >> 2) + 4 * lh + (r & 3)][lr] = p;
     }
-    __syncthreads();
-    // O += P V: A = P[q = lr][key = 2 s + lh], B = V[key][dim]
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const float pa = ps[wave][lr][2 * s + lh];
-      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa, vs[2 * s + lh][lr], o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa, vs[2 * s + lh][32 + lr], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[s], sacc[s], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[16 + s], sacc[s], o1, 0, 0, 0);
     }
+  }
+  // merge the four waves: O^T accumulator r of block b is dim 32 b + 8 (r / 4) + 4 lh + r % 4 of query lr
+  if (lh == 0) {
+    mS[wave][lr] = m;
+    lS[wave][lr] = l;
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int64_t qrow = q0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-    if (qrow < t) {
-      const float inv = 1.0f / lrow[r];
-      float* o = out + qrow * D + h * HD;
-      o[lr] = o0[r] * inv + bias[2 * D + h * HD + lr];
-      o[32 + lr] = o1[r] * inv + bias[2 * D + h * HD + 32 + lr];
-    }
+    const int d = 8 * (r >> 2) + 4 * lh + (r & 3);
+    oS[wave][lr][d] = o0[r];
+    oS[wave][lr][32 + d] = o1[r];
+  }
+  __syncthreads();
+  const int q = tid >> 3, d0 = (tid & 7) * 8;
+  const int64_t qrow = q0 + q;
+  if (qrow >= t) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mS[w][q]);
+  float wsum = 0.0f, sc[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    sc[w] = lS[w][q] > 0.0f ? __builtin_amdgcn_exp2f(mS[w][q] - mx) : 0.0f;
+    wsum += sc[w] * lS[w][q];
+  }
+  const float inv = 1.0f / wsum;
+  float* o = out + qrow * D + h * HD;
+  const float* bv = bias + 2 * D + h * HD;
+#pragma unroll
+  for (int d = d0; d < d0 + 8; ++d) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) acc += sc[w] * oS[w][q][d];
+    o[d] = acc * inv + bv[d];
   }
 }
 
@@ -241,7 +238,7 @@ int lk_hip_bias_gelu_f32(const float* x, const float* bias, float* out, int64_t 
 int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, int64_t t, int heads, int causal,
                              void* stream) {
   if (t <= 0) return t == 0 ? 0 : 1;
-  dim3 grid(lkh::ceilDiv(t, 128), static_cast<unsigned>(heads));
+  dim3 grid(lkh::ceilDiv(t, 32), static_cast<unsigned>(heads));
   hipLaunchKernelGGL(lkd::attnMfmaKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), qkv, bias, out, t,
                      heads, causal);
   return hipGetLastError() == hipSuccess ? 0 : 2;

@@ -122,6 +122,16 @@ def test_attention_qkv(gpu, t, causal):
     close(got, K.attention_qkv(qkv, bias, heads, causal), 1e-4)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_qkv_peaked(gpu, causal):
+    """Scores spanning hundreds (near one-hot softmax rows, running max replaced many times across key tiles)."""
+    lk = gpu
+    t, heads = 333, 12
+    qkv, bias = rng.standard_normal((t, 3 * 768)) * 4.0, rng.standard_normal(3 * 768)
+    got = lk.ops.attention_qkv_f32_gpu(G(lk, qkv), G(lk, bias), heads, causal=causal)
+    close(got, K.attention_qkv(qkv, bias, heads, causal), 1e-4)
+
+
 @pytest.mark.parametrize("pos", [0, 1, 31, 32, 100, 512, 1023])
 def test_attention_decode_split(gpu, pos):
     lk = gpu
