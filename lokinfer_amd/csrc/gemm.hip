@@ -283,6 +283,187 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
   storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
 }
 
+// GEMM for few output tiles (M of a few hundred, e.g. ALBERT at T = 487 or an LSTM input projection): 64 x BN
+// workgroup tiles with K staged 64 deep, and wave w of the 4 computing the WHOLE tile over k-slice w (16 deep) of
+// every stage. One barrier then covers 8 * 2 * BN / 32 MFMAs per wave (32 at BN = 64) instead of the 8 of a
+// 64x64 tile split 2x2 over the waves; the four partial tiles are summed through LDS in a fixed order at the end
+// (deterministic), followed by the phased epilogue. A: row-major [M, lda]. B: NN [K, ldb] staged k-major
+// ([k][BN + 8]: the two lane halves of a read sit 4 rows = 32 banks apart), or NT [N, ldb] staged like A.
+// A (and NT B) tiles are [row][4 slots of 4 k], slot swizzled by (row >> 2) & 3; a slice's 16 k are fed to the
+// MFMAs in the order 8 g + 4 half + q, as in the conv kernel. Needs K, lda, ldb (and N for NN) % 4 == 0 and
+// 16-byte aligned operands (checked by the launcher).
+template <int BN, int BMODE>
+__global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
+  constexpr int BM = 64, KS = 64;
+  constexpr int TM = 2, TN = BN / 32;
+  constexpr int LDBK = BN + 8;
+  constexpr int A4 = BM * KS / 4 / NT, B4 = BN * KS / 4 / NT;
+  constexpr int A_FL = 2 * 4 * BM * 16;                                // floats of the A buffers
+  constexpr int B_FL = BMODE == B_NN ? 2 * KS * LDBK : 2 * 4 * BN * 16;
+  constexpr int RED_FL = 4 * BM * BN;
+  constexpr int SMEM = A_FL + B_FL > RED_FL ? A_FL + B_FL : RED_FL;
+  static_assert(A4 >= 1 && B4 >= 1, "staging slots");
+  __shared__ __attribute__((aligned(16))) float smem[SMEM];
+  v4f* As = reinterpret_cast<v4f*>(smem);             // [buf][slice][BM * 4]
+  float* Bsf = smem + A_FL;                            // NN: [buf][KS * LDBK]
+  v4f* Bsv = reinterpret_cast<v4f*>(smem + A_FL);     // NT: [buf][slice][BN * 4]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lk = lane >> 5;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM, n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
+
+  // two register sets: the next stage's tile is stored to LDS while the one after it is still in flight
+  v4f ra[2][A4], rb[2][B4];
+  auto gload = [&](int64_t k0, v4f (&ra)[A4], v4f (&rb)[B4]) {
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int idx = tid + i * NT, row = idx >> 4, kq = (idx & 15) * 4;
+      ra[i] = *reinterpret_cast<const v4f*>(p.a + min<int64_t>(m0 + row, lastRow) * p.lda +
+                                            min<int64_t>(k0 + kq, p.k - 4));
+    }
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      if constexpr (BMODE == B_NN) {
+        const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
+        rb[i] = *reinterpret_cast<const v4f*>(p.b + min<int64_t>(k0 + kr, p.k - 1) * p.ldb +
+                                              min<int64_t>(n0 + nq, p.n - 4));
+      } else {
+        const int col = idx >> 4, kq = (idx & 15) * 4;
+        rb[i] = *reinterpret_cast<const v4f*>(p.b + min<int64_t>(n0 + col, lastCol) * p.ldb +
+                                              min<int64_t>(k0 + kq, p.k - 4));
+      }
+    }
+  };
+  // The k tail (k >= K, loaded from clamped addresses) is zeroed here, when the data is first touched, so that
+  // no wait for the loads sits between their issue and the MFMAs.
+  auto sstore = [&](int buf, int64_t k0, const v4f (&ra)[A4], const v4f (&rb)[B4]) {
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int idx = tid + i * NT, row = idx >> 4, kq = (idx & 15) * 4;
+      const int slice = kq >> 4, slot = (kq >> 2) & 3;
+      As[(buf * 4 + slice) * BM * 4 + row * 4 + (slot ^ ((row >> 2) & 3))] = k0 + kq < p.k ? ra[i] : zero;
+    }
+#pragma unroll
+    for (int i = 0; i < B4; ++i) {
+      const int idx = tid + i * NT;
+      if constexpr (BMODE == B_NN) {
+        const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
+        *reinterpret_cast<v4f*>(Bsf + buf * KS * LDBK + kr * LDBK + nq) = k0 + kr < p.k ? rb[i] : zero;
+      } else {
+        const int col = idx >> 4, kq = (idx & 15) * 4;
+        const int slice = kq >> 4, slot = (kq >> 2) & 3;
+        Bsv[(buf * 4 + slice) * BN * 4 + col * 4 + (slot ^ ((col >> 2) & 3))] = k0 + kq < p.k ? rb[i] : zero;
+      }
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t stages = (p.k + KS - 1) / KS;
+  auto stage = [&](int64_t st, int buf, v4f (&ra_next)[A4], v4f (&rb_next)[B4], v4f (&ra_far)[A4],
+                   v4f (&rb_far)[B4]) {
+    v4f af[2][TM];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = i * 32 + lr;
+        af[g][i] = As[(buf * 4 + wave) * BM * 4 + row * 4 + ((2 * g + lk) ^ ((row >> 2) & 3))];
+      }
+    float bq[2][4][TN];
+    if constexpr (BMODE == B_NN) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            bq[g][q][j] = Bsf[buf * KS * LDBK + (16 * wave + 8 * g + 4 * lk + q) * LDBK + j * 32 + lr];
+    } else {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = j * 32 + lr;
+          const v4f bv = Bsv[(buf * 4 + wave) * BN * 4 + col * 4 + ((2 * g + lk) ^ ((col >> 2) & 3))];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bq[g][q][j] = bv[q];
+        }
+    }
+    if (st + 2 < stages) gload((st + 2) * KS, ra_far, rb_far);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][i][q], bq[g][q][j], acc[i][j], 0, 0, 0);
+    if (st + 1 < stages) sstore(buf ^ 1, (st + 1) * KS, ra_next, rb_next);
+    __syncthreads();
+  };
+  // stage st computes from LDS buffer st & 1, stores stage st + 1 (register set (st + 1) & 1) and has stage st + 2
+  // in flight into register set st & 1
+  gload(0, ra[0], rb[0]);
+  sstore(0, 0, ra[0], rb[0]);
+  if (stages > 1) gload(KS, ra[1], rb[1]);
+  __syncthreads();
+  for (int64_t st = 0; st < stages; st += 2) {
+    stage(st, 0, ra[1], rb[1], ra[0], rb[0]);
+    if (st + 1 < stages) stage(st + 1, 1, ra[0], rb[0], ra[1], rb[1]);
+  }
+
+  // partial tiles -> LDS (the staging buffers are free after the last barrier), fixed-order sum, epilogue
+  float* red = smem;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        red[(wave * BM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3)) * BN + j * 32 + lr] = acc[i][j][r];
+  __syncthreads();
+  constexpr int PER = BM * BN / NT;  // outputs per thread: 4 threads per row, PER contiguous columns each
+  const int row = tid >> 2, c0 = (tid & 3) * PER;
+  const int64_t grow = m0 + row;
+  float v[PER];
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    const int o = row * BN + c0 + c;
+    v[c] = ((red[o] + red[BM * BN + o]) + red[2 * BM * BN + o]) + red[3 * BM * BN + o];
+  }
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    const int64_t gcol = min<int64_t>(n0 + c0 + c, lastCol);
+    float x = v[c] + (p.bias ? p.bias[gcol] : 0.0f);
+    if (p.act == ACT_RELU) x = fmaxf(x, 0.0f);
+    else if (p.act == ACT_GELU) x = geluTanh(x);
+    v[c] = x;
+  }
+  if (p.res) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c)
+      v[c] += p.res[min<int64_t>(grow, lastRow) * p.ldr + min<int64_t>(n0 + c0 + c, lastCol)];
+  }
+  if (grow <= lastRow) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int64_t gcol = n0 + c0 + c;
+      if (gcol <= lastCol) p.c[grow * p.ldc + gcol] = v[c] * p.scale;
+    }
+  }
+}
+
 // Stride-1 channel-last conv with the taps innermost. For each 16-channel input chunk a workgroup stages the
 // halo rows its BM output rows need (BM + (K-1) dil rows x 16 channels) once, with the affine + Snake / leaky
 // prologue applied once per element; then every tap kk is a 16-deep MFMA step whose A operand is the same halo
@@ -525,9 +706,21 @@ using lkd::GemmParams;
 template <int AM, int BMODE>
 static void launchGemm(const GemmParams& p, hipStream_t s) {
   const int64_t big = static_cast<int64_t>(ceilDiv(p.m, 128)) * ceilDiv(p.n, 128);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.b)) & 15) == 0 &&
+                       p.k % 4 == 0 && p.lda % 4 == 0 && p.ldb % 4 == 0 && p.k >= 4 &&
+                       (BMODE == lkd::B_NT || (p.n % 4 == 0 && p.n >= 4));
   if (big >= 512) {
     dim3 grid(ceilDiv(p.n, 128), ceilDiv(p.m, 128));
     hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+  } else if (AM == lkd::A_ROWMAJOR && aligned) {
+    // few output tiles: K split over the waves of a workgroup; 32-column tiles when 64 would leave CUs idle
+    if (static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 192) {
+      dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+    } else {
+      dim3 grid(ceilDiv(p.n, 32), ceilDiv(p.m, 64));
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+    }
   } else {
     dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
     hipLaunchKernelGGL((lkd::gemmMfmaKernel<64, 64, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);

@@ -27,14 +27,16 @@ def close(got, ref, tol):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 128, 784), (59, 2304, 768), (487, 768, 2048), (130, 70, 33), (256, 256, 512),
-                                   (1000, 1536, 256)])
+                                   (1000, 1536, 256), (487, 2304, 768), (487, 2048, 768), (100, 36, 20), (65, 68, 132),
+                                   (2, 4, 4)])
 def test_gemm(gpu, m, n, k):
     lk = gpu
     a, b = rng.standard_normal((m, k)), rng.standard_normal((k, n)) / np.sqrt(k)
     close(lk.ops.gemm_f32_gpu_mps(G(lk, a), G(lk, b)), K.gemm(a, b), 1e-5)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 50257, 768), (3, 1000, 64), (200, 300, 96)])
+@pytest.mark.parametrize("m,n,k", [(1, 50257, 768), (3, 1000, 64), (200, 300, 96), (487, 2048, 640), (70, 45, 100),
+                                   (1, 7, 4)])
 def test_gemm_nt(gpu, m, n, k):
     lk = gpu
     a, b = rng.standard_normal((m, k)), rng.standard_normal((n, k)) / np.sqrt(k)
