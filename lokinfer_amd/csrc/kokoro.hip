@@ -32,21 +32,25 @@ __global__ __launch_bounds__(256) void statsKernel(const float* __restrict__ x, 
   const int64_t t0 = s * kStatChunk;
   const int n = static_cast<int>(min<int64_t>(kStatChunk, l - t0));
   const bool ok = ch < c;
-  const int r0 = min(g * 32, n), r1 = min(r0 + 32, n);
+  const int r0 = g * 32;
   const float* col = x + t0 * c + (ok ? ch : 0);
+  // the thread's 32 rows are loaded once (independent loads in flight) and kept for both passes
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = (ok && r0 + i < n) ? col[static_cast<int64_t>(r0 + i) * c] : 0.0f;
   float sum = 0.0f;
-  if (ok)
-    for (int i = r0; i < r1; ++i) sum += col[static_cast<int64_t>(i) * c];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) sum += v[i];
   part[g][cl] = sum;
   __syncthreads();
   const float mean = (part[0][cl] + part[1][cl] + part[2][cl] + part[3][cl]) / static_cast<float>(n);
   __syncthreads();
   float m2 = 0.0f;
-  if (ok)
-    for (int i = r0; i < r1; ++i) {
-      const float d = col[static_cast<int64_t>(i) * c] - mean;
-      m2 += d * d;
-    }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float d = v[i] - mean;
+    if (r0 + i < n) m2 += d * d;
+  }
   part[g][cl] = m2;
   __syncthreads();
   if (g == 0 && ok) {
