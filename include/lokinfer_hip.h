@@ -56,7 +56,9 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
 
 /* ---- GEMV (reference: gemv4*_f32_gpu transformer_gpu.cpp:233-251; gemv_rows / gemv1_bias kokoro_lc.cpp:227-267) */
 int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,
-                    int64_t k, int act, void* stream);
+                    int64_t k, int act, void* workspace, int64_t workspace_bytes, void* stream);
+/* workspace (optional, 16-byte aligned): 4 * ceil(K / 64) * N floats of partial sums for the two-launch path;
+ * with none (or N % 4 != 0) a single-pass kernel runs. act: 0 none, 2 gelu_tanh. */
 int lk_hip_rowdot_f32(const float* mat, const float* vec, const float* bias, int bias_per_row, float* out,
                       int64_t rows, int64_t k, int nvec, int64_t ldo, void* stream);
 

@@ -66,6 +66,7 @@ void registerKokoroKernels();
 void registerFrontendKernels();
 void registerSequenceKernels();
 void registerSignalKernels();
+void registerDecodeFusedKernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 

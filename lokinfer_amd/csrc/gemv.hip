@@ -6,14 +6,21 @@
 //                     for the GPT-2 LM head, gemv_rows_f32_gpu kokoro_lc.cpp:227-254, gemv1_bias_f32_gpu
 //                     kokoro_lc.cpp:257-267 / vision.metal:266-284)
 //
-// gemv: one 1024-thread workgroup (16 waves) owns a 16-column slab of W over the whole K: 4 lanes x float4
-// cover the 16 columns (64 contiguous bytes of a row) and the 256 row slots stride K, so every thread has
-// K / 256 independent loads in flight. The 256 partial sums per column are reduced in LDS in a fixed order:
-// no cross-workgroup communication, deterministic results, one launch. N / 16 workgroups (48 at N = 768,
-// 192 at N = 3072) each stream K x 64 B.
+// gemv, two launches (the default when a workspace is given): at decode sizes (2-10 MB per matrix) the
+// stream is latency-bound unless nearly the whole matrix is in flight at once, so
+//   1. gemvPartialKernel: a wave covers 256 columns (64 lanes x float4, 1 KB of a row) x 16 rows and issues its
+//      16 loads back to back; grid = ceil(N / 256) x ceil(K / 64) workgroups of 4 waves. Each wave writes its
+//      16-row partial sums (summed in row order) to the workspace as slice s = 4 * blockIdx.y + wave;
+//   2. gemvReduceKernel: per column, the K / 16 slices are summed in a fixed order (4 interleaved chains, then
+//      (c0 + c1) + (c2 + c3)) and the epilogue (bias, gelu, residual) applied.
+// Deterministic; no cross-workgroup communication inside a launch.
+// gemv without a workspace (or N % 4 != 0): one 1024-thread workgroup (16 waves) owns a 16-column slab of W over
+// the whole K: 4 lanes x float4 cover the 16 columns and the 256 row slots stride K; the 256 partial sums per
+// column are reduced in LDS in a fixed order.
 #include "common.h"
 
 #include <algorithm>
+#include <cstdint>
 
 namespace lkd {
 
@@ -95,6 +102,50 @@ __global__ __launch_bounds__(kGemvThreads) void gemvKernel(GemvParams p) {
   }
 }
 
+constexpr int kGemvRowsPerWave = 16;
+
+__global__ __launch_bounds__(256) void gemvPartialKernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                        float* __restrict__ part, int64_t n, int64_t k) {
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64 + kGemvRowsPerWave * wv;
+  const int64_t slice = static_cast<int64_t>(blockIdx.y) * 4 + wv;
+  if (col >= n) return;
+  f4v wr[kGemvRowsPerWave];
+#pragma unroll
+  for (int i = 0; i < kGemvRowsPerWave; ++i)
+    wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + i, k - 1) * n + col));
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kGemvRowsPerWave; ++i) {
+    const float xv = r0 + i < k ? x[r0 + i] : 0.0f;
+    acc += xv * wr[i];
+  }
+  *reinterpret_cast<f4v*>(part + slice * n + col) = acc;
+}
+
+__global__ __launch_bounds__(256) void gemvReduceKernel(const float* __restrict__ part, GemvParams p,
+                                                       int64_t slices) {
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + c;
+  float s = 0.0f;
+  if (col < p.n) {
+#pragma unroll 8
+    for (int64_t sl = q; sl < slices; sl += 4) s += part[sl * p.n + col];
+  }
+  red[q][c] = s;
+  __syncthreads();
+  if (q == 0 && col < p.n) {
+    float o = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+    if (p.bias) o += p.bias[col];
+    if (p.act == 2) o = geluTanh(o);
+    if (p.res) o += p.res[col];
+    p.out[col] = o;
+  }
+}
+
 // One wave per matrix row: out[m * ldo + r] = sum_k vec[m, k] mat[r, k] (+ bias). K % 4 == 0 (float4 loads).
 template <int MV>
 __global__ __launch_bounds__(256) void rowdotKernel(const float* __restrict__ mat, const float* __restrict__ vec,
@@ -131,7 +182,7 @@ __global__ __launch_bounds__(256) void rowdotKernel(const float* __restrict__ ma
 extern "C" {
 
 int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,
-                    int64_t k, int act, void* stream) {
+                    int64_t k, int act, void* workspace, int64_t workspaceBytes, void* stream) {
   if (n <= 0 || k < 0) return n == 0 ? 0 : 1;
   lkd::GemvParams p{};
   p.x = x;
@@ -142,8 +193,18 @@ int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const flo
   p.n = n;
   p.k = k;
   p.act = act;
-  const unsigned blocks = lkh::ceilDiv(n, lkd::kGemvCols);
-  hipLaunchKernelGGL(lkd::gemvKernel, dim3(blocks), dim3(lkd::kGemvThreads), 0, static_cast<hipStream_t>(stream), p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t kBlocks = (k + 63) / 64, slices = 4 * kBlocks;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(workspace)) & 15) == 0;
+  if (k > 0 && n % 4 == 0 && aligned && workspace && workspaceBytes >= slices * n * 4 && kBlocks < 65536) {
+    float* part = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(lkd::gemvPartialKernel, dim3(lkh::ceilDiv(n, 256), static_cast<unsigned>(kBlocks)), dim3(256),
+                       0, s, x, w, part, n, k);
+    hipLaunchKernelGGL(lkd::gemvReduceKernel, dim3(lkh::ceilDiv(n, 64)), dim3(256), 0, s, part, p, slices);
+  } else {
+    const unsigned blocks = lkh::ceilDiv(n, lkd::kGemvCols);
+    hipLaunchKernelGGL(lkd::gemvKernel, dim3(blocks), dim3(lkd::kGemvThreads), 0, s, p);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -104,7 +104,9 @@ void runGemv(ExecCtx& ctx, const KernelArgs& a) {
   int idx = 2;
   const float* bias = BIAS ? P<float>(a, idx++) : nullptr;
   const float* res = RES ? P<float>(a, idx++) : nullptr;
-  status(ctx, lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), bias, res, P<float>(a, idx), n, k, ACT, ctx.stream),
+  status(ctx,
+         lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), bias, res, P<float>(a, idx), n, k, ACT, ctx.workspace,
+                         ctx.workspaceBytes, ctx.stream),
          "gemv: launch failed");
 }
 
@@ -476,6 +478,7 @@ static void registerAll() {
     registerFrontendKernels();
     registerSequenceKernels();
     registerSignalKernels();
+    registerDecodeFusedKernels();
     std::sort(names().begin(), names().end());
   });
 }

@@ -10,6 +10,11 @@ Per step (inputs tok i64[1], pos i64[1], both on the device):
   logits = ln . wte^T (tied LM head, gemm_nt);  next = argmax(logits) on the device
 The reference does the two embedding lookups on the CPU and the argmax in Python; here they are device kernels
 so a step is one captured HIP graph.
+
+By default (fused=True) each layer runs the same arithmetic in 5 launches instead of 13: the GEMVs write
+row-slice partial sums and the consumer of each GEMV sums the slices itself (the decode-attention chunk kernel
+for qkv; the next partial GEMV for the attention merge, for gelu(c_fc) and for bias + residual + LayerNorm, the
+new residual stream written by one of its workgroups). fused=False keeps the reference's op sequence.
 """
 from __future__ import annotations
 
@@ -53,17 +58,41 @@ class Gpt2Decoder:
     """Weights uploaded once; 12 persistent K/V caches f32[1024, 768] on the device (the reference's
     lk.persistent_buffer caches, models/gpt2.py:186-188)."""
 
-    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True):
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, fused: bool = True):
         self.w = {k: from_numpy(v, device="gpu", copy=True) for k, v in sd.items()}
         dev = self.w["transformer.wte.weight"].t.device
         self.caches = [(Tensor(torch.zeros(N_POS, D, device=dev)), Tensor(torch.zeros(N_POS, D, device=dev)))
                        for _ in range(N_LAYER)]
+        self.fused = fused
         self.step_model = lk_compile(self._step, graph=graph)
 
     def _step(self, tok: Tensor, pos: Tensor):
         w = self.w
         P = "transformer."
         h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos)
+        if self.fused:
+            # 5 launches per layer: each GEMV writes row-slice partial sums and its consumer reduces them (the
+            # decode-attention chunk kernel for qkv, the next partial GEMV for the attention merge, for gelu(c_fc)
+            # and for bias + residual + LayerNorm)
+            qp, h = ops.gemv_partial_ln_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"],
+                                                w[P + "h.0.attn.c_attn.weight"], eps=LN_EPS)
+            for i, (kc, vc) in enumerate(self.caches):
+                L = f"{P}h.{i}."
+                ch = ops.attention_decode_part_f32_gpu(qp, kc, vc, pos, w[L + "attn.c_attn.bias"], heads=HEADS)
+                op = ops.gemv_partial_attn_f32_gpu(ch, w[L + "attn.c_proj.weight"])
+                fp, h = ops.gemv_partial_res_ln_f32_gpu(op, w[L + "attn.c_proj.bias"], h, w[L + "ln_2.weight"],
+                                                        w[L + "ln_2.bias"], w[L + "mlp.c_fc.weight"], eps=LN_EPS)
+                mp = ops.gemv_partial_gelu_f32_gpu(fp, w[L + "mlp.c_fc.bias"], w[L + "mlp.c_proj.weight"])
+                if i + 1 < N_LAYER:
+                    N = f"{P}h.{i + 1}."
+                    qp, h = ops.gemv_partial_res_ln_f32_gpu(mp, w[L + "mlp.c_proj.bias"], h, w[N + "ln_1.weight"],
+                                                            w[N + "ln_1.bias"], w[N + "attn.c_attn.weight"],
+                                                            eps=LN_EPS)
+                else:
+                    h, ln = ops.reduce_bias_res_ln2_f32_gpu(mp, w[L + "mlp.c_proj.bias"], h, w[P + "ln_f.weight"],
+                                                            w[P + "ln_f.bias"], eps=LN_EPS)
+            logits = ops.gemm_nt_f32_gpu_mps(ln, w[P + "wte.weight"])
+            return logits, ops.argmax_f32_gpu(logits)
         ln = ops.layernorm_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"], eps=LN_EPS)
         for i, (kc, vc) in enumerate(self.caches):
             L = f"{P}h.{i}."

@@ -334,6 +334,91 @@ def attention_decode_split_f32_gpu(qkv, kcache, vcache, pos, bias, heads, splits
                   dict(heads=int(heads), nsg=int(nsg), single=int(single), splits=int(splits)))
 
 
+# ---- fused decode step (backend ops; they replace one layer's gemv4 / attention_decode_split /
+# add_bias_layernorm2 sequence, reference ops/transformer.py:51-64, 323-382) ------------------------------------
+
+def gemv_partial_slices(k: int) -> int:
+    """Row slices of a partial GEMV over K (16 rows per wave up to K = 1024, else 64)."""
+    rpw = 16 if k <= 1024 else 64
+    return -(-int(k) // (4 * rpw))
+
+
+def gemv_partial_f32_gpu(x, w):
+    """Row-slice partial sums of x f32[1, K] @ w f32[K, N] -> f32[S, N], S = gemv_partial_slices(K); the slices
+    are summed (in order) by the consuming op."""
+    _f32(x, w, rank=2)
+    check(x.shape[0] == 1 and x.shape[1] == w.shape[0], "x must be f32[1, K] and w f32[K, N]")
+    check(w.shape[1] % 4 == 0, "N must be a multiple of 4")
+    return _launch("gemv_partial_f32_gpu", [x, w], [(gemv_partial_slices(w.shape[0]), w.shape[1])])
+
+
+def gemv_partial_gelu_f32_gpu(xpart, xbias, w):
+    """Partial GEMV whose input is gelu_tanh(sum of the slices of xpart f32[Sx, K] + xbias f32[K])."""
+    _f32(xpart, w, rank=2)
+    k = xpart.shape[1]
+    check(w.shape[0] == k and w.shape[1] % 4 == 0, "w must be f32[K, N] with N % 4 == 0")
+    _bias_ok(xbias, k)
+    return _launch("gemv_partial_gelu_f32_gpu", [xpart, xbias, w], [(gemv_partial_slices(k), w.shape[1])])
+
+
+def gemv_partial_attn_f32_gpu(chunks, w):
+    """Partial GEMV whose input is the merged decode attention of chunks f32[H, C, 66] (64 dims per head)."""
+    _f32(chunks, rank=3)
+    _f32(w, rank=2)
+    check(chunks.shape[2] == 66 and w.shape[0] == 64 * chunks.shape[0] and w.shape[1] % 4 == 0,
+          "expected chunks [H, C, 66] and w [64 H, N], N % 4 == 0")
+    return _launch("gemv_partial_attn_f32_gpu", [chunks, w], [(gemv_partial_slices(w.shape[0]), w.shape[1])])
+
+
+def gemv_partial_res_ln_f32_gpu(xpart, xbias, res, gamma, beta, w, eps=1e-5):
+    """(part, s): partial GEMV of LN(s) with s = (slices of xpart f32[Sx, K]) + xbias + res f32[1, K], K <= 1024;
+    s is returned as the new residual stream."""
+    _f32(xpart, res, w, rank=2)
+    k = xpart.shape[1]
+    check(tuple(res.shape) == (1, k) and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024,
+          "expected res [1, K], w [K, N] with N % 4 == 0, K <= 1024")
+    for v in (xbias, gamma, beta):
+        _bias_ok(v, k)
+    return _launch("gemv_partial_res_ln_f32_gpu", [xpart, xbias, res, gamma, beta, w],
+                   [(gemv_partial_slices(k), w.shape[1]), (1, k)], dict(eps=float(eps)))
+
+
+def gemv_partial_ln_f32_gpu(x, gamma, beta, w, eps=1e-5):
+    """(part, x'): partial GEMV of LN(x) for x f32[1, K], K <= 1024 (x' is a copy of x)."""
+    _f32(x, w, rank=2)
+    k = x.shape[1]
+    check(x.shape[0] == 1 and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024,
+          "expected x [1, K], w [K, N] with N % 4 == 0, K <= 1024")
+    for v in (gamma, beta):
+        _bias_ok(v, k)
+    return _launch("gemv_partial_ln_f32_gpu", [x, gamma, beta, w], [(gemv_partial_slices(k), w.shape[1]), (1, k)],
+                   dict(eps=float(eps)))
+
+
+def attention_decode_part_f32_gpu(qkv_part, kcache, vcache, pos, bias, heads):
+    """Decode attention over cache rows 0..pos with q, k, v = slice sums of qkv_part f32[S, 3D] + bias; writes
+    row pos of both caches (in place) and returns the per-(head, 64-key chunk) partials f32[H, C, 66]."""
+    _f32(qkv_part, kcache, vcache, rank=2)
+    d = kcache.shape[1]
+    check(qkv_part.shape[1] == 3 * d and vcache.shape == kcache.shape and d == 64 * heads, "bad decode shapes")
+    check(pos.dtype == i64 and tuple(pos.shape) == (1,), "pos must be i64[1]")
+    check(tuple(bias.shape) == (3 * d,), "bias must be f32[3D]")
+    chunks = -(-kcache.shape[0] // 64)
+    return _launch("attention_decode_part_f32_gpu", [qkv_part, kcache, vcache, pos, bias], [(heads, chunks, 66)],
+                   dict(heads=int(heads)))
+
+
+def reduce_bias_res_ln2_f32_gpu(part, bias, res, gamma, beta, eps=1e-5):
+    """(s, LN(s)) with s = (sum of the slices of part f32[S, N]) + bias + res; N <= 1024."""
+    _f32(part, res, rank=2)
+    n = part.shape[1]
+    check(tuple(res.shape) == (1, n), "res must be f32[1, N]")
+    for v in (bias, gamma, beta):
+        _bias_ok(v, n)
+    return _launch("reduce_bias_res_ln2_f32_gpu", [part, bias, res, gamma, beta], [(1, n), (1, n)],
+                   dict(eps=float(eps)))
+
+
 def attention_decode_kvw_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
     s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
     return _launch("attention_decode_kvw_f32_gpu", [qkv, kcache, vcache, pos, bias], [s], dict(heads=int(heads)))

@@ -25,9 +25,10 @@ def _dev(lk, v):
     return lk.from_numpy(np.array([v], np.int64), device="gpu", copy=True)
 
 
-def test_decode_512(setup):
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_512(setup, fused):
     lk, G, sd, ids, nxt, ref = setup
-    dec = G.Gpt2Decoder(sd)
+    dec = G.Gpt2Decoder(sd, fused=fused)
     dec.prefill(ids)
     logits, am = dec.step(_dev(lk, nxt), _dev(lk, 512))
     got = logits.numpy()[0]
@@ -48,3 +49,17 @@ def test_eager_equals_graph(setup):
         lb, _ = b.step(_dev(lk, int(t)), _dev(lk, p))
         torch.cuda.synchronize()
         assert np.array_equal(la.numpy(), lb.numpy())
+
+
+def test_fused_matches_reference_op_sequence(setup):
+    """The fused 7-launch layer and the reference's gemv4 / attention_decode_split / add_bias_layernorm2 sequence
+    agree step by step (only the order of the K-sum changes)."""
+    lk, G, sd, ids, nxt, ref = setup
+    a = G.Gpt2Decoder(sd, fused=True)
+    b = G.Gpt2Decoder(sd, fused=False)
+    for p, t in enumerate(ids[:20]):
+        la, aa = a.step(_dev(lk, int(t)), _dev(lk, p))
+        lb, ab = b.step(_dev(lk, int(t)), _dev(lk, p))
+        x, y = la.numpy()[0], lb.numpy()[0]
+        assert np.abs(x - y).max() <= 1e-5 * np.abs(y).max(), p
+        assert int(aa.numpy()[0]) == int(ab.numpy()[0])

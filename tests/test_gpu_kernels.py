@@ -71,7 +71,8 @@ def test_mnist_mlp_plumbing(gpu):
     assert int(got.argmax()) == int(ref.argmax())
 
 
-@pytest.mark.parametrize("n,k", [(2304, 768), (768, 768), (3072, 768), (768, 3072), (100, 40)])
+@pytest.mark.parametrize("n,k", [(2304, 768), (768, 768), (3072, 768), (768, 3072), (100, 40), (4, 1), (260, 130),
+                                 (1028, 65)])
 @pytest.mark.parametrize("variant", ["plain", "bias", "gelu", "res"])
 def test_gemv4(gpu, n, k, variant):
     lk = gpu
@@ -79,7 +80,7 @@ def test_gemv4(gpu, n, k, variant):
         pytest.skip("gemv4 needs N % 4 == 0")
     x, w, b, r = rng.standard_normal((1, k)), rng.standard_normal((k, n)) / np.sqrt(k), rng.standard_normal(n), rng.standard_normal((1, n))
     X, W, B, R = G(lk, x), G(lk, w), G(lk, b), G(lk, r)
-    for _ in range(3):  # ticket counters must be restored between calls
+    for _ in range(3):  # repeated calls reuse the workspace
         if variant == "plain":
             got, ref = lk.ops.gemv4_f32_gpu(X, W), K.gemm(x, w)
         elif variant == "bias":
@@ -302,3 +303,65 @@ def test_conv_tap_kernel_large(gpu, l, c, co, k, d, act):
         ref = (full + res[s0:s1]) * 0.5
         close(got[s0:s1], ref, 1e-4)
     del lo_in, hi_in
+
+
+@pytest.mark.parametrize("k,n", [(768, 2304), (3072, 768), (100, 36)])
+def test_gemv_partial_reduce_ln(gpu, k, n):
+    lk = gpu
+    x, w = rng.standard_normal((1, k)), rng.standard_normal((k, n)) / np.sqrt(k)
+    bias, res, g, b = rng.standard_normal(n), rng.standard_normal((1, n)), rng.standard_normal(n), rng.standard_normal(n)
+    part = lk.ops.gemv_partial_f32_gpu(G(lk, x), G(lk, w))
+    assert part.shape == (lk.ops.gemv_partial_slices(k), n)
+    close(part.numpy().sum(0)[None], K.gemm(x, w), 1e-5)
+    if n <= 1024:
+        s, ln = lk.ops.reduce_bias_res_ln2_f32_gpu(part, G(lk, bias), G(lk, res), G(lk, g), G(lk, b), 1e-5)
+        rs, rl = K.add_bias_layernorm2(K.gemm(x, w), bias, res, g, b, 1e-5)
+        close(s, rs, 1e-5)
+        close(ln, rl, 2e-5)
+
+
+def test_gemv_partial_gelu(gpu):
+    lk = gpu
+    k0, k, n = 768, 3072, 768
+    x, w1, b1 = rng.standard_normal((1, k0)), rng.standard_normal((k0, k)) / np.sqrt(k0), rng.standard_normal(k) * 0.1
+    w2 = rng.standard_normal((k, n)) / np.sqrt(k)
+    p1 = lk.ops.gemv_partial_f32_gpu(G(lk, x), G(lk, w1))
+    p2 = lk.ops.gemv_partial_gelu_f32_gpu(p1, G(lk, b1), G(lk, w2))
+    ref = K.gemm(K.gelu_tanh(K.gemm(x, w1, b1)), w2)
+    close(p2.numpy().sum(0)[None], ref, 1e-5)
+
+
+@pytest.mark.parametrize("pos", [0, 63, 64, 511, 1023])
+def test_attention_decode_part(gpu, pos):
+    lk = gpu
+    heads, d, cap = 12, 768, 1024
+    x = rng.standard_normal((1, d))
+    w = rng.standard_normal((d, 3 * d)) / np.sqrt(d)
+    bias = rng.standard_normal(3 * d) * 0.1
+    kc, vc = rng.standard_normal((cap, d)), rng.standard_normal((cap, d))
+    wo = rng.standard_normal((d, d)) / np.sqrt(d)
+    KC, VC = G(lk, kc), G(lk, vc)
+    qp = lk.ops.gemv_partial_f32_gpu(G(lk, x), G(lk, w))
+    ch = lk.ops.attention_decode_part_f32_gpu(qp, KC, VC, lk.from_numpy(np.array([pos], np.int64), device="gpu", copy=True),
+                                            G(lk, bias), heads)
+    op = lk.ops.gemv_partial_attn_f32_gpu(ch, G(lk, wo))
+    att, kref, vref = K.attention_decode(K.gemm(x, w), kc, vc, pos, bias, heads)
+    close(op.numpy().sum(0)[None], K.gemm(att, wo), 1e-5)
+    close(KC.numpy()[pos], kref[pos], 1e-6)
+    close(VC.numpy()[pos], vref[pos], 1e-6)
+
+
+def test_gemv_partial_res_ln(gpu):
+    lk = gpu
+    k, n = 768, 2304
+    x, w0 = rng.standard_normal((1, 3072)), rng.standard_normal((3072, k)) / 55
+    bias, res, g, b = rng.standard_normal(k), rng.standard_normal((1, k)), rng.standard_normal(k), rng.standard_normal(k)
+    w = rng.standard_normal((k, n)) / np.sqrt(k)
+    xp = lk.ops.gemv_partial_f32_gpu(G(lk, x), G(lk, w0))
+    part, s = lk.ops.gemv_partial_res_ln_f32_gpu(xp, G(lk, bias), G(lk, res), G(lk, g), G(lk, b), G(lk, w), 1e-5)
+    rs, rl = K.add_bias_layernorm2(K.gemm(x, w0), bias, res, g, b, 1e-5)
+    close(s, rs, 1e-5)
+    close(part.numpy().sum(0)[None], K.gemm(rl, w), 2e-5)
+    part2, x2 = lk.ops.gemv_partial_ln_f32_gpu(G(lk, res), G(lk, g), G(lk, b), G(lk, w), 1e-5)
+    close(x2, res.astype(np.float32), 0)
+    close(part2.numpy().sum(0)[None], K.gemm(K.layernorm(res, g, b, 1e-5), w), 2e-5)
