@@ -56,6 +56,16 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t rBase = static_cast<int64_t>(blockIdx.y) * ROWS;
+  // The weight loads do not depend on x: the first batch is issued before x is formed, so its latency overlaps
+  // the prologue's own loads and reductions.
+  constexpr int B0 = RPW < 32 ? RPW : 32;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
+  const int64_t r0 = rBase + static_cast<int64_t>(wv) * RPW;
+  const int64_t colc = min<int64_t>(col, n - 4);  // columns past N compute on a valid column, never stored
+  f4v wr[B0];
+#pragma unroll
+  for (int i = 0; i < B0; ++i)
+    wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + i, k - 1) * n + colc));
   if constexpr (XMODE == 0) {
     for (int t = tid; t < ROWS; t += 256) xs[t] = rBase + t < k ? x[rBase + t] : 0.0f;
   } else if constexpr (XMODE == 1) {
@@ -141,19 +151,17 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
     // NaN when the chunk kernel flagged an invalid position
   }
   __syncthreads();
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
-  const int64_t r0 = rBase + static_cast<int64_t>(wv) * RPW;
   f4v acc = {0.f, 0.f, 0.f, 0.f};
-  const int64_t colc = min<int64_t>(col, n - 4);  // columns past N compute on a valid column, never stored
 #pragma unroll
-  for (int b = 0; b < RPW; b += 16) {
-    f4v wr[16];
+  for (int i = 0; i < B0; ++i) acc += xs[wv * RPW + i] * wr[i];  // xs is 0 past K
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+  for (int b = B0; b < RPW; b += 32) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
       wr[i] = __builtin_nontemporal_load(
           reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + b + i, k - 1) * n + colc));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc += xs[wv * RPW + b + i] * wr[i];  // xs is 0 past K
+    for (int i = 0; i < 32; ++i) acc += xs[wv * RPW + b + i] * wr[i];
   }
   wsum[wv][lane] = acc;
   __syncthreads();
