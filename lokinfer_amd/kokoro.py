@@ -68,7 +68,7 @@ class KokoroGpu:
         self._per_t: dict[tuple, Tensor] = {}
         self.banks = {root: self._bank(root) for root in ("predictor", "decoder")}
         # side streams for the graph's concurrent branches (default priority)
-        self.streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        self.streams = [torch.cuda.Stream() for _ in range(4)]
         self.model = lk_compile(self._forward, graph=graph)
         self.debug: dict | None = None  # set to {} to keep named intermediates (eager runs only)
 
@@ -175,6 +175,16 @@ class KokoroGpu:
             x, st = y if j < 2 else (y, None)
         return x
 
+    def noise_block(self, har: Tensor, bank, i: int) -> Tensor:
+        """noise_convs.i (stride 6 for stage 0, 1x1 for stage 1) then noise_res.i (AdaINResBlock1, K = 7 / 11)."""
+        G = "decoder.generator."
+        xs = ops.conv1d_lc_f32_gpu(har, self.g(G + f"noise_convs.{i}.weight", _w_lc_32),
+                                   self.g(G + f"noise_convs.{i}.bias"), **({"stride": 6, "padding": 3} if i == 0 else {}))
+        self._keep(f"xs{i}_conv", xs)
+        xs = self.resblock1(xs, bank, f"{G}noise_res.{i}", (7, 11)[i])
+        self._keep(f"xs{i}", xs)
+        return xs
+
     def lstm(self, x: Tensor, p: str) -> Tensor:
         return ops.lstm_bidir_t_f32_gpu(x, *self.lstm_w(p))
 
@@ -253,6 +263,22 @@ class KokoroGpu:
         with ctx.branch(self.streams[1], 2):
             n_curve = curve("N")
         f0 = curve("F0")
+        # The generator's noise path (harmonic source -> STFT -> noise_convs.i -> noise_res.i) depends only on F0:
+        # it runs beside the decoder, stage 0's block on one side stream and stage 1's on another that waits only
+        # for the STFT; the generator joins each just before adding it.
+        G = "decoder.generator."
+        har_ready = torch.cuda.Event()
+        with ctx.branch(self.streams[2], 3):
+            har_src = ops.harmonic_source_f32_gpu(f0, noise, self.g(G + "m_source.l_linear.weight", _flat),
+                                                  self.g(G + "m_source.l_linear.bias"))
+            har = ops.stft_magphase_lc_f32_gpu(har_src, 20, 5, cpad=32)  # [120 F + 1, 32]
+            har_ready.record(self.streams[2])
+            self._keep("har_source", har_src)
+            self._keep("har", har)
+            xs_stage = [self.noise_block(har, bank_d, 0)]
+        with ctx.branch(self.streams[3], 4):
+            self.streams[3].wait_event(har_ready)
+            xs_stage.append(self.noise_block(har, bank_d, 1))
         ctx.join(self.streams[1])
         ctx.join(self.streams[0])
         # decoder
@@ -270,25 +296,21 @@ class KokoroGpu:
                             1024 if i < 3 else 512, i == 3)
         self._keep("dec", x)
         # generator
-        G = "decoder.generator."
-        har_src = ops.harmonic_source_f32_gpu(f0, noise, self.g(G + "m_source.l_linear.weight", _flat),
-                                              self.g(G + "m_source.l_linear.bias"))
-        har = ops.stft_magphase_lc_f32_gpu(har_src, 20, 5, cpad=32)  # [120 F + 1, 32]
-        self._keep("har_source", har_src)
-        self._keep("har", har)
-        for i, (k_up, u, k_noise) in enumerate(((20, 10, 7), (12, 6, 11))):
-            xs = ops.conv1d_lc_f32_gpu(har, self.g(G + f"noise_convs.{i}.weight", _w_lc_32),
-                                       self.g(G + f"noise_convs.{i}.bias"),
-                                       **({"stride": 6, "padding": 3} if i == 0 else {}))
-            self._keep(f"xs{i}_conv", xs)
-            xs = self.resblock1(xs, bank_d, f"{G}noise_res.{i}", k_noise)
-            self._keep(f"xs{i}", xs)
+        for i, (k_up, u) in enumerate(((20, 10), (12, 6))):
             x = ops.leaky_lc_f32_gpu(x, 0.1)
             y = ops.gemm_f32_gpu_mps(x, self.g(G + f"ups.{i}.weight", _w_convt))  # [Lin, K * Co]
-            x = ops.convt_gather_lc_f32_gpu(y, self.g(G + f"ups.{i}.bias"), k_up, u, (k_up - u) // 2, add=xs,
-                                            reflect_left=(i == 1))
+            ctx.join(self.streams[2 + i])
+            x = ops.convt_gather_lc_f32_gpu(y, self.g(G + f"ups.{i}.bias"), k_up, u, (k_up - u) // 2,
+                                            add=xs_stage[i], reflect_left=(i == 1))
             xst = ops.channel_stats_lc_f32_gpu(x)  # shared by the three resblocks' first AdaIN
-            rb = [self.resblock1(x, bank_d, f"{G}resblocks.{3 * i + j}", kk, xst) for j, kk in enumerate((3, 7, 11))]
+            # the three resblocks of a stage are independent: two run on side streams
+            rb = [None, None, None]
+            for j, kk in ((0, 3), (1, 7)):
+                with ctx.branch(self.streams[j], 1 + j):
+                    rb[j] = self.resblock1(x, bank_d, f"{G}resblocks.{3 * i + j}", kk, xst)
+            rb[2] = self.resblock1(x, bank_d, f"{G}resblocks.{3 * i + 2}", 11, xst)
+            ctx.join(self.streams[0])
+            ctx.join(self.streams[1])
             self._keep(f"ups{i}", x)
             x = ops.add3_scale_f32_gpu(rb[0], rb[1], rb[2], 1.0 / 3.0)
             self._keep(f"stage{i}", x)
