@@ -76,6 +76,25 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
                         void* stream);
 
+/* ---- fused batch-1 decode layer (backend ops; one layer's reference sequence gemv4*_f32_gpu ->
+ * attention_decode_split_f32_gpu -> gemv4 -> add_bias_layernorm2_f32_gpu, transformer_gpu.cpp:122-251,
+ * kokoro_tok.metal:36-117, in 5 launches instead of 13). GEMVs write row-slice partial sums part[S, N]
+ * (S = lk_hip_gemv_partial_slices(K)); the consumer reduces the slices in order. */
+int64_t lk_hip_gemv_partial_slices(int64_t k);
+/* xmode 0: x is a vector [K]; 1: x = gelu_tanh(sum of xpart[xslices, K] + xbias); 2: x = merge of decode
+ * chunk partials xpart[K / 64, chunks, 66]; 3: sum = (slices of xpart) + xbias + res is written to sum_out and
+ * x = LayerNorm(sum; gamma, beta, eps) (K <= 1024; xpart / xbias may be null). N % 4 == 0. */
+int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const float* xbias, int64_t xslices,
+                            int chunks, const float* res, const float* gamma, const float* beta, float* sum_out,
+                            float eps, const float* w, float* part, int64_t n, int64_t k, void* stream);
+/* q, k, v = slice sums of qkv_part[slices, 3D] + bias; writes row pos of kc / vc and the per-(head, 64-key
+ * chunk) partials chunk_part[heads, ceil(cap / 64), 66] = (max, sum, acc[64]); an invalid pos writes NaN. */
+int lk_hip_attention_decode_part_f32(const float* qkv_part, int64_t slices, float* kc, float* vc, const int64_t* pos,
+                                     const float* bias, float* chunk_part, int64_t cap, int heads, void* stream);
+/* sum = (slices of part[slices, N]) + bias + res; ln = LayerNorm(sum); one workgroup, N <= 1024 */
+int lk_hip_reduce_ln_f32(const float* part, int64_t slices, const float* bias, const float* res, const float* gamma,
+                         const float* beta, float* sum_out, float* ln_out, int64_t n, float eps, void* stream);
+
 /* ---- Kokoro frame-rate, channel-last (reference: kokoro_lc.metal:143-398) ---- */
 int lk_hip_channel_stats_lc_f32(const float* x, float* stats, int64_t l, int64_t c, void* stream);
 int lk_hip_adain_affine_lc_f32(const float* stats, const float* gb, float* affine, int64_t l, int64_t c,
