@@ -143,6 +143,24 @@ int lk_hip_stft_magphase_lc_f32(const float* x, float* out, int64_t s, int nfft,
 int lk_hip_conv1d_1ch_f32(const float* x, const float* w, const float* b, float* out, int64_t l, int k, int stride,
                           int pad, void* stream);
 
+/* ---- Winograd / Toom-Cook conv1d (reference: wino_tf*, wino_mm*, wino_adain_affine ops/winograd.py:128-218,
+ *      launchers winograd.cpp:73-160). U [A, n Ci, Co] and tr = [BT | AT] come from the host weight transform
+ *      (lokinfer_amd/winograd.py wino_weights); A = 6 (K = 3), 4 (K = 3, tile 2), 7 (K = 4..12, n = 2 or 3). ---- */
+/* x [L, C] -> V [d, A, rmax, C] (v_rows = d A rmax), of h = x (act 0), snake(affine(x), alpha) (1) or
+ * leaky(affine(x), slope) (2); padding % dilation == 0, C % 4 == 0 */
+int lk_hip_wino_tf_lc_f32(const float* x, const float* tr, const float* affine, const float* alpha, float* v,
+                          int64_t l, int64_t c, int dilation, int padding, int kernel, int tile, int64_t v_rows,
+                          int act, float slope, void* stream);
+/* out [Lo, Co] = (AT (V_xi U_xi) + bias [+ res]) * scale; Ci % 16 == 0, Co % 64 == 0; stats (optional)
+ * [d ceil(ceil(Lo / d) / 128), Co, 2]: (mean, M2) per 128-row chunk of each residue class */
+int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
+                          const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
+                          int dilation, int groups, int kernel, int tile, float scale, void* stream);
+/* stats [s, c, 2] of a length-row output -> af [3, c] = (mean, (1 + g) / sqrt(var + eps), b), gb [2 creal];
+ * channels >= creal get 0 */
+int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
+                                    int64_t creal, int dilation, int64_t length, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,7 @@ void registerFrontendKernels();
 void registerSequenceKernels();
 void registerSignalKernels();
 void registerDecodeFusedKernels();
+void registerWinogradKernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 

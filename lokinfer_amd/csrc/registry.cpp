@@ -479,6 +479,7 @@ static void registerAll() {
     registerSequenceKernels();
     registerSignalKernels();
     registerDecodeFusedKernels();
+    registerWinogradKernels();
     std::sort(names().begin(), names().end());
   });
 }

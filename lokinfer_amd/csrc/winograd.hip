@@ -1,0 +1,443 @@
+// The reference's Winograd / Toom-Cook 1-D conv op family (wino_tf[_snake|_leaky]_lc_f32_gpu,
+// wino_mm[_res][_stats]_lc_f32_gpu, wino_adain_affine_lc_f32_gpu: python/lokinfer/ops/winograd.py:120-218,
+// kernels/gpu/winograd.cpp:73-160 in lariaus/lokinfer), with the reference's operand layouts so that a graph built
+// on those ops runs unchanged:
+//   V  [d, A, rmax, C]: V[rho, xi, r, c] = sum_j BT[xi, j] h[rho + d (r M + j - pad / d), c], h = act(x), zero
+//                       outside the residue class's rows
+//   U  [A, N Ci, Co]   = G w per tap group (host wino_weights), tr = [BT (A x A) | AT (M x A)]
+//   out[o, co] = (b + sum_xi AT[j, xi] sum_{g, ci} V[rho, xi, t + g, ci] U[xi, g Ci + ci, co] [+ res]) * scale,
+//                o = rho + d (t M + j)
+//   stats [d chunks, Co, 2]: (mean, M2) of each 128 output rows of a residue class
+// This backend's own Kokoro graph runs the direct tap kernel with the same prologue fused (the Winograd form
+// measured no faster on CDNA4's f32 MFMA), so these kernels serve callers that build the reference's graph.
+//
+// wino_mm: one workgroup per (64 output channels, 64 tiles, residue); 4 waves in 2 x 2, each 32 tiles x 32
+// channels. Steps = points x 16-channel chunks; per step the V rows of the workgroup's tiles (+ N - 1 for the
+// group shift) are staged [row][4 slots] (swizzled by (row >> 2) & 3) and U's N x 16 rows k-major; the point's
+// GEMM accumulates over the groups with the A rows shifted by g, and after a point's last chunk AT[j, xi] folds
+// it into the M output accumulators.
+#include "common.h"
+#include "lokinfer_hip.h"
+
+#include <algorithm>
+#include <cstdint>
+
+namespace lkd {
+
+typedef float v16w __attribute__((ext_vector_type(16)));
+typedef float v4w __attribute__((ext_vector_type(4)));
+
+constexpr int kWinoRows = 128;  // output rows per statistics chunk
+
+// V[rho, xi, r, c4 .. c4 + 3]: one thread per (rho, r, c4). act: 0 none, 1 snake(affine), 2 leaky(affine).
+template <int M, int A>
+__global__ __launch_bounds__(256) void winoTfKernel(const float* __restrict__ x, const float* __restrict__ tr,
+                                                   const float* __restrict__ af, const float* __restrict__ alpha,
+                                                   float* __restrict__ v, int64_t l, int64_t c, int d, int padq,
+                                                   int64_t rmax, int act, float slope) {
+  const int64_t c4n = c / 4;
+  const int64_t total = static_cast<int64_t>(d) * rmax * c4n;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t c4 = i % c4n, rr = (i / c4n) % rmax;
+    const int rho = static_cast<int>(i / (c4n * rmax));
+    const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
+    const int64_t q0 = rr * M - padq;
+    v4w mean = {0.f, 0.f, 0.f, 0.f}, scale = {1.f, 1.f, 1.f, 1.f}, beta = {0.f, 0.f, 0.f, 0.f};
+    v4w al = {1.f, 1.f, 1.f, 1.f}, inv = {1.f, 1.f, 1.f, 1.f};
+    if (act != 0) {
+      mean = *reinterpret_cast<const v4w*>(af + 4 * c4);
+      scale = *reinterpret_cast<const v4w*>(af + c + 4 * c4);
+      beta = *reinterpret_cast<const v4w*>(af + 2 * c + 4 * c4);
+    }
+    if (act == 1) {
+      al = *reinterpret_cast<const v4w*>(alpha + 4 * c4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) inv[e] = 1.0f / al[e];
+    }
+    v4w raw[A];
+#pragma unroll
+    for (int j = 0; j < A; ++j) {
+      const int64_t q = q0 + j;
+      v4w h = {0.f, 0.f, 0.f, 0.f};
+      if (q >= 0 && q < lr) {
+        h = *reinterpret_cast<const v4w*>(x + (rho + q * d) * c + 4 * c4);
+        if (act == 1) {
+          h = (h - mean) * scale + beta;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = h[e] + inv[e] * snakeSinSq(al[e] * h[e]);
+        } else if (act == 2) {
+          h = (h - mean) * scale + beta;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = h[e] >= 0.0f ? h[e] : h[e] * slope;
+        }
+      }
+      raw[j] = h;
+    }
+#pragma unroll
+    for (int xi = 0; xi < A; ++xi) {
+      v4w o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < A; ++j) o += tr[xi * A + j] * raw[j];
+      *reinterpret_cast<v4w*>(v + ((static_cast<int64_t>(rho) * A + xi) * rmax + rr) * c + 4 * c4) = o;
+    }
+  }
+}
+
+struct WinoMmArgs {
+  const float* v;
+  const float* u;
+  const float* bias;
+  const float* res;
+  float* out;
+  const float* tr;
+  float* stats;
+  int64_t lo, ci, co, rmax, chunks;
+  int d;
+  float scale;
+};
+
+template <int M, int A, int N>
+__global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
+  constexpr int TT = 64;              // tiles per workgroup
+  constexpr int ROWS = TT + N - 1;    // staged V rows (group shift)
+  constexpr int LDB = 64 + 8;         // k-major U rows: the two lane halves read 4 rows = 32 banks apart
+  __shared__ v4w As[2][ROWS * 4];
+  __shared__ float Bs[2][N * 16 * LDB];
+  __shared__ float red[2][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
+  const int rho = blockIdx.z, d = p.d;
+  const int64_t lor = rho < p.lo ? (p.lo - rho + d - 1) / d : 0;  // output rows of this residue class
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * TT;
+  if (t0 * M >= lor) return;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int chunks = static_cast<int>(p.ci / 16);
+  const int steps = A * chunks;
+  const int64_t nci = static_cast<int64_t>(N) * p.ci;
+
+  // staging: A rows (ROWS x 4 slots) over 256 threads, U (N x 16 rows x 16 float4) over 256 threads
+  constexpr int AQ = ROWS * 4;
+  constexpr int BQ = N * 16 * 16;
+  constexpr int AS = (AQ + 255) / 256, BSL = BQ / 256;
+  v4w ra[AS], rb[BSL];
+  auto gload = [&](int s) {
+    const int xi = s / chunks, ch = s - xi * chunks;
+    const float* vx = p.v + (static_cast<int64_t>(rho) * A + xi) * p.rmax * p.ci + static_cast<int64_t>(ch) * 16;
+#pragma unroll
+    for (int i = 0; i < AS; ++i) {
+      const int idx = tid + 256 * i;
+      const int row = min(idx >> 2, ROWS - 1), slot = idx & 3;
+      const int64_t t = min<int64_t>(t0 + row, p.rmax - 1);  // rows past rmax only feed tiles never stored
+      ra[i] = *reinterpret_cast<const v4w*>(vx + t * p.ci + 4 * slot);
+    }
+    const float* ux = p.u + static_cast<int64_t>(xi) * nci * p.co + c0;
+#pragma unroll
+    for (int i = 0; i < BSL; ++i) {
+      const int idx = tid + 256 * i;
+      const int c4 = idx & 15, gk = idx >> 4, g = gk >> 4, k = gk & 15;
+      rb[i] = *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 + k) * p.co + 4 * c4);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AS; ++i) {
+      const int idx = tid + 256 * i;
+      if (AQ % 256 == 0 || idx < AQ) {
+        const int row = idx >> 2, slot = idx & 3;
+        As[buf][row * 4 + (slot ^ ((row >> 2) & 3))] = ra[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BSL; ++i) {
+      const int idx = tid + 256 * i;
+      const int c4 = idx & 15, gk = idx >> 4;
+      *reinterpret_cast<v4w*>(&Bs[buf][gk * LDB + 4 * c4]) = rb[i];
+    }
+  };
+
+  v16w acc, y[M];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < M; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) y[j][r] = 0.0f;
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int arow = 32 * wm + lr, bcol = 32 * wn + lr;
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    const int xi = s / chunks, ch = s - xi * chunks;
+    v4w af[N][2];
+    float bq[N][2][4];
+#pragma unroll
+    for (int g = 0; g < N; ++g) {
+      const int row = arow + g;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) af[g][h] = As[buf][row * 4 + ((2 * h + lk) ^ ((row >> 2) & 3))];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bq[g][h][q] = Bs[buf][(g * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
+    }
+    if (s + 1 < steps) gload(s + 1);
+#pragma unroll
+    for (int g = 0; g < N; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][h][q], bq[g][h][q], acc, 0, 0, 0);
+    if (ch == chunks - 1) {  // the point is complete: fold it into the output rows
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        const float at = p.tr[A * A + j * A + xi];
+        y[j] += at * acc;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    }
+    if (s + 1 < steps) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: register r = tile t0 + 32 wm + 8 (r / 4) + 4 lk + r % 4, channel c0 + bcol
+  const int64_t col = c0 + bcol;
+  const float bias = p.bias[col];
+#pragma unroll
+  for (int j = 0; j < M; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t t = t0 + 32 * wm + 8 * (r >> 2) + 4 * lk + (r & 3);
+      const int64_t uo = t * M + j;
+      float o = y[j][r] + bias;
+      if (p.res && uo < lor) o += p.res[(rho + uo * d) * p.co + col];
+      o *= p.scale;
+      y[j][r] = o;
+      if (uo < lor) p.out[(rho + uo * d) * p.co + col] = o;
+    }
+  if (p.stats) {
+    // chunks of 128 rows of this residue class: M = 4: 32 tiles = one wave row (chunk 2 by + wm), reduced in the
+    // wave; M = 2: 64 tiles = the workgroup (chunk by), the two wave rows combined through LDS.
+    constexpr int TPC = kWinoRows / M;  // tiles per chunk
+    const int64_t chunk = (t0 + 32 * wm) / TPC;
+    const int64_t cbase = chunk * kWinoRows;
+    const float nrows = static_cast<float>(min<int64_t>(kWinoRows, lor - cbase));
+    float s1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < M; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t uo = (t0 + 32 * wm + 8 * (r >> 2) + 4 * lk + (r & 3)) * M + j;
+        if (uo < lor) s1 += y[j][r];
+      }
+    s1 += __shfl_xor(s1, 32, 64);
+    if constexpr (TPC == 64) {
+      if (lk == 0) red[wm][bcol] = s1;
+      __syncthreads();
+      s1 = red[0][bcol] + red[1][bcol];
+      __syncthreads();
+    }
+    const float mean = s1 / nrows;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < M; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t uo = (t0 + 32 * wm + 8 * (r >> 2) + 4 * lk + (r & 3)) * M + j;
+        const float dv = y[j][r] - mean;
+        if (uo < lor) s2 += dv * dv;
+      }
+    s2 += __shfl_xor(s2, 32, 64);
+    if constexpr (TPC == 64) {
+      if (lk == 0) red[wm][bcol] = s2;
+      __syncthreads();
+      s2 = red[0][bcol] + red[1][bcol];
+    }
+    const bool writer = lk == 0 && (TPC == 32 || wm == 0) && nrows > 0.0f;
+    if (writer) {
+      float* st = p.stats + ((static_cast<int64_t>(rho) * p.chunks + chunk) * p.co + col) * 2;
+      st[0] = mean;
+      st[1] = s2;
+    }
+  }
+}
+
+// AdaIN affine from wino_mm statistics: chunk i = (rho, y) = (i / chunks, i % chunks) holds
+// clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows; combined exactly in double like adainAffineWaveKernel.
+__global__ __launch_bounds__(256) void winoAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
+                                                       float* __restrict__ af, int64_t l, int64_t c, int d,
+                                                       int64_t chunks, int64_t creal, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (ch >= c) return;
+  if (ch >= creal) {
+    if (lane == 0) af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
+    return;
+  }
+  const int64_t total = static_cast<int64_t>(d) * chunks;
+  auto count = [&](int64_t i) -> double {
+    const int64_t rho = i / chunks, yy = i % chunks;
+    const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
+    return static_cast<double>(min<int64_t>(max<int64_t>(lr - yy * kWinoRows, 0), kWinoRows));
+  };
+  double s = 0.0;
+  for (int64_t i = lane; i < total; i += 64) {
+    const double n = count(i);
+    if (n > 0.0) s += static_cast<double>(st[(i * c + ch) * 2]) * n;
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const double mean = s / static_cast<double>(l);
+  double m2 = 0.0;
+  for (int64_t i = lane; i < total; i += 64) {
+    const double n = count(i);
+    if (n > 0.0) {
+      const double dm = static_cast<double>(st[(i * c + ch) * 2]) - mean;
+      m2 += static_cast<double>(st[(i * c + ch) * 2 + 1]) + n * dm * dm;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) m2 += __shfl_xor(m2, o, 64);
+  if (lane == 0) {
+    const float var = static_cast<float>(m2 / static_cast<double>(l));
+    af[ch] = static_cast<float>(mean);
+    af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
+    af[2 * c + ch] = gb[creal + ch];
+  }
+}
+
+}  // namespace lkd
+
+extern "C" {
+
+int lk_hip_wino_tf_lc_f32(const float* x, const float* tr, const float* affine, const float* alpha, float* v,
+                          int64_t l, int64_t c, int dilation, int padding, int kernel, int tile, int64_t v_rows,
+                          int act, float slope, void* stream) {
+  if (c % 4 != 0 || dilation < 1 || padding % dilation != 0 || (tile != 2 && tile != 4)) return 1;
+  const int a = tile == 2 ? 4 : kernel == 3 ? 6 : 7;
+  if (v_rows % (static_cast<int64_t>(dilation) * a) != 0) return 1;
+  const int64_t rmax = v_rows / (static_cast<int64_t>(dilation) * a);
+  const int64_t total = static_cast<int64_t>(dilation) * rmax * (c / 4);
+  if (total == 0) return 0;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int padq = padding / dilation;
+  if (a == 4)
+    hipLaunchKernelGGL((lkd::winoTfKernel<2, 4>), dim3(blocks), dim3(256), 0, s, x, tr, affine, alpha, v, l, c,
+                       dilation, padq, rmax, act, slope);
+  else if (a == 6)
+    hipLaunchKernelGGL((lkd::winoTfKernel<4, 6>), dim3(blocks), dim3(256), 0, s, x, tr, affine, alpha, v, l, c,
+                       dilation, padq, rmax, act, slope);
+  else
+    hipLaunchKernelGGL((lkd::winoTfKernel<4, 7>), dim3(blocks), dim3(256), 0, s, x, tr, affine, alpha, v, l, c,
+                       dilation, padq, rmax, act, slope);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
+                          const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
+                          int dilation, int groups, int kernel, int tile, float scale, void* stream) {
+  const int a = tile == 2 ? 4 : kernel == 3 ? 6 : 7;
+  if (ci % 16 != 0 || co % 64 != 0 || dilation < 1 || groups < 1 || groups > 3 || lo < 1) return 1;
+  if ((tile == 2 && groups != 1) || (a == 6 && groups != 1) || (a == 7 && groups < 2)) return 1;
+  const int64_t rmax = v_rows / (static_cast<int64_t>(dilation) * a);
+  const int m = tile;
+  const int64_t tiles = ((lo + dilation - 1) / dilation + m - 1) / m;  // residue class 0 is the longest
+  lkd::WinoMmArgs p{v, u, bias, res, out, tr, stats, lo, ci, co, rmax,
+                    ((lo + dilation - 1) / dilation + lkd::kWinoRows - 1) / lkd::kWinoRows, dilation, scale};
+  if (rmax < tiles + groups - 1) return 1;  // V must hold every tile and its group shifts
+  const dim3 grid(static_cast<unsigned>(co / 64), static_cast<unsigned>((tiles + 63) / 64),
+                  static_cast<unsigned>(dilation));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a == 4)
+    hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1>), grid, dim3(256), 0, s, p);
+  else if (a == 6)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1>), grid, dim3(256), 0, s, p);
+  else if (groups == 2)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3>), grid, dim3(256), 0, s, p);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
+                                    int64_t creal, int dilation, int64_t length, float eps, void* stream) {
+  if (dilation < 1 || s % dilation != 0 || length < 1 || creal > c) return 1;
+  hipLaunchKernelGGL(lkd::winoAffineKernel, dim3(lkh::ceilDiv(c, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     stats, gb, af, length, c, dilation, s / dilation, creal, eps);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"
+
+namespace lkh {
+
+namespace {
+
+// wino_tf[_snake|_leaky]_lc_f32_gpu. ptrs: x, tr, [affine], [alpha], v. ints: x(L, C), tr(T), [affine(3, C)],
+// [alpha(C)], v(R, C), dilation, groups, kernel, padding, tile; floats (leaky): slope.
+template <int ACT>
+void runWinoTf(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t l = a.ints[0], c = a.ints[1];
+  const int o = ACT == 1 ? 6 : ACT == 2 ? 5 : 3;  // v dims
+  const int64_t vr = a.ints[o];
+  const int d = static_cast<int>(a.ints[o + 2]), k = static_cast<int>(a.ints[o + 4]);
+  const int pad = static_cast<int>(a.ints[o + 5]), tile = static_cast<int>(a.ints[o + 6]);
+  LK_REQUIRE(ctx, a.ints[o + 1] == c, "wino_tf: v must be f32[R, C]");
+  const int vp = ACT == 1 ? 4 : ACT == 2 ? 3 : 2;
+  const float slope = ACT == 2 && a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 0.0f;
+  if (lk_hip_wino_tf_lc_f32(P<float>(a, 0), P<float>(a, 1), ACT ? P<float>(a, 2) : nullptr,
+                            ACT == 1 ? P<float>(a, 3) : nullptr, P<float>(a, vp), l, c, d, pad, k, tile, vr, ACT, slope,
+                            ctx.stream))
+    ctx.error = "wino_tf: invalid configuration";
+}
+
+// wino_mm[_res][_stats]_lc_f32_gpu. ptrs: v, u, b, tr, x, [res], out, [stats]. ints: v(R, Ci), u(A, N Ci, Co),
+// b(Co), tr(T), x(L, Ci), [res(Lo, Co)], out(Lo, Co), [stats(d chunks, Co, 2)], dilation, groups, kernel,
+// padding, tile; floats: [oscale].
+template <bool RES, bool STATS>
+void runWinoMm(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t vr = a.ints[0], ci = a.ints[1], co = a.ints[4];
+  const int o = RES ? 11 : 9;
+  const int at = o + 2 + (STATS ? 3 : 0);
+  const int64_t lo = a.ints[o];
+  const int d = static_cast<int>(a.ints[at]), groups = static_cast<int>(a.ints[at + 1]);
+  const int k = static_cast<int>(a.ints[at + 2]), tile = static_cast<int>(a.ints[at + 4]);
+  LK_REQUIRE(ctx, a.ints[o + 1] == co && a.ints[3] == groups * ci, "wino_mm: u must be f32[A, N Ci, Co]");
+  const int outp = RES ? 6 : 5;
+  const float scale = RES && a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1.0f;
+  if (lk_hip_wino_mm_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), RES ? P<float>(a, 5) : nullptr,
+                            P<float>(a, outp), P<float>(a, 3), STATS ? P<float>(a, outp + 1) : nullptr, vr, ci, co, lo,
+                            d, groups, k, tile, scale, ctx.stream))
+    ctx.error = "wino_mm: invalid configuration";
+}
+
+// wino_adain_affine_lc_f32_gpu. ptrs: stats, gb, af. ints: stats(S, C, 2), gb(2 Creal), af(3, C), dilation,
+// length; floats: eps.
+void runWinoAffine(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t s = a.ints[0], c = a.ints[1], g2 = a.ints[3];
+  const int d = static_cast<int>(a.ints[6]);
+  const int64_t length = a.ints[7];
+  const float eps = a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1e-5f;
+  LK_REQUIRE(ctx, a.ints[2] == 2 && g2 % 2 == 0 && g2 / 2 <= c, "wino_adain_affine: bad stats / gb");
+  if (lk_hip_wino_adain_affine_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), s, c, g2 / 2, d, length, eps,
+                                      ctx.stream))
+    ctx.error = "wino_adain_affine: invalid configuration";
+}
+
+}  // namespace
+
+void registerWinogradKernels() {
+  const Device G = Device::Gpu;
+  registerKernel({"wino_tf_lc_f32_gpu", G, runWinoTf<0>, 2, 1});
+  registerKernel({"wino_tf_snake_lc_f32_gpu", G, runWinoTf<1>, 4, 1});
+  registerKernel({"wino_tf_leaky_lc_f32_gpu", G, runWinoTf<2>, 3, 1});
+  registerKernel({"wino_mm_lc_f32_gpu", G, runWinoMm<false, false>, 5, 1});
+  registerKernel({"wino_mm_res_lc_f32_gpu", G, runWinoMm<true, false>, 6, 1});
+  registerKernel({"wino_mm_stats_lc_f32_gpu", G, runWinoMm<false, true>, 5, 2});
+  registerKernel({"wino_mm_res_stats_lc_f32_gpu", G, runWinoMm<true, true>, 6, 2});
+  registerKernel({"wino_adain_affine_lc_f32_gpu", G, runWinoAffine, 2, 1});
+}
+
+}  // namespace lkh

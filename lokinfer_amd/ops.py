@@ -14,6 +14,7 @@ import torch
 
 from . import trace as _trace
 from .runtime import GpuContext
+from . import winograd as _wino
 from .tensor import Tensor, f32, i64
 
 STAT_CHUNK = 128
@@ -260,6 +261,108 @@ def conv1d_act_lc_f32_gpu(x, w, b, affine, alpha=None, act="snake", slope=0.0, r
         return _launch(f"conv1d_act_lc{sfx}_f32_gpu", [x, w, b, affine, alpha], shapes, attrs)
     check(tuple(residual.shape) == s, "residual shape mismatch")
     return _launch(f"conv1d_act_lc_res{sfx}_f32_gpu", [x, w, b, affine, alpha, residual], shapes, attrs)
+
+
+# ---- Winograd / Toom-Cook conv1d (reference ops/winograd.py:98-247) ------------------------------------------
+# x [L, Ci] -> V [d * A * rmax, Ci] (input transform, activation fused) -> per point a GEMM V_xi . U_xi over
+# (group, ci) with the AT output transform, bias, [residual * scale] and [128-row channel statistics] in the
+# epilogue. U and tr come from winograd.wino_weights(w) on the host, once per weight.
+
+def _wino_lo(x, kernel, dilation, padding):
+    lo = x.shape[0] + 2 * padding - dilation * (kernel - 1)
+    check(lo >= 1, "empty conv output")
+    return lo
+
+
+def _wino_attrs_ok(x, dilation, groups, kernel, padding, tile):
+    _f32(x, rank=2)
+    check(x.shape[1] % 16 == 0, "Ci must be a multiple of 16")
+    check((tile == _wino.TILE or (tile == 2 and kernel == 3)) and _wino.variant(kernel)[1] == groups,
+          "groups / tile don't match the kernel size")
+    check(dilation >= 1 and padding >= 0 and padding % dilation == 0, "padding must be a multiple of dilation")
+
+
+def _wino_v_shape(x, dilation, groups, kernel, padding, tile):
+    _wino_attrs_ok(x, dilation, groups, kernel, padding, tile)
+    lo = _wino_lo(x, kernel, dilation, padding)
+    return (_wino.tiles_rows(lo, dilation, groups, tile, kernel), x.shape[1])
+
+
+def wino_tf_lc_f32_gpu(x, tr, dilation, groups, kernel, padding, tile, affine=None, alpha=None, slope=None):
+    """Input transform V[rho, xi, r, c] = sum_j BT[xi, j] h[rho + d (r M + j) - pad] of h = x, or of snake(affine(x))
+    (affine and alpha) / leaky(affine(x), slope) (affine and slope). Reference winograd.py:128-154."""
+    s = _wino_v_shape(x, dilation, groups, kernel, padding, tile)
+    a = _wino.alpha_of(kernel, tile)
+    _f32(tr, rank=1)
+    check(tr.shape[0] == a * (a + tile), "bad transform table")
+    attrs = dict(dilation=int(dilation), groups=int(groups), kernel=int(kernel), padding=int(padding), tile=int(tile))
+    if affine is None:
+        return _launch("wino_tf_lc_f32_gpu", [x, tr], [s], attrs)
+    _f32(affine, rank=2)
+    check(affine.shape == (3, x.shape[1]), "affine must be f32[3, C]")
+    if slope is not None:
+        check(alpha is None, "give either alpha (snake) or slope (leaky)")
+        return _launch("wino_tf_leaky_lc_f32_gpu", [x, tr, affine], [s], dict(attrs, slope=float(slope)))
+    check(alpha is not None and alpha.shape == (x.shape[1],), "alpha must be f32[C]")
+    return _launch("wino_tf_snake_lc_f32_gpu", [x, tr, affine, alpha], [s], attrs)
+
+
+def wino_mm_lc_f32_gpu(v, u, b, tr, x, dilation, groups, kernel, padding, tile, residual=None, out_scale=1.0,
+                       stats=False):
+    """Per-point GEMM + AT output transform + bias [+ residual * out_scale] [+ per-128-row channel (mean, M2)],
+    out [Lo, Co], stats [d * chunks, Co, 2]. Reference winograd.py:157-202."""
+    _wino_attrs_ok(x, dilation, groups, kernel, padding, tile)
+    _f32(v, rank=2)
+    _f32(u, rank=3)
+    _f32(b, tr, rank=1)
+    a, nci, co = u.shape
+    check(a == _wino.alpha_of(kernel, tile), "u must come from wino_weights for this kernel size")
+    check(nci == groups * x.shape[1], "u must be f32[A, groups * Ci, Co]")
+    check(co % 64 == 0, "Co must be a multiple of 64")
+    check(b.shape[0] == co, "bias must be f32[Co]")
+    check(tr.shape[0] == a * (a + tile), "bad transform table")
+    check(tuple(v.shape) == _wino_v_shape(x, dilation, groups, kernel, padding, tile), "v must be wino_tf of x")
+    lo = _wino_lo(x, kernel, dilation, padding)
+    shapes = [(lo, co)]
+    if stats:
+        shapes.append((_wino.stats_chunks(lo, dilation) * dilation, co, 2))
+    attrs = dict(dilation=int(dilation), groups=int(groups), kernel=int(kernel), padding=int(padding), tile=int(tile))
+    sfx = "_stats" if stats else ""
+    if residual is None:
+        check(out_scale == 1.0, "out_scale needs a residual")
+        return _launch(f"wino_mm{sfx}_lc_f32_gpu", [v, u, b, tr, x], shapes, attrs)
+    _f32(residual, rank=2)
+    check(tuple(residual.shape) == (lo, co), "residual shape mismatch")
+    return _launch(f"wino_mm_res{sfx}_lc_f32_gpu", [v, u, b, tr, x, residual], shapes,
+                   dict(attrs, oscale=float(out_scale)))
+
+
+def wino_adain_affine_lc_f32_gpu(stats, gb, length, dilation=1, eps=1e-5):
+    """AdaIN affine f32[3, C] = (mean, (1 + g) / std, b) from the Winograd epilogue statistics over `length` output
+    rows (chunk i = (rho, y), rows clamp(ceil((length - rho) / d) - 128 y, 0, 128)); channels >= Creal get 0.
+    Reference winograd.py:204-218."""
+    _f32(stats, rank=3)
+    _f32(gb, rank=1)
+    check(stats.shape[2] == 2, "stats must be f32[S, C, 2]")
+    check(gb.shape[0] % 2 == 0 and gb.shape[0] // 2 <= stats.shape[1], "gb must be f32[2 Creal] with Creal <= C")
+    check(stats.shape[0] == _wino.stats_chunks(int(length), dilation) * dilation, "stats chunks don't match length")
+    return _launch("wino_adain_affine_lc_f32_gpu", [stats, gb], [(3, stats.shape[1])],
+                   dict(dilation=int(dilation), eps=float(eps), length=int(length)))
+
+
+def conv1d_wino_lc_f32_gpu(x, u, b, tr, kernel, residual=None, out_scale=1.0, padding=0, dilation=1, affine=None,
+                           alpha=None, slope=None, stats=False):
+    """(conv1d(h, w) + b [+ residual]) * out_scale with (u, tr) = winograd.wino_weights(w), h = x, or
+    snake(affine(x), alpha), or leaky(affine(x), slope); stats=True also returns the output's channel statistics
+    for wino_adain_affine_lc_f32_gpu. Two launches: transform, GEMM. Reference winograd.py:221-247."""
+    kernel = int(kernel)
+    _, n = _wino.variant(kernel)
+    tile = 2 if u.shape[0] == 4 else _wino.TILE
+    attrs = dict(dilation=int(dilation), groups=n, kernel=kernel, padding=int(padding), tile=tile)
+    if affine is None:
+        check(alpha is None and slope is None, "alpha / slope need an affine")
+    v = wino_tf_lc_f32_gpu(x, tr, affine=affine, alpha=alpha, slope=slope, **attrs)
+    return wino_mm_lc_f32_gpu(v, u, b, tr, x, residual=residual, out_scale=out_scale, stats=stats, **attrs)
 
 
 # ---- transformer --------------------------------------------------------------------------------------------
