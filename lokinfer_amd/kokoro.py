@@ -15,8 +15,10 @@ Stages (channel-last [L, C] at frame rate, [T, C] at token rate):
                                                                                           (model.py:479-508)
 Where the reference keeps work on the host CPU (LSTMs, embeddings, alignment, harmonic source, STFT, strided and
 single-channel convs, the ALBERT embeddings) this backend runs device kernels, so a forward is one captured HIP
-graph with no host round trips. Every conv is one implicit-GEMM MFMA kernel with the AdaIN affine and Snake /
-leaky activation fused into its operand staging (the reference fuses them into its Winograd input transform).
+graph with no host round trips. The generator's Snake resblock convs run as the Winograd pair (input transform
+with AdaIN affine + Snake fused, per-point MFMA GEMM with the channel statistics in its epilogue) when the grid
+is large enough, as the reference does; every other conv is one implicit-GEMM MFMA kernel with the affine and
+activation fused into its operand staging.
 
 The durations predictor (predictor.lstm + duration_proj) is not computed: with forced durations its output is
 unused, and the reference's dead-code pass removes it from the compiled graph as well.
@@ -28,12 +30,14 @@ import math
 import numpy as np
 import torch
 
-from . import ops
+from . import ops, winograd
 from .compiler import compile as lk_compile
 from .runtime import GpuContext
 from .tensor import Tensor, from_numpy
 
 SQRT1_2 = 1.0 / math.sqrt(2.0)
+# Winograd conv when its GEMM grid has at least this many 64 x 64 workgroups (below, the tap conv is faster)
+WINO_MIN_GRID = 256
 
 
 def _pad16(n: int) -> int:
@@ -134,8 +138,10 @@ class KokoroGpu:
         off, n = offs[prefix]
         return ops.view(vec, [n], off)
 
-    def affine(self, x: Tensor, bank, prefix: str, stats: Tensor | None = None) -> Tensor:
+    def affine(self, x: Tensor, bank, prefix: str, stats: Tensor | None = None, dilation: int = 1) -> Tensor:
         st = ops.channel_stats_lc_f32_gpu(x) if stats is None else stats
+        if dilation > 1:  # statistics of a dilated Winograd conv: chunks per residue class
+            return ops.wino_adain_affine_lc_f32_gpu(st, self.style(bank, prefix), x.shape[0], dilation=dilation)
         return ops.adain_affine_lc_f32_gpu(st, self.style(bank, prefix), length=x.shape[0])
 
     def resblk(self, x: Tensor, bank, p: str, cin: int, cout: int, upsample: bool) -> Tensor:
@@ -160,19 +166,38 @@ class KokoroGpu:
         return ops.conv1d_act_lc_f32_gpu(h, self.g(p + ".conv2.weight", _w_lc), self.g(p + ".conv2.bias"), af2,
                                          act="leaky", slope=0.2, padding=1, residual=sc, out_scale=SQRT1_2)
 
+    def wino(self, key: str):
+        """(U, tr) of conv weight `key` for the Winograd ops, transformed once on the host."""
+        k = key + "#wino"
+        if k not in self._g:
+            u, tr = winograd.wino_weights(self.sd[key])
+            self._g[k] = (from_numpy(u, device="gpu", copy=True), from_numpy(tr, device="gpu", copy=True))
+        return self._g[k]
+
+    def snake_conv(self, x: Tensor, p: str, af: Tensor, alpha: Tensor, k: int, d: int, residual=None, stats=False):
+        """conv(snake(affine(x))) [+ residual] with stats of the output, on the Winograd pair when its GEMM grid
+        fills the chip (>= 256 workgroups of 64 tiles x 64 channels), else on the tap conv. Returns (y, stats,
+        stats_dilation): Winograd statistics are per residue class of the dilation."""
+        co = self.sd[p + ".weight"].shape[0]
+        lo = x.shape[0]
+        if (co // 64) * -(-(-(-lo // d)) // 256) * d >= WINO_MIN_GRID:
+            u, tr = self.wino(p + ".weight")
+            y = ops.conv1d_wino_lc_f32_gpu(x, u, self.g(p + ".bias"), tr, k, residual=residual, padding=d * (k - 1) // 2,
+                                           dilation=d, affine=af, alpha=alpha, stats=stats)
+            return (y + (d,)) if stats else (y, None, 1)
+        y = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".weight", _w_lc), self.g(p + ".bias"), af, alpha, act="snake",
+                                      padding=d * (k - 1) // 2, dilation=d, residual=residual, stats=stats)
+        return (y + (1,)) if stats else (y, None, 1)
+
     def resblock1(self, x: Tensor, bank, p: str, k: int, x_stats: Tensor | None = None) -> Tensor:
-        """AdaINResBlock1 (Snake), dilations 1, 3, 5; every conv has AdaIN affine + Snake fused in its staging."""
-        st = ops.channel_stats_lc_f32_gpu(x) if x_stats is None else x_stats
+        """AdaINResBlock1 (Snake), dilations 1, 3, 5; every conv has AdaIN affine + Snake fused in its prologue."""
+        st, sd = (ops.channel_stats_lc_f32_gpu(x) if x_stats is None else x_stats), 1
         for j, d in enumerate((1, 3, 5)):
-            af = self.affine(x, bank, f"{p}.adain1.{j}.fc", st)
-            h, hst = ops.conv1d_act_lc_f32_gpu(x, self.g(f"{p}.convs1.{j}.weight", _w_lc),
-                                               self.g(f"{p}.convs1.{j}.bias"), af, self.g(f"{p}.alpha1.{j}", _flat),
-                                               act="snake", padding=d * (k - 1) // 2, dilation=d, stats=True)
-            af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc", hst)
-            y = ops.conv1d_act_lc_f32_gpu(h, self.g(f"{p}.convs2.{j}.weight", _w_lc), self.g(f"{p}.convs2.{j}.bias"),
-                                          af2, self.g(f"{p}.alpha2.{j}", _flat), act="snake", padding=(k - 1) // 2,
-                                          residual=x, stats=j < 2)
-            x, st = y if j < 2 else (y, None)
+            af = self.affine(x, bank, f"{p}.adain1.{j}.fc", st, sd)
+            h, hst, hd = self.snake_conv(x, f"{p}.convs1.{j}", af, self.g(f"{p}.alpha1.{j}", _flat), k, d, stats=True)
+            af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc", hst, hd)
+            x, st, sd = self.snake_conv(h, f"{p}.convs2.{j}", af2, self.g(f"{p}.alpha2.{j}", _flat), k, 1, residual=x,
+                                        stats=j < 2)
         return x
 
     def noise_block(self, har: Tensor, bank, i: int) -> Tensor:
