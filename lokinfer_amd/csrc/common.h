@@ -107,7 +107,6 @@ __device__ __forceinline__ float waveMax(float v) {
   return v;
 }
 
-// torch's gelu(approximate="tanh") in torch's op order: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
 // sin(y)^2 for the Snake activation x + sin(a x)^2 / a. sin^2 has period pi, so y is reduced to
 // r = y - n pi, |r| <= pi / 2, by Cody-Waite with pi split into its nearest float and the remainder
 // (pi - 3.14159274f = -8.74227766e-8f), each product formed by one fma; sin(r) then comes from the hardware
@@ -121,9 +120,88 @@ __device__ __forceinline__ float snakeSinSq(float y) {
   return sn * sn;
 }
 
+// torch's gelu(approximate="tanh") in torch's op order: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
 __device__ __forceinline__ float geluTanh(float v) {
   const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
   return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+// AdaIN affine af [3, C] = (mean, (1 + g) / sqrt(var + eps), b) from per-chunk (mean, M2) statistics st [S, C, 2]
+// of an L-row tensor; gb [2 creal]; channels >= creal get 0. Chunk i = (rho, y) = (i / chunks, i % chunks) holds
+// the rows of residue class rho of the dilation d from 128 y on: clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows
+// (d = 1: the plain 128-row chunks; chunks with no rows are never read). Two passes in double, as instance norm
+// with a biased variance: mean = sum n_i m_i / L, then M2 = sum (M2_i + n_i (m_i - mean)^2), var = M2 / L.
+// Workgroup of 256 = 16 channels x 16 chunk slices: a slice row reads 16 consecutive channels (128 B), the
+// slices' partial sums merge through LDS in a fixed order. Small workgroups, so the kernel still schedules
+// while long conv kernels hold most of the chip on other streams.
+__device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, const float* __restrict__ gb,
+                                                  float* __restrict__ af, int64_t l, int64_t c, int d,
+                                                  int64_t chunks, int64_t creal, float eps) {
+  __shared__ double red[16][16];
+  const int cl = threadIdx.x & 15, sl = threadIdx.x >> 4;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 16 + cl;
+  const bool live = ch < creal && ch < c;
+  const int64_t total = static_cast<int64_t>(d) * chunks;
+  const float2* sp = reinterpret_cast<const float2*>(st);
+  // rows of chunk (rho, yy)
+  auto rows = [&](int64_t rho, int64_t yy) -> double {
+    const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
+    return static_cast<double>(min<int64_t>(max<int64_t>(lr - yy * 128, 0), 128));
+  };
+  double s = 0.0;
+  if (live) {
+    int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
+#pragma unroll 4
+    for (int64_t i = sl; i < total; i += 16) {
+      const double n = rows(rho, yy);
+      if (n > 0.0) s += static_cast<double>(sp[i * c + ch].x) * n;
+      yy += 16;
+      while (yy >= chunks) {
+        yy -= chunks;
+        ++rho;
+      }
+    }
+  }
+  red[sl][cl] = s;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += red[w][cl];
+  const double mean = tot / static_cast<double>(l);
+  __syncthreads();
+  double m2 = 0.0;
+  if (live) {
+    int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
+#pragma unroll 4
+    for (int64_t i = sl; i < total; i += 16) {
+      const double n = rows(rho, yy);
+      if (n > 0.0) {
+        const float2 v = sp[i * c + ch];
+        const double dm = static_cast<double>(v.x) - mean;
+        m2 += static_cast<double>(v.y) + n * dm * dm;
+      }
+      yy += 16;
+      while (yy >= chunks) {
+        yy -= chunks;
+        ++rho;
+      }
+    }
+  }
+  red[sl][cl] = m2;
+  __syncthreads();
+  if (sl == 0 && ch < c) {
+    if (!live) {
+      af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
+    } else {
+      double M2 = 0.0;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) M2 += red[w][cl];
+      const float var = static_cast<float>(M2 / static_cast<double>(l));
+      af[ch] = static_cast<float>(mean);
+      af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
+      af[2 * c + ch] = gb[creal + ch];
+    }
+  }
 }
 
 }  // namespace lkd

@@ -59,105 +59,11 @@ __global__ __launch_bounds__(256) void statsKernel(const float* __restrict__ x, 
   }
 }
 
-// One wave per channel: the chunk partials are combined exactly in double (mean = sum n_i m_i / N,
-// M2 = sum M2_i + sum n_i (m_i - mean)^2), then var = M2 / N (biased, like instance norm). Used when a channel
-// has few chunks.
-__global__ __launch_bounds__(256) void adainAffineWaveKernel(const float* __restrict__ st,
-                                                            const float* __restrict__ gb, float* __restrict__ af,
-                                                            int64_t l, int64_t c, int64_t creal, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (ch >= c) return;
-  if (ch >= creal) {
-    if (lane == 0) af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
-    return;
-  }
-  const int64_t chunks = (l + kStatChunk - 1) / kStatChunk;
-  const float2* sp = reinterpret_cast<const float2*>(st);
-  double s = 0.0;
-#pragma unroll 4
-  for (int64_t i = lane; i < chunks; i += 64) {
-    const double n = static_cast<double>(min<int64_t>(kStatChunk, l - i * kStatChunk));
-    s += static_cast<double>(sp[i * c + ch].x) * n;
-  }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  const double mean = s / static_cast<double>(l);
-  double m2 = 0.0;
-#pragma unroll 4
-  for (int64_t i = lane; i < chunks; i += 64) {
-    const double n = static_cast<double>(min<int64_t>(kStatChunk, l - i * kStatChunk));
-    const float2 v = sp[i * c + ch];
-    const double dm = static_cast<double>(v.x) - mean;
-    m2 += static_cast<double>(v.y) + n * dm * dm;
-  }
-  for (int o = 32; o > 0; o >>= 1) m2 += __shfl_xor(m2, o, 64);
-  if (lane == 0) {
-    const float var = static_cast<float>(m2 / static_cast<double>(l));
-    af[ch] = static_cast<float>(mean);
-    af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
-    af[2 * c + ch] = gb[creal + ch];
-  }
-}
-
-// One 1024-thread workgroup per channel. Each of its 16 waves reduces a contiguous range of the chunk partials to
-// (n_s, mean_s, M2_s) in double (two passes over its range: mean_s = sum n_i m_i / n_s,
-// M2_s = sum M2_i + sum n_i (m_i - mean_s)^2); the ranges then merge in a fixed order by Chan's parallel formula
-// (mean = sum n_s mean_s / N, M2 = sum M2_s + sum n_s (mean_s - mean)^2), and var = M2 / N (biased, like
-// instance norm). Splitting a channel's 2k+ chunks over 16 waves keeps the long generator convs from being
-// load-latency bound.
-__global__ __launch_bounds__(1024) void adainAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
+// AdaIN affine from channel_stats_lc statistics (128-row chunks), 16 channels per workgroup.
+__global__ __launch_bounds__(256) void adainAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
                                                          float* __restrict__ af, int64_t l, int64_t c, int64_t creal,
                                                          float eps) {
-  __shared__ double part[16][3];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t ch = blockIdx.x;
-  if (ch >= creal) {
-    if (threadIdx.x == 0) af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
-    return;
-  }
-  const int64_t chunks = (l + kStatChunk - 1) / kStatChunk;
-  const int64_t per = (chunks + 15) / 16;
-  const int64_t i0 = min<int64_t>(chunks, wv * per), i1 = min<int64_t>(chunks, i0 + per);
-  const float2* sp = reinterpret_cast<const float2*>(st);
-  double s = 0.0, ns = 0.0;
-  for (int64_t i = i0 + lane; i < i1; i += 64) {
-    const double n = static_cast<double>(min<int64_t>(kStatChunk, l - i * kStatChunk));
-    s += static_cast<double>(sp[i * c + ch].x) * n;
-    ns += n;
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    s += __shfl_xor(s, o, 64);
-    ns += __shfl_xor(ns, o, 64);
-  }
-  const double ms = ns > 0.0 ? s / ns : 0.0;
-  double m2 = 0.0;
-  for (int64_t i = i0 + lane; i < i1; i += 64) {
-    const double n = static_cast<double>(min<int64_t>(kStatChunk, l - i * kStatChunk));
-    const float2 v = sp[i * c + ch];
-    const double dm = static_cast<double>(v.x) - ms;
-    m2 += static_cast<double>(v.y) + n * dm * dm;
-  }
-  for (int o = 32; o > 0; o >>= 1) m2 += __shfl_xor(m2, o, 64);
-  if (lane == 0) {
-    part[wv][0] = ns;
-    part[wv][1] = ms;
-    part[wv][2] = m2;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double tot = 0.0;
-    for (int w = 0; w < 16; ++w) tot += part[w][0] * part[w][1];
-    const double mean = tot / static_cast<double>(l);
-    double M2 = 0.0;
-    for (int w = 0; w < 16; ++w) {
-      const double dm = part[w][1] - mean;
-      M2 += part[w][2] + part[w][0] * dm * dm;
-    }
-    const float var = static_cast<float>(M2 / static_cast<double>(l));
-    af[ch] = static_cast<float>(mean);
-    af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
-    af[2 * c + ch] = gb[creal + ch];
-  }
+  adainAffineSlices(st, gb, af, l, c, 1, (l + kStatChunk - 1) / kStatChunk, creal, eps);
 }
 
 // act: 1 snake, 2 leaky (0: affine only).
@@ -359,13 +265,8 @@ int lk_hip_channel_stats_lc_f32(const float* x, float* st, int64_t l, int64_t c,
 int lk_hip_adain_affine_lc_f32(const float* st, const float* gb, float* af, int64_t l, int64_t c, int64_t creal,
                                float eps, void* stream) {
   if (l <= 0 || c <= 0 || creal > c) return 1;
-  const int64_t chunks = (l + lkd::kStatChunk - 1) / lkd::kStatChunk;
-  if (chunks >= 1024)  // the long generator tensors: 16 waves per channel
-    hipLaunchKernelGGL(lkd::adainAffineKernel, dim3(static_cast<unsigned>(c)), dim3(1024), 0,
-                       static_cast<hipStream_t>(stream), st, gb, af, l, c, creal, eps);
-  else
-    hipLaunchKernelGGL(lkd::adainAffineWaveKernel, dim3(lkh::ceilDiv(c, 4)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), st, gb, af, l, c, creal, eps);
+  hipLaunchKernelGGL(lkd::adainAffineKernel, dim3(lkh::ceilDiv(c, 16)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), st, gb, af, l, c, creal, eps);
   LK_RET;
 }
 

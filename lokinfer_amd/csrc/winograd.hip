@@ -120,8 +120,9 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   constexpr int AQ = ROWS * 4;
   constexpr int BQ = N * 16 * 16;
   constexpr int AS = (AQ + 255) / 256, BSL = BQ / 256;
-  v4w ra[AS], rb[BSL];
-  auto gload = [&](int s) {
+  // two register sets: step t's operands live in set t & 1, loaded two steps ahead of their LDS store
+  v4w ra0[AS], rb0[BSL], ra1[AS], rb1[BSL];
+  auto gload = [&](int s, v4w(&ra)[AS], v4w(&rb)[BSL]) {
     const int xi = s / chunks, ch = s - xi * chunks;
     const float* vx = p.v + (static_cast<int64_t>(rho) * A + xi) * p.rmax * p.ci + static_cast<int64_t>(ch) * 16;
 #pragma unroll
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
       rb[i] = *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 + k) * p.co + 4 * c4);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const v4w(&ra)[AS], const v4w(&rb)[BSL]) {
 #pragma unroll
     for (int i = 0; i < AS; ++i) {
       const int idx = tid + 256 * i;
@@ -164,11 +165,10 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) y[j][r] = 0.0f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int arow = 32 * wm + lr, bcol = 32 * wn + lr;
-  for (int s = 0; s < steps; ++s) {
+  // one step: MFMAs on LDS buffer s & 1; loads step s + 2 into (lra, lrb) = set s & 1 (its step s is already in
+  // LDS), stores step s + 1 from (sra, srb) = set (s + 1) & 1 into the other buffer
+  auto step = [&](int s, v4w(&lra)[AS], v4w(&lrb)[BSL], const v4w(&sra)[AS], const v4w(&srb)[BSL]) {
     const int buf = s & 1;
     const int xi = s / chunks, ch = s - xi * chunks;
     v4w af[N][2];
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) bq[g][h][q] = Bs[buf][(g * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
     }
-    if (s + 1 < steps) gload(s + 1);
+    if (s + 2 < steps) gload(s + 2, lra, lrb);
 #pragma unroll
     for (int g = 0; g < N; ++g)
 #pragma unroll
@@ -199,8 +199,17 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
     }
-    if (s + 1 < steps) sstore(buf ^ 1);
+    if (s + 1 < steps) sstore(buf ^ 1, sra, srb);
     __syncthreads();
+  };
+
+  gload(0, ra0, rb0);
+  sstore(0, ra0, rb0);
+  if (steps > 1) gload(1, ra1, rb1);
+  __syncthreads();
+  for (int s = 0; s < steps; s += 2) {
+    step(s, ra0, rb0, ra1, rb1);
+    if (s + 1 < steps) step(s + 1, ra1, rb1, ra0, rb0);
   }
 
   // epilogue: register r = tile t0 + 32 wm + 8 (r / 4) + 4 lk + r % 4, channel c0 + bcol
@@ -265,46 +274,11 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   }
 }
 
-// AdaIN affine from wino_mm statistics: chunk i = (rho, y) = (i / chunks, i % chunks) holds
-// clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows; combined exactly in double like adainAffineWaveKernel.
+// AdaIN affine from wino_mm statistics (chunks per residue class of the dilation), 16 channels per workgroup.
 __global__ __launch_bounds__(256) void winoAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
                                                        float* __restrict__ af, int64_t l, int64_t c, int d,
                                                        int64_t chunks, int64_t creal, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (ch >= c) return;
-  if (ch >= creal) {
-    if (lane == 0) af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
-    return;
-  }
-  const int64_t total = static_cast<int64_t>(d) * chunks;
-  auto count = [&](int64_t i) -> double {
-    const int64_t rho = i / chunks, yy = i % chunks;
-    const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
-    return static_cast<double>(min<int64_t>(max<int64_t>(lr - yy * kWinoRows, 0), kWinoRows));
-  };
-  double s = 0.0;
-  for (int64_t i = lane; i < total; i += 64) {
-    const double n = count(i);
-    if (n > 0.0) s += static_cast<double>(st[(i * c + ch) * 2]) * n;
-  }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  const double mean = s / static_cast<double>(l);
-  double m2 = 0.0;
-  for (int64_t i = lane; i < total; i += 64) {
-    const double n = count(i);
-    if (n > 0.0) {
-      const double dm = static_cast<double>(st[(i * c + ch) * 2]) - mean;
-      m2 += static_cast<double>(st[(i * c + ch) * 2 + 1]) + n * dm * dm;
-    }
-  }
-  for (int o = 32; o > 0; o >>= 1) m2 += __shfl_xor(m2, o, 64);
-  if (lane == 0) {
-    const float var = static_cast<float>(m2 / static_cast<double>(l));
-    af[ch] = static_cast<float>(mean);
-    af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
-    af[2 * c + ch] = gb[creal + ch];
-  }
+  adainAffineSlices(st, gb, af, l, c, d, chunks, creal, eps);
 }
 
 }  // namespace lkd
@@ -364,7 +338,7 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
                                     int64_t creal, int dilation, int64_t length, float eps, void* stream) {
   if (dilation < 1 || s % dilation != 0 || length < 1 || creal > c) return 1;
-  hipLaunchKernelGGL(lkd::winoAffineKernel, dim3(lkh::ceilDiv(c, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(lkd::winoAffineKernel, dim3(lkh::ceilDiv(c, 16)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      stats, gb, af, length, c, dilation, s / dilation, creal, eps);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }

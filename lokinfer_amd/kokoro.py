@@ -152,41 +152,50 @@ class KokoroGpu:
             h = ops.leaky_lc_f32_gpu(x, 0.2, affine=af)
             h = ops.dwconvt_lc_f32_gpu(h, self.const(p + "#pool_w", lambda: _pool_pad(self.sd[p + ".pool.weight"], cp)),
                                        self.const(p + "#pool_b", lambda: _vec_pad(self.sd[p + ".pool.bias"], cp)))
-            ident = self.const(f"identity_affine{cp}", lambda: np.stack([np.zeros(cp), np.ones(cp), np.zeros(cp)]))
-            h, hst = ops.conv1d_act_lc_f32_gpu(h, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), ident,
-                                               act="none", padding=1, stats=True)
+            h, hst, hd = self.conv(h, p + ".conv1", None, 3, stats=True)
         else:
-            h, hst = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".conv1.weight", _w_lc), self.g(p + ".conv1.bias"), af,
-                                               act="leaky", slope=0.2, padding=1, stats=True)
-        af2 = self.affine(h, bank, p + ".norm2.fc", hst)
+            h, hst, hd = self.conv(x, p + ".conv1", af, 3, act="leaky", slope=0.2, stats=True)
+        af2 = self.affine(h, bank, p + ".norm2.fc", hst, hd)
         sc = ops.upsample2_lc_f32_gpu(x) if upsample else x
         if p + ".conv1x1.weight" in self.sd:
             sc = ops.conv1d_lc_f32_gpu(sc, self.g(p + ".conv1x1.weight", _w_lc),
                                        self.const(f"zeros#{cout}", lambda: np.zeros(cout)))
-        return ops.conv1d_act_lc_f32_gpu(h, self.g(p + ".conv2.weight", _w_lc), self.g(p + ".conv2.bias"), af2,
-                                         act="leaky", slope=0.2, padding=1, residual=sc, out_scale=SQRT1_2)
+        return self.conv(h, p + ".conv2", af2, 3, act="leaky", slope=0.2, residual=sc, out_scale=SQRT1_2)[0]
 
-    def wino(self, key: str):
-        """(U, tr) of conv weight `key` for the Winograd ops, transformed once on the host."""
-        k = key + "#wino"
+    def wino(self, key: str, ci_pad: int):
+        """(U, tr) of conv weight `key` for the Winograd ops, input channels zero-padded to ci_pad, transformed
+        once on the host."""
+        k = f"{key}#wino{ci_pad}"
         if k not in self._g:
-            u, tr = winograd.wino_weights(self.sd[key])
+            w = self.sd[key]
+            wp = np.zeros((w.shape[0], ci_pad, w.shape[2]), np.float32)
+            wp[:, : w.shape[1]] = w
+            u, tr = winograd.wino_weights(wp)
             self._g[k] = (from_numpy(u, device="gpu", copy=True), from_numpy(tr, device="gpu", copy=True))
         return self._g[k]
 
-    def snake_conv(self, x: Tensor, p: str, af: Tensor, alpha: Tensor, k: int, d: int, residual=None, stats=False):
-        """conv(snake(affine(x))) [+ residual] with stats of the output, on the Winograd pair when its GEMM grid
-        fills the chip (>= 256 workgroups of 64 tiles x 64 channels), else on the tap conv. Returns (y, stats,
-        stats_dilation): Winograd statistics are per residue class of the dilation."""
-        co = self.sd[p + ".weight"].shape[0]
-        lo = x.shape[0]
-        if (co // 64) * -(-(-(-lo // d)) // 256) * d >= WINO_MIN_GRID:
-            u, tr = self.wino(p + ".weight")
-            y = ops.conv1d_wino_lc_f32_gpu(x, u, self.g(p + ".bias"), tr, k, residual=residual, padding=d * (k - 1) // 2,
-                                           dilation=d, affine=af, alpha=alpha, stats=stats)
+    def conv(self, x: Tensor, p: str, af: Tensor | None, k: int, d: int = 1, act: str = "none", alpha=None,
+             slope: float = 0.0, residual=None, out_scale: float = 1.0, stats: bool = False):
+        """conv(act(affine(x))) (+ residual) * out_scale, optionally with the output's channel statistics, on the
+        Winograd pair or the tap conv, whichever is faster at this shape (measured on MI355X: Winograd once its
+        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 128 with Ci * Co >= 512^2). Returns
+        (y, stats, stats_dilation): Winograd statistics come per residue class of the dilation."""
+        co, ci = self.sd[p + ".weight"].shape[:2]
+        grid = (co // 64) * -(-(-(-x.shape[0] // d)) // 256) * d
+        pad = d * (k - 1) // 2
+        if co % 64 == 0 and (grid >= WINO_MIN_GRID or (grid >= WINO_MIN_GRID // 2 and ci * co >= 1 << 18)):
+            u, tr = self.wino(p + ".weight", x.shape[1])
+            kw = {"alpha": alpha} if act == "snake" else {"slope": slope} if act == "leaky" else {}
+            y = ops.conv1d_wino_lc_f32_gpu(x, u, self.g(p + ".bias"), tr, k, residual=residual, out_scale=out_scale,
+                                           padding=pad, dilation=d, affine=af if act != "none" else None,
+                                           stats=stats, **kw)
             return (y + (d,)) if stats else (y, None, 1)
-        y = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".weight", _w_lc), self.g(p + ".bias"), af, alpha, act="snake",
-                                      padding=d * (k - 1) // 2, dilation=d, residual=residual, stats=stats)
+        if af is None:
+            cp = x.shape[1]
+            af = self.const(f"identity_affine{cp}", lambda: np.stack([np.zeros(cp), np.ones(cp), np.zeros(cp)]))
+        y = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".weight", _w_lc), self.g(p + ".bias"), af, alpha, act=act,
+                                      slope=slope, padding=pad, dilation=d, residual=residual, out_scale=out_scale,
+                                      stats=stats)
         return (y + (1,)) if stats else (y, None, 1)
 
     def resblock1(self, x: Tensor, bank, p: str, k: int, x_stats: Tensor | None = None) -> Tensor:
@@ -194,10 +203,11 @@ class KokoroGpu:
         st, sd = (ops.channel_stats_lc_f32_gpu(x) if x_stats is None else x_stats), 1
         for j, d in enumerate((1, 3, 5)):
             af = self.affine(x, bank, f"{p}.adain1.{j}.fc", st, sd)
-            h, hst, hd = self.snake_conv(x, f"{p}.convs1.{j}", af, self.g(f"{p}.alpha1.{j}", _flat), k, d, stats=True)
+            h, hst, hd = self.conv(x, f"{p}.convs1.{j}", af, k, d, "snake", alpha=self.g(f"{p}.alpha1.{j}", _flat),
+                                   stats=True)
             af2 = self.affine(h, bank, f"{p}.adain2.{j}.fc", hst, hd)
-            x, st, sd = self.snake_conv(h, f"{p}.convs2.{j}", af2, self.g(f"{p}.alpha2.{j}", _flat), k, 1, residual=x,
-                                        stats=j < 2)
+            x, st, sd = self.conv(h, f"{p}.convs2.{j}", af2, k, 1, "snake", alpha=self.g(f"{p}.alpha2.{j}", _flat),
+                                  residual=x, stats=j < 2)
         return x
 
     def noise_block(self, har: Tensor, bank, i: int) -> Tensor:
