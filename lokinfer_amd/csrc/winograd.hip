@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   constexpr int TT = 64;              // tiles per workgroup
   constexpr int ROWS = TT + N - 1;    // staged V rows (group shift)
   constexpr int LDB = 64 + 8;         // k-major U rows: the two lane halves read 4 rows = 32 banks apart
-  __shared__ v4w As[2][ROWS * 4];
+  constexpr int AQ = ROWS * 4;
+  constexpr int AS = (AQ + 255) / 256;
+  __shared__ v4w As[2][AS * 256];  // rows past ROWS: every thread stores, so no store sits behind a branch
   __shared__ float Bs[2][N * 16 * LDB];
   __shared__ float red[2][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -117,9 +119,8 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   const int64_t nci = static_cast<int64_t>(N) * p.ci;
 
   // staging: A rows (ROWS x 4 slots) over 256 threads, U (N x 16 rows x 16 float4) over 256 threads
-  constexpr int AQ = ROWS * 4;
   constexpr int BQ = N * 16 * 16;
-  constexpr int AS = (AQ + 255) / 256, BSL = BQ / 256;
+  constexpr int BSL = BQ / 256;
   // two register sets: step t's operands live in set t & 1, loaded two steps ahead of their LDS store
   v4w ra0[AS], rb0[BSL], ra1[AS], rb1[BSL];
   auto gload = [&](int s, v4w(&ra)[AS], v4w(&rb)[BSL]) {
@@ -144,10 +145,8 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
     for (int i = 0; i < AS; ++i) {
       const int idx = tid + 256 * i;
-      if (AQ % 256 == 0 || idx < AQ) {
-        const int row = idx >> 2, slot = idx & 3;
-        As[buf][row * 4 + (slot ^ ((row >> 2) & 3))] = ra[i];
-      }
+      const int row = idx >> 2, slot = idx & 3;
+      As[buf][row * 4 + (slot ^ ((row >> 2) & 3))] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < BSL; ++i) {
@@ -183,7 +182,9 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) bq[g][h][q] = Bs[buf][(g * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
     }
-    if (s + 2 < steps) gload(s + 2, lra, lrb);
+    // unconditional (the last two steps reload the final step), so the wait before each LDS store counts only
+    // the loads of the set it stores and never the ones just issued
+    gload(min(s + 2, steps - 1), lra, lrb);
 #pragma unroll
     for (int g = 0; g < N; ++g)
 #pragma unroll
@@ -199,18 +200,22 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
     }
-    if (s + 1 < steps) sstore(buf ^ 1, sra, srb);
+    sstore(buf ^ 1, sra, srb);  // after the last step, into a buffer nothing reads
     __syncthreads();
   };
 
   gload(0, ra0, rb0);
   sstore(0, ra0, rb0);
-  if (steps > 1) gload(1, ra1, rb1);
+  gload(min(1, steps - 1), ra1, rb1);
   __syncthreads();
-  for (int s = 0; s < steps; s += 2) {
+  // pairs of steps with no branch inside, so every loop edge carries the same outstanding loads; an odd last
+  // step is peeled
+  int s = 0;
+  for (; s + 1 < steps; s += 2) {
     step(s, ra0, rb0, ra1, rb1);
-    if (s + 1 < steps) step(s + 1, ra1, rb1, ra0, rb0);
+    step(s + 1, ra1, rb1, ra0, rb0);
   }
+  if (s < steps) step(s, ra0, rb0, ra1, rb1);
 
   // epilogue: register r = tile t0 + 32 wm + 8 (r / 4) + 4 lk + r % 4, channel c0 + bcol
   const int64_t col = c0 + bcol;
