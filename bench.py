@@ -157,8 +157,8 @@ def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
             "flops": kokoro_conv_flops(tokens, frames), "sd": sd, "inputs": (ids, ref_s, dur, noise)}
 
 
-ROOFLINE_SHAPE = (292201, 128, 11, 5)  # L = 120 F + 1 at 487 tokens, C = 128, K = 11, dilation 5
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv_tap_snake_k11_L292201_traffic.txt")
+ROOFLINE_SHAPE = (293281, 128, 11, 5)  # L = 120 F + 1 at 487 tokens (F = 2444), C = 128, K = 11, dilation 5
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "wino_mm_k11_L293281_traffic.txt")
 
 
 def measured_traffic() -> float | None:
@@ -174,34 +174,54 @@ def measured_traffic() -> float | None:
     return None
 
 
-def roofline_conv(launches: int = 20, calibrate: bool = False) -> dict:
-    """The dominant kernel of the Kokoro forward: the implicit-GEMM conv with the AdaIN + Snake prologue, at the
-    generator's stage-1 resblock shape (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11, d = 5).
-    Algorithmic work per launch: 2 L C_in C_out K FLOPs. With calibrate, also launches add_f32_gpu over
-    2^26 floats (reads 512 MiB, writes 256 MiB) as the reference kernel for the --pmc byte counters."""
+def wino_tiles(lo: int, d: int, m: int = 4) -> int:
+    """Output tiles of a dilated Winograd conv: sum over residue classes of ceil(rows / M)."""
+    return sum(-(-len(range(r, lo, d)) // m) for r in range(d))
+
+
+def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
+    """The dominant kernel of the Kokoro forward: the Winograd GEMM (winoMmKernel<4,7,3>, wino_mm_lc_f32_gpu) of a
+    generator stage-1 resblock conv (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11 as 3 nested
+    F(4,4) tap groups, d = 5). Its algorithm is A = 7 point GEMMs over (group, channel): 2 A T (N Ci) Co FLOPs
+    per launch for T output tiles of 4 rows. The whole conv (input transform + GEMM, snake prologue) is timed
+    beside it and reported against the direct conv's 2 L Ci Co K FLOPs. With calibrate, also launches add_f32_gpu
+    over 2^26 floats (reads 512 MiB, writes 256 MiB) as the reference kernel for the --pmc byte counters."""
     import lokinfer_amd as lk
+    from lokinfer_amd import winograd as W
 
     rng = np.random.default_rng(0)
     l, c, k, d = ROOFLINE_SHAPE
+    pad = d * (k - 1) // 2
     G = lambda a: lk.from_numpy(np.ascontiguousarray(a, np.float32), device="gpu", copy=True)  # noqa: E731
-    x, w, b = G(rng.standard_normal((l, c))), G(rng.standard_normal((c, k, c)) / 40), G(rng.standard_normal(c))
+    u, tr = W.wino_weights(rng.standard_normal((c, c, k)) / np.sqrt(c * k))
+    x, u, tr, b = G(rng.standard_normal((l, c))), G(u), G(tr), G(rng.standard_normal(c))
     af = G(np.stack([np.zeros(c), np.ones(c), np.zeros(c)]))
     alpha = G(np.ones(c))
-    fn = lambda: lk.ops.conv1d_act_lc_f32_gpu(x, w, b, af, alpha, act="snake", padding=d * (k - 1) // 2, dilation=d)  # noqa: E731
-    fn()
-    ms = statistics.mean(event_times(fn, launches))
+    _, n = W.variant(k)
+    attrs = dict(dilation=d, groups=n, kernel=k, padding=pad, tile=4)
+    v = lk.ops.wino_tf_lc_f32_gpu(x, tr, affine=af, alpha=alpha, **attrs)
+    mm = lambda: lk.ops.wino_mm_lc_f32_gpu(v, u, b, tr, x, **attrs)  # noqa: E731
+    conv = lambda: lk.ops.conv1d_wino_lc_f32_gpu(x, u, b, tr, k, padding=pad, dilation=d, affine=af,  # noqa: E731
+                                                 alpha=alpha)
+    mm()
+    ms = statistics.mean(event_times(mm, launches))
+    conv()
+    conv_ms = statistics.mean(event_times(conv, max(5, launches // 2)))
     if calibrate:
-        n = 1 << 26
-        p = lk.Tensor(torch.ones(n, device="cuda"))
-        q = lk.Tensor(torch.ones(n, device="cuda"))
+        q = 1 << 26
+        p1 = lk.Tensor(torch.ones(q, device="cuda"))
+        p2 = lk.Tensor(torch.ones(q, device="cuda"))
         for _ in range(5):
-            lk.ops.add_f32_gpu(p, q)
+            lk.ops.add_f32_gpu(p1, p2)
         torch.cuda.synchronize()
-    flops = 2.0 * l * c * c * k
-    return {"kernel": "convTapKernel<128,128> (conv1d_act_lc_f32_gpu, AdaIN affine + Snake prologue)",
+    a = W.alpha_of(k)
+    flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c
+    direct = 2.0 * l * c * c * k
+    return {"kernel": "winoMmKernel<4,7,3> (wino_mm_lc_f32_gpu: K = 11 Winograd GEMM, generator stage 1)",
             "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
-            "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops}
+            "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops,
+            "conv_ms": conv_ms, "conv_direct_equiv_tflops": direct / (conv_ms * 1e-3) / 1e12}
 
 
 def cpu_kokoro(sd, inputs, budget_s: float = 30.0) -> dict:
@@ -231,7 +251,7 @@ def main():
                     help="launch only the roofline kernel (and the copy-calibration kernel), for rocprofv3 runs")
     a = ap.parse_args()
     if a.roofline_only:
-        r = roofline_conv(launches=a.steps, calibrate=True)
+        r = roofline_wino(launches=a.steps, calibrate=True)
         print(json.dumps({k: v for k, v in r.items()}))
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -262,7 +282,7 @@ def main():
         g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=False)
         extra = {"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
                  "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_lm_head_roofline": g["roofline"]}
-    roof = roofline_conv()
+    roof = roofline_wino()
     cpu = None if a.no_cpu else cpu_kokoro(r["sd"], r["inputs"])
     line = {
         "metric": "median Kokoro-82M f32 forward ms @59 & 487 tok; GPT-2 decode ms/token",
@@ -275,6 +295,7 @@ def main():
                    "global_batch": 1, "seq_len": tokens, "parallelism": "none"},
         "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": roof["kernel"], "roofline_avg_launch_ms": roof["avg_launch_ms"],
+        "roofline_conv_ms": roof["conv_ms"], "roofline_conv_direct_equiv_tflops": roof["conv_direct_equiv_tflops"],
         "forward_algorithmic_tflops": round(r["flops"] / (r["median_ms"] * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,
     }
