@@ -126,6 +126,22 @@ __device__ __forceinline__ float geluTanh(float v) {
   return 0.5f * v * (1.0f + tanhf(inner));
 }
 
+// Work item (x, y, z) of this workgroup in an XCD-aware order. Workgroups go to the 8 XCDs round-robin by linear
+// id L, so L runs on XCD L % 8 as that XCD's (L / 8)-th workgroup. Here XCD c owns the contiguous range of work
+// items [c per + min(c, rem), ...) (per = total / 8, rem = total % 8; a bijection on 0 .. total - 1) with work
+// item w = x + gx (y + gy z): neighbouring x (the column blocks that read the same input rows) share one L2.
+struct GridItem {
+  int x, y, z;
+};
+__device__ __forceinline__ GridItem xcdOrder() {
+  const unsigned gx = gridDim.x, gy = gridDim.y;
+  const unsigned total = gx * gy * gridDim.z;
+  const unsigned l = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const unsigned per = total / 8, rem = total % 8, xcd = l % 8, k = l / 8;
+  const unsigned w = xcd * per + min(xcd, rem) + k;
+  return GridItem{static_cast<int>(w % gx), static_cast<int>((w / gx) % gy), static_cast<int>(w / (gx * gy))};
+}
+
 // AdaIN affine af [3, C] = (mean, (1 + g) / sqrt(var + eps), b) from per-chunk (mean, M2) statistics st [S, C, 2]
 // of an L-row tensor; gb [2 creal]; channels >= creal get 0. Chunk i = (rho, y) = (i / chunks, i % chunks) holds
 // the rows of residue class rho of the dilation d from 128 y on: clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows

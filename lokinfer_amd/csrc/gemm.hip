@@ -198,8 +198,9 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const GridItem gi = xcdOrder();  // column blocks of one row block share an XCD's L2
+  const int64_t m0 = static_cast<int64_t>(gi.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(gi.x) * BN;
 
   v16f acc[TM][TN];
 #pragma unroll
@@ -310,7 +311,8 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, lk = lane >> 5;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM, n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const GridItem gi = xcdOrder();  // column blocks of one row block share an XCD's L2
+  const int64_t m0 = static_cast<int64_t>(gi.y) * BM, n0 = static_cast<int64_t>(gi.x) * BN;
   const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
 
   // two register sets: the next stage's tile is stored to LDS while the one after it is still in flight
@@ -500,8 +502,9 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const GridItem gi = xcdOrder();  // column blocks of one row block share an XCD's L2
+  const int64_t m0 = static_cast<int64_t>(gi.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(gi.x) * BN;
   const int64_t ci = p.convCi;
   const int chunks = static_cast<int>(ci / BK);
   const int steps = chunks * taps;
@@ -637,7 +640,7 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
   if (BM == 128 && p.stats) {
     // Per-(128-row chunk, channel) (mean, M2) of the stored output, two passes over the registers: this tile is
-    // exactly chunk blockIdx.y. A column's 128 rows sit in (wm, i, lane half, r); reduce r and i in registers,
+    // exactly chunk gi.y. A column's 128 rows sit in (wm, i, lane half, r); reduce r and i in registers,
     // the two lane halves with a shuffle, and the two wm waves through LDS.
     float* red = reinterpret_cast<float*>(&Hs[0][0]);  // reuse the staging LDS (free after the last barrier)
     const int n = static_cast<int>(min<int64_t>(BM, p.m - m0));
@@ -687,7 +690,7 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
         const int c = wn * WTN + j * 32 + lrow;
         const int64_t col = n0 + c;
         if (col < p.n) {
-          float* st = p.stats + (static_cast<int64_t>(blockIdx.y) * p.n + col) * 2;
+          float* st = p.stats + (static_cast<int64_t>(gi.y) * p.n + col) * 2;
           st[0] = mean[j];
           st[1] = red[c] + red[BN + c];
         }

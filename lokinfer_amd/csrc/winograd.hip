@@ -84,21 +84,6 @@ __global__ __launch_bounds__(256) void winoTfKernel(const float* __restrict__ x,
   }
 }
 
-struct WinoWork {
-  int x, y, z;
-};
-
-// Work item of this workgroup for a (gx, gy, gz) grid in the XCD-aware order: linear id L runs on XCD L % 8 as
-// that XCD's (L / 8)-th workgroup; XCD c owns the contiguous work range [c per + min(c, rem), ...), per =
-// total / 8, rem = total % 8 (a bijection on 0 .. total - 1), and work item w = x + gx (y + gy z).
-__device__ __forceinline__ WinoWork winoWork(unsigned gx, unsigned gy, unsigned gz) {
-  const unsigned total = gx * gy * gz;
-  const unsigned l = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-  const unsigned per = total / 8, rem = total % 8, xcd = l % 8, k = l / 8;
-  const unsigned w = xcd * per + min(xcd, rem) + k;
-  return WinoWork{static_cast<int>(w % gx), static_cast<int>((w / gx) % gy), static_cast<int>(w / (gx * gy))};
-}
-
 struct WinoMmArgs {
   const float* v;
   const float* u;
@@ -124,9 +109,8 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   __shared__ float red[2][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
-  // XCD-aware order: workgroups go to the 8 XCDs round-robin by linear id, so each XCD takes a contiguous run of
-  // work items (channel block fastest) and the channel blocks of a tile block read its V rows through one L2.
-  const WinoWork wk = winoWork(gridDim.x, gridDim.y, gridDim.z);
+  // XCD-aware order: the channel blocks of a tile block read its V rows through one L2
+  const GridItem wk = xcdOrder();
   const int rho = wk.z, d = p.d;
   const int64_t lor = rho < p.lo ? (p.lo - rho + d - 1) / d : 0;  // output rows of this residue class
   const int64_t t0 = static_cast<int64_t>(wk.y) * TT;

@@ -36,8 +36,6 @@ from .runtime import GpuContext
 from .tensor import Tensor, from_numpy
 
 SQRT1_2 = 1.0 / math.sqrt(2.0)
-# Winograd conv when its GEMM grid has at least this many 64 x 64 workgroups (below, the tap conv is faster)
-WINO_MIN_GRID = 256
 
 
 def _pad16(n: int) -> int:
@@ -162,39 +160,46 @@ class KokoroGpu:
                                        self.const(f"zeros#{cout}", lambda: np.zeros(cout)))
         return self.conv(h, p + ".conv2", af2, 3, act="leaky", slope=0.2, residual=sc, out_scale=SQRT1_2)[0]
 
-    def wino(self, key: str, ci_pad: int):
-        """(U, tr) of conv weight `key` for the Winograd ops, input channels zero-padded to ci_pad, transformed
-        once on the host."""
-        k = f"{key}#wino{ci_pad}"
+    def wino(self, key: str, ci_pad: int, co_pad: int):
+        """(U, tr) of conv weight `key` for the Winograd ops, input channels zero-padded to ci_pad and output
+        channels to co_pad, transformed once on the host."""
+        k = f"{key}#wino{ci_pad}x{co_pad}"
         if k not in self._g:
             w = self.sd[key]
-            wp = np.zeros((w.shape[0], ci_pad, w.shape[2]), np.float32)
-            wp[:, : w.shape[1]] = w
+            wp = np.zeros((co_pad, ci_pad, w.shape[2]), np.float32)
+            wp[: w.shape[0], : w.shape[1]] = w
             u, tr = winograd.wino_weights(wp)
             self._g[k] = (from_numpy(u, device="gpu", copy=True), from_numpy(tr, device="gpu", copy=True))
         return self._g[k]
 
     def conv(self, x: Tensor, p: str, af: Tensor | None, k: int, d: int = 1, act: str = "none", alpha=None,
-             slope: float = 0.0, residual=None, out_scale: float = 1.0, stats: bool = False):
+             slope: float = 0.0, residual=None, out_scale: float = 1.0, stats: bool = False, co_pad: int = 0):
         """conv(act(affine(x))) (+ residual) * out_scale, optionally with the output's channel statistics, on the
         Winograd pair or the tap conv, whichever is faster at this shape (measured on MI355X: Winograd once its
-        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 128 with Ci * Co >= 512^2). Returns
-        (y, stats, stats_dilation): Winograd statistics come per residue class of the dilation."""
+        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 128 with Ci * Co >= 512^2, or 64 with
+        K >= 7). co_pad > Co: output channels past Co are zero (zero weights and bias). Returns (y, stats,
+        stats_dilation): Winograd statistics come per residue class of the dilation."""
         co, ci = self.sd[p + ".weight"].shape[:2]
-        grid = (co // 64) * -(-(-(-x.shape[0] // d)) // 256) * d
+        cop = max(co, co_pad)
+        grid = (cop // 64) * -(-(-(-x.shape[0] // d)) // 256) * d
         pad = d * (k - 1) // 2
-        if co % 64 == 0 and (grid >= WINO_MIN_GRID or (grid >= WINO_MIN_GRID // 2 and ci * co >= 1 << 18)):
-            u, tr = self.wino(p + ".weight", x.shape[1])
+        bias = self.g(p + ".bias") if cop == co else self.const(f"{p}.bias#pad{cop}",
+                                                                 lambda: _vec_pad(self.sd[p + ".bias"], cop))
+        if cop % 64 == 0 and (grid >= 256 or (grid >= 128 and ci * cop >= 1 << 18) or (grid >= 64 and k >= 7)):
+            u, tr = self.wino(p + ".weight", x.shape[1], cop)
             kw = {"alpha": alpha} if act == "snake" else {"slope": slope} if act == "leaky" else {}
-            y = ops.conv1d_wino_lc_f32_gpu(x, u, self.g(p + ".bias"), tr, k, residual=residual, out_scale=out_scale,
+            y = ops.conv1d_wino_lc_f32_gpu(x, u, bias, tr, k, residual=residual, out_scale=out_scale,
                                            padding=pad, dilation=d, affine=af if act != "none" else None,
                                            stats=stats, **kw)
             return (y + (d,)) if stats else (y, None, 1)
+        w = self.g(p + ".weight", _w_lc) if cop == co else self.const(
+            f"{p}#lc{cop}", lambda: _w_lc(np.concatenate([self.sd[p + ".weight"],
+                                                          np.zeros((cop - co, *self.sd[p + ".weight"].shape[1:]),
+                                                                   np.float32)])))
         if af is None:
             cp = x.shape[1]
             af = self.const(f"identity_affine{cp}", lambda: np.stack([np.zeros(cp), np.ones(cp), np.zeros(cp)]))
-        y = ops.conv1d_act_lc_f32_gpu(x, self.g(p + ".weight", _w_lc), self.g(p + ".bias"), af, alpha, act=act,
-                                      slope=slope, padding=pad, dilation=d, residual=residual, out_scale=out_scale,
+        y = ops.conv1d_act_lc_f32_gpu(x, w, bias, af, alpha, act=act, slope=slope, padding=pad, dilation=d, residual=residual, out_scale=out_scale,
                                       stats=stats)
         return (y + (1,)) if stats else (y, None, 1)
 
@@ -350,15 +355,16 @@ class KokoroGpu:
             x = ops.add3_scale_f32_gpu(rb[0], rb[1], rb[2], 1.0 / 3.0)
             self._keep(f"stage{i}", x)
         ident = self.const("identity_affine128", lambda: np.stack([np.zeros(128), np.ones(128), np.zeros(128)]))
-        post = ops.conv1d_act_lc_f32_gpu(x, self.g(G + "conv_post.weight", _w_lc), self.g(G + "conv_post.bias"), ident,
-                                         act="leaky", slope=0.01, padding=3)  # [120 F + 1, 22]
+        # [120 F + 1, 64]: the 22 iSTFT logit columns, zero past them (output channels padded to a 64 block)
+        post = self.conv(x, G + "conv_post", ident, 7, act="leaky", slope=0.01, co_pad=64)[0]
         audio = ops.istft_logits_lc_f32_gpu(post, n_fft=20, hop=5)
         return audio, f0, n_curve, post
 
     # ---- host API ----------------------------------------------------------------------------------------------
     def forward(self, ids, ref_s, dur, noise, inplace: bool = False):
         """One forward from host or device tensors; checks sum(dur) == F on the host (the reference's
-        repeat_interleave reports a mismatch, kokoro_misc.cpp:253-260). Returns (audio, f0, n, post)."""
+        repeat_interleave reports a mismatch, kokoro_misc.cpp:253-260). Returns (audio, f0, n, post); post is
+        f32[120 F + 1, 64]: the 22 iSTFT logit columns, then zeros."""
         dur_h = np.asarray(dur.numpy() if isinstance(dur, Tensor) else dur, np.int64)
         noise_rows = (noise.shape if isinstance(noise, Tensor) else np.shape(noise))[0]
         if noise_rows % 600 or int(dur_h.sum()) != noise_rows // 600 or (dur_h < 0).any():
