@@ -152,10 +152,14 @@ int lk_hip_wino_tf_lc_f32(const float* x, const float* tr, const float* affine, 
                           int64_t l, int64_t c, int dilation, int padding, int kernel, int tile, int64_t v_rows,
                           int act, float slope, void* stream);
 /* out [Lo, Co] = (AT (V_xi U_xi) + bias [+ res]) * scale; Ci % 16 == 0, Co % 64 == 0; stats (optional)
- * [d ceil(ceil(Lo / d) / 128), Co, 2]: (mean, M2) per 128-row chunk of each residue class */
+ * [d ceil(ceil(Lo / d) / 128), Co, 2]: (mean, M2) per 128-row chunk of each residue class. workspace
+ * (optional, may be NULL): with dilation 1 and a grid too small for the chip, the point-chunk steps are split
+ * over up to 8 workgroups whose partial rows (split * Lo * Co floats past the first 64 KiB) a second kernel
+ * sums; calls sharing a workspace must be stream-ordered */
 int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
                           const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
-                          int dilation, int groups, int kernel, int tile, float scale, void* stream);
+                          int dilation, int groups, int kernel, int tile, float scale, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 /* stats [s, c, 2] of a length-row output -> af [3, c] = (mean, (1 + g) / sqrt(var + eps), b), gb [2 creal];
  * channels >= creal get 0 */
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,

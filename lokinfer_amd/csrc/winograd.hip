@@ -92,8 +92,9 @@ struct WinoMmArgs {
   float* out;
   const float* tr;
   float* stats;
+  float* part;  // split > 1: per-split raw output rows [split][Lo][Co], summed by winoSplitReduceKernel
   int64_t lo, ci, co, rmax, chunks;
-  int d;
+  int d, split;
   float scale;
 };
 
@@ -111,13 +112,18 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
   // XCD-aware order: the channel blocks of a tile block read its V rows through one L2
   const GridItem wk = xcdOrder();
-  const int rho = wk.z, d = p.d;
+  const int d = p.d, rho = wk.z % d, sp = wk.z / d;
   const int64_t lor = rho < p.lo ? (p.lo - rho + d - 1) / d : 0;  // output rows of this residue class
   const int64_t t0 = static_cast<int64_t>(wk.y) * TT;
   if (t0 * M >= lor) return;
   const int64_t c0 = static_cast<int64_t>(wk.x) * 64;
   const int chunks = static_cast<int>(p.ci / 16);
   const int steps = A * chunks;
+  // split-K: this workgroup runs steps [sb, se) of the point-major step sequence; a point cut by the range is
+  // folded with AT at the range's end, and AT is linear, so the splits' outputs sum to the full one
+  const int sb = static_cast<int>(static_cast<int64_t>(steps) * sp / p.split);
+  const int se = static_cast<int>(static_cast<int64_t>(steps) * (sp + 1) / p.split);
+  const int nsteps = se - sb;
   const int64_t nci = static_cast<int64_t>(N) * p.ci;
 
   // staging: A rows (ROWS x 4 slots) over 256 threads, U (N x 16 rows x 16 float4) over 256 threads
@@ -169,8 +175,8 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   const int arow = 32 * wm + lr, bcol = 32 * wn + lr;
   // one step: MFMAs on LDS buffer s & 1; loads step s + 2 into (lra, lrb) = set s & 1 (its step s is already in
   // LDS), stores step s + 1 from (sra, srb) = set (s + 1) & 1 into the other buffer
-  auto step = [&](int s, v4w(&lra)[AS], v4w(&lrb)[BSL], const v4w(&sra)[AS], const v4w(&srb)[BSL]) {
-    const int buf = s & 1;
+  auto step = [&](int sl, v4w(&lra)[AS], v4w(&lrb)[BSL], const v4w(&sra)[AS], const v4w(&srb)[BSL]) {
+    const int buf = sl & 1, s = sb + sl;
     const int xi = s / chunks, ch = s - xi * chunks;
     v4w af[N][2];
     float bq[N][2][4];
@@ -186,14 +192,14 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
     }
     // unconditional (the last two steps reload the final step), so the wait before each LDS store counts only
     // the loads of the set it stores and never the ones just issued
-    gload(min(s + 2, steps - 1), lra, lrb);
+    gload(min(s + 2, se - 1), lra, lrb);
 #pragma unroll
     for (int g = 0; g < N; ++g)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][h][q], bq[g][h][q], acc, 0, 0, 0);
-    if (ch == chunks - 1) {  // the point is complete: fold it into the output rows
+    if (ch == chunks - 1 || s == se - 1) {  // the point (or this split's part of it) is complete: fold it
 #pragma unroll
       for (int j = 0; j < M; ++j) {
         const float at = p.tr[A * A + j * A + xi];
@@ -206,18 +212,30 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
     __syncthreads();
   };
 
-  gload(0, ra0, rb0);
+  gload(sb, ra0, rb0);
   sstore(0, ra0, rb0);
-  gload(min(1, steps - 1), ra1, rb1);
+  gload(min(sb + 1, se - 1), ra1, rb1);
   __syncthreads();
   // pairs of steps with no branch inside, so every loop edge carries the same outstanding loads; an odd last
   // step is peeled
-  int s = 0;
-  for (; s + 1 < steps; s += 2) {
-    step(s, ra0, rb0, ra1, rb1);
-    step(s + 1, ra1, rb1, ra0, rb0);
+  int sl = 0;
+  for (; sl + 1 < nsteps; sl += 2) {
+    step(sl, ra0, rb0, ra1, rb1);
+    step(sl + 1, ra1, rb1, ra0, rb0);
   }
-  if (s < steps) step(s, ra0, rb0, ra1, rb1);
+  if (sl < nsteps) step(sl, ra0, rb0, ra1, rb1);
+
+  if (p.split > 1) {  // raw partial rows; bias, residual, scale and statistics come in the reduction
+    float* pp = p.part + static_cast<int64_t>(sp) * p.lo * p.co;
+#pragma unroll
+    for (int j = 0; j < M; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t uo = (t0 + 32 * wm + 8 * (r >> 2) + 4 * lk + (r & 3)) * M + j;
+        if (uo < lor) pp[(rho + uo * d) * p.co + c0 + 32 * wn + lr] = y[j][r];
+      }
+    return;
+  }
 
   // epilogue: register r = tile t0 + 32 wm + 8 (r / 4) + 4 lk + r % 4, channel c0 + bcol
   const int64_t col = c0 + bcol;
@@ -281,6 +299,57 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   }
 }
 
+// Split-K reduction (dilation 1): out = (sum_s part[s] + bias [+ res]) * scale over a 128-row x 64-channel block
+// per workgroup (4 row groups of 32 rows x 64 channels), in split order; with stats, the block's (mean, M2) per
+// channel, which is the channel_stats_lc layout [chunk][C][2].
+__global__ __launch_bounds__(256) void winoSplitReduceKernel(const float* __restrict__ part, int split,
+                                                            const float* __restrict__ bias,
+                                                            const float* __restrict__ res, float* __restrict__ out,
+                                                            float* __restrict__ stats, int64_t lo, int64_t co,
+                                                            float scale) {
+  __shared__ float red[4][64];
+  const int cl = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + cl;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kWinoRows;
+  const float b = bias[col];
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int64_t row = min<int64_t>(r0 + rg * 32 + i, lo - 1);
+    float sum = 0.0f;
+    for (int s = 0; s < split; ++s) sum += part[(static_cast<int64_t>(s) * lo + row) * co + col];
+    float o = sum + b;
+    if (res) o += res[row * co + col];
+    v[i] = o * scale;
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    if (r0 + rg * 32 + i < lo) out[(r0 + rg * 32 + i) * co + col] = v[i];
+  if (!stats) return;
+  const int n = static_cast<int>(min<int64_t>(kWinoRows, lo - r0));
+  float s1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    if (rg * 32 + i < n) s1 += v[i];
+  red[rg][cl] = s1;
+  __syncthreads();
+  const float mean = (red[0][cl] + red[1][cl] + red[2][cl] + red[3][cl]) / static_cast<float>(n);
+  __syncthreads();
+  float s2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float dv = v[i] - mean;
+    if (rg * 32 + i < n) s2 += dv * dv;
+  }
+  red[rg][cl] = s2;
+  __syncthreads();
+  if (rg == 0) {
+    float* st = stats + (static_cast<int64_t>(blockIdx.y) * co + col) * 2;
+    st[0] = mean;
+    st[1] = red[0][cl] + red[1][cl] + red[2][cl] + red[3][cl];
+  }
+}
+
 // AdaIN affine from wino_mm statistics (chunks per residue class of the dilation), 16 channels per workgroup.
 __global__ __launch_bounds__(256) void winoAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
                                                        float* __restrict__ af, int64_t l, int64_t c, int d,
@@ -318,18 +387,32 @@ int lk_hip_wino_tf_lc_f32(const float* x, const float* tr, const float* affine, 
 
 int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
                           const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
-                          int dilation, int groups, int kernel, int tile, float scale, void* stream) {
+                          int dilation, int groups, int kernel, int tile, float scale, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
   const int a = tile == 2 ? 4 : kernel == 3 ? 6 : 7;
   if (ci % 16 != 0 || co % 64 != 0 || dilation < 1 || groups < 1 || groups > 3 || lo < 1) return 1;
   if ((tile == 2 && groups != 1) || (a == 6 && groups != 1) || (a == 7 && groups < 2)) return 1;
   const int64_t rmax = v_rows / (static_cast<int64_t>(dilation) * a);
   const int m = tile;
   const int64_t tiles = ((lo + dilation - 1) / dilation + m - 1) / m;  // residue class 0 is the longest
-  lkd::WinoMmArgs p{v, u, bias, res, out, tr, stats, lo, ci, co, rmax,
-                    ((lo + dilation - 1) / dilation + lkd::kWinoRows - 1) / lkd::kWinoRows, dilation, scale};
   if (rmax < tiles + groups - 1) return 1;  // V must hold every tile and its group shifts
+  // split-K when the grid is too small to fill the chip (two workgroups per CU): dilation 1 only (the reduction
+  // writes the plain 128-row statistics), at least 32 steps per split (fewer measured slower than no split on
+  // MI355X: the partial rows' round trip and the second launch outweigh the extra workgroups), partials in the
+  // workspace past its 64 KiB counter area
+  const int64_t base = (co / 64) * ((tiles + 63) / 64) * dilation;
+  const int steps = a * static_cast<int>(ci / 16);
+  int split = 1;
+  if (dilation == 1 && workspace && base < 512) {
+    split = static_cast<int>(std::min<int64_t>({8, 512 / base, steps / 32}));
+    while (split > 1 && 65536 + static_cast<int64_t>(split) * lo * co * 4 > workspace_bytes) --split;
+    split = std::max(split, 1);
+  }
+  float* part = split > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + 65536) : nullptr;
+  lkd::WinoMmArgs p{v, u, bias, res, out, tr, stats, part, lo, ci, co, rmax,
+                    ((lo + dilation - 1) / dilation + lkd::kWinoRows - 1) / lkd::kWinoRows, dilation, split, scale};
   const dim3 grid(static_cast<unsigned>(co / 64), static_cast<unsigned>((tiles + 63) / 64),
-                  static_cast<unsigned>(dilation));
+                  static_cast<unsigned>(dilation * split));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a == 4)
     hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1>), grid, dim3(256), 0, s, p);
@@ -339,6 +422,9 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2>), grid, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3>), grid, dim3(256), 0, s, p);
+  if (split > 1)
+    hipLaunchKernelGGL(lkd::winoSplitReduceKernel, dim3(static_cast<unsigned>(co / 64), lkh::ceilDiv(lo, 128)),
+                       dim3(256), 0, s, part, split, bias, res, out, stats, lo, co, scale);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -390,7 +476,8 @@ void runWinoMm(ExecCtx& ctx, const KernelArgs& a) {
   const float scale = RES && a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1.0f;
   if (lk_hip_wino_mm_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), RES ? P<float>(a, 5) : nullptr,
                             P<float>(a, outp), P<float>(a, 3), STATS ? P<float>(a, outp + 1) : nullptr, vr, ci, co, lo,
-                            d, groups, k, tile, scale, ctx.stream))
+                            d, groups, k, tile, scale, ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes),
+                            ctx.stream))
     ctx.error = "wino_mm: invalid configuration";
 }
 

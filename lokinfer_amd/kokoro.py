@@ -176,8 +176,8 @@ class KokoroGpu:
              slope: float = 0.0, residual=None, out_scale: float = 1.0, stats: bool = False, co_pad: int = 0):
         """conv(act(affine(x))) (+ residual) * out_scale, optionally with the output's channel statistics, on the
         Winograd pair or the tap conv, whichever is faster at this shape (measured on MI355X: Winograd once its
-        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 128 with Ci * Co >= 512^2, or 64 with
-        K >= 7). co_pad > Co: output channels past Co are zero (zero weights and bias). Returns (y, stats,
+        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 64 with K >= 7 or Ci >= 512, or at any grid
+        with Ci >= 1024, where its split-K fills the chip). co_pad > Co: output channels past Co are zero (zero weights and bias). Returns (y, stats,
         stats_dilation): Winograd statistics come per residue class of the dilation."""
         co, ci = self.sd[p + ".weight"].shape[:2]
         cop = max(co, co_pad)
@@ -185,7 +185,7 @@ class KokoroGpu:
         pad = d * (k - 1) // 2
         bias = self.g(p + ".bias") if cop == co else self.const(f"{p}.bias#pad{cop}",
                                                                  lambda: _vec_pad(self.sd[p + ".bias"], cop))
-        if cop % 64 == 0 and (grid >= 256 or (grid >= 128 and ci * cop >= 1 << 18) or (grid >= 64 and k >= 7)):
+        if cop % 64 == 0 and (grid >= 256 or (grid >= 64 and (k >= 7 or ci >= 512)) or ci >= 1024):
             u, tr = self.wino(p + ".weight", x.shape[1], cop)
             kw = {"alpha": alpha} if act == "snake" else {"slope": slope} if act == "leaky" else {}
             y = ops.conv1d_wino_lc_f32_gpu(x, u, bias, tr, k, residual=residual, out_scale=out_scale,
