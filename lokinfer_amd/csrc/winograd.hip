@@ -8,14 +8,15 @@
 //   out[o, co] = (b + sum_xi AT[j, xi] sum_{g, ci} V[rho, xi, t + g, ci] U[xi, g Ci + ci, co] [+ res]) * scale,
 //                o = rho + d (t M + j)
 //   stats [d chunks, Co, 2]: (mean, M2) of each 128 output rows of a residue class
-// This backend's own Kokoro graph runs the direct tap kernel with the same prologue fused (the Winograd form
-// measured no faster on CDNA4's f32 MFMA), so these kernels serve callers that build the reference's graph.
+// The same kernels run this backend's Kokoro graph wherever their grid fills the chip (the generator's resblock
+// and noise convs, the decoder's wide convs, conv_post).
 //
 // wino_mm: one workgroup per (64 output channels, 64 tiles, residue); 4 waves in 2 x 2, each 32 tiles x 32
 // channels. Steps = points x 16-channel chunks; per step the V rows of the workgroup's tiles (+ N - 1 for the
 // group shift) are staged [row][4 slots] (swizzled by (row >> 2) & 3) and U's N x 16 rows k-major; the point's
 // GEMM accumulates over the groups with the A rows shifted by g, and after a point's last chunk AT[j, xi] folds
-// it into the M output accumulators.
+// it into the M output accumulators. Small grids split the steps over workgroups (split-K) and sum the partial
+// rows in winoSplitReduceKernel.
 #include "common.h"
 #include "lokinfer_hip.h"
 
