@@ -182,8 +182,8 @@ __device__ __forceinline__ void storeTile(const GemmParams& p, v16f (&acc)[TM][T
     }
 }
 
-template <int BM, int BN, int AM, int BMODE>
-__global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
+template <int BM, int BN, int AM, int BMODE, bool FAST = false>
+__global__ __launch_bounds__(NT, 2) void gemmMfmaKernel(GemmParams p) {
   constexpr int WTM = BM / 2, WTN = BN / 2;    // wave tile
   constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
   constexpr int PADA = 4, PADB = 4;
@@ -210,28 +210,45 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  float4 ra[A4], rb[B4];
-  auto gload = [&](int64_t kt) {
+  // FAST (row-major A, 16-byte aligned operands, K % BK == 0, N % 4 == 0 for NN; checked by the launcher):
+  // float4 loads from clamped indices (rows / columns past the matrix feed outputs that are never stored) into
+  // two register sets, issued unconditionally one stage ahead of their LDS store, pairs of stages with no branch
+  // inside (a load or store behind a branch makes the compiler's wait counting assume the path without it).
+  // Otherwise one register set with element-guarded loads.
+  using RA = float4[A4];
+  using RB = float4[B4];
+  float4 ra0[A4], rb0[B4], ra1[A4], rb1[B4];
+  const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
+  auto gload = [&](int64_t kt, RA& ra, RB& rb) {
     const int64_t k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < A4; ++i) {
       const int idx = tid + i * NT;
       const int row = idx >> 2, kq = (idx & 3) * 4;
-      ra[i] = loadA4<AM>(p, m0 + row, k0 + kq);
+      if constexpr (FAST)
+        ra[i] = *reinterpret_cast<const float4*>(p.a + min<int64_t>(m0 + row, lastRow) * p.lda + k0 + kq);
+      else
+        ra[i] = loadA4<AM>(p, m0 + row, k0 + kq);
     }
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
       const int idx = tid + i * NT;
       if constexpr (BMODE == B_NN) {
         const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
-        rb[i] = loadBnn4(p, k0 + kr, n0 + nq);
+        if constexpr (FAST)
+          rb[i] = *reinterpret_cast<const float4*>(p.b + (k0 + kr) * p.ldb + min<int64_t>(n0 + nq, p.n - 4));
+        else
+          rb[i] = loadBnn4(p, k0 + kr, n0 + nq);
       } else {
         const int col = idx >> 2, kq = (idx & 3) * 4;
-        rb[i] = loadBnt4(p, n0 + col, k0 + kq);
+        if constexpr (FAST)
+          rb[i] = *reinterpret_cast<const float4*>(p.b + min<int64_t>(n0 + col, lastCol) * p.ldb + k0 + kq);
+        else
+          rb[i] = loadBnt4(p, n0 + col, k0 + kq);
       }
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const RA& ra, const RB& rb) {
 #pragma unroll
     for (int i = 0; i < A4; ++i) {
       const int idx = tid + i * NT;
@@ -258,13 +275,8 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
   };
 
   const int64_t nk = (p.k + BK - 1) / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int lrow = lane & 31, lk = lane >> 5;
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = static_cast<int>(kt & 1);
-    if (kt + 1 < nk) gload(kt + 1);
+  auto mfmas = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < BK; ks += 2) {
       float av[TM], bv[TN];
@@ -277,8 +289,35 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+  };
+  gload(0, ra0, rb0);
+  sstore(0, ra0, rb0);
+  if constexpr (FAST) {
+    // stage kt computes from buffer kt & 1 while stage kt + 1 (register set (kt + 1) & 1) is in flight; it
+    // stores that set into the other buffer at its end (the last stage stores an unread copy)
+    gload(min<int64_t>(1, nk - 1), ra1, rb1);
     __syncthreads();
+    auto stage = [&](int64_t kt, RA& nra, RB& nrb, RA& fra, RB& frb) {
+      mfmas(static_cast<int>(kt & 1));
+      sstore(static_cast<int>((kt + 1) & 1), nra, nrb);
+      gload(min<int64_t>(kt + 2, nk - 1), fra, frb);
+      __syncthreads();
+    };
+    int64_t kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      stage(kt, ra1, rb1, ra0, rb0);
+      stage(kt + 1, ra0, rb0, ra1, rb1);
+    }
+    if (kt < nk) stage(kt, ra1, rb1, ra0, rb0);
+  } else {
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int buf = static_cast<int>(kt & 1);
+      if (kt + 1 < nk) gload(kt + 1, ra0, rb0);
+      mfmas(buf);
+      if (kt + 1 < nk) sstore(buf ^ 1, ra0, rb0);
+      __syncthreads();
+    }
   }
 
   storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
@@ -293,7 +332,9 @@ __global__ __launch_bounds__(NT) void gemmMfmaKernel(GemmParams p) {
 // A (and NT B) tiles are [row][4 slots of 4 k], slot swizzled by (row >> 2) & 3; a slice's 16 k are fed to the
 // MFMAs in the order 8 g + 4 half + q, as in the conv kernel. Needs K, lda, ldb (and N for NN) % 4 == 0 and
 // 16-byte aligned operands (checked by the launcher).
-template <int BN, int BMODE>
+// KTAIL: K is not a multiple of the 64-deep stage, so the last stage's tail is zeroed when staged (without it,
+// no select on the loaded registers exists to pull the wait for a load ahead of the MFMAs that cover it).
+template <int BN, int BMODE, bool KTAIL>
 __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
   constexpr int BM = 64, KS = 64;
   constexpr int TM = 2, TN = BN / 32;
@@ -346,18 +387,18 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
     for (int i = 0; i < A4; ++i) {
       const int idx = tid + i * NT, row = idx >> 4, kq = (idx & 15) * 4;
       const int slice = kq >> 4, slot = (kq >> 2) & 3;
-      As[(buf * 4 + slice) * BM * 4 + row * 4 + (slot ^ ((row >> 2) & 3))] = k0 + kq < p.k ? ra[i] : zero;
+      As[(buf * 4 + slice) * BM * 4 + row * 4 + (slot ^ ((row >> 2) & 3))] = !KTAIL || k0 + kq < p.k ? ra[i] : zero;
     }
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
       const int idx = tid + i * NT;
       if constexpr (BMODE == B_NN) {
         const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
-        *reinterpret_cast<v4f*>(Bsf + buf * KS * LDBK + kr * LDBK + nq) = k0 + kr < p.k ? rb[i] : zero;
+        *reinterpret_cast<v4f*>(Bsf + buf * KS * LDBK + kr * LDBK + nq) = !KTAIL || k0 + kr < p.k ? rb[i] : zero;
       } else {
         const int col = idx >> 4, kq = (idx & 15) * 4;
         const int slice = kq >> 4, slot = (kq >> 2) & 3;
-        Bsv[(buf * 4 + slice) * BN * 4 + col * 4 + (slot ^ ((col >> 2) & 3))] = k0 + kq < p.k ? rb[i] : zero;
+        Bsv[(buf * 4 + slice) * BN * 4 + col * 4 + (slot ^ ((col >> 2) & 3))] = !KTAIL || k0 + kq < p.k ? rb[i] : zero;
       }
     }
   };
@@ -401,7 +442,9 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
           for (int q = 0; q < 4; ++q) bq[g][q][j] = bv[q];
         }
     }
-    if (st + 2 < stages) gload((st + 2) * KS, ra_far, rb_far);
+    // unconditional, clamped to the last stage (a load or store behind a branch makes the compiler's wait
+    // counting assume the path without it, i.e. wait for the loads just issued before every LDS store)
+    gload(min<int64_t>(st + 2, stages - 1) * KS, ra_far, rb_far);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -411,19 +454,21 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][i][q], bq[g][q][j], acc[i][j], 0, 0, 0);
-    if (st + 1 < stages) sstore(buf ^ 1, (st + 1) * KS, ra_next, rb_next);
+    sstore(buf ^ 1, min<int64_t>(st + 1, stages - 1) * KS, ra_next, rb_next);  // last stage: unread copy
     __syncthreads();
   };
   // stage st computes from LDS buffer st & 1, stores stage st + 1 (register set (st + 1) & 1) and has stage st + 2
-  // in flight into register set st & 1
+  // in flight into register set st & 1; pairs of stages with no branch inside, an odd last stage peeled
   gload(0, ra[0], rb[0]);
   sstore(0, 0, ra[0], rb[0]);
-  if (stages > 1) gload(KS, ra[1], rb[1]);
+  gload(min<int64_t>(1, stages - 1) * KS, ra[1], rb[1]);
   __syncthreads();
-  for (int64_t st = 0; st < stages; st += 2) {
+  int64_t st = 0;
+  for (; st + 1 < stages; st += 2) {
     stage(st, 0, ra[1], rb[1], ra[0], rb[0]);
-    if (st + 1 < stages) stage(st + 1, 1, ra[0], rb[0], ra[1], rb[1]);
+    stage(st + 1, 1, ra[0], rb[0], ra[1], rb[1]);
   }
+  if (st < stages) stage(st, 0, ra[1], rb[1], ra[0], rb[0]);
 
   // partial tiles -> LDS (the staging buffers are free after the last barrier), fixed-order sum, epilogue
   float* red = smem;
@@ -714,15 +759,25 @@ static void launchGemm(const GemmParams& p, hipStream_t s) {
                        (BMODE == lkd::B_NT || (p.n % 4 == 0 && p.n >= 4));
   if (big >= 512) {
     dim3 grid(ceilDiv(p.n, 128), ceilDiv(p.m, 128));
-    hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+    if (AM == lkd::A_ROWMAJOR && aligned && p.k % lkd::BK == 0)
+      hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE, AM == lkd::A_ROWMAJOR>), grid, dim3(lkd::NT), 0, s,
+                         p);
+    else
+      hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
   } else if (AM == lkd::A_ROWMAJOR && aligned) {
     // few output tiles: K split over the waves of a workgroup; 32-column tiles when 64 would leave CUs idle
     if (static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 192) {
       dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
-      hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+      if (p.k % 64)
+        hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE, true>), grid, dim3(lkd::NT), 0, s, p);
+      else
+        hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE, false>), grid, dim3(lkd::NT), 0, s, p);
     } else {
       dim3 grid(ceilDiv(p.n, 32), ceilDiv(p.m, 64));
-      hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE>), grid, dim3(lkd::NT), 0, s, p);
+      if (p.k % 64)
+        hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE, true>), grid, dim3(lkd::NT), 0, s, p);
+      else
+        hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE, false>), grid, dim3(lkd::NT), 0, s, p);
     }
   } else {
     dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
