@@ -43,9 +43,13 @@ const char* lk_last_error(void);
 
 /* ---- GEMM / conv (reference: gemm_f32_gpu_mps mps.mm:41-84; gemm_bias[_relu]_f32_gpu kokoro_lc.cpp:460-581;
  *      gemm_steel* kokoro_lc.cpp:391-409; conv1d_lc[_res]_f32_gpu kokoro_lc.cpp:81-109) ---- */
-/* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu */
+/* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu.
+ * workspace (optional, may be NULL): with few output tiles and a long K, K is split across workgroups whose
+ * partial tiles (split * M * N floats past the first 64 KiB) a second kernel sums; calls sharing a workspace
+ * must be stream-ordered */
 int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
-                    int64_t n, int64_t k, int nt, int act, float scale, void* stream);
+                    int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 /* channel-last conv1d: x [L, Ci] (Ci % 16 == 0), w [Co, K, Ci] -> out [Lo, Co] = (conv(pre(x)) + b + res) * scale;
  * pre = optional affine [3, Ci] (mean, scale, beta) then snake(alpha) (pre 1) / leaky(slope) (pre 2) */
 int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,

@@ -48,6 +48,11 @@ struct GemmParams {
   float slope;
   // optional per-(128-row chunk, channel) (mean, M2) of the output, [ceil(M / 128), N, 2] (conv tap kernel)
   float* stats;
+  // split-K across workgroups (gemmSplitKKernel): grid z = split, K range [z kSplit, (z + 1) kSplit); with
+  // splitk > 1 the raw tile sums go to part [splitk][M][N] and gemmSplitReduceKernel applies the epilogue
+  float* part;
+  int64_t kSplit;
+  int splitk;
 };
 
 constexpr int BK = 16;
@@ -355,6 +360,9 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
   const GridItem gi = xcdOrder();  // column blocks of one row block share an XCD's L2
   const int64_t m0 = static_cast<int64_t>(gi.y) * BM, n0 = static_cast<int64_t>(gi.x) * BN;
   const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
+  // this workgroup's K range (the whole K without a split)
+  const int64_t kb = p.splitk > 1 ? gi.z * p.kSplit : 0;
+  const int64_t ke = p.splitk > 1 ? min<int64_t>(kb + p.kSplit, p.k) : p.k;
 
   // two register sets: the next stage's tile is stored to LDS while the one after it is still in flight
   v4f ra[2][A4], rb[2][B4];
@@ -363,19 +371,19 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
     for (int i = 0; i < A4; ++i) {
       const int idx = tid + i * NT, row = idx >> 4, kq = (idx & 15) * 4;
       ra[i] = *reinterpret_cast<const v4f*>(p.a + min<int64_t>(m0 + row, lastRow) * p.lda +
-                                            min<int64_t>(k0 + kq, p.k - 4));
+                                            min<int64_t>(k0 + kq, ke - 4));
     }
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
       const int idx = tid + i * NT;
       if constexpr (BMODE == B_NN) {
         const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
-        rb[i] = *reinterpret_cast<const v4f*>(p.b + min<int64_t>(k0 + kr, p.k - 1) * p.ldb +
+        rb[i] = *reinterpret_cast<const v4f*>(p.b + min<int64_t>(k0 + kr, ke - 1) * p.ldb +
                                               min<int64_t>(n0 + nq, p.n - 4));
       } else {
         const int col = idx >> 4, kq = (idx & 15) * 4;
         rb[i] = *reinterpret_cast<const v4f*>(p.b + min<int64_t>(n0 + col, lastCol) * p.ldb +
-                                              min<int64_t>(k0 + kq, p.k - 4));
+                                              min<int64_t>(k0 + kq, ke - 4));
       }
     }
   };
@@ -387,18 +395,18 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
     for (int i = 0; i < A4; ++i) {
       const int idx = tid + i * NT, row = idx >> 4, kq = (idx & 15) * 4;
       const int slice = kq >> 4, slot = (kq >> 2) & 3;
-      As[(buf * 4 + slice) * BM * 4 + row * 4 + (slot ^ ((row >> 2) & 3))] = !KTAIL || k0 + kq < p.k ? ra[i] : zero;
+      As[(buf * 4 + slice) * BM * 4 + row * 4 + (slot ^ ((row >> 2) & 3))] = !KTAIL || k0 + kq < ke ? ra[i] : zero;
     }
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
       const int idx = tid + i * NT;
       if constexpr (BMODE == B_NN) {
         const int kr = idx / (BN / 4), nq = (idx % (BN / 4)) * 4;
-        *reinterpret_cast<v4f*>(Bsf + buf * KS * LDBK + kr * LDBK + nq) = !KTAIL || k0 + kr < p.k ? rb[i] : zero;
+        *reinterpret_cast<v4f*>(Bsf + buf * KS * LDBK + kr * LDBK + nq) = !KTAIL || k0 + kr < ke ? rb[i] : zero;
       } else {
         const int col = idx >> 4, kq = (idx & 15) * 4;
         const int slice = kq >> 4, slot = (kq >> 2) & 3;
-        Bsv[(buf * 4 + slice) * BN * 4 + col * 4 + (slot ^ ((col >> 2) & 3))] = !KTAIL || k0 + kq < p.k ? rb[i] : zero;
+        Bsv[(buf * 4 + slice) * BN * 4 + col * 4 + (slot ^ ((col >> 2) & 3))] = !KTAIL || k0 + kq < ke ? rb[i] : zero;
       }
     }
   };
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int64_t stages = (p.k + KS - 1) / KS;
+  const int64_t stages = (ke - kb + KS - 1) / KS;
   auto stage = [&](int64_t st, int buf, v4f (&ra_next)[A4], v4f (&rb_next)[B4], v4f (&ra_far)[A4],
                    v4f (&rb_far)[B4]) {
     v4f af[2][TM];
@@ -444,7 +452,7 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
     }
     // unconditional, clamped to the last stage (a load or store behind a branch makes the compiler's wait
     // counting assume the path without it, i.e. wait for the loads just issued before every LDS store)
-    gload(min<int64_t>(st + 2, stages - 1) * KS, ra_far, rb_far);
+    gload(kb + min<int64_t>(st + 2, stages - 1) * KS, ra_far, rb_far);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -454,14 +462,14 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][i][q], bq[g][q][j], acc[i][j], 0, 0, 0);
-    sstore(buf ^ 1, min<int64_t>(st + 1, stages - 1) * KS, ra_next, rb_next);  // last stage: unread copy
+    sstore(buf ^ 1, kb + min<int64_t>(st + 1, stages - 1) * KS, ra_next, rb_next);  // last stage: unread copy
     __syncthreads();
   };
   // stage st computes from LDS buffer st & 1, stores stage st + 1 (register set (st + 1) & 1) and has stage st + 2
   // in flight into register set st & 1; pairs of stages with no branch inside, an odd last stage peeled
-  gload(0, ra[0], rb[0]);
-  sstore(0, 0, ra[0], rb[0]);
-  gload(min<int64_t>(1, stages - 1) * KS, ra[1], rb[1]);
+  gload(kb, ra[0], rb[0]);
+  sstore(0, kb, ra[0], rb[0]);
+  gload(kb + min<int64_t>(1, stages - 1) * KS, ra[1], rb[1]);
   __syncthreads();
   int64_t st = 0;
   for (; st + 1 < stages; st += 2) {
@@ -489,6 +497,17 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
     const int o = row * BN + c0 + c;
     v[c] = ((red[o] + red[BM * BN + o]) + red[2 * BM * BN + o]) + red[3 * BM * BN + o];
   }
+  if (p.splitk > 1) {  // raw sums of this K range; the reduction applies the epilogue
+    float* pp = p.part + static_cast<int64_t>(gi.z) * p.m * p.n;
+    if (grow <= lastRow) {
+#pragma unroll
+      for (int c = 0; c < PER; ++c) {
+        const int64_t gcol = n0 + c0 + c;
+        if (gcol <= lastCol) pp[grow * p.n + gcol] = v[c];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < PER; ++c) {
     const int64_t gcol = min<int64_t>(n0 + c0 + c, lastCol);
@@ -508,6 +527,22 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
       const int64_t gcol = n0 + c0 + c;
       if (gcol <= lastCol) p.c[grow * p.ldc + gcol] = v[c] * p.scale;
     }
+  }
+}
+
+// Split-K reduction of gemmSplitKKernel: c = (act(sum_z part[z] + bias) + res) * scale, the z sum in order.
+__global__ __launch_bounds__(256) void gemmSplitReduceKernel(GemmParams p) {
+  const int64_t total = p.m * p.n;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = i / p.n, col = i - row * p.n;
+    float x = 0.0f;
+    for (int z = 0; z < p.splitk; ++z) x += p.part[z * total + i];
+    x += p.bias ? p.bias[col] : 0.0f;
+    if (p.act == ACT_RELU) x = fmaxf(x, 0.0f);
+    else if (p.act == ACT_GELU) x = geluTanh(x);
+    if (p.res) x += p.res[row * p.ldr + col];
+    p.c[row * p.ldc + col] = x * p.scale;
   }
 }
 
@@ -752,7 +787,7 @@ using lkd::GemmParams;
 // Tile choice: 128x128 when it still yields a few hundred workgroups, else 64x64 (small M, e.g. ALBERT at
 // T = 59 or the MNIST layers).
 template <int AM, int BMODE>
-static void launchGemm(const GemmParams& p, hipStream_t s) {
+static void launchGemm(GemmParams p, hipStream_t s, void* ws = nullptr, int64_t wsBytes = 0) {
   const int64_t big = static_cast<int64_t>(ceilDiv(p.m, 128)) * ceilDiv(p.n, 128);
   const bool aligned = ((reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.b)) & 15) == 0 &&
                        p.k % 4 == 0 && p.lda % 4 == 0 && p.ldb % 4 == 0 && p.k >= 4 &&
@@ -766,19 +801,38 @@ static void launchGemm(const GemmParams& p, hipStream_t s) {
       hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
   } else if (AM == lkd::A_ROWMAJOR && aligned) {
     // few output tiles: K split over the waves of a workgroup; 32-column tiles when 64 would leave CUs idle
-    if (static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 192) {
-      dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
+    const bool wide = static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 192;
+    const int64_t tiles = static_cast<int64_t>(ceilDiv(p.n, wide ? 64 : 32)) * ceilDiv(p.m, 64);
+    // and across workgroups when the grid still leaves CUs idle and K is long: 64-aligned K ranges of at least
+    // 256, partial tiles in the workspace past its 64 KiB counter area, summed by gemmSplitReduceKernel
+    int split = 1;
+    if (ws && tiles < 128 && p.k >= 512) {
+      split = static_cast<int>(std::min<int64_t>({8, 512 / tiles, p.k / 256}));
+      while (split > 1 && 65536 + static_cast<int64_t>(split) * p.m * p.n * 4 > wsBytes) --split;
+      split = std::max(split, 1);
+    }
+    if (split > 1) {
+      p.kSplit = ((p.k + split - 1) / split + 63) / 64 * 64;
+      split = static_cast<int>((p.k + p.kSplit - 1) / p.kSplit);
+      p.splitk = split;
+      p.part = reinterpret_cast<float*>(static_cast<char*>(ws) + 65536);
+    }
+    const dim3 grid(ceilDiv(p.n, wide ? 64 : 32), ceilDiv(p.m, 64), static_cast<unsigned>(split));
+    if (wide) {
       if (p.k % 64)
         hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE, true>), grid, dim3(lkd::NT), 0, s, p);
       else
         hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, BMODE, false>), grid, dim3(lkd::NT), 0, s, p);
     } else {
-      dim3 grid(ceilDiv(p.n, 32), ceilDiv(p.m, 64));
       if (p.k % 64)
         hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE, true>), grid, dim3(lkd::NT), 0, s, p);
       else
         hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, BMODE, false>), grid, dim3(lkd::NT), 0, s, p);
     }
+    if (split > 1)
+      hipLaunchKernelGGL(lkd::gemmSplitReduceKernel,
+                         dim3(static_cast<unsigned>(std::min<int64_t>((p.m * p.n + 255) / 256, 8192))), dim3(256), 0,
+                         s, p);
   } else {
     dim3 grid(ceilDiv(p.n, 64), ceilDiv(p.m, 64));
     hipLaunchKernelGGL((lkd::gemmMfmaKernel<64, 64, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
@@ -800,7 +854,8 @@ extern "C" {
 
 // out[M, N] = act(A[M, K] . B + bias) + res, then * scale. nt: B is given as B^T [N, K].
 int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
-                    int64_t n, int64_t k, int nt, int act, float scale, void* stream) {
+                    int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
   if (m <= 0 || n <= 0 || k <= 0) return m >= 0 && n >= 0 && k >= 0 ? 0 : 1;
   lkd::GemmParams p = lkh::baseParams();
   p.a = a;
@@ -818,8 +873,8 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
   p.act = act;
   p.scale = scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s);
-  else lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NN>(p, s);
+  if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s, workspace, workspace_bytes);
+  else lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NN>(p, s, workspace, workspace_bytes);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -89,7 +89,7 @@ void runGemm(ExecCtx& ctx, const KernelArgs& a) {
     return;
   }
   status(ctx, lk_hip_gemm_f32(P<float>(a, 0), P<float>(a, 1), bias, res, out, m, n, k, NT ? 1 : 0, ACT, 1.0f,
-                              ctx.stream),
+                              ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
          "gemm: launch failed");
 }
 

@@ -259,7 +259,7 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (h < 1 || h > 256 || t < 1) return 1;
   if (!workspace || workspaceBytes < t * 8 * h * 4) return 3;
   float* g = static_cast<float*>(workspace);
-  int rc = lk_hip_gemm_f32(x, wih, b, nullptr, g, t, 8 * h, in, 1, 0, 1.0f, stream);
+  int rc = lk_hip_gemm_f32(x, wih, b, nullptr, g, t, 8 * h, in, 1, 0, 1.0f, nullptr, 0, stream);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;

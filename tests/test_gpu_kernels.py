@@ -60,6 +60,24 @@ def test_gemm_epilogues(gpu, act):
         close(lk.ops.gemm_bias_relu_f32_gpu(A, B, BI), ref, 1e-5)
 
 
+@pytest.mark.parametrize("m,n,k", [(59, 768, 2048), (59, 2304, 768), (487, 768, 2048), (33, 100, 1000), (1, 64, 4096)])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu", "res"])
+def test_gemm_split_k(gpu, m, n, k, act):
+    """Few output tiles and a long K: K is split across workgroups (64-aligned ranges, partial tiles in the
+    workspace) and a reduction applies the epilogue; same result as the one-pass kernel within f32 rounding."""
+    lk = gpu
+    a, b, bias, r = rng.standard_normal((m, k)), rng.standard_normal((k, n)) / np.sqrt(k), rng.standard_normal(n), rng.standard_normal((m, n))
+    A, B, BI, R = G(lk, a), G(lk, b), G(lk, bias), G(lk, r)
+    if act == "res":
+        got = lk.ops.gemm_steel_f32_gpu(A, B, BI, residual=R)
+        ref = K.gemm(a, b, bias, residual=r)
+    else:
+        got = lk.ops.gemm_steel_f32_gpu(A, B, BI, act=act)
+        ref = K.gemm(a, b, bias, act=act)
+    close(got, ref, 1e-5)
+    close(lk.ops.gemm_f32_gpu_mps(A, B), K.gemm(a, b), 1e-5)
+
+
 def test_mnist_mlp_plumbing(gpu):
     lk = gpu
     x, (w1, b1, w2, b2) = mnist.mlp_inputs(1)
