@@ -147,15 +147,19 @@ __device__ __forceinline__ GridItem xcdOrder() {
 // the rows of residue class rho of the dilation d from 128 y on: clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows
 // (d = 1: the plain 128-row chunks; chunks with no rows are never read). Two passes in double, as instance norm
 // with a biased variance: mean = sum n_i m_i / L, then M2 = sum (M2_i + n_i (m_i - mean)^2), var = M2 / L.
-// Workgroup of 256 = 16 channels x 16 chunk slices: a slice row reads 16 consecutive channels (128 B), the
-// slices' partial sums merge through LDS in a fixed order. Small workgroups, so the kernel still schedules
-// while long conv kernels hold most of the chip on other streams.
+// Workgroup of 256 = CH channels x (256 / CH) chunk slices; the slices' partial sums merge through LDS in a fixed
+// order. Many short slices rather than few long ones: the chunk loads are independent, so a slice's time is its
+// number of load round trips, and the kernel sits on the dependency chain between two convs (a generator tensor
+// has ~2300 chunks per channel). Small workgroups, so it still schedules while long conv kernels hold most of the
+// chip on other streams.
+template <int CH>
 __device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, const float* __restrict__ gb,
                                                   float* __restrict__ af, int64_t l, int64_t c, int d,
                                                   int64_t chunks, int64_t creal, float eps) {
-  __shared__ double red[16][16];
-  const int cl = threadIdx.x & 15, sl = threadIdx.x >> 4;
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 16 + cl;
+  constexpr int SL = 256 / CH;
+  __shared__ double red[SL][CH];
+  const int cl = threadIdx.x % CH, sl = threadIdx.x / CH;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * CH + cl;
   const bool live = ch < creal && ch < c;
   const int64_t total = static_cast<int64_t>(d) * chunks;
   const float2* sp = reinterpret_cast<const float2*>(st);
@@ -168,10 +172,10 @@ __device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, 
   if (live) {
     int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
 #pragma unroll 4
-    for (int64_t i = sl; i < total; i += 16) {
+    for (int64_t i = sl; i < total; i += SL) {
       const double n = rows(rho, yy);
       if (n > 0.0) s += static_cast<double>(sp[i * c + ch].x) * n;
-      yy += 16;
+      yy += SL;
       while (yy >= chunks) {
         yy -= chunks;
         ++rho;
@@ -181,22 +185,21 @@ __device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, 
   red[sl][cl] = s;
   __syncthreads();
   double tot = 0.0;
-#pragma unroll
-  for (int w = 0; w < 16; ++w) tot += red[w][cl];
+  for (int w = 0; w < SL; ++w) tot += red[w][cl];
   const double mean = tot / static_cast<double>(l);
   __syncthreads();
   double m2 = 0.0;
   if (live) {
     int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
 #pragma unroll 4
-    for (int64_t i = sl; i < total; i += 16) {
+    for (int64_t i = sl; i < total; i += SL) {
       const double n = rows(rho, yy);
       if (n > 0.0) {
         const float2 v = sp[i * c + ch];
         const double dm = static_cast<double>(v.x) - mean;
         m2 += static_cast<double>(v.y) + n * dm * dm;
       }
-      yy += 16;
+      yy += SL;
       while (yy >= chunks) {
         yy -= chunks;
         ++rho;
@@ -210,8 +213,7 @@ __device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, 
       af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
     } else {
       double M2 = 0.0;
-#pragma unroll
-      for (int w = 0; w < 16; ++w) M2 += red[w][cl];
+      for (int w = 0; w < SL; ++w) M2 += red[w][cl];
       const float var = static_cast<float>(M2 / static_cast<double>(l));
       af[ch] = static_cast<float>(mean);
       af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
