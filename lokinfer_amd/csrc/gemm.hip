@@ -537,7 +537,9 @@ __global__ __launch_bounds__(256) void gemmSplitReduceKernel(GemmParams p) {
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t row = i / p.n, col = i - row * p.n;
     float x = 0.0f;
-    for (int z = 0; z < p.splitk; ++z) x += p.part[z * total + i];
+#pragma unroll
+    for (int z = 0; z < 8; ++z)  // splitk <= 8, predicated so the loads are issued together
+      if (z < p.splitk) x += p.part[z * total + i];
     x += p.bias ? p.bias[col] : 0.0f;
     if (p.act == ACT_RELU) x = fmaxf(x, 0.0f);
     else if (p.act == ACT_GELU) x = geluTanh(x);

@@ -16,7 +16,7 @@
 // group shift) are staged [row][4 slots] (swizzled by (row >> 2) & 3) and U's N x 16 rows k-major; the point's
 // GEMM accumulates over the groups with the A rows shifted by g, and after a point's last chunk AT[j, xi] folds
 // it into the M output accumulators. Small grids split the steps over workgroups (split-K) and sum the partial
-// rows in winoSplitReduceKernel.
+// rows in winoSplitReduceKernel (statistics then from the channel-stats kernel).
 #include "common.h"
 #include "lokinfer_hip.h"
 
@@ -317,54 +317,23 @@ __global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
   }
 }
 
-// Split-K reduction (dilation 1): out = (sum_s part[s] + bias [+ res]) * scale over a 128-row x 64-channel block
-// per workgroup (4 row groups of 32 rows x 64 channels), in split order; with stats, the block's (mean, M2) per
-// channel, which is the channel_stats_lc layout [chunk][C][2].
+// Split-K reduction (dilation 1): out = (sum_s part[s] + bias [+ res]) * scale, the s sum in split order; one
+// float4 of one row per thread, grid-stride (Co % 64 == 0, so a float4 never straddles two rows).
 __global__ __launch_bounds__(256) void winoSplitReduceKernel(const float* __restrict__ part, int split,
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ res, float* __restrict__ out,
-                                                            float* __restrict__ stats, int64_t lo, int64_t co,
-                                                            float scale) {
-  __shared__ float red[4][64];
-  const int cl = threadIdx.x & 63, rg = threadIdx.x >> 6;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + cl;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kWinoRows;
-  const float b = bias[col];
-  float v[32];
+                                                            int64_t lo, int64_t co, float scale) {
+  const int64_t n4 = lo * co / 4, plane = lo * co;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t e = 4 * i, col = e % co;
+    v4w sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const int64_t row = min<int64_t>(r0 + rg * 32 + i, lo - 1);
-    float sum = 0.0f;
-    for (int s = 0; s < split; ++s) sum += part[(static_cast<int64_t>(s) * lo + row) * co + col];
-    float o = sum + b;
-    if (res) o += res[row * co + col];
-    v[i] = o * scale;
-  }
-#pragma unroll
-  for (int i = 0; i < 32; ++i)
-    if (r0 + rg * 32 + i < lo) out[(r0 + rg * 32 + i) * co + col] = v[i];
-  if (!stats) return;
-  const int n = static_cast<int>(min<int64_t>(kWinoRows, lo - r0));
-  float s1 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i)
-    if (rg * 32 + i < n) s1 += v[i];
-  red[rg][cl] = s1;
-  __syncthreads();
-  const float mean = (red[0][cl] + red[1][cl] + red[2][cl] + red[3][cl]) / static_cast<float>(n);
-  __syncthreads();
-  float s2 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const float dv = v[i] - mean;
-    if (rg * 32 + i < n) s2 += dv * dv;
-  }
-  red[rg][cl] = s2;
-  __syncthreads();
-  if (rg == 0) {
-    float* st = stats + (static_cast<int64_t>(blockIdx.y) * co + col) * 2;
-    st[0] = mean;
-    st[1] = red[0][cl] + red[1][cl] + red[2][cl] + red[3][cl];
+    for (int sp = 0; sp < 8; ++sp)  // split <= 8
+      if (sp < split) sum += *reinterpret_cast<const v4w*>(part + sp * plane + e);
+    v4w o = sum + *reinterpret_cast<const v4w*>(bias + col);
+    if (res) o += *reinterpret_cast<const v4w*>(res + e);
+    *reinterpret_cast<v4w*>(out + e) = o * scale;
   }
 }
 
@@ -441,9 +410,13 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2>), grid, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3>), grid, dim3(256), 0, s, p);
-  if (split > 1)
-    hipLaunchKernelGGL(lkd::winoSplitReduceKernel, dim3(static_cast<unsigned>(co / 64), lkh::ceilDiv(lo, 128)),
-                       dim3(256), 0, s, part, split, bias, res, out, stats, lo, co, scale);
+  if (split > 1) {
+    hipLaunchKernelGGL(lkd::winoSplitReduceKernel,
+                       dim3(static_cast<unsigned>(std::min<int64_t>((lo * co / 4 + 255) / 256, 8192))), dim3(256), 0,
+                       s, part, split, bias, res, out, lo, co, scale);
+    // dilation 1: the statistics are the plain 128-row chunks of the output
+    if (stats && lk_hip_channel_stats_lc_f32(out, stats, lo, co, stream)) return 2;
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
