@@ -54,9 +54,13 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
  * pre = optional affine [3, Ci] (mean, scale, beta) then snake(alpha) (pre 1) / leaky(slope) (pre 2) */
 int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
                          int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
-                         const float* affine, const float* alpha, int pre, float slope, float* stats, void* stream);
+                         const float* affine, const float* alpha, int pre, float slope, float* stats, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 /* stats (optional): per-(128-row chunk, channel) (mean, M2) of out, [ceil(Lo / 128), Co, 2], the layout of
- * lk_hip_channel_stats_lc_f32; computed in the conv's epilogue when its tiles are 128 rows, else by a stats pass. */
+ * lk_hip_channel_stats_lc_f32; computed in the conv's epilogue when its tiles are 128 rows, else by a stats pass.
+ * workspace (optional, may be NULL): with few output tiles the 16-channel chunks are split over workgroups whose
+ * partial tiles (split * Lo * Co floats past the first 64 KiB) a second kernel sums; calls sharing a workspace
+ * must be stream-ordered */
 
 /* ---- GEMV (reference: gemv4*_f32_gpu transformer_gpu.cpp:233-251; gemv_rows / gemv1_bias kokoro_lc.cpp:227-267) */
 int lk_hip_gemv_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t n,

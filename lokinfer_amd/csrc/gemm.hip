@@ -588,8 +588,11 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   const int64_t m0 = static_cast<int64_t>(gi.y) * BM;
   const int64_t n0 = static_cast<int64_t>(gi.x) * BN;
   const int64_t ci = p.convCi;
-  const int chunks = static_cast<int>(ci / BK);
-  const int steps = chunks * taps;
+  // split-K (grid z): this workgroup's 16-channel chunks [cb, ce); the whole range without a split
+  const int allChunks = static_cast<int>(ci / BK);
+  const int cb = p.splitk > 1 ? static_cast<int>(gi.z * p.kSplit) : 0;
+  const int ce = p.splitk > 1 ? min(allChunks, static_cast<int>(cb + p.kSplit)) : allChunks;
+  const int steps = (ce - cb) * taps;
   const int64_t rowBase = m0 - p.convPad;  // input row of halo row 0
   const int cq = (tid & 3) * 4;            // the 4 channels of a chunk this thread stages (same for every slot)
   const int lastRow = static_cast<int>(p.convL - 1);
@@ -660,7 +663,7 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
   // B for step s = chunk * taps + kk: w[co][kk][chunk * 16 .. +15] (w is [Co, K, Ci] row-major = ldb K * Ci);
   // columns past N read the last valid row (never stored).
   auto loadB = [&](int s) {
-    const int chunk = s / taps, kk = s - chunk * taps;
+    const int chunk = cb + s / taps, kk = s % taps;
     const float* src = p.b + static_cast<int64_t>(kk) * ci + static_cast<int64_t>(chunk) * BK + cq;
 #pragma unroll
     for (int i = 0; i < B4; ++i) {
@@ -677,16 +680,16 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
     }
   };
 
-  loadHalo(0);
-  storeHalo(0, 0);
+  loadHalo(cb);
+  storeHalo(0, cb);
   loadB(0);
   storeB(0);
   __syncthreads();
   const int lrow = lane & 31, lk = lane >> 5;
   const int aRow = wm * WTM + lrow, bRow = wn * WTN + lrow;
   for (int s = 0; s < steps; ++s) {
-    const int chunk = s / taps, kk = s - chunk * taps;
-    const int hbuf = chunk & 1, bbuf = s & 1;
+    const int lc = s / taps, kk = s - lc * taps, chunk = cb + lc;
+    const int hbuf = lc & 1, bbuf = s & 1;
     const bool more = s + 1 < steps;
     const bool newChunk = more && kk == taps - 1;
     const int shift = kk * p.convDil;
@@ -719,6 +722,21 @@ __global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, i
     __syncthreads();
   }
 
+  if (p.splitk > 1) {  // raw partial tile of this chunk range; gemmSplitReduceKernel applies the epilogue
+    float* pp = p.part + static_cast<int64_t>(gi.z) * p.m * p.n;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (row < p.m && col < p.n) pp[row * p.n + col] = acc[i][j][r];
+        }
+      }
+    return;
+  }
   storeTile<TM, TN>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lrow, lk);
   if (BM == 128 && p.stats) {
     // Per-(128-row chunk, channel) (mean, M2) of the stored output, two passes over the registers: this tile is
@@ -885,7 +903,8 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
 // then snake(alpha [Ci]) (pre = 1) or leaky(slope) (pre = 2); zero padding applies after pre.
 int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
                          int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
-                         const float* affine, const float* alpha, int pre, float slope, float* stats, void* stream) {
+                         const float* affine, const float* alpha, int pre, float slope, float* stats, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
   if (ci % 16 != 0 || stride < 1 || dilation < 1 || padding < 0) return 1;
   const int64_t lo = (l + 2 * padding - static_cast<int64_t>(dilation) * (kw - 1) - 1) / stride + 1;
   if (lo <= 0 || co <= 0) return lo == 0 ? 0 : 1;
@@ -925,9 +944,29 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
       hipLaunchKernelGGL((lkd::convTapKernel<128, 128>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
                          static_cast<int>(128 + reach));
     } else {  // few output tiles (decoder / F0-N at frame rate): 64 x 64 tiles fill more of the 256 CUs
-      dim3 grid(lkh::ceilDiv(co, 64), lkh::ceilDiv(lo, 64));
+      // and split the 16-channel chunks over workgroups when even those leave CUs idle (at least 2 chunks per
+      // split, partial tiles in the workspace past its 64 KiB counter area, epilogue in gemmSplitReduceKernel)
+      const int64_t base = static_cast<int64_t>(lkh::ceilDiv(co, 64)) * lkh::ceilDiv(lo, 64);
+      const int64_t chunks = ci / lkd::BK;
+      int split = 1;
+      if (workspace && base < 256 && chunks >= 4) {
+        split = static_cast<int>(std::min<int64_t>({8, 512 / base, chunks / 2}));
+        while (split > 1 && 65536 + static_cast<int64_t>(split) * lo * co * 4 > workspace_bytes) --split;
+        split = std::max(split, 1);
+      }
+      if (split > 1) {
+        p.kSplit = (chunks + split - 1) / split;
+        split = static_cast<int>((chunks + p.kSplit - 1) / p.kSplit);
+        p.splitk = split;
+        p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 65536);
+      }
+      dim3 grid(lkh::ceilDiv(co, 64), lkh::ceilDiv(lo, 64), static_cast<unsigned>(split));
       hipLaunchKernelGGL((lkd::convTapKernel<64, 64>), grid, dim3(lkd::NT), 0, s, p, static_cast<int>(kw),
                          static_cast<int>(64 + reach));
+      if (split > 1)
+        hipLaunchKernelGGL(lkd::gemmSplitReduceKernel,
+                           dim3(static_cast<unsigned>(std::min<int64_t>((lo * co + 255) / 256, 8192))), dim3(256), 0,
+                           s, p);
     }
   } else {
     lkh::launchGemm<lkd::A_CONV, lkd::B_NT>(p, s);

@@ -146,7 +146,8 @@ void runConvLc(ExecCtx& ctx, const KernelArgs& a) {
   const float* res = RES ? P<float>(a, 3) : nullptr;
   float* out = P<float>(a, RES ? 4 : 3);
   status(ctx, lk_hip_conv1d_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), res, out, l, ci, co, kw, str, pad,
-                                   dil, scale, nullptr, nullptr, 0, 0.0f, nullptr, ctx.stream),
+                                   dil, scale, nullptr, nullptr, 0, 0.0f, nullptr, ctx.workspace,
+                                   static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
          "conv1d_lc: invalid configuration");
 }
 
@@ -175,7 +176,8 @@ void runConvActLc(ExecCtx& ctx, const KernelArgs& a) {
   float* out = P<float>(a, RES ? 6 : 5);
   float* stats = STATS ? P<float>(a, RES ? 7 : 6) : nullptr;
   status(ctx, lk_hip_conv1d_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), res, out, l, ci, co, kw, str, pad,
-                                   dil, scale, P<float>(a, 3), P<float>(a, 4), act, slope, stats, ctx.stream),
+                                   dil, scale, P<float>(a, 3), P<float>(a, 4), act, slope, stats, ctx.workspace,
+                                   static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
          "conv1d_act_lc: invalid configuration");
 }
 
