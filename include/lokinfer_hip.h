@@ -83,6 +83,24 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
                                 int64_t workspace_bytes, void* stream);
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
                         void* stream);
+/* chunked prefill / generate (reference kv_write_rows_f32_gpu, attention_cache[_sg]_f32_gpu,
+ * python/lokinfer/ops/transformer.py:239-268, 348-351; kernels/gpu/kokoro_lc.cpp:887-965): the T rows of qkv sit at
+ * positions pos..pos+T-1 (pos a device i64[1]). kv_write_rows writes k, v (+ bias) there (rows >= cap dropped);
+ * attention_cache attends query i causally over cache rows 0..pos+i (q bias added, head_dim 64; a query at
+ * position >= cap gets NaN). The reference rejects pos + T > cap on the host; here pos lives on the device. */
+int lk_hip_kv_write_rows_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias,
+                             int64_t t, int64_t d, int64_t cap, void* stream);
+int lk_hip_attention_cache_f32(const float* qkv, const float* kc, const float* vc, const int64_t* pos,
+                               const float* bias, float* out, int64_t t, int heads, int64_t cap, void* stream);
+/* split-K partials and their consumer (reference gemm_splitk_f32_gpu / add_bias_layernorm2_sk_f32_gpu,
+ * transformer_gpu.cpp:253-320, python/lokinfer/ops/transformer.py:441-472): part[s] = A[:, sK/S:(s+1)K/S] .
+ * B[sK/S:(s+1)K/S, :] for s < splits, part f32[S, M, N], K % (16 S) == 0, K and N % 4 == 0, 16-byte aligned;
+ * then sum = part[0] + ... + part[S-1] + bias + r, out = LN(sum), cols <= 2048 */
+int lk_hip_gemm_splitk_f32(const float* a, const float* b, float* part, int64_t m, int64_t n, int64_t k, int splits,
+                           void* stream);
+int lk_hip_add_bias_ln_sk_f32(const float* parts, int64_t splits, const float* bias, const float* r,
+                              const float* gamma, const float* beta, float* sum, float* out, int64_t rows,
+                              int64_t cols, float eps, void* stream);
 
 /* ---- fused batch-1 decode layer (backend ops; one layer's reference sequence gemv4*_f32_gpu ->
  * attention_decode_split_f32_gpu -> gemv4 -> add_bias_layernorm2_f32_gpu, transformer_gpu.cpp:122-251,
@@ -125,6 +143,8 @@ int lk_hip_istft_lc_f32(const float* x, float* out, int64_t l, int64_t cpad, int
  *      GPT-2 argmax in Python models/gpt2.py:348-359) ---- */
 int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* table2, const int64_t* ids2, float* out,
                          int64_t n, int64_t d, int64_t rows, int64_t rows2, void* stream);
+/* out[i] = pos[0] + i (reference host kernel arange_offset_i64_cpu, kernels/cpu/decode.cpp:221) */
+int lk_hip_arange_offset_i64(const int64_t* pos, int64_t* out, int64_t n, void* stream);
 int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
                       int64_t workspace_bytes, void* stream);
 

@@ -38,8 +38,12 @@ class _Entry:
             with torch.cuda.graph(self.graph):
                 out = fn(*self.inputs)
         self.outputs = [out] if self.single else list(out)
+        self.fresh = not use_graph  # eager: the warm-up already computed the first call's outputs
 
     def run(self, args):
+        if self.fresh:
+            self.fresh = False
+            return self.outputs
         for s, a in zip(self.inputs, args):
             s.t.copy_(a.t, non_blocking=True)
         if self.graph is not None:

@@ -4,6 +4,8 @@
 //
 //   lk_hip_embedding_f32   out[i] = table[ids[i]] (+ table2[ids2[i]])   ids out of range -> row of NaN
 //   lk_hip_argmax_f32      per row: index of the first maximum (int64)
+//   lk_hip_arange_offset_i64  out[i] = pos[0] + i (position ids of a chunk of new tokens; reference host kernel
+//                          arange_offset_i64_cpu, kernels/cpu/decode.cpp:221, python/lokinfer/ops/transformer.py:272-282)
 #include "common.h"
 
 namespace lkd {
@@ -77,9 +79,21 @@ __global__ __launch_bounds__(256) void argmaxKernel(const float* __restrict__ x,
   }
 }
 
+__global__ void arangeOffsetKernel(const int64_t* __restrict__ pos, int64_t* __restrict__ out, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = *pos + i;
+}
+
 }  // namespace lkd
 
 extern "C" {
+
+int lk_hip_arange_offset_i64(const int64_t* pos, int64_t* out, int64_t n, void* stream) {
+  if (n <= 0) return n == 0 ? 0 : 1;
+  hipLaunchKernelGGL(lkd::arangeOffsetKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), pos, out, n);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* table2, const int64_t* ids2, float* out,
                          int64_t n, int64_t d, int64_t rows, int64_t rows2, void* stream) {
@@ -142,6 +156,13 @@ void runArgmax(ExecCtx& ctx, const KernelArgs& a) {
     ctx.error = "argmax: launch failed";
 }
 
+// arange_offset_i64_gpu(pos i64[1]) -> i64[length]; attr length
+void runArangeOffset(ExecCtx& ctx, const KernelArgs& a) {
+  LK_REQUIRE(ctx, a.ints[0] == 1, "arange_offset: pos must be i64[1]");
+  if (lk_hip_arange_offset_i64(P<int64_t>(a, 0), P<int64_t>(a, 1), a.ints[1], ctx.stream))
+    ctx.error = "arange_offset: launch failed";
+}
+
 }  // namespace
 
 void registerFrontendKernels() {
@@ -149,6 +170,7 @@ void registerFrontendKernels() {
   registerKernel({"embedding_f32_gpu", G, runEmbedding, 2, 1});
   registerKernel({"embedding2_add_f32_gpu", G, runEmbedding2, 4, 1});
   registerKernel({"argmax_f32_gpu", G, runArgmax, 1, 1});
+  registerKernel({"arange_offset_i64_gpu", G, runArangeOffset, 1, 1});
 }
 
 }  // namespace lkh

@@ -898,6 +898,47 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
+// Split-K partials part[s] = A[:, s K/S : (s+1) K/S] . B[s K/S : (s+1) K/S, :] for s < splits, part [S, M, N]; the
+// consumer sums the planes (lk_hip_add_bias_ln_sk_f32). K % (16 splits) == 0, K, N % 4 == 0, 16-byte aligned.
+int lk_hip_gemm_splitk_f32(const float* a, const float* b, float* part, int64_t m, int64_t n, int64_t k, int splits,
+                           void* stream) {
+  if (splits < 1 || splits > 64 || k <= 0 || k % (16 * splits) != 0 || n % 4 != 0 || n <= 0) return 1;
+  if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) != 0) return 1;
+  if (m <= 0) return m == 0 ? 0 : 1;
+  lkd::GemmParams p = lkh::baseParams();
+  p.a = a;
+  p.b = b;
+  p.c = part;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.lda = k;
+  p.ldb = n;
+  p.ldc = n;
+  p.ldr = n;
+  if (splits > 1) {
+    p.splitk = splits;
+    p.kSplit = k / splits;
+    p.part = part;
+  }
+  const int64_t kRange = k / splits;
+  const bool wide = static_cast<int64_t>(lkh::ceilDiv(m, 64)) * lkh::ceilDiv(n, 64) * splits >= 192;
+  const dim3 grid(lkh::ceilDiv(n, wide ? 64 : 32), lkh::ceilDiv(m, 64), static_cast<unsigned>(splits));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (wide) {
+    if (kRange % 64)
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, lkd::B_NN, true>), grid, dim3(lkd::NT), 0, s, p);
+    else
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<64, lkd::B_NN, false>), grid, dim3(lkd::NT), 0, s, p);
+  } else {
+    if (kRange % 64)
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, lkd::B_NN, true>), grid, dim3(lkd::NT), 0, s, p);
+    else
+      hipLaunchKernelGGL((lkd::gemmSplitKKernel<32, lkd::B_NN, false>), grid, dim3(lkd::NT), 0, s, p);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
 // Channel-last conv1d as an implicit GEMM: x [L, Ci] (Ci % 16 == 0), w [Co, K, Ci], bias [Co] (or null),
 // res [Lo, Co] (or null) -> out [Lo, Co] = (conv(pre(x)) + bias + res) * scale; pre = optional affine [3, Ci]
 // then snake(alpha [Ci]) (pre = 1) or leaky(slope) (pre = 2); zero padding applies after pre.

@@ -295,6 +295,123 @@ void runKvWrite(ExecCtx& ctx, const KernelArgs& a) {
          "kv_write: launch failed");
 }
 
+// kv_write_rows_f32_gpu (inout kc, vc): kc[cap, D], vc[cap, D], qkv[T, 3D], pos[1], bias[3D]; no outs. Rows past
+// the cache are dropped on the device (the reference's host check "pos + T exceeds the cache" needs pos on the host).
+void runKvWriteRows(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t cap = it.next(), d = it.next();
+  it.skip(2);
+  const int64_t t = it.next(), d3 = it.next();
+  LK_REQUIRE(ctx, d3 == 3 * d && d % 4 == 0, "kv_write_rows: qkv must be f32[T, 3D] over caches f32[P, D]");
+  status(ctx, lk_hip_kv_write_rows_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
+                                       P<float>(a, 4), t, d, cap, ctx.stream),
+         "kv_write_rows: launch failed");
+}
+
+// attention_cache[_sg]_f32_gpu: qkv[T, 3D], kc[cap, D], vc[cap, D], pos[1], bias[3D] -> out[T, D]; attrs heads[, nsg]
+void runAttnCache(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t t = it.next(), d3 = it.next(), cap = it.next(), d = it.next();
+  it.skip(2 + 1 + 1 + 2);  // vc, pos, bias, out
+  const int heads = static_cast<int>(it.next());
+  LK_REQUIRE(ctx, d3 == 3 * d && d == 64 * heads, "attention_cache: head_dim must be 64, qkv f32[T, 3D]");
+  status(ctx, lk_hip_attention_cache_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
+                                         P<float>(a, 4), P<float>(a, 5), t, heads, cap, ctx.stream),
+         "attention_cache: launch failed");
+}
+
+// attention_gen[2]_f32_gpu (inout kc, vc): same operands as attention_cache. T = 1 -> the split-key decode attention
+// that also writes row pos; T > 1 -> kv_write_rows, then the flash attention over the cache.
+void runAttnGen(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t t = it.next(), d3 = it.next(), cap = it.next(), d = it.next();
+  it.skip(2 + 1 + 1 + 2);
+  const int heads = static_cast<int>(it.next());
+  LK_REQUIRE(ctx, d3 == 3 * d && d == 64 * heads && d % 4 == 0, "attention_gen: head_dim must be 64");
+  if (t == 1) {
+    const int rc = lk_hip_attention_decode_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
+                                               P<float>(a, 4), P<float>(a, 5), cap, heads, cap, 1, ctx.workspace,
+                                               static_cast<int64_t>(ctx.workspaceBytes), ctx.stream);
+    status(ctx, rc, rc == 3 ? "attention_gen: workspace too small" : "attention_gen: launch failed");
+    return;
+  }
+  status(ctx, lk_hip_kv_write_rows_f32(P<float>(a, 1), P<float>(a, 2), P<float>(a, 0), P<int64_t>(a, 3),
+                                       P<float>(a, 4), t, d, cap, ctx.stream),
+         "attention_gen: kv_write_rows failed");
+  if (ctx.error) return;
+  status(ctx, lk_hip_attention_cache_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
+                                         P<float>(a, 4), P<float>(a, 5), t, heads, cap, ctx.stream),
+         "attention_gen: attention_cache failed");
+}
+
+// Split-K pays while the 64 x 64 output tiles leave most of the 256 CUs idle; above that (and for M = 1, where the
+// work is one GEMV) the producer writes one plane and the consumer reads one. The rule is shared by
+// gemm_splitk / gemm_auto_sk and add_bias_layernorm2_sk (reference splitKEffective, transformer_gpu.cpp:253-268,
+// whose threshold is tuned for its own GPU).
+constexpr int64_t kSplitKMaxTiles = 64;
+int64_t splitKPlanes(int64_t m, int64_t n, int64_t splits) {
+  return m > 1 && ((m + 63) / 64) * ((n + 63) / 64) < kSplitKMaxTiles ? splits : 1;
+}
+
+// gemm_splitk / gemm_auto_sk: a[M, K], b[K, N] -> out[S, M, N]; attrs splits, tile. Planes past splitKPlanes are
+// not written (their consumer does not read them).
+template <bool AUTO>
+void runGemmSplitK(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t m = it.next(), k = it.next();
+  LK_REQUIRE(ctx, it.next() == k, "gemm_splitk: inner dimensions differ");
+  const int64_t n = it.next();
+  it.skip(3);
+  const int64_t splits = it.next(), tile = it.next();
+  LK_REQUIRE(ctx, splits >= 1 && k % (16 * splits) == 0, "gemm_splitk: K must be divisible by 16*splits");
+  LK_REQUIRE(ctx, tile == 32 || tile == 64, "gemm_splitk: tile must be 32 or 64");
+  const int64_t planes = splitKPlanes(m, n, splits);
+  if (planes == 1) {
+    if (AUTO && m == 1)
+      status(ctx, lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), nullptr, nullptr, P<float>(a, 2), n, k, 0,
+                                  ctx.workspace, ctx.workspaceBytes, ctx.stream),
+             "gemm_auto_sk: launch failed");
+    else
+      status(ctx, lk_hip_gemm_f32(P<float>(a, 0), P<float>(a, 1), nullptr, nullptr, P<float>(a, 2), m, n, k, 0, 0,
+                                  1.0f, ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
+             "gemm_splitk: launch failed");
+    return;
+  }
+  status(ctx, lk_hip_gemm_splitk_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), m, n, k,
+                                     static_cast<int>(planes), ctx.stream),
+         "gemm_splitk: launch failed (K, N % 4 and 16-byte aligned operands needed)");
+}
+
+// add_bias_layernorm2_sk: parts[S, R, C], bias[C], r[R, C], gamma, beta -> (sum, LN); float eps
+void runAddBiasLnSk(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t s = it.next(), r = it.next(), c = it.next();
+  LK_REQUIRE(ctx, c <= 2048, "add_bias_layernorm2_sk: C must be <= 2048");
+  status(ctx, lk_hip_add_bias_ln_sk_f32(P<float>(a, 0), splitKPlanes(r, c, s), P<float>(a, 1), P<float>(a, 2),
+                                        P<float>(a, 3), P<float>(a, 4), P<float>(a, 5), P<float>(a, 6), r, c,
+                                        F(a, 0, 1e-5f), ctx.stream),
+         "add_bias_layernorm2_sk: launch failed");
+}
+
+// gemm_auto[_bias_gelu]: x[M, K], w[K, N][, bias[N]] -> [M, N]; M = 1 -> GEMV, else the MFMA GEMM
+template <bool GELU>
+void runGemmAuto(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t m = it.next(), k = it.next();
+  LK_REQUIRE(ctx, it.next() == k, "gemm_auto: inner dimensions differ");
+  const int64_t n = it.next();
+  const float* bias = GELU ? P<float>(a, 2) : nullptr;
+  float* out = P<float>(a, GELU ? 3 : 2);
+  if (m == 1)
+    status(ctx, lk_hip_gemv_f32(P<float>(a, 0), P<float>(a, 1), bias, nullptr, out, n, k, GELU ? 2 : 0, ctx.workspace,
+                                ctx.workspaceBytes, ctx.stream),
+           "gemm_auto: launch failed");
+  else
+    status(ctx, lk_hip_gemm_f32(P<float>(a, 0), P<float>(a, 1), bias, nullptr, out, m, n, k, 0, GELU ? 2 : 0, 1.0f,
+                                ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream),
+           "gemm_auto: launch failed");
+}
+
 }  // namespace
 
 void registerTransformerKernels() {
@@ -311,6 +428,16 @@ void registerTransformerKernels() {
   registerKernel({"attention_decode_kvw_f32_gpu", G, runAttnDecode<true, false>, 5, 1});
   registerKernel({"attention_decode_f32_gpu", G, runAttnDecode<false, false>, 5, 1});
   registerKernel({"kv_write_f32_gpu", G, runKvWrite, 5, 0});
+  registerKernel({"kv_write_rows_f32_gpu", G, runKvWriteRows, 5, 0});
+  registerKernel({"attention_cache_f32_gpu", G, runAttnCache, 5, 1});
+  registerKernel({"attention_cache_sg_f32_gpu", G, runAttnCache, 5, 1});
+  registerKernel({"attention_gen_f32_gpu", G, runAttnGen, 5, 1});
+  registerKernel({"attention_gen2_f32_gpu", G, runAttnGen, 5, 1});
+  registerKernel({"gemm_splitk_f32_gpu", G, runGemmSplitK<false>, 2, 1});
+  registerKernel({"gemm_auto_sk_f32_gpu", G, runGemmSplitK<true>, 2, 1});
+  registerKernel({"add_bias_layernorm2_sk_f32_gpu", G, runAddBiasLnSk, 5, 2});
+  registerKernel({"gemm_auto_f32_gpu", G, runGemmAuto<false>, 2, 1});
+  registerKernel({"gemm_auto_bias_gelu_f32_gpu", G, runGemmAuto<true>, 3, 1});
 }
 
 // ---- Kokoro frame-rate ------------------------------------------------------------------------------------

@@ -11,6 +11,11 @@ Per step (inputs tok i64[1], pos i64[1], both on the device):
 The reference does the two embedding lookups on the CPU and the argmax in Python; here they are device kernels
 so a step is one captured HIP graph.
 
+Gpt2Generator is the reference's `build_generate` (models/gpt2.py:250-333): chunked prefill and decode over the same
+persistent caches. A call with T new tokens at start position pos returns the logits of the last one; T = 1 runs the
+decode step above, T > 1 the chunk forward (GEMM, kv_write_rows + flash attention over the cache, split-K
+projections into bias + residual + LayerNorm).
+
 By default (fused=True) each layer runs the same arithmetic in 5 launches instead of 13: the GEMVs write
 row-slice partial sums and the consumer of each GEMV sums the slices itself (the decode-attention chunk kernel
 for qkv; the next partial GEMV for the attention merge, for gelu(c_fc) and for bias + residual + LayerNorm, the
@@ -119,3 +124,85 @@ class Gpt2Decoder:
         dev = self.w["transformer.wte.weight"].t.device
         for p, t in enumerate(np.asarray(ids, np.int64)):
             self.step(Tensor(torch.tensor([int(t)], device=dev)), Tensor(torch.tensor([p], device=dev)))
+
+
+class Gpt2Generator(Gpt2Decoder):
+    """Chunked prefill + decode sharing the caches (reference build_generate, models/gpt2.py:250-333). sk: split-K
+    factors of the two N = 768 projections for T > 1 ((0, 0) = plain GEMM + add_bias_layernorm2). chunk_graph:
+    capture each chunk length's forward as a HIP graph (pays off when one length recurs; a one-off prompt runs
+    eagerly)."""
+
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, fused: bool = True, sk=(2, 4),
+                 chunk_graph: bool = False):
+        super().__init__(sd, graph=graph, fused=fused)
+        self.sk = tuple(sk)
+        dev = self.w["transformer.wte.weight"].t.device
+        self.positions = torch.arange(N_POS, dtype=torch.int64, device=dev)  # device pos views, no host copies
+        self.chunk_model = lk_compile(self._chunk, graph=chunk_graph)
+
+    def _chunk(self, ids: Tensor, pos: Tensor):
+        w = self.w
+        P = "transformer."
+        T = ids.shape[0]
+        pids = ops.arange_offset_i64_gpu(pos, T)
+        h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], ids, w[P + "wpe.weight"], pids)
+        ln = ops.layernorm_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"], eps=LN_EPS)
+
+        def proj_ln(x, wk, res, ln_key, splits):  # (res + x @ W + b, LN of it)
+            if splits:
+                parts = ops.gemm_auto_sk_f32_gpu(x, w[wk + "weight"], splits)
+                return ops.add_bias_layernorm2_sk_f32_gpu(parts, w[wk + "bias"], res, w[ln_key + "weight"],
+                                                          w[ln_key + "bias"], eps=LN_EPS)
+            return ops.add_bias_layernorm2_f32_gpu(ops.gemm_auto_f32_gpu(x, w[wk + "weight"]), w[wk + "bias"], res,
+                                                   w[ln_key + "weight"], w[ln_key + "bias"], eps=LN_EPS)
+
+        for i, (kc, vc) in enumerate(self.caches):
+            L = f"{P}h.{i}."
+            nxt = f"{P}h.{i + 1}.ln_1." if i + 1 < N_LAYER else P + "ln_f."
+            qkv = ops.gemm_auto_f32_gpu(ln, w[L + "attn.c_attn.weight"])
+            att = ops.attention_gen2_f32_gpu(qkv, kc, vc, pos, w[L + "attn.c_attn.bias"], heads=HEADS)
+            h, ln = proj_ln(att, L + "attn.c_proj.", h, L + "ln_2.", self.sk[0])
+            f = ops.gemm_auto_bias_gelu_f32_gpu(ln, w[L + "mlp.c_fc.weight"], w[L + "mlp.c_fc.bias"])
+            h, ln = proj_ln(f, L + "mlp.c_proj.", h, nxt, self.sk[1])
+        logits = ops.gemm_nt_f32_gpu_mps(ops.view(ln, [1, D], offset=(T - 1) * D), w[P + "wte.weight"])
+        return logits, ops.argmax_f32_gpu(logits)
+
+    def _ids(self, ids) -> Tensor:
+        if isinstance(ids, Tensor):
+            return ids if ids.device == "gpu" else Tensor(ids.t.to(self.positions.device))
+        return Tensor(torch.as_tensor(np.asarray(ids, np.int64).reshape(-1)).to(self.positions.device))
+
+    def run(self, ids, pos: int):
+        """T = len(ids) new tokens at positions pos..pos+T-1 -> (logits f32[1, 50257] of the last one, its argmax
+        i64[1]), both the compiled forward's own buffers (overwritten by the next call). Requires pos + T <= 1024."""
+        ids = self._ids(ids)
+        T = ids.shape[0]
+        if not (T >= 1 and 0 <= pos and pos + T <= N_POS):
+            raise ValueError(f"generate: positions {pos}..{pos + T - 1} outside the {N_POS}-row caches")
+        p = Tensor(self.positions[pos:pos + 1])
+        if T == 1:
+            return self.step(ids, p)
+        return self.chunk_model.run_inplace(ids, p)
+
+    def __call__(self, ids, pos: int):
+        """Reference model(ids, pos) call: logits f32[1, 50257] of the last new token (a host copy)."""
+        return self.run(ids, pos)[0].numpy()
+
+    def prefill(self, ids: np.ndarray) -> None:
+        """Fills the caches with the prompt in one chunk forward at position 0."""
+        self.run(ids, 0)
+
+
+def generate(model: Gpt2Generator, prompt: list[int], n_new: int) -> list[int]:
+    """Greedy generation (reference models/gpt2.py:335-344): one prefill call, then one decode call per new token.
+    Each step's argmax stays on the device and feeds the next step directly; the tokens come back in one copy."""
+    out = torch.empty(n_new, dtype=torch.int64, device=model.positions.device)
+    _, am = model.run(prompt, 0)
+    pos = len(prompt)
+    for i in range(n_new):
+        out[i:i + 1].copy_(am.t)
+        if i + 1 == n_new:
+            break
+        _, am = model.run(Tensor(out[i:i + 1]), pos)
+        pos += 1
+    return [int(v) for v in out.cpu()]

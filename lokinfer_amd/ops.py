@@ -537,6 +537,120 @@ def kv_write_f32_gpu(kcache, vcache, qkv, pos, bias):
     return _launch("kv_write_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[])
 
 
+# ---- chunked prefill / generate (reference python/lokinfer/ops/transformer.py:220-282, 348-351, 441-517) ------
+
+def _rows_check(kc, vc, qkv, pos, bias):
+    _f32(kc, vc, qkv, rank=2)
+    check(kc.shape == vc.shape, "caches must be f32[P, D]")
+    check(qkv.shape[1] == 3 * kc.shape[1], "qkv must be f32[T, 3D]")
+    check(pos.dtype == i64 and tuple(pos.shape) == (1,), "pos must be i64[1] (start position)")
+    _f32(bias, rank=1)
+    check(bias.shape[0] == qkv.shape[1], "bias must be f32[3D]")
+    _gpu(pos)
+
+
+def kv_write_rows_f32_gpu(kcache, vcache, qkv, pos, bias):
+    """kcache[pos + i] = k_i + bk, vcache[pos + i] = v_i + bv for the T rows of qkv f32[T, 3D]; in place. pos is a
+    device i64[1]; rows at or past the cache's end are dropped (the reference reports an error on the host)."""
+    _rows_check(kcache, vcache, qkv, pos, bias)
+    check(kcache.shape[1] % 4 == 0, "D must be a multiple of 4")
+    return _launch("kv_write_rows_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[])
+
+
+def _cache_attn(name, qkv, kcache, vcache, pos, bias, heads, attrs):
+    _rows_check(kcache, vcache, qkv, pos, bias)
+    check(kcache.shape[1] == 64 * int(heads), "head_dim must be 64")
+    return _launch(name, [qkv, kcache, vcache, pos, bias], [(qkv.shape[0], kcache.shape[1])], attrs)
+
+
+def attention_cache_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
+    """Causal attention of the T queries of qkv f32[T, 3D] (positions pos .. pos+T-1, q bias added) over cache rows
+    0 .. pos+i, which must already hold the chunk's k / v (kv_write_rows) -> f32[T, D]; head_dim 64, scale 1/8."""
+    return _cache_attn("attention_cache_f32_gpu", qkv, kcache, vcache, pos, bias, heads, dict(heads=int(heads)))
+
+
+def attention_cache_sg_f32_gpu(qkv, kcache, vcache, pos, bias, heads, nsg=4):
+    """attention_cache_f32_gpu; nsg (the reference's simdgroups per threadgroup: 2, 4, 8) is validated and has no
+    meaning on CDNA4, where one MFMA kernel serves both."""
+    check(int(nsg) in (2, 4, 8), "nsg must be 2, 4 or 8")
+    return _cache_attn("attention_cache_sg_f32_gpu", qkv, kcache, vcache, pos, bias, heads,
+                       dict(heads=int(heads), nsg=int(nsg)))
+
+
+def attention_gen_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
+    """Writes the T new k / v rows (+ bias) at pos.. (in place) and attends causally over rows 0..pos+i: T = 1 -> the
+    split-key decode attention, T > 1 -> kv_write_rows + attention_cache."""
+    return _cache_attn("attention_gen_f32_gpu", qkv, kcache, vcache, pos, bias, heads, dict(heads=int(heads)))
+
+
+def attention_gen2_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
+    """attention_gen_f32_gpu (the reference's second kernel set; on CDNA4 both names run the same kernels)."""
+    return _cache_attn("attention_gen2_f32_gpu", qkv, kcache, vcache, pos, bias, heads, dict(heads=int(heads)))
+
+
+def _splitk_check(a, b, splits, tile):
+    _f32(a, b, rank=2)
+    check(a.shape[1] == b.shape[0], "inner dimensions differ")
+    check(int(splits) >= 1 and a.shape[1] % (16 * int(splits)) == 0, "K must be divisible by 16*splits")
+    check(int(tile) in (32, 64), "tile must be 32 or 64")
+    check(b.shape[1] % 4 == 0, "N must be a multiple of 4")
+    return (int(splits), a.shape[0], b.shape[1])
+
+
+def gemm_splitk_f32_gpu(a, b, splits, tile=64):
+    """Split-K partials f32[S, M, N], part s = a[:, sK/S:(s+1)K/S] @ b[sK/S:(s+1)K/S, :], consumed by
+    add_bias_layernorm2_sk_f32_gpu. While the output tiles fill the GPU (and for M = 1) only plane 0 is written,
+    holding the whole product, and the consumer reads only that plane (rule splitk_planes)."""
+    s = _splitk_check(a, b, splits, tile)
+    return _launch("gemm_splitk_f32_gpu", [a, b], [s], dict(splits=int(splits), tile=int(tile)))
+
+
+def gemm_auto_sk_f32_gpu(a, b, splits, tile=32):
+    """gemm_splitk_f32_gpu for a graph serving T = 1 and T > 1: M = 1 -> GEMV into plane 0."""
+    s = _splitk_check(a, b, splits, tile)
+    return _launch("gemm_auto_sk_f32_gpu", [a, b], [s], dict(splits=int(splits), tile=int(tile)))
+
+
+SPLITK_MAX_TILES = 64
+
+
+def splitk_planes(m: int, n: int, splits: int) -> int:
+    """Planes of a split-K partial tensor that hold data: splits while M > 1 and the 64 x 64 output tiles number
+    fewer than SPLITK_MAX_TILES, else 1."""
+    return splits if m > 1 and (-(-m // 64)) * (-(-n // 64)) < SPLITK_MAX_TILES else 1
+
+
+def add_bias_layernorm2_sk_f32_gpu(parts, bias, r, gamma, beta, eps=1e-5):
+    """add_bias_layernorm2_f32_gpu with a = the sum of the split-K partials parts f32[S, R, C] -> (sum, LN(sum))."""
+    _f32(parts, rank=3)
+    _f32(r, rank=2)
+    _f32(bias, gamma, beta, rank=1)
+    check(tuple(parts.shape[1:]) == tuple(r.shape), "parts must be f32[S, R, C] over r f32[R, C]")
+    check(r.shape[1] <= 2048 and bias.shape[0] == gamma.shape[0] == beta.shape[0] == r.shape[1], "C must be <= 2048")
+    return _launch("add_bias_layernorm2_sk_f32_gpu", [parts, bias, r, gamma, beta], [tuple(r.shape)] * 2,
+                   dict(eps=float(eps)))
+
+
+def gemm_auto_f32_gpu(x, w):
+    """x f32[M, K] @ w f32[K, N]: M = 1 -> GEMV (decode), else the MFMA GEMM (chunked prefill)."""
+    _f32(x, w, rank=2)
+    check(x.shape[1] == w.shape[0], "inner dimensions differ")
+    return _launch("gemm_auto_f32_gpu", [x, w], [(x.shape[0], w.shape[1])])
+
+
+def gemm_auto_bias_gelu_f32_gpu(x, w, b):
+    """gelu_tanh(x @ w + b): M = 1 -> GEMV with the fused epilogue, else the GEMM with it."""
+    _f32(x, w, rank=2)
+    check(x.shape[1] == w.shape[0] and tuple(b.shape) == (w.shape[1],), "shape mismatch")
+    return _launch("gemm_auto_bias_gelu_f32_gpu", [x, w, b], [(x.shape[0], w.shape[1])])
+
+
+def arange_offset_i64_gpu(pos, length):
+    """(MI355X backend; the reference's arange_offset_i64_cpu on the device) i64[length] = pos[0] + [0 .. length-1]."""
+    check(pos.dtype == i64 and tuple(pos.shape) == (1,), "pos must be i64[1]")
+    return _launch("arange_offset_i64_gpu", [pos], [(int(length),)], dict(length=int(length)), out_dtypes=[i64])
+
+
 # ---- Kokoro frame-rate (channel-last) -------------------------------------------------------------------------
 
 def channel_stats_lc_f32_gpu(x):

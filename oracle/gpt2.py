@@ -43,3 +43,23 @@ def prefill(m, ids: np.ndarray):
 def decode_step(m, past, tok: int):
     out = m(torch.tensor([[tok]]), past_key_values=past, use_cache=True)
     return out.logits[0, -1].numpy(), out.past_key_values
+
+
+# ---- chunked generate (reference build_generate / generate, models/gpt2.py:250-344; its tests compare against
+# HF's full forward and HF generate, tests/models/test_gpt2.py:64-106) -------------------------------------------
+
+GEN_PROMPT = [464, 3290, 286, 4881, 318, 6342, 13, 383, 3139, 286]  # tests/models/test_gpt2.py:69
+
+
+@torch.no_grad()
+def last_logits(m, ids) -> np.ndarray:
+    """Logits of the last token of the full causal forward over ids -> f32[1, V]."""
+    return m(torch.as_tensor(np.asarray(ids, np.int64))[None]).logits[0, -1:].numpy()
+
+
+@torch.no_grad()
+def greedy(m, prompt, n_new: int) -> list[int]:
+    """HF generate(do_sample=False) continuation tokens."""
+    out = m.generate(torch.tensor([list(prompt)]), max_new_tokens=n_new, do_sample=False, pad_token_id=50256,
+                     attention_mask=torch.ones(1, len(prompt), dtype=torch.int64))
+    return out[0, len(prompt):].tolist()

@@ -93,6 +93,40 @@ def attention_decode(qkv, kc, vc, pos, bias, heads):
     return out, kc, vc
 
 
+def kv_write_rows(kc, vc, qkv, pos, bias):
+    """Copies of the caches with rows pos..pos+T-1 = k, v of qkv [T, 3D] + bias (kv_write_rows_f32_gpu,
+    python/lokinfer/ops/transformer.py:239-242; host form kernels/cpu/decode.cpp:115-128, which rejects
+    pos + T > cap). Returns (kc', vc')."""
+    x = _d(qkv) + _d(bias)
+    t, d3 = x.shape
+    d = d3 // 3
+    kc, vc = _d(kc).copy(), _d(vc).copy()
+    if pos < 0 or pos + t > kc.shape[0]:
+        raise ValueError("kv_write_rows: pos + T exceeds the cache")
+    kc[pos:pos + t] = x[:, d:2 * d]
+    vc[pos:pos + t] = x[:, 2 * d:]
+    return kc, vc
+
+
+def attention_cache(qkv, kc, vc, pos, bias, heads):
+    """Query i of qkv [T, 3D] (+ q bias) at position pos + i attends over cache rows 0..pos+i, scale 1/sqrt(64)
+    (attention_cache_f32_gpu, python/lokinfer/ops/transformer.py:255-268; host form kernels/cpu/decode.cpp:130-175).
+    The caches must already hold the chunk's rows."""
+    x = _d(qkv) + _d(bias)
+    kc, vc = _d(kc), _d(vc)
+    t, d3 = x.shape
+    d = d3 // 3
+    hd = d // heads
+    out = np.zeros((t, d))
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        for i in range(t):
+            s = kc[:pos + i + 1, sl] @ x[i, sl] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[i, sl] = (p / p.sum()) @ vc[:pos + i + 1, sl]
+    return out
+
+
 # ---- Kokoro channel-last (kokoro_lc.metal:143-398) --------------------------------------------------------------
 
 def channel_stats_lc(x):

@@ -44,3 +44,15 @@ def test_first_block_matches_numpy_restatement():
     with torch.no_grad():
         hs = m.transformer(torch.from_numpy(ids)[None], output_hidden_states=True).hidden_states[1][0].numpy()
     np.testing.assert_allclose(h, hs, rtol=1e-9, atol=1e-9)
+
+
+def test_greedy_equals_argmax_of_full_forward():
+    """HF generate's greedy continuation is, token by token, the argmax of the full forward over the tokens so far
+    (pins the generate oracle against the forward oracle pinned above)."""
+    sd = G.random_weights()
+    m = O.model(sd)
+    toks = O.greedy(m, O.GEN_PROMPT, 6)
+    seq = list(O.GEN_PROMPT)
+    for t in toks:
+        assert int(np.argmax(O.last_logits(m, seq)[0])) == t
+        seq.append(t)

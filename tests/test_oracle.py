@@ -96,6 +96,36 @@ def test_attention_decode_equals_full_causal_row():
         np.testing.assert_allclose(out[0], full[p], rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("chunks", [(6,), (1, 1, 1, 1, 1, 1), (2, 3, 1), (4, 2)])
+def test_attention_cache_chunks_equal_full_causal(chunks):
+    """kv_write_rows + attention_cache over any split of a sequence into chunks reproduce the rows of the full
+    causal attention_qkv (a wrong causal offset, a dropped bias or a transposed cache index breaks a row)."""
+    heads, t = 2, sum(chunks)
+    d = 64 * heads
+    qkv, bias = rng.standard_normal((t, 3 * d)), rng.standard_normal(3 * d)
+    full = K.attention_qkv(qkv, bias, heads, causal=True)
+    kc, vc = np.full((9, d), np.nan), np.full((9, d), np.nan)  # unwritten rows must never be read
+    pos = 0
+    for n in chunks:
+        kc, vc = K.kv_write_rows(kc, vc, qkv[pos:pos + n], pos, bias)
+        out = K.attention_cache(qkv[pos:pos + n], kc, vc, pos, bias, heads)
+        np.testing.assert_allclose(out, full[pos:pos + n], rtol=1e-10, atol=1e-12)
+        pos += n
+
+
+def test_attention_cache_one_row_equals_decode():
+    heads, d = 1, 64
+    qkv, bias = rng.standard_normal((1, 3 * d)), rng.standard_normal(3 * d)
+    kc, vc = rng.standard_normal((8, d)), rng.standard_normal((8, d))
+    dec, kd, vd = K.attention_decode(qkv, kc, vc, 5, bias, heads)
+    kr, vr = K.kv_write_rows(kc, vc, qkv, 5, bias)
+    np.testing.assert_array_equal(kr, kd)
+    np.testing.assert_array_equal(vr, vd)
+    np.testing.assert_allclose(K.attention_cache(qkv, kr, vr, 5, bias, heads), dec, rtol=1e-12)
+    with pytest.raises(ValueError):
+        K.kv_write_rows(kc, vc, np.zeros((4, 3 * d)), 5, bias)
+
+
 def test_channel_stats_and_adain_affine_closed_form():
     x = rng.standard_normal((300, 6)) * 3 + 1
     st = K.channel_stats_lc(x)
