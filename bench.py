@@ -42,6 +42,12 @@ def event_times(fn, n: int) -> list[float]:
 
 # ---- GPT-2 decode ---------------------------------------------------------------------------------------------
 
+# algorithmic flops of the 512-token prefill: 12 layers x 2 x 512 x (768 x 2304 + 768 x 768 + 2 x 768 x 3072)
+# for the projections, causal attention 12 layers x 12 heads x 2 x 2 x 64 x (512 x 513 / 2), LM head on the last row
+PREFILL512_FLOPS = 12 * 2 * 512 * (768 * 2304 + 768 * 768 + 2 * 768 * 3072) + 12 * 12 * 4 * 64 * (512 * 513 // 2) \
+    + 2 * 768 * 50257
+
+
 def bench_gpt2(steps: int, warmup: int, cpu: bool = True) -> dict:
     import lokinfer_amd as lk
     from lokinfer_amd import gpt2 as G
@@ -49,8 +55,11 @@ def bench_gpt2(steps: int, warmup: int, cpu: bool = True) -> dict:
 
     sd = G.random_weights()
     ids, nxt = O.decode_inputs()
-    dec = G.Gpt2Decoder(sd)
-    dec.prefill(ids)
+    dec = G.Gpt2Generator(sd, chunk_graph=True)
+    dec.prefill(ids)  # one 512-token chunk forward at pos 0
+    # prefill of the 512-token prompt (captured chunk forward; rerunning it at pos 0 rewrites the same cache rows)
+    pids = lk.from_numpy(ids, device="gpu", copy=True)
+    pre = event_times(lambda: dec.run(pids, 0), 20)
     tok = lk.from_numpy(np.array([nxt], np.int64), device="gpu", copy=True)
     pos = lk.from_numpy(np.array([512], np.int64), device="gpu", copy=True)
     for _ in range(warmup):
@@ -75,6 +84,8 @@ def bench_gpt2(steps: int, warmup: int, cpu: bool = True) -> dict:
                      "frac": lm_bytes / (kt * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
                      "avg_launch_ms": kt, "bytes_per_launch": lm_bytes},
         "step_bytes": 532.4e6,
+        "prefill512_ms": statistics.median(pre),
+        "prefill512_tflops": PREFILL512_FLOPS / (statistics.median(pre) * 1e-3) / 1e12,
     }
     if cpu:
         res["cpu_baseline"] = cpu_gpt2(sd, ids, nxt)
@@ -271,6 +282,8 @@ def main():
                        "global_batch": 1, "seq_len": 513, "parallelism": "none"},
             "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
             "roofline_kernel": r["roofline"]["kernel"], "cpu_baseline": r.get("cpu_baseline"),
+            "gpt2_prefill512_ms": round(r["prefill512_ms"], 4),
+            "gpt2_prefill512_tflops": round(r["prefill512_tflops"], 2),
         }
         print(json.dumps(line))
         return
@@ -281,7 +294,9 @@ def main():
         r59 = bench_kokoro(59, a.steps, a.warmup)
         g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=False)
         extra = {"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
-                 "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_lm_head_roofline": g["roofline"]}
+                 "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_lm_head_roofline": g["roofline"],
+                 "gpt2_prefill512_ms": round(g["prefill512_ms"], 4),
+                 "gpt2_prefill512_tflops": round(g["prefill512_tflops"], 2)}
     roof = roofline_wino()
     cpu = None if a.no_cpu else cpu_kokoro(r["sd"], r["inputs"])
     line = {
