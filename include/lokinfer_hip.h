@@ -193,6 +193,48 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
                                     int64_t creal, int dilation, int64_t length, float eps, void* stream);
 
+/* ---- f16 language model (Qwen3-ASR LM; reference f16 GPU op family kernels/gpu/f16_gpu.cpp:1011-1050, contracts
+ *      python/lokinfer/ops/f16.py, f16_gpu.py). f16 storage (pointers to IEEE half), f32 math and accumulation, one
+ *      rounding at each output. Weights of the GEMM-like ops are packed once as W^T f16[N', K]
+ *      (lk_hip_f16_transpose); the reference fixes only the math and leaves the layout to the kernel. ---- */
+/* out f16[M, N] = x f16[M, K] @ W (+ bias f16[N]) (+ res f16[M, N]), or silu(x @ Wg) * (x @ Wu) with swiglu = 1
+ * (W^T rows [gate | up], N' = 2N): gemm[_bias]_f16_gpu, gemm[_bias|_add|_swiglu]_opt_f16_gpu. K % 8 == 0, 16-byte
+ * aligned x and W^T. M = 1 runs a GEMV. workspace (optional): split-K partials when the grid is small. */
+int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void* res, void* out, int64_t m, int64_t n,
+                    int64_t k, int swiglu, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t lk_hip_f16_gemm_workspace_bytes(int64_t m, int64_t n, int swiglu);
+/* rmsnorm_gemm[_swiglu]_opt_f16_gpu: out = rmsnorm(x, g) @ W [swiglu]; ws f16[M, K] receives the normalized rows
+ * when M > 1 (unused at M = 1, where the GEMV normalizes the row itself) */
+int lk_hip_f16_rms_gemm(const void* x, const void* g, const void* wt, void* out, void* ws, int64_t m, int64_t n,
+                        int64_t k, float eps, int swiglu, void* workspace, int64_t workspace_bytes, void* stream);
+/* lm_head_last[_opt]_f16_gpu: out f32[1, V] = x[T-1] . table f16[V, D]^T */
+int lk_hip_f16_lm_head(const void* x, const void* table, float* out, int64_t t, int64_t d, int64_t v, void* stream);
+/* rmsnorm[_heads]_f16_gpu: groups of `width` values of x f16[rows, C] (width = C, or the head width) */
+int lk_hip_f16_rmsnorm(const void* x, const void* g, void* out, int64_t rows, int64_t c, int64_t width, float eps,
+                       void* stream);
+/* rope_f16_gpu: rotate_half RoPE per 128-wide head at positions pos + i (pos a device i64[1]) */
+int lk_hip_f16_rope(const void* x, const int64_t* pos, void* out, int64_t t, int64_t c, float theta, void* stream);
+/* qknorm_rope_kv_opt_f16_gpu: qkv f16[T, 128 (qh + 2 kvh)] -> q f16[T, 128 qh]; k, v to cache rows pos.. */
+int lk_hip_f16_qknorm_rope_kv(const void* qkv, const void* qg, const void* kg, const int64_t* pos, void* kc, void* vc,
+                              void* q, int64_t t, int qh, int kvh, int64_t cap, float eps, float theta, void* stream);
+/* attention_gqa[_opt]_f16_gpu: causal GQA of q f16[T, 128 qh] over the caches f16[cap, 128 kvh]; T = 1 needs
+ * lk_hip_f16_attention_workspace_bytes of workspace (returns 3 when short) */
+int64_t lk_hip_f16_attention_workspace_bytes(int qh, int64_t cap);
+int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int64_t t,
+                             int qh, int kvh, int64_t cap, void* workspace, int64_t workspace_bytes, void* stream);
+/* kv_write_f16_gpu, embedding_f16_gpu, scatter_audio_f16_gpu, add_f16_gpu (op 0), silu_mul_f16_gpu (op 1). A device
+ * kernel cannot raise the reference's host errors: rows past the cache are dropped, an id out of range or a pad row
+ * without an audio row gives a NaN row. */
+int lk_hip_f16_kv_write(void* kc, void* vc, const void* k, const void* v, const int64_t* pos, int64_t t, int64_t d,
+                        int64_t cap, void* stream);
+int lk_hip_f16_embedding(const int64_t* ids, const void* table, void* out, int64_t t, int64_t vocab, int64_t d,
+                         void* stream);
+int lk_hip_f16_scatter_audio(const void* x, const int64_t* ids, const void* audio, void* out, int64_t t, int64_t d,
+                             int64_t na, int64_t pad_id, void* stream);
+int lk_hip_f16_elementwise(const void* a, const void* b, void* out, int64_t n, int op, void* stream);
+/* weight packing: W f16[K, N] -> W^T f16[N, K] */
+int lk_hip_f16_transpose(const void* w, void* wt, int64_t k, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,7 +6,10 @@ live in liblokinfer_hip.so (lokinfer_amd/csrc, C-ABI in include/lokinfer_hip.h);
 """
 from .tensor import DType, Tensor, empty, f16, f32, from_numpy, from_torch, i32, i64, randn, tensor, u8, zeros  # noqa: F401
 from . import ops  # noqa: F401
+from . import f16_gpu as _f16_gpu
 from ._lib import LokinferError, registered_kernels  # noqa: F401
 from .compiler import CompiledModel, compile  # noqa: F401
+
+ops.f16_gpu = _f16_gpu  # lk.ops.f16_gpu.<name>_f16_gpu, as in the reference
 
 __version__ = "0.1.0"

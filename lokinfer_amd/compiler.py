@@ -23,11 +23,16 @@ def _sig(args) -> tuple:
 
 
 class _Entry:
-    def __init__(self, fn, args: list[Tensor], use_graph: bool):
+    def __init__(self, fn, args: list[Tensor], use_graph: bool, mutable: tuple = ()):
         ctx = GpuContext.shared()
-        self.inputs = [Tensor(torch.empty_like(a.t, device=ctx.device)) for a in args]
-        for s, a in zip(self.inputs, args):
-            s.t.copy_(a.t)
+        self.mutable = frozenset(mutable)
+        # mutable inputs (written in place, e.g. a caller-owned KV cache) are bound by reference: the entry (and its
+        # graph) uses the caller's buffer itself; the others are copied into the entry's own input buffers
+        self.inputs = [a if i in self.mutable else Tensor(torch.empty_like(a.t, device=ctx.device))
+                       for i, a in enumerate(args)]
+        for i, (s, a) in enumerate(zip(self.inputs, args)):
+            if i not in self.mutable:
+                s.t.copy_(a.t)
         out = fn(*self.inputs)  # eager warm-up: binds shapes, builds lazy constants
         self.single = not isinstance(out, (tuple, list))
         self.graph = None
@@ -44,8 +49,9 @@ class _Entry:
         if self.fresh:
             self.fresh = False
             return self.outputs
-        for s, a in zip(self.inputs, args):
-            s.t.copy_(a.t, non_blocking=True)
+        for i, (s, a) in enumerate(zip(self.inputs, args)):
+            if i not in self.mutable:
+                s.t.copy_(a.t, non_blocking=True)
         if self.graph is not None:
             self.graph.replay()
             outs = self.outputs
@@ -58,16 +64,18 @@ class _Entry:
 class CompiledModel:
     """Callable compiled function (reference CompiledModel, python/lokinfer/compiler.py:94-184)."""
 
-    def __init__(self, fn, use_graph: bool = True):
+    def __init__(self, fn, use_graph: bool = True, mutable: tuple = ()):
         self.fn = fn
         self.use_graph = use_graph
+        self.mutable = tuple(mutable)
         self._entries: dict[tuple, _Entry] = {}
 
     def _entry(self, args) -> _Entry:
-        key = _sig(args)
+        # a mutable input is part of the signature by address: the captured graph writes that buffer
+        key = _sig(args) + tuple(args[i].t.data_ptr() for i in self.mutable)
         e = self._entries.get(key)
         if e is None:
-            e = _Entry(self.fn, list(args), self.use_graph)
+            e = _Entry(self.fn, list(args), self.use_graph, self.mutable)
             self._entries[key] = e
         return e
 
@@ -83,10 +91,11 @@ class CompiledModel:
         return res[0] if len(res) == 1 else tuple(res)
 
 
-def compile(fn, inputs=None, input_types=None, graph: bool = True) -> CompiledModel:
+def compile(fn, inputs=None, input_types=None, graph: bool = True, mutable: tuple = ()) -> CompiledModel:
     """Compiles `fn` (reference lk.compile, python/lokinfer/compiler.py:187-212). `inputs` / `input_types` are
-    accepted for API compatibility; shapes are bound per call signature."""
-    m = CompiledModel(fn, use_graph=graph)
+    accepted for API compatibility; shapes are bound per call signature. `mutable`: indices of the inputs that the
+    function writes in place (the reference's lk.MutableType inputs): bound by reference, one entry per buffer."""
+    m = CompiledModel(fn, use_graph=graph, mutable=mutable)
     if inputs is not None:
         m._entry(list(inputs))
     return m

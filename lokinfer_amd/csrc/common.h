@@ -68,6 +68,7 @@ void registerSequenceKernels();
 void registerSignalKernels();
 void registerDecodeFusedKernels();
 void registerWinogradKernels();
+void registerF16Kernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
@@ -80,6 +81,25 @@ inline T* P(const KernelArgs& a, int i) {
 inline void checkLaunch(ExecCtx& ctx) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess && !ctx.error) ctx.error = hipGetErrorString(e);
+}
+
+// Sequential reader over KernelArgs::ints (operand dims, out dims, then int attrs).
+struct Ints {
+  const KernelArgs& a;
+  uint32_t i = 0;
+  explicit Ints(const KernelArgs& args) : a(args) {}
+  int64_t next() { return i < a.numInts ? a.ints[i++] : 0; }
+  void skip(int n) { i += n; }
+};
+
+// float attr i (attribute-name order), or dflt when absent
+inline float F(const KernelArgs& a, uint32_t i, float dflt = 0.0f) {
+  return i < a.numFloats ? static_cast<float>(a.floats[i]) : dflt;
+}
+
+// records a launcher's nonzero return code as the kernel's error (the first one wins)
+inline void status(ExecCtx& ctx, int rc, const char* what) {
+  if (rc != 0 && !ctx.error) ctx.error = what;
 }
 
 #define LK_REQUIRE(ctx, cond, msg) \

@@ -35,23 +35,6 @@ std::vector<std::string>& names() {
 
 thread_local std::string tlsError;
 
-// Sequential reader over KernelArgs::ints.
-struct Ints {
-  const KernelArgs& a;
-  uint32_t i = 0;
-  explicit Ints(const KernelArgs& args) : a(args) {}
-  int64_t next() { return i < a.numInts ? a.ints[i++] : 0; }
-  void skip(int n) { i += n; }
-};
-
-inline float F(const KernelArgs& a, uint32_t i, float dflt = 0.0f) {
-  return i < a.numFloats ? static_cast<float>(a.floats[i]) : dflt;
-}
-
-inline void status(ExecCtx& ctx, int rc, const char* what) {
-  if (rc != 0 && !ctx.error) ctx.error = what;
-}
-
 }  // namespace
 
 void registerKernel(const KernelEntry& e) {
@@ -609,6 +592,7 @@ static void registerAll() {
     registerSignalKernels();
     registerDecodeFusedKernels();
     registerWinogradKernels();
+    registerF16Kernels();
     std::sort(names().begin(), names().end());
   });
 }
