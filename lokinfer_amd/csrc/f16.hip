@@ -197,7 +197,11 @@ struct GemvF16Params {
 
 __device__ __forceinline__ float siluMul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <int EPI, bool RMS>
+// CH > 0: K == 512 CH, and every lane's CH chunks of both rows are loaded before any math (the x chunks first: the
+// in-order memory counter then lets the RMS statistics wait for x alone while the weights stream in). The statistics
+// use rowSumSq's order (the lane's chunks ascending, then the butterfly), so the prologue matches the row kernel
+// bit for bit. CH = 0: any K % 8 == 0, chunk by chunk.
+template <int EPI, bool RMS, int CH>
 __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
   const int lane = threadIdx.x & 63;
   const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -213,12 +217,8 @@ __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
   }
   const h16* w0 = p.wt + r0 * p.k;
   const h16* w1 = p.wt + r1 * p.k;
-  float r = 1.0f;
-  if constexpr (RMS) r = rmsFactor(rowSumSq(p.x, p.k, lane), p.k, p.eps);
   float a0 = 0.0f, a1 = 0.0f;
-  auto chunk = [&](int64_t c) {
-    const half8 u = ld8(w0 + 8 * c), v = ld8(w1 + 8 * c);
-    half8 xv = ld8(p.x + 8 * c);
+  auto dot = [&](half8 xv, const half8& u, const half8& v, int64_t c, float r) {
     if constexpr (RMS) {
       const half8 gv = ld8(p.gamma + 8 * c);
 #pragma unroll
@@ -231,10 +231,40 @@ __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
       a1 = fmaf(xf, static_cast<float>(v[e]), a1);
     }
   };
-  const int64_t chunks = p.k / 8, full = chunks / 64;
+  if constexpr (CH > 0) {
+    half8 xs[CH], u[CH], v[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xs[j] = ld8(p.x + 8 * (lane + 64 * j));
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      u[j] = ld8(w0 + 8 * (lane + 64 * j));
+      v[j] = ld8(w1 + 8 * (lane + 64 * j));
+    }
+    float r = 1.0f;
+    if constexpr (RMS) {
+      float sq = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq = fmaf(static_cast<float>(xs[j][e]), static_cast<float>(xs[j][e]), sq);
+      r = rmsFactor(waveSum(sq), p.k, p.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) dot(xs[j], u[j], v[j], lane + 64 * j, r);
+  } else {
+    float r = 1.0f;
+    if constexpr (RMS) r = rmsFactor(rowSumSq(p.x, p.k, lane), p.k, p.eps);
+    const int64_t chunks = p.k / 8, full = chunks / 64;
 #pragma unroll 4
-  for (int64_t i = 0; i < full; ++i) chunk(lane + 64 * i);
-  if (lane + 64 * full < chunks) chunk(lane + 64 * full);
+    for (int64_t i = 0; i < full; ++i) {
+      const int64_t c = lane + 64 * i;
+      dot(ld8(p.x + 8 * c), ld8(w0 + 8 * c), ld8(w1 + 8 * c), c, r);
+    }
+    if (lane + 64 * full < chunks) {
+      const int64_t c = lane + 64 * full;
+      dot(ld8(p.x + 8 * c), ld8(w0 + 8 * c), ld8(w1 + 8 * c), c, r);
+    }
+  }
   a0 = waveSum(a0);
   a1 = waveSum(a1);
   if (lane != 0) return;
@@ -258,6 +288,17 @@ __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
     o[r0] = toH16(y0);
     if (r1 != r0) o[r1] = toH16(y1);
   }
+}
+
+// launches the GEMV with the chunk count fixed at compile time for K = 2048 and 6144 (Qwen3's inner sizes)
+template <int EPI, bool RMS>
+void launchGemvF16(const GemvF16Params& p, unsigned blocks, hipStream_t s) {
+  if (p.k == 2048)
+    hipLaunchKernelGGL((gemvF16Kernel<EPI, RMS, 4>), dim3(blocks), dim3(256), 0, s, p);
+  else if (p.k == 6144)
+    hipLaunchKernelGGL((gemvF16Kernel<EPI, RMS, 12>), dim3(blocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemvF16Kernel<EPI, RMS, 0>), dim3(blocks), dim3(256), 0, s, p);
 }
 
 // ---- GEMM (M > 1) on f16 MFMA 32x32x16 ----------------------------------------------------------------------
@@ -590,6 +631,20 @@ __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
   }
 }
 
+// merged decode attention value d of one head from its chunk partials (m, l, o[128]), in chunk order
+__device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
+  float m = -INFINITY;
+  for (int c = 0; c < used; ++c) m = fmaxf(m, part[c * (QHD + 2)]);
+  float l = 0.0f, acc = 0.0f;
+  for (int c = 0; c < used; ++c) {
+    const float* pc = part + c * (QHD + 2);
+    const float w = __builtin_amdgcn_exp2f(pc[0] - m);
+    l = fmaf(w, pc[1], l);
+    acc = fmaf(w, pc[2 + d], acc);
+  }
+  return toH16(acc / l);
+}
+
 // ---- causal GQA, T = 1: one wave per (q head, 64-key chunk), partial (m, l, o[128]) to the workspace, then one
 // workgroup per q head merges the chunks in order. Scores: lane j owns key kb + j (16 x 16-byte loads of its K row,
 // q from LDS). P.V: lane (key group g = lane / 16, dim octet lane % 16) sums keys g, g + 4, ... of the chunk, then a
@@ -672,17 +727,242 @@ __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
     *o = static_cast<h16>(__builtin_nanf(""));
     return;
   }
-  const int used = static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH));
-  float m = -INFINITY;
-  for (int c = 0; c < used; ++c) m = fmaxf(m, part[c * (QHD + 2)]);
-  float l = 0.0f, acc = 0.0f;
-  for (int c = 0; c < used; ++c) {
-    const float* pc = part + c * (QHD + 2);
-    const float w = __builtin_amdgcn_exp2f(pc[0] - m);
-    l = fmaf(w, pc[1], l);
-    acc = fmaf(w, pc[2 + d], acc);
+  *o = mergeDim(part, static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH)), d);
+}
+
+// ---- T = 1 with the QK-norm / RoPE / KV write folded in: a chunk wave normalizes and rotates its q head from the
+// raw projections itself; the chunk holding pos takes the new key and value from them too (never from the cache
+// row being written), and the first q head of each kv group writes that row to both caches. Values and roundings
+// are those of qkRopeKvKernel + gqaDecodeChunkKernel (the same helpers), so the partials are identical.
+struct GqaDecParams {
+  const h16* qkv;  // [1, qh 128 + 2 kvh 128]
+  const h16* qg;
+  const h16* kg;
+  const int64_t* pos;
+  h16* kc;
+  h16* vc;
+  float* part;  // [qh, chunks, 130]
+  int64_t cap;
+  int qh, kvh, chunks;
+  float scale, eps;
+  RopeTable tab;
+};
+
+// All loads are issued first, in the order the in-order memory counter needs: the raw q / k / v values (the norms
+// wait for them alone), then the chunk's K and V rows.
+__global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
+  __shared__ float qs[QHD];
+  __shared__ float ps[DCH];
+  __shared__ __attribute__((aligned(16))) h16 kn[QHD];
+  __shared__ __attribute__((aligned(16))) h16 vn[QHD];
+  const int h = blockIdx.x, ch = blockIdx.y, lane = threadIdx.x;
+  const int grp = p.qh / p.kvh;
+  const int64_t dq = static_cast<int64_t>(p.qh) * QHD, dk = static_cast<int64_t>(p.kvh) * QHD;
+  const int64_t kvOff = static_cast<int64_t>(h / grp) * QHD;
+  const int64_t p0 = *p.pos;
+  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
+  const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
+  const int64_t kb = static_cast<int64_t>(ch) * DCH;
+  if (kb >= nk) {
+    if (lane == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    part[2 + lane] = 0.0f;
+    part[2 + 64 + lane] = 0.0f;
+    return;
   }
-  *o = toH16(acc / l);
+  const bool hasNew = p0 < kb + DCH;  // this chunk holds key pos (kb <= pos here)
+  const int cl = lane & 15;           // rowSumSq's chunk of a 128-wide head (lanes 16.. add nothing)
+  const h16* xq = p.qkv + h * QHD;
+  const h16* xk = p.qkv + dq + kvOff;
+  const h16* xv = p.qkv + dq + dk + kvOff;
+  const half8 qc = ld8(xq + 8 * cl);
+  const h16 q0 = xq[lane], q1 = xq[lane + 64], gq0 = p.qg[lane], gq1 = p.qg[lane + 64];
+  half8 kc8 = {};
+  h16 k0 = 0, k1 = 0, gk0 = 0, gk1 = 0, v0 = 0, v1 = 0;
+  if (hasNew) {
+    kc8 = ld8(xk + 8 * cl);
+    k0 = xk[lane];
+    k1 = xk[lane + 64];
+    gk0 = p.kg[lane];
+    gk1 = p.kg[lane + 64];
+    v0 = xv[lane];
+    v1 = xv[lane + 64];
+  }
+  const int64_t key = kb + lane;
+  const h16* kr = p.kc + min<int64_t>(key, nk - 1) * dk + kvOff;
+  half8 kv[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) kv[c] = ld8(kr + 8 * c);
+  const int g = lane >> 4, oc = lane & 15;
+  half8 vv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    vv[i] = ld8(p.vc + min<int64_t>(kb + g + 4 * i, nk - 1) * dk + kvOff + 8 * oc);
+  auto headSumSq = [&](const half8& c8) {
+    float sq = 0.0f;
+    if (lane < 16) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq = fmaf(static_cast<float>(c8[e]), static_cast<float>(c8[e]), sq);
+    }
+    return waveSum(sq);
+  };
+  {
+    const float r = rmsFactor(headSumSq(qc), QHD, p.eps);
+    h16 a, b;
+    ropePair(static_cast<float>(rmsElem(q0, gq0, r)), static_cast<float>(rmsElem(q1, gq1, r)), p0, p.tab.invf[lane],
+             a, b);
+    qs[lane] = static_cast<float>(a);
+    qs[lane + 64] = static_cast<float>(b);
+  }
+  if (hasNew) {
+    const float r = rmsFactor(headSumSq(kc8), QHD, p.eps);
+    h16 a, b;
+    ropePair(static_cast<float>(rmsElem(k0, gk0, r)), static_cast<float>(rmsElem(k1, gk1, r)), p0, p.tab.invf[lane],
+             a, b);
+    kn[lane] = a;
+    kn[lane + 64] = b;
+    vn[lane] = v0;
+    vn[lane + 64] = v1;
+    if (h % grp == 0) {  // one wave per kv head writes the new row to both caches
+      p.kc[p0 * dk + kvOff + lane] = a;
+      p.kc[p0 * dk + kvOff + lane + 64] = b;
+      p.vc[p0 * dk + kvOff + lane] = v0;
+      p.vc[p0 * dk + kvOff + lane + 64] = v1;
+    }
+  }
+  __syncthreads();
+  if (key == p0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) kv[c] = ld8(kn + 8 * c);
+  }
+  float dot = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dot = fmaf(qs[8 * c + e], static_cast<float>(kv[c][e]), dot);
+  const float sc = key < nk ? dot * p.scale * kLog2e : -INFINITY;
+  const float mc = waveMax(sc);
+  const float pv = __builtin_amdgcn_exp2f(sc - mc);
+  const float lc = waveSum(pv);
+  ps[lane] = pv;
+  __syncthreads();
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  const half8 vnew = ld8(vn + 8 * oc);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (hasNew && kb + g + 4 * i == p0) vv[i] = vnew;
+    const float w = ps[g + 4 * i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, static_cast<float>(vv[i][e]), acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += __shfl_xor(acc[e], 16, 64);
+    acc[e] += __shfl_xor(acc[e], 32, 64);
+  }
+  if (lane == 0) {
+    part[0] = mc;
+    part[1] = lc;
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[2 + 8 * oc + e] = acc[e];
+  }
+}
+
+// ---- the o projection (+ residual) of a decode step with the attention merge folded in: each workgroup merges all
+// heads' chunk partials into LDS (mergeDim: the merge kernel's arithmetic, so x is the same f16 row), then runs the
+// GEMV rows of its waves on it. Weight loads are issued before the merge.
+struct GemvAttnParams {
+  const float* part;  // [qh, chunks, 130]
+  const int64_t* pos;
+  const h16* wt;      // W_o^T [N, K], K = qh 128
+  const h16* res;     // [N]
+  h16* out;           // [N]
+  int64_t n, k;
+  int chunks;
+};
+
+// The merge in two phases with mergeDim's operation order: one thread per head forms its chunk weights
+// w_c = exp2(m_c - m) and sum l (chunks in order) into LDS; then each value is sum_c w_c o_c[d] (chunks in order,
+// their loads issued together: at most MAXC chunks, predicated), divided by l.
+constexpr int MAXC = 16;
+
+template <int CH>
+__global__ __launch_bounds__(256) void gemvAttnF16Kernel(GemvAttnParams p) {
+  constexpr int K = CH * 512, HEADS = K / QHD;
+  __shared__ __attribute__((aligned(16))) h16 xl[K];
+  __shared__ float wS[HEADS][MAXC], lS[HEADS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + (tid >> 6);
+  const int64_t r0 = min<int64_t>(2 * wv, p.n - 1), r1 = min<int64_t>(2 * wv + 1, p.n - 1);
+  const h16* w0 = p.wt + r0 * p.k;
+  const h16* w1 = p.wt + r1 * p.k;
+  half8 u[CH], v[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    u[j] = ld8(w0 + 8 * (lane + 64 * j));
+    v[j] = ld8(w1 + 8 * (lane + 64 * j));
+  }
+  const int64_t p0 = *p.pos;
+  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH));
+  const int64_t hstride = static_cast<int64_t>(p.chunks) * (QHD + 2);
+  if (tid < HEADS) {
+    const float* ph = p.part + tid * hstride;
+    float mc[MAXC], lc[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      mc[c] = c < used ? ph[c * (QHD + 2)] : -INFINITY;
+      lc[c] = c < used ? ph[c * (QHD + 2) + 1] : 0.0f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (c < used) m = fmaxf(m, mc[c]);
+    float l = 0.0f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const float w = __builtin_amdgcn_exp2f(mc[c] - m);
+      if (c < used) l = fmaf(w, lc[c], l);
+      wS[tid][c] = w;
+    }
+    lS[tid] = l;
+  }
+  __syncthreads();
+  for (int i = tid; i < K; i += 256) {
+    const int hh = i / QHD, d = i % QHD;
+    const float* ph = p.part + hh * hstride + 2 + d;
+    float o[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) o[c] = c < used ? ph[c * (QHD + 2)] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (c < used) acc = fmaf(wS[hh][c], o[c], acc);
+    xl[i] = toH16(acc / lS[hh]);
+  }
+  __syncthreads();
+  if (2 * wv >= p.n) return;
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const half8 xv = ld8(xl + 8 * (lane + 64 * j));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xf = static_cast<float>(xv[e]);
+      a0 = fmaf(xf, static_cast<float>(u[j][e]), a0);
+      a1 = fmaf(xf, static_cast<float>(v[j][e]), a1);
+    }
+  }
+  a0 = waveSum(a0);
+  a1 = waveSum(a1);
+  if (lane != 0) return;
+  p.out[r0] = toH16(static_cast<float>(p.res[r0]) + a0);
+  if (r1 != r0) p.out[r1] = toH16(static_cast<float>(p.res[r1]) + a1);
 }
 
 // ---- row copies, gathers, elementwise -----------------------------------------------------------------------
@@ -771,6 +1051,9 @@ int launched() { return hipGetLastError() == hipSuccess ? 0 : 2; }
 
 extern "C" {
 
+int lk_hip_f16_rms_lm_head(const void* x, const void* g, const void* table, float* out, int64_t t, int64_t d, int64_t v,
+                           float eps, void* stream);
+
 int64_t lk_hip_f16_gemm_workspace_bytes(int64_t m, int64_t n, int swiglu) {
   return 8 * m * n * (swiglu ? 2 : 1) * 4;
 }
@@ -790,8 +1073,8 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
                     static_cast<const h16*>(res), out, n, k, 0.0f};
     const int64_t waves = swiglu ? n : (n + 1) / 2;
     const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
-    if (swiglu) hipLaunchKernelGGL((gemvF16Kernel<EPI_SWIGLU, false>), dim3(blocks), dim3(256), 0, s, g);
-    else hipLaunchKernelGGL((gemvF16Kernel<EPI_PLAIN, false>), dim3(blocks), dim3(256), 0, s, g);
+    if (swiglu) launchGemvF16<EPI_SWIGLU, false>(g, blocks, s);
+    else launchGemvF16<EPI_PLAIN, false>(g, blocks, s);
     return launched();
   }
   GemmF16Params p{static_cast<const h16*>(x), static_cast<const h16*>(wt), static_cast<const h16*>(bias),
@@ -840,8 +1123,8 @@ int lk_hip_f16_rms_gemm(const void* x, const void* g, const void* wt, void* out,
                     nullptr, out, n, k, eps};
     const int64_t waves = swiglu ? n : (n + 1) / 2;
     const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
-    if (swiglu) hipLaunchKernelGGL((gemvF16Kernel<EPI_SWIGLU, true>), dim3(blocks), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gemvF16Kernel<EPI_PLAIN, true>), dim3(blocks), dim3(256), 0, s, p);
+    if (swiglu) launchGemvF16<EPI_SWIGLU, true>(p, blocks, s);
+    else launchGemvF16<EPI_PLAIN, true>(p, blocks, s);
     return launched();
   }
   if (!aligned16(ws)) return 1;
@@ -853,12 +1136,19 @@ int lk_hip_f16_rms_gemm(const void* x, const void* g, const void* wt, void* out,
 
 // out f32[1, V] = x[T-1] . table[V, D]^T
 int lk_hip_f16_lm_head(const void* x, const void* table, float* out, int64_t t, int64_t d, int64_t v, void* stream) {
+  return lk_hip_f16_rms_lm_head(x, nullptr, table, out, t, d, v, 0.0f, stream);
+}
+
+// out f32[1, V] = rmsnorm(x[T-1], g) . table^T (g null: no norm); the row is normalized by every wave itself
+int lk_hip_f16_rms_lm_head(const void* x, const void* g, const void* table, float* out, int64_t t, int64_t d, int64_t v,
+                           float eps, void* stream) {
   using namespace lkd;
-  if (t <= 0 || v <= 0 || d <= 0 || d % 8 != 0 || !aligned16(x) || !aligned16(table)) return 1;
-  GemvF16Params p{static_cast<const h16*>(x) + (t - 1) * d, nullptr, static_cast<const h16*>(table), nullptr,
-                  nullptr, out, v, d, 0.0f};
+  if (t <= 0 || v <= 0 || d <= 0 || d % 8 != 0 || !aligned16(x) || !aligned16(table) || (g && !aligned16(g))) return 1;
+  GemvF16Params p{static_cast<const h16*>(x) + (t - 1) * d, static_cast<const h16*>(g), static_cast<const h16*>(table),
+                  nullptr, nullptr, out, v, d, eps};
   const unsigned blocks = static_cast<unsigned>(((v + 1) / 2 + 3) / 4);
-  hipLaunchKernelGGL((gemvF16Kernel<EPI_F32, false>), dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  if (g) launchGemvF16<EPI_F32, true>(p, blocks, static_cast<hipStream_t>(stream));
+  else launchGemvF16<EPI_F32, false>(p, blocks, static_cast<hipStream_t>(stream));
   return launched();
 }
 
@@ -928,6 +1218,37 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
   }
   hipLaunchKernelGGL(gqaFlashKernel, dim3(static_cast<unsigned>((t + 31) / 32), static_cast<unsigned>(qh)), dim3(256),
                      0, s, p);
+  return launched();
+}
+
+// decode step (T = 1) attention with the QK-norm / RoPE / KV write folded in: qkv f16[1, 128 (qh + 2 kvh)] -> chunk
+// partials part f32[qh, ceil(cap / 64), 130]; row pos of both caches written
+int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void* kg, const int64_t* pos, void* kc,
+                                    void* vc, float* part, int qh, int kvh, int64_t cap, float eps, float theta,
+                                    void* stream) {
+  using namespace lkd;
+  if (qh <= 0 || kvh <= 0 || qh % kvh != 0 || cap <= 0 || !aligned16(qkv) || !aligned16(kc) || !aligned16(vc)) return 1;
+  const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
+  GqaDecParams p{static_cast<const h16*>(qkv), static_cast<const h16*>(qg), static_cast<const h16*>(kg), pos,
+                 static_cast<h16*>(kc), static_cast<h16*>(vc), part, cap, qh, kvh, chunks,
+                 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta)};
+  hipLaunchKernelGGL(gqaDecodeQkrKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return launched();
+}
+
+// out f16[1, N] = res + merge(part) @ W_o (W_o^T f16[N, K], K = qh 128 in {2048, 4096}); part from
+// lk_hip_f16_attention_decode_qkr (chunks = its second dimension, at most 16: caches up to 1024 rows)
+int lk_hip_f16_gemm_attn(const float* part, const int64_t* pos, const void* wt, const void* res, void* out, int64_t n,
+                         int64_t k, int chunks, void* stream) {
+  using namespace lkd;
+  if (n <= 0 || (k != 2048 && k != 4096) || chunks <= 0 || chunks > MAXC || !aligned16(wt)) return 1;
+  GemvAttnParams p{part, pos, static_cast<const h16*>(wt), static_cast<const h16*>(res), static_cast<h16*>(out), n, k,
+                   chunks};
+  const unsigned blocks = static_cast<unsigned>(((n + 1) / 2 + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (k == 2048) hipLaunchKernelGGL(gemvAttnF16Kernel<4>, dim3(blocks), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(gemvAttnF16Kernel<8>, dim3(blocks), dim3(256), 0, s, p);
   return launched();
 }
 
@@ -1121,6 +1442,47 @@ void runScatterAudioF16(ExecCtx& ctx, const KernelArgs& a) {
          "scatter_audio_f16: launch failed");
 }
 
+// attention_decode_qkr_opt (backend; inout kc, vc): qkv[1, W], qg[128], kg[128], pos[1], kc[P, Dk], vc[P, Dk]
+// -> part f32[qh, chunks, 130]; floats eps, theta
+void runDecQkrF16(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  LK_REQUIRE(ctx, it.next() == 1, "attention_decode_qkr_f16: qkv must be f16[1, W]");
+  const int64_t w = it.next();
+  it.skip(3);
+  const int64_t cap = it.next(), dk = it.next();
+  it.skip(2);
+  const int64_t qh = it.next(), chunks = it.next();
+  LK_REQUIRE(ctx, dk % 128 == 0 && w - 2 * dk == 128 * qh && chunks == (cap + 63) / 64,
+             "attention_decode_qkr_f16: bad shapes");
+  status(ctx, lk_hip_f16_attention_decode_qkr(a.ptrs[0], a.ptrs[1], a.ptrs[2], P<int64_t>(a, 3), a.ptrs[4], a.ptrs[5],
+                                              P<float>(a, 6), static_cast<int>(qh), static_cast<int>(dk / 128), cap,
+                                              F(a, 0, 1e-6f), F(a, 1, 1e6f), ctx.stream),
+         "attention_decode_qkr_f16: launch failed");
+}
+
+// gemm_attn_add_opt (backend): part f32[qh, chunks, 130], pos[1], wt[N, K], res[1, N] -> [1, N]
+void runGemmAttnF16(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t qh = it.next(), chunks = it.next();
+  it.skip(2);
+  const int64_t n = it.next(), k = it.next();
+  LK_REQUIRE(ctx, k == 128 * qh, "gemm_attn_add_f16: w must be packed W_o^T f16[N, qh 128]");
+  status(ctx, lk_hip_f16_gemm_attn(P<float>(a, 0), P<int64_t>(a, 1), a.ptrs[2], a.ptrs[3], a.ptrs[4], n, k,
+                                   static_cast<int>(chunks), ctx.stream),
+         "gemm_attn_add_f16: launch failed (K must be 2048 or 4096)");
+}
+
+// rmsnorm_lm_head_last_opt (backend): x[T, D], g[D], table[V, D] -> f32[1, V]; float eps
+void runRmsLmHeadF16(ExecCtx& ctx, const KernelArgs& a) {
+  Ints it(a);
+  const int64_t t = it.next(), d = it.next();
+  it.skip(1);
+  const int64_t v = it.next();
+  status(ctx, lk_hip_f16_rms_lm_head(a.ptrs[0], a.ptrs[1], a.ptrs[2], P<float>(a, 3), t, d, v, F(a, 0, 1e-6f),
+                                     ctx.stream),
+         "rmsnorm_lm_head_last_f16: launch failed");
+}
+
 template <int OP>
 void runEltF16(ExecCtx& ctx, const KernelArgs& a) {
   status(ctx, lk_hip_f16_elementwise(a.ptrs[0], a.ptrs[1], a.ptrs[2], a.ints[0] * a.ints[1], OP, ctx.stream),
@@ -1158,6 +1520,9 @@ void registerF16Kernels() {
   registerKernel({"add_f16_gpu", G, runEltF16<0>, 2, 1});
   registerKernel({"silu_mul_f16_gpu", G, runEltF16<1>, 2, 1});
   registerKernel({"transpose_f16_gpu", G, runTransposeF16, 1, 1});
+  registerKernel({"attention_decode_qkr_opt_f16_gpu", G, runDecQkrF16, 6, 1});
+  registerKernel({"gemm_attn_add_opt_f16_gpu", G, runGemmAttnF16, 4, 1});
+  registerKernel({"rmsnorm_lm_head_last_opt_f16_gpu", G, runRmsLmHeadF16, 3, 1});
 }
 
 }  // namespace lkh

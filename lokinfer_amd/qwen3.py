@@ -7,7 +7,7 @@ one row when there are none), pos (tokens already in the cache) and the caller-o
 kv f16[L, 2, P, kvh 128] (written in place), and returns the logits f32[1, V] of the last new token. Prefill chunks
 and decode steps are the same call; one compiled graph per (T, A, P) signature (decode steps replay one graph).
 
-Per layer (variant "opt", the reference's _lm_layer_opt):
+Per layer (variant "opt", the reference's _lm_layer_opt; at T = 1 two fusions of its ops, `_layer_decode`):
   qkv = rmsnorm_gemm_opt(h, ln1, [q|k|v])                      M = 1: one GEMV that normalizes the row itself
   q   = qknorm_rope_kv_opt(qkv, qn, kn, pos, kc, vc)            QK-norm + RoPE, k and v written to the cache
   att = attention_gqa_opt(q, kc, vc, pos)                       causal GQA 16 / 8 heads x 128
@@ -153,15 +153,31 @@ class Qwen3Lm:
         g = F.silu_mul_f16_gpu(F.gemm_f16_gpu(a, L["gate"]), F.gemm_f16_gpu(a, L["up"]))
         return F.add_f16_gpu(h, F.gemm_f16_gpu(g, L["down"]))
 
+    def _layer_decode(self, L, h, pos, kc, vc):
+        """The opt layer at T = 1 in 4 launches: the QK-norm / RoPE / KV write run inside the attention chunks, the
+        attention merge inside the o projection (each fusion equals its composition bit for bit)."""
+        c = self.cfg
+        qkv, _ = F.rmsnorm_gemm_opt_f16_gpu(h, L["ln1.g"], L["qkv"], c.eps)
+        part = F.attention_decode_qkr_opt_f16_gpu(qkv, L["qn.g"], L["kn.g"], pos, kc, vc, c.eps, c.theta)
+        h = F.gemm_attn_add_opt_f16_gpu(part, pos, L["o"], h)
+        m, _ = F.rmsnorm_gemm_swiglu_opt_f16_gpu(h, L["ln2.g"], L["gateup"], c.eps)
+        return F.gemm_add_opt_f16_gpu(m, L["down"], h)
+
     def _fn(self, ids: Tensor, audio: Tensor, pos: Tensor, kv: Tensor):
         c = self.cfg
         h = F.scatter_audio_f16_gpu(F.embedding_f16_gpu(ids, self.embed), ids, audio)
-        layer = self._layer_opt if self.variant == "opt" else self._layer_basic
+        opt = self.variant == "opt"
+        layer = self._layer_basic
+        if opt:
+            fused = ids.shape[0] == 1 and c.dq in (2048, 4096) and kv.shape[2] <= 1024  # the merge fusion's limits
+            layer = self._layer_decode if fused else self._layer_opt
         for i, L in enumerate(self.layers):
             kc, vc = Tensor(kv.t[i, 0]), Tensor(kv.t[i, 1])  # views of the caller's cache
             h = layer(L, h, pos, kc, vc)
-        head = F.lm_head_last_opt_f16_gpu if self.variant == "opt" else F.lm_head_last_f16_gpu
-        logits = head(F.rmsnorm_f16_gpu(h, self.norm, c.eps), self.embed)
+        if opt:
+            logits = F.rmsnorm_lm_head_last_opt_f16_gpu(h, self.norm, self.embed, c.eps)
+        else:
+            logits = F.lm_head_last_f16_gpu(F.rmsnorm_f16_gpu(h, self.norm, c.eps), self.embed)
         return logits, ops.argmax_f32_gpu(logits)
 
     def run(self, ids, audio, pos: int, kv: Tensor):
