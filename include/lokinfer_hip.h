@@ -222,17 +222,16 @@ int lk_hip_f16_qknorm_rope_kv(const void* qkv, const void* qg, const void* kg, c
 int64_t lk_hip_f16_attention_workspace_bytes(int qh, int64_t cap);
 int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int64_t t,
                              int qh, int kvh, int64_t cap, void* workspace, int64_t workspace_bytes, void* stream);
-/* decode step (T = 1) fusions (backend ops; the reference runs qknorm_rope_kv_opt -> attention_gqa_opt -> gemm_add_opt
- * and rmsnorm -> lm_head_last_opt, model.py:393-401, 287-288): attention_decode_qkr_opt_f16_gpu writes chunk partials
- * part f32[qh, ceil(cap / 64), 130] (and row pos of both caches) straight from the raw qkv projections;
- * gemm_attn_add_opt_f16_gpu merges them and applies o_proj + residual (K = 2048 or 4096);
+/* decode step (T = 1) fusions (backend ops; the reference runs qknorm_rope_kv_opt -> attention_gqa_opt and
+ * rmsnorm -> lm_head_last_opt, model.py:393-401, 287-288): attention_decode_qkr_opt_f16_gpu goes from the raw qkv
+ * projections f16[1, 128 (qh + 2 kvh)] to the attention output f16[1, 128 qh] in one launch (QK-norm, RoPE, row pos of
+ * both caches, key-split chunks, and their merge by the last chunk of each head to finish; counters: qh unsigned
+ * ints, zero before the first call and left zero; workspace as lk_hip_f16_attention_workspace_bytes, 3 when short);
  * rmsnorm_lm_head_last_opt_f16_gpu normalizes the last row inside the LM-head GEMV. Each equals its composition bit
  * for bit. */
 int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void* kg, const int64_t* pos, void* kc,
-                                    void* vc, float* part, int qh, int kvh, int64_t cap, float eps, float theta,
-                                    void* stream);
-int lk_hip_f16_gemm_attn(const float* part, const int64_t* pos, const void* wt, const void* res, void* out, int64_t n,
-                         int64_t k, int chunks, void* stream);
+                                    void* vc, void* out, unsigned* counters, int qh, int kvh, int64_t cap, float eps,
+                                    float theta, void* workspace, int64_t workspace_bytes, void* stream);
 int lk_hip_f16_rms_lm_head(const void* x, const void* g, const void* table, float* out, int64_t t, int64_t d, int64_t v,
                            float eps, void* stream);
 /* kv_write_f16_gpu, embedding_f16_gpu, scatter_audio_f16_gpu, add_f16_gpu (op 0), silu_mul_f16_gpu (op 1). A device

@@ -12,6 +12,8 @@ Functions must be capturable: GPU work only between inputs and outputs (no host 
 """
 from __future__ import annotations
 
+import gc
+
 import torch
 
 from .runtime import GpuContext
@@ -40,8 +42,18 @@ class _Entry:
         if use_graph:
             torch.cuda.synchronize()
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                out = fn(*self.inputs)
+            # No garbage collection while capturing: a collected model (models reference their compiled function
+            # and back, so only the cycle collector frees them) destroys its own captured graphs and their memory
+            # pools, which must not happen during a capture. Unreachable objects are collected before it instead.
+            gc.collect()
+            enabled = gc.isenabled()
+            gc.disable()
+            try:
+                with torch.cuda.graph(self.graph):
+                    out = fn(*self.inputs)
+            finally:
+                if enabled:
+                    gc.enable()
         self.outputs = [out] if self.single else list(out)
         self.fresh = not use_graph  # eager: the warm-up already computed the first call's outputs
 

@@ -631,16 +631,39 @@ __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
   }
 }
 
-// merged decode attention value d of one head from its chunk partials (m, l, o[128]), in chunk order
+// merged decode attention value d of one head from its chunk partials (m, l, o[128]), in chunk order:
+// M = max m_c, out = sum_c w_c o_c[d] / sum_c w_c l_c with w_c = 2^(m_c - M). The chunks go in blocks of 16 whose
+// loads are issued together (predicated), so a merge costs a few memory round trips instead of one per chunk.
+constexpr int MB = 16;
 __device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
   float m = -INFINITY;
-  for (int c = 0; c < used; ++c) m = fmaxf(m, part[c * (QHD + 2)]);
+  for (int c0 = 0; c0 < used; c0 += MB) {
+    float mc[MB];
+#pragma unroll
+    for (int c = 0; c < MB; ++c) mc[c] = c0 + c < used ? part[(c0 + c) * (QHD + 2)] : -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MB; ++c)
+      if (c0 + c < used) m = fmaxf(m, mc[c]);
+  }
   float l = 0.0f, acc = 0.0f;
-  for (int c = 0; c < used; ++c) {
-    const float* pc = part + c * (QHD + 2);
-    const float w = __builtin_amdgcn_exp2f(pc[0] - m);
-    l = fmaf(w, pc[1], l);
-    acc = fmaf(w, pc[2 + d], acc);
+  for (int c0 = 0; c0 < used; c0 += MB) {
+    float mc[MB], lc[MB], oc[MB];
+#pragma unroll
+    for (int c = 0; c < MB; ++c) {
+      const bool in = c0 + c < used;
+      const float* pc = part + (c0 + c) * (QHD + 2);
+      mc[c] = in ? pc[0] : 0.0f;
+      lc[c] = in ? pc[1] : 0.0f;
+      oc[c] = in ? pc[2 + d] : 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < MB; ++c) {
+      if (c0 + c < used) {
+        const float w = __builtin_amdgcn_exp2f(mc[c] - m);
+        l = fmaf(w, lc[c], l);
+        acc = fmaf(w, oc[c], acc);
+      }
+    }
   }
   return toH16(acc / l);
 }
@@ -730,10 +753,13 @@ __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
   *o = mergeDim(part, static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH)), d);
 }
 
-// ---- T = 1 with the QK-norm / RoPE / KV write folded in: a chunk wave normalizes and rotates its q head from the
-// raw projections itself; the chunk holding pos takes the new key and value from them too (never from the cache
-// row being written), and the first q head of each kv group writes that row to both caches. Values and roundings
-// are those of qkRopeKvKernel + gqaDecodeChunkKernel (the same helpers), so the partials are identical.
+// ---- T = 1 with the QK-norm / RoPE / KV write and the merge folded in: a chunk wave normalizes and rotates its q
+// head from the raw projections itself; the chunk holding pos takes the new key and value from them too (never
+// from the cache row being written), and the first q head of each kv group writes that row to both caches. Each
+// wave then writes its chunk partial, fences it and counts itself on its head's counter; the last wave of the head
+// to arrive (no wave ever waits) reads all the head's partials after an acquire fence, merges them as the merge
+// kernel does (mergeDim) and resets the counter. Values and roundings are those of qkRopeKvKernel +
+// gqaDecodeChunkKernel + gqaDecodeMergeKernel (the same helpers), so the output is identical.
 struct GqaDecParams {
   const h16* qkv;  // [1, qh 128 + 2 kvh 128]
   const h16* qg;
@@ -741,12 +767,30 @@ struct GqaDecParams {
   const int64_t* pos;
   h16* kc;
   h16* vc;
-  float* part;  // [qh, chunks, 130]
+  float* part;         // [qh, chunks, 130] (workspace)
+  h16* out;            // [1, qh 128]
+  unsigned* counters;  // [qh], zero between launches
   int64_t cap;
   int qh, kvh, chunks;
   float scale, eps;
   RopeTable tab;
 };
+
+__device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, int lane) {
+  __shared__ unsigned lastFlag;
+  __threadfence();  // release: this wave's partial is in L2 before it is counted
+  if (lane == 0) lastFlag = atomicAdd(&p.counters[h], 1u) == static_cast<unsigned>(p.chunks - 1);
+  __syncthreads();
+  if (!lastFlag) return;
+  __threadfence();  // acquire: the other waves' partials (and no stale L1 lines) from here on
+  const int64_t p0 = *p.pos;
+  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH));
+  const float* ph = p.part + static_cast<int64_t>(h) * p.chunks * (QHD + 2);
+  h16* o = p.out + static_cast<int64_t>(h) * QHD;
+  o[lane] = mergeDim(ph, used, lane);
+  o[lane + 64] = mergeDim(ph, used, lane + 64);
+  if (lane == 0) p.counters[h] = 0u;
+}
 
 // All loads are issued first, in the order the in-order memory counter needs: the raw q / k / v values (the norms
 // wait for them alone), then the chunk's K and V rows.
@@ -770,6 +814,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     }
     part[2 + lane] = 0.0f;
     part[2 + 64 + lane] = 0.0f;
+    decodeMergeIfLast(p, h, lane);
     return;
   }
   const bool hasNew = p0 < kb + DCH;  // this chunk holds key pos (kb <= pos here)
@@ -872,98 +917,9 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) part[2 + 8 * oc + e] = acc[e];
   }
+  decodeMergeIfLast(p, h, lane);
 }
 
-// ---- the o projection (+ residual) of a decode step with the attention merge folded in: each workgroup merges all
-// heads' chunk partials into LDS (mergeDim: the merge kernel's arithmetic, so x is the same f16 row), then runs the
-// GEMV rows of its waves on it. Weight loads are issued before the merge.
-struct GemvAttnParams {
-  const float* part;  // [qh, chunks, 130]
-  const int64_t* pos;
-  const h16* wt;      // W_o^T [N, K], K = qh 128
-  const h16* res;     // [N]
-  h16* out;           // [N]
-  int64_t n, k;
-  int chunks;
-};
-
-// The merge in two phases with mergeDim's operation order: one thread per head forms its chunk weights
-// w_c = exp2(m_c - m) and sum l (chunks in order) into LDS; then each value is sum_c w_c o_c[d] (chunks in order,
-// their loads issued together: at most MAXC chunks, predicated), divided by l.
-constexpr int MAXC = 16;
-
-template <int CH>
-__global__ __launch_bounds__(256) void gemvAttnF16Kernel(GemvAttnParams p) {
-  constexpr int K = CH * 512, HEADS = K / QHD;
-  __shared__ __attribute__((aligned(16))) h16 xl[K];
-  __shared__ float wS[HEADS][MAXC], lS[HEADS];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + (tid >> 6);
-  const int64_t r0 = min<int64_t>(2 * wv, p.n - 1), r1 = min<int64_t>(2 * wv + 1, p.n - 1);
-  const h16* w0 = p.wt + r0 * p.k;
-  const h16* w1 = p.wt + r1 * p.k;
-  half8 u[CH], v[CH];
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    u[j] = ld8(w0 + 8 * (lane + 64 * j));
-    v[j] = ld8(w1 + 8 * (lane + 64 * j));
-  }
-  const int64_t p0 = *p.pos;
-  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH));
-  const int64_t hstride = static_cast<int64_t>(p.chunks) * (QHD + 2);
-  if (tid < HEADS) {
-    const float* ph = p.part + tid * hstride;
-    float mc[MAXC], lc[MAXC];
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      mc[c] = c < used ? ph[c * (QHD + 2)] : -INFINITY;
-      lc[c] = c < used ? ph[c * (QHD + 2) + 1] : 0.0f;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c)
-      if (c < used) m = fmaxf(m, mc[c]);
-    float l = 0.0f;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const float w = __builtin_amdgcn_exp2f(mc[c] - m);
-      if (c < used) l = fmaf(w, lc[c], l);
-      wS[tid][c] = w;
-    }
-    lS[tid] = l;
-  }
-  __syncthreads();
-  for (int i = tid; i < K; i += 256) {
-    const int hh = i / QHD, d = i % QHD;
-    const float* ph = p.part + hh * hstride + 2 + d;
-    float o[MAXC];
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) o[c] = c < used ? ph[c * (QHD + 2)] : 0.0f;
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c)
-      if (c < used) acc = fmaf(wS[hh][c], o[c], acc);
-    xl[i] = toH16(acc / lS[hh]);
-  }
-  __syncthreads();
-  if (2 * wv >= p.n) return;
-  float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const half8 xv = ld8(xl + 8 * (lane + 64 * j));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xf = static_cast<float>(xv[e]);
-      a0 = fmaf(xf, static_cast<float>(u[j][e]), a0);
-      a1 = fmaf(xf, static_cast<float>(v[j][e]), a1);
-    }
-  }
-  a0 = waveSum(a0);
-  a1 = waveSum(a1);
-  if (lane != 0) return;
-  p.out[r0] = toH16(static_cast<float>(p.res[r0]) + a0);
-  if (r1 != r0) p.out[r1] = toH16(static_cast<float>(p.res[r1]) + a1);
-}
 
 // ---- row copies, gathers, elementwise -----------------------------------------------------------------------
 // kv_write: rows pos..pos+T-1 of both caches = k, v (8 halves per thread); rows past the cache are dropped
@@ -1221,36 +1177,27 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
   return launched();
 }
 
-// decode step (T = 1) attention with the QK-norm / RoPE / KV write folded in: qkv f16[1, 128 (qh + 2 kvh)] -> chunk
-// partials part f32[qh, ceil(cap / 64), 130]; row pos of both caches written
+// decode step (T = 1) attention with the QK-norm / RoPE / KV write and the chunk merge folded in:
+// qkv f16[1, 128 (qh + 2 kvh)] -> out f16[1, 128 qh]; row pos of both caches written. counters: qh unsigned ints,
+// zero before the first call (every call leaves them zero); workspace: lk_hip_f16_attention_workspace_bytes
+// (returns 3 when short). Calls sharing counters or workspace must be stream-ordered.
 int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void* kg, const int64_t* pos, void* kc,
-                                    void* vc, float* part, int qh, int kvh, int64_t cap, float eps, float theta,
-                                    void* stream) {
+                                    void* vc, void* out, unsigned* counters, int qh, int kvh, int64_t cap, float eps,
+                                    float theta, void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace lkd;
-  if (qh <= 0 || kvh <= 0 || qh % kvh != 0 || cap <= 0 || !aligned16(qkv) || !aligned16(kc) || !aligned16(vc)) return 1;
+  if (qh <= 0 || kvh <= 0 || qh % kvh != 0 || cap <= 0 || !counters || !aligned16(qkv) || !aligned16(kc) ||
+      !aligned16(vc))
+    return 1;
+  if (!workspace || workspace_bytes < lk_hip_f16_attention_workspace_bytes(qh, cap)) return 3;
   const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
   GqaDecParams p{static_cast<const h16*>(qkv), static_cast<const h16*>(qg), static_cast<const h16*>(kg), pos,
-                 static_cast<h16*>(kc), static_cast<h16*>(vc), part, cap, qh, kvh, chunks,
-                 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta)};
+                 static_cast<h16*>(kc), static_cast<h16*>(vc), static_cast<float*>(workspace), static_cast<h16*>(out),
+                 counters, cap, qh, kvh, chunks, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta)};
   hipLaunchKernelGGL(gqaDecodeQkrKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), p);
   return launched();
 }
 
-// out f16[1, N] = res + merge(part) @ W_o (W_o^T f16[N, K], K = qh 128 in {2048, 4096}); part from
-// lk_hip_f16_attention_decode_qkr (chunks = its second dimension, at most 16: caches up to 1024 rows)
-int lk_hip_f16_gemm_attn(const float* part, const int64_t* pos, const void* wt, const void* res, void* out, int64_t n,
-                         int64_t k, int chunks, void* stream) {
-  using namespace lkd;
-  if (n <= 0 || (k != 2048 && k != 4096) || chunks <= 0 || chunks > MAXC || !aligned16(wt)) return 1;
-  GemvAttnParams p{part, pos, static_cast<const h16*>(wt), static_cast<const h16*>(res), static_cast<h16*>(out), n, k,
-                   chunks};
-  const unsigned blocks = static_cast<unsigned>(((n + 1) / 2 + 3) / 4);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (k == 2048) hipLaunchKernelGGL(gemvAttnF16Kernel<4>, dim3(blocks), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(gemvAttnF16Kernel<8>, dim3(blocks), dim3(256), 0, s, p);
-  return launched();
-}
 
 int lk_hip_f16_kv_write(void* kc, void* vc, const void* k, const void* v, const int64_t* pos, int64_t t, int64_t d,
                         int64_t cap, void* stream) {
@@ -1442,8 +1389,8 @@ void runScatterAudioF16(ExecCtx& ctx, const KernelArgs& a) {
          "scatter_audio_f16: launch failed");
 }
 
-// attention_decode_qkr_opt (backend; inout kc, vc): qkv[1, W], qg[128], kg[128], pos[1], kc[P, Dk], vc[P, Dk]
-// -> part f32[qh, chunks, 130]; floats eps, theta
+// attention_decode_qkr_opt (backend; inout kc, vc, counters): qkv[1, W], qg[128], kg[128], pos[1], kc[P, Dk],
+// vc[P, Dk], counters i32[qh] -> out f16[1, Dq]; floats eps, theta
 void runDecQkrF16(ExecCtx& ctx, const KernelArgs& a) {
   Ints it(a);
   LK_REQUIRE(ctx, it.next() == 1, "attention_decode_qkr_f16: qkv must be f16[1, W]");
@@ -1451,25 +1398,13 @@ void runDecQkrF16(ExecCtx& ctx, const KernelArgs& a) {
   it.skip(3);
   const int64_t cap = it.next(), dk = it.next();
   it.skip(2);
-  const int64_t qh = it.next(), chunks = it.next();
-  LK_REQUIRE(ctx, dk % 128 == 0 && w - 2 * dk == 128 * qh && chunks == (cap + 63) / 64,
-             "attention_decode_qkr_f16: bad shapes");
-  status(ctx, lk_hip_f16_attention_decode_qkr(a.ptrs[0], a.ptrs[1], a.ptrs[2], P<int64_t>(a, 3), a.ptrs[4], a.ptrs[5],
-                                              P<float>(a, 6), static_cast<int>(qh), static_cast<int>(dk / 128), cap,
-                                              F(a, 0, 1e-6f), F(a, 1, 1e6f), ctx.stream),
-         "attention_decode_qkr_f16: launch failed");
-}
-
-// gemm_attn_add_opt (backend): part f32[qh, chunks, 130], pos[1], wt[N, K], res[1, N] -> [1, N]
-void runGemmAttnF16(ExecCtx& ctx, const KernelArgs& a) {
-  Ints it(a);
-  const int64_t qh = it.next(), chunks = it.next();
-  it.skip(2);
-  const int64_t n = it.next(), k = it.next();
-  LK_REQUIRE(ctx, k == 128 * qh, "gemm_attn_add_f16: w must be packed W_o^T f16[N, qh 128]");
-  status(ctx, lk_hip_f16_gemm_attn(P<float>(a, 0), P<int64_t>(a, 1), a.ptrs[2], a.ptrs[3], a.ptrs[4], n, k,
-                                   static_cast<int>(chunks), ctx.stream),
-         "gemm_attn_add_f16: launch failed (K must be 2048 or 4096)");
+  const int64_t qh = it.next();
+  LK_REQUIRE(ctx, dk % 128 == 0 && w - 2 * dk == 128 * qh, "attention_decode_qkr_f16: bad shapes");
+  const int rc = lk_hip_f16_attention_decode_qkr(a.ptrs[0], a.ptrs[1], a.ptrs[2], P<int64_t>(a, 3), a.ptrs[4],
+                                                 a.ptrs[5], a.ptrs[7], P<unsigned>(a, 6), static_cast<int>(qh),
+                                                 static_cast<int>(dk / 128), cap, F(a, 0, 1e-6f), F(a, 1, 1e6f),
+                                                 wsPtr(ctx), wsBytes(ctx), ctx.stream);
+  status(ctx, rc, rc == 3 ? "attention_decode_qkr_f16: workspace too small" : "attention_decode_qkr_f16: launch failed");
 }
 
 // rmsnorm_lm_head_last_opt (backend): x[T, D], g[D], table[V, D] -> f32[1, V]; float eps
@@ -1520,8 +1455,7 @@ void registerF16Kernels() {
   registerKernel({"add_f16_gpu", G, runEltF16<0>, 2, 1});
   registerKernel({"silu_mul_f16_gpu", G, runEltF16<1>, 2, 1});
   registerKernel({"transpose_f16_gpu", G, runTransposeF16, 1, 1});
-  registerKernel({"attention_decode_qkr_opt_f16_gpu", G, runDecQkrF16, 6, 1});
-  registerKernel({"gemm_attn_add_opt_f16_gpu", G, runGemmAttnF16, 4, 1});
+  registerKernel({"attention_decode_qkr_opt_f16_gpu", G, runDecQkrF16, 7, 1});
   registerKernel({"rmsnorm_lm_head_last_opt_f16_gpu", G, runRmsLmHeadF16, 3, 1});
 }
 

@@ -19,7 +19,7 @@ import torch
 
 from .ops import _launch, check
 from .runtime import GpuContext
-from .tensor import Tensor, f16, f32, i64
+from .tensor import Tensor, f16, f32, i32, i64
 
 PAD_ID = 151676  # <|audio_pad|> (reference models/qwen3_asr/reference.py)
 
@@ -268,10 +268,10 @@ def qknorm_rope_kv_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, eps=1e-6, theta=1e6):
 
 # ---- decode-step fusions (MI355X backend) -------------------------------------------------------------------
 
-def attention_decode_qkr_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, eps=1e-6, theta=1e6):
-    """(MI355X backend) T = 1: qknorm_rope_kv_opt + attention_gqa_opt's key-split chunks in one launch. qkv
-    f16[1, Dq + 2 Dk] -> chunk partials f32[Dq / 128, ceil(P / 64), 130] (max, sum, o[128] per head and 64-key chunk);
-    writes row pos of both caches. Feed to gemm_attn_add_opt_f16_gpu."""
+def attention_decode_qkr_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, counters, eps=1e-6, theta=1e6):
+    """(MI355X backend) T = 1: qknorm_rope_kv_opt + attention_gqa_opt in one launch. qkv f16[1, Dq + 2 Dk] ->
+    f16[1, Dq]; writes row pos of both caches. counters: i32[Dq / 128] on the device, zero before the first call
+    (each call leaves them zero; calls sharing them must be stream-ordered). Bit-identical to the two ops."""
     _f16(qkv, kc, vc, rank=2)
     _f16(qg, kg, rank=1)
     _pos(pos)
@@ -280,22 +280,10 @@ def attention_decode_qkr_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, eps=1e-6, theta=1
     check(tuple(kc.shape) == tuple(vc.shape) and kc.shape[1] % 128 == 0, "caches must both be f16[P, Dk]")
     dq = qkv.shape[1] - 2 * kc.shape[1]
     check(dq > 0 and dq % 128 == 0 and (dq // 128) % (kc.shape[1] // 128) == 0, "qkv must be f16[1, Dq + 2 Dk]")
-    shape = (dq // 128, -(-kc.shape[0] // 64), 130)
-    return _launch("attention_decode_qkr_opt_f16_gpu", [qkv, qg, kg, pos, kc, vc], [shape],
-                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f32])
-
-
-def gemm_attn_add_opt_f16_gpu(part, pos, w, res):
-    """(MI355X backend) res + merge(part) @ w: the decode attention merge folded into the o projection GEMV (the
-    merged row is the f16 attention output attention_gqa_opt gives). part from attention_decode_qkr_opt_f16_gpu."""
-    check(isinstance(part, Tensor) and part.dtype == f32 and part.ndim == 3 and part.shape[2] == 130, "bad partials")
-    check(part.shape[1] <= 16, "at most 16 chunks (caches up to 1024 rows): merge separately beyond")
-    _pos(pos)
-    pw = _w(w)
-    _f16(res, rank=2)
-    check(pw.shape[0] == 128 * part.shape[0] and pw.shape[0] in (2048, 4096), "w must be f16[qh 128, N], K 2048/4096")
-    check(tuple(res.shape) == (1, pw.shape[1]), "res must be f16[1, N]")
-    return _launch("gemm_attn_add_opt_f16_gpu", [part, pos, pw.wt, res], [(1, pw.shape[1])], out_dtypes=[f16])
+    check(isinstance(counters, Tensor) and counters.dtype == i32 and tuple(counters.shape) == (dq // 128,),
+          "counters must be i32[q heads]")
+    return _launch("attention_decode_qkr_opt_f16_gpu", [qkv, qg, kg, pos, kc, vc, counters], [(1, dq)],
+                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f16])
 
 
 def rmsnorm_lm_head_last_opt_f16_gpu(x, g, table, eps=1e-6):

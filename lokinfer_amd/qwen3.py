@@ -124,6 +124,7 @@ class Qwen3Lm:
             L["down"] = F.pack(sd[p + "down.w"])
             self.layers.append(L)
         self.positions = torch.arange(1 << 16, dtype=torch.int64, device=dev)  # device pos views, no host copies
+        self.counters = Tensor(torch.zeros(cfg.qh, dtype=torch.int32, device=dev))  # decode attention merge counters
         self.model = lk_compile(self._fn, graph=graph, mutable=(3,))  # kv: the caller's cache, written in place
 
     def kv_cache(self, capacity: int) -> Tensor:
@@ -154,12 +155,12 @@ class Qwen3Lm:
         return F.add_f16_gpu(h, F.gemm_f16_gpu(g, L["down"]))
 
     def _layer_decode(self, L, h, pos, kc, vc):
-        """The opt layer at T = 1 in 4 launches: the QK-norm / RoPE / KV write run inside the attention chunks, the
-        attention merge inside the o projection (each fusion equals its composition bit for bit)."""
+        """The opt layer at T = 1 in 5 launches: QK-norm / RoPE / KV write, the key-split attention and its merge in
+        one (equal to qknorm_rope_kv_opt + attention_gqa_opt bit for bit)."""
         c = self.cfg
         qkv, _ = F.rmsnorm_gemm_opt_f16_gpu(h, L["ln1.g"], L["qkv"], c.eps)
-        part = F.attention_decode_qkr_opt_f16_gpu(qkv, L["qn.g"], L["kn.g"], pos, kc, vc, c.eps, c.theta)
-        h = F.gemm_attn_add_opt_f16_gpu(part, pos, L["o"], h)
+        att = F.attention_decode_qkr_opt_f16_gpu(qkv, L["qn.g"], L["kn.g"], pos, kc, vc, self.counters, c.eps, c.theta)
+        h = F.gemm_add_opt_f16_gpu(att, L["o"], h)
         m, _ = F.rmsnorm_gemm_swiglu_opt_f16_gpu(h, L["ln2.g"], L["gateup"], c.eps)
         return F.gemm_add_opt_f16_gpu(m, L["down"], h)
 
@@ -169,8 +170,7 @@ class Qwen3Lm:
         opt = self.variant == "opt"
         layer = self._layer_basic
         if opt:
-            fused = ids.shape[0] == 1 and c.dq in (2048, 4096) and kv.shape[2] <= 1024  # the merge fusion's limits
-            layer = self._layer_decode if fused else self._layer_opt
+            layer = self._layer_decode if ids.shape[0] == 1 else self._layer_opt
         for i, L in enumerate(self.layers):
             kc, vc = Tensor(kv.t[i, 0]), Tensor(kv.t[i, 1])  # views of the caller's cache
             h = layer(L, h, pos, kc, vc)
