@@ -304,9 +304,9 @@ void launchGemvF16(const GemvF16Params& p, unsigned blocks, hipStream_t s) {
 // ---- GEMM (M > 1) on f16 MFMA 32x32x16 ----------------------------------------------------------------------
 // A f16 [M, lda] row-major, B given as W^T [rows, K] (both K-contiguous, so every MFMA operand of a lane is one
 // 16-byte run of 8 k). Workgroup tile 64 (M) x 128 (B rows), 4 waves as 2 x 2, each 32 rows x two 32-column blocks
-// (the A fragment feeds two MFMAs). K stages of 32 through padded LDS rows (40 halves: the 32 lanes of a fragment
-// read hit distinct banks), double-buffered, with two register sets so the next stage's loads are in flight during
-// this stage's MFMAs; loads and stores are unconditional (clamped) and the last odd stage is peeled.
+// (the A fragment feeds two MFMAs). K stages of 64 through padded LDS rows (72 halves: the 32 lanes of a fragment
+// read hit distinct banks), double-buffered, fed from a ring of four register sets (loads run three stages ahead);
+// loads and stores are unconditional (clamped), four stages per loop iteration, the remainder peeled.
 // SwiGLU: the tile's B rows are 64 gate rows (W^T rows o0..o0+63) and the 64 matching up rows (N + o0 ..), so a
 // wave's two blocks hold gate and up of the same outputs and the epilogue is elementwise in registers.
 // Split-K: grid z = split, K range [z kSplit, ...); raw tile sums go to part [split][M][W] (W = N, or 2N with the
@@ -323,7 +323,8 @@ struct GemmF16Params {
   int split;
 };
 
-constexpr int GBM = 64, GBN = 128, GBK = 32, GLD = 40;
+constexpr int GBM = 64, GBN = 128, GBK = 64, GLD = GBK + 8;
+constexpr int GA = GBM * GBK / 8 / 256, GB = GBN * GBK / 8 / 256;  // 16-byte chunks per thread per stage
 
 template <bool SWIGLU, bool KTAIL>
 __global__ __launch_bounds__(256, 2) void gemmF16Kernel(GemmF16Params p) {
@@ -335,74 +336,83 @@ __global__ __launch_bounds__(256, 2) void gemmF16Kernel(GemmF16Params p) {
   const int64_t m0 = static_cast<int64_t>(gi.y) * GBM;
   const int64_t kb = p.split > 1 ? gi.z * p.kSplit : 0;
   const int64_t ke = p.split > 1 ? min<int64_t>(kb + p.kSplit, p.k) : p.k;
-  // staging: thread -> tile row sr (A row, and B rows sr and 64 + sr), 8-half chunk sc
-  const int sr = tid >> 2, sc = (tid & 3) * 8;
-  const h16* ap = p.a + min<int64_t>(m0 + sr, p.m - 1) * p.lda;
-  int64_t b0, b1;
-  if constexpr (SWIGLU) {
-    const int64_t o = min<int64_t>(static_cast<int64_t>(gi.x) * 64 + sr, p.n - 1);
-    b0 = o;
-    b1 = p.n + o;
-  } else {
-    const int64_t n0 = static_cast<int64_t>(gi.x) * GBN;
-    b0 = min<int64_t>(n0 + sr, p.n - 1);
-    b1 = min<int64_t>(n0 + 64 + sr, p.n - 1);
+  // staging: chunk id = tid + 256 i -> tile row id / 8, k offset 8 (id % 8)
+  constexpr int CPR = GBK / 8;
+  const int sc = (tid % CPR) * 8;
+  const h16* ap[GA];
+  const h16* bp[GB];
+#pragma unroll
+  for (int i = 0; i < GA; ++i) ap[i] = p.a + min<int64_t>(m0 + (tid + 256 * i) / CPR, p.m - 1) * p.lda;
+#pragma unroll
+  for (int i = 0; i < GB; ++i) {
+    const int r = (tid + 256 * i) / CPR;
+    int64_t row;
+    if constexpr (SWIGLU) {
+      const int64_t o = min<int64_t>(static_cast<int64_t>(gi.x) * 64 + (r & 63), p.n - 1);
+      row = r < 64 ? o : p.n + o;
+    } else {
+      row = min<int64_t>(static_cast<int64_t>(gi.x) * GBN + r, p.n - 1);
+    }
+    bp[i] = p.bt + row * p.k;
   }
-  const h16* bp0 = p.bt + b0 * p.k;
-  const h16* bp1 = p.bt + b1 * p.k;
-  half8 ra[2], rb0[2], rb1[2];
+  // a ring of GD register sets: stage s's tile is loaded into set s % GD while it is GD - 1 stages ahead of the
+  // stage whose MFMAs run, so each load has GD - 2 stages of MFMA work to arrive in before its LDS store
+  constexpr int GD = 4;
+  half8 ra[GD][GA], rb[GD][GB];
   auto gload = [&](int64_t k0, int s) {
     const int64_t kk = min<int64_t>(k0 + sc, ke - 8);
-    ra[s] = ld8(ap + kk);
-    rb0[s] = ld8(bp0 + kk);
-    rb1[s] = ld8(bp1 + kk);
+#pragma unroll
+    for (int i = 0; i < GA; ++i) ra[s][i] = ld8(ap[i] + kk);
+#pragma unroll
+    for (int i = 0; i < GB; ++i) rb[s][i] = ld8(bp[i] + kk);
   };
   auto sstore = [&](int buf, int64_t k0, int s) {
-    half8 x = ra[s], y = rb0[s], z = rb1[s];
-    if constexpr (KTAIL) {
-      if (k0 + sc >= ke) {
-        const half8 zero = {};
-        x = zero;
-        y = zero;
-        z = zero;
-      }
-    }
-    st8(&As[buf][sr * GLD + sc], x);
-    st8(&Bs[buf][sr * GLD + sc], y);
-    st8(&Bs[buf][(64 + sr) * GLD + sc], z);
+    const bool zero = KTAIL && k0 + sc >= ke;
+    const half8 z = {};
+#pragma unroll
+    for (int i = 0; i < GA; ++i) st8(&As[buf][((tid + 256 * i) / CPR) * GLD + sc], zero ? z : ra[s][i]);
+#pragma unroll
+    for (int i = 0; i < GB; ++i) st8(&Bs[buf][((tid + 256 * i) / CPR) * GLD + sc], zero ? z : rb[s][i]);
   };
   f32x16 acc0, acc1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.0f;
   const int64_t stages = (ke - kb + GBK - 1) / GBK;
-  auto stage = [&](int64_t st, int buf, int sNext, int sFar) {
-    half8 af[2], bf0[2], bf1[2];
+  auto kOf = [&](int64_t st) { return kb + min<int64_t>(st, stages - 1) * GBK; };
+  // stage st: MFMAs on LDS buffer st & 1; loads stage st + GD - 1 into set (st + GD - 1) % GD; stores stage st + 1
+  // from set (st + 1) % GD into the other buffer. Loads past the last stage reload it (unconditional).
+  auto stage = [&](int64_t st, int buf, int sLoad, int sStore) {
+    constexpr int Q = GBK / 16;
+    half8 af[Q], bf0[Q], bf1[Q];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < Q; ++q) {
       af[q] = ld8(&As[buf][(32 * wr + lr) * GLD + 16 * q + 8 * lh]);
       bf0[q] = ld8(&Bs[buf][(32 * wc + lr) * GLD + 16 * q + 8 * lh]);
       bf1[q] = ld8(&Bs[buf][(64 + 32 * wc + lr) * GLD + 16 * q + 8 * lh]);
     }
-    gload(kb + min<int64_t>(st + 2, stages - 1) * GBK, sFar);
+    gload(kOf(st + GD - 1), sLoad);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < Q; ++q) {
       acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[q], bf0[q], acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[q], bf1[q], acc1, 0, 0, 0);
     }
-    sstore(buf ^ 1, kb + min<int64_t>(st + 1, stages - 1) * GBK, sNext);
+    sstore(buf ^ 1, kOf(st + 1), sStore);
     __syncthreads();
   };
-  gload(kb, 0);
+#pragma unroll
+  for (int j = 0; j < GD - 1; ++j) gload(kOf(j), j);
   sstore(0, kb, 0);
-  gload(kb + min<int64_t>(1, stages - 1) * GBK, 1);
   __syncthreads();
   int64_t st = 0;
-  for (; st + 1 < stages; st += 2) {
-    stage(st, 0, 1, 0);
-    stage(st + 1, 1, 0, 1);
+  for (; st + GD <= stages; st += GD) {
+    stage(st, 0, 3, 1);
+    stage(st + 1, 1, 0, 2);
+    stage(st + 2, 0, 1, 3);
+    stage(st + 3, 1, 2, 0);
   }
-  if (st < stages) stage(st, 0, 1, 0);
-
+  if (st < stages) stage(st, 0, 3, 1);
+  if (st + 1 < stages) stage(st + 1, 1, 0, 2);
+  if (st + 2 < stages) stage(st + 2, 0, 1, 3);
   // accumulator r of a block: row 8 (r / 4) + 4 lh + r % 4 of the wave's 32, column lr of the block
   const int64_t lastRow = p.m - 1;
   if (p.split > 1) {
