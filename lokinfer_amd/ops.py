@@ -12,7 +12,6 @@ from __future__ import annotations
 
 import torch
 
-from . import trace as _trace
 from .runtime import GpuContext
 from . import winograd as _wino
 from .tensor import Tensor, f32, i64
@@ -68,7 +67,6 @@ def _launch(name: str, operands: list[Tensor], out_shapes: list[tuple], attrs: d
             raise OpError(f"attribute {k}: unsupported type {type(v).__name__}")
     ptrs = [x.data_ptr() for x in list(operands) + list(outs)]
     ctx.run(name, ptrs, ints, floats)
-    _trace.record(name, operands, outs, ints, floats)
     if not outs:
         return None
     return outs[0] if len(outs) == 1 else tuple(outs)
@@ -78,7 +76,6 @@ def _launch(name: str, operands: list[Tensor], out_shapes: list[tuple], attrs: d
 
 def to_gpu(x: Tensor) -> Tensor:
     out = Tensor(x.t.to(GpuContext.shared().device, non_blocking=False))
-    _trace.record_copy(x, out)
     return out
 
 
