@@ -71,3 +71,21 @@ def test_chunk_graph_equals_eager(setup):
     for pos in (0, 32, 64):  # the same T three times: graph capture, then replays
         la, lb = a(ids[pos:pos + 32], pos), b(ids[pos:pos + 32], pos)
         assert np.array_equal(la, lb), pos
+
+
+def test_generate_to_cache_capacity(setup):
+    """A 1000-token prompt in one chunk, then decode steps up to position 1023 (the last cache row; 16 decode chunks
+    and 32 key tiles of the cache attention): every step's logits match HF's full forward over the tokens so far."""
+    G, O, sd, m = setup
+    model = G.Gpt2Generator(sd)
+    ids = np.random.default_rng(9).integers(0, G.VOCAB, 1024).astype(np.int64)
+    got = model(ids[:1000], 0)
+    assert rel(got, O.last_logits(m, ids[:1000])) <= 1e-4
+    for pos in (1000, 1001, 1023):
+        if pos > 1001:
+            for p in range(1002, pos):
+                model(ids[p:p + 1], p)
+        got = model(ids[pos:pos + 1], pos)
+        assert rel(got, O.last_logits(m, ids[:pos + 1])) <= 1e-4, pos
+    with pytest.raises(ValueError):
+        model(ids[:2], 1023)  # past the cache: refused on the host

@@ -105,3 +105,24 @@ def test_config5_prefill_and_greedy_decode(gpu):
         ref = orc([tok], dummy, pos)
         pos += 1
         assert rel(got, ref) <= 1e-2, (i, rel(got, ref))
+
+
+def test_small_long_chunk_and_many_decode_chunks(small):
+    """A 1100-id prefill chunk (35 query blocks of the flash attention) over a 1200-row cache, then decode steps whose
+    attention spans 18 key chunks (more than one merge block), against the oracle."""
+    M, Q, cfg, sd, _, _ = small
+    r = np.random.default_rng(21)
+    ids = r.integers(0, 150000, 1100).astype(np.int64)
+    ids[9:409] = M.F.PAD_ID
+    audio = (r.standard_normal((400, cfg.d)) * 0.5).astype(np.float16)
+    lm = M.Qwen3Lm(sd, cfg)
+    kv = lm.kv_cache(1200)
+    orc = Q.OracleLm(sd, cfg, Q.Ops(np.float32), 1200)
+    got, ref = lm(ids, audio, 0, kv), orc(ids, audio, 0)
+    assert rel(got, ref) <= 1e-2, rel(got, ref)
+    dummy = np.zeros((1, cfg.d), np.float16)
+    pos = 1100
+    for tok in (5, 77, 150000):
+        got, ref = lm([tok], dummy, pos, kv), orc([tok], dummy, pos)
+        assert rel(got, ref) <= 1e-2, (pos, rel(got, ref))
+        pos += 1
