@@ -225,6 +225,11 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
         for _ in range(5):
             lk.ops.add_f32_gpu(p1, p2)
         torch.cuda.synchronize()
+    # the register-only f32 MFMA rate of this GPU under a chip-wide load (what the clock allows)
+    pit, pwg = 512, 1024
+    lk.ops.mfma_probe_f32_gpu(pit, pwg)
+    probe_ms = statistics.median(event_times(lambda: lk.ops.mfma_probe_f32_gpu(pit, pwg), 5))
+    ceiling = pwg * 4 * pit * 8 * 4096 / (probe_ms * 1e-3) / 1e12
     a = W.alpha_of(k)
     flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c
     direct = 2.0 * l * c * c * k
@@ -232,7 +237,8 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
             "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
             "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops,
-            "conv_ms": conv_ms, "conv_direct_equiv_tflops": direct / (conv_ms * 1e-3) / 1e12}
+            "conv_ms": conv_ms, "conv_direct_equiv_tflops": direct / (conv_ms * 1e-3) / 1e12,
+            "mfma_ceiling_tflops": ceiling}
 
 
 def cpu_kokoro(sd, inputs, budget_s: float = 30.0) -> dict:
@@ -360,6 +366,7 @@ def main():
                    "global_batch": 1, "seq_len": tokens, "parallelism": "none"},
         "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": roof["kernel"], "roofline_avg_launch_ms": roof["avg_launch_ms"],
+        "roofline_mfma_ceiling_tflops": round(roof["mfma_ceiling_tflops"], 1),
         "roofline_conv_ms": roof["conv_ms"], "roofline_conv_direct_equiv_tflops": roof["conv_direct_equiv_tflops"],
         "forward_algorithmic_tflops": round(r["flops"] / (r["median_ms"] * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,

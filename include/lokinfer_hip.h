@@ -247,6 +247,10 @@ int lk_hip_f16_elementwise(const void* a, const void* b, void* out, int64_t n, i
 /* weight packing: W f16[K, N] -> W^T f16[N, K] */
 int lk_hip_f16_transpose(const void* w, void* wt, int64_t k, int64_t n, void* stream);
 
+/* ---- measurement (no counterpart in the reference): register-only f32 MFMA loop, out f32[workgroups * 256];
+ *      FLOPs = workgroups * 4 * iters * 8 * 4096 */
+int lk_hip_mfma_f32_probe(float* out, int iters, int workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

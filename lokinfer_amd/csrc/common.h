@@ -69,6 +69,7 @@ void registerSignalKernels();
 void registerDecodeFusedKernels();
 void registerWinogradKernels();
 void registerF16Kernels();
+void registerProbeKernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 

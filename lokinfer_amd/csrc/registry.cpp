@@ -593,6 +593,7 @@ static void registerAll() {
     registerDecodeFusedKernels();
     registerWinogradKernels();
     registerF16Kernels();
+    registerProbeKernels();
     std::sort(names().begin(), names().end());
   });
 }

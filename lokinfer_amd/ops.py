@@ -850,3 +850,10 @@ def conv1d_1ch_f32_gpu(x, w, b, stride=1, padding=0, out=None):
         check(out.dtype == f32 and tuple(out.shape) == (lo,), "out must be f32[Lo]")
     return _launch("conv1d_1ch_f32_gpu", [x, w, b], [(lo,)], dict(padding=int(padding), stride=int(stride)),
                    outs=None if out is None else [out])
+
+
+def mfma_probe_f32_gpu(iters: int = 512, workgroups: int = 1024):
+    """(MI355X backend, measurement) register-only f32 MFMA loop: workgroups x 4 waves x iters x 8 x 4096 FLOPs."""
+    check(iters > 0 and workgroups > 0, "iters and workgroups must be positive")
+    return _launch("mfma_probe_f32_gpu", [], [(workgroups * 256,)], dict(iters=int(iters), workgroups=int(workgroups)))
+
