@@ -89,3 +89,30 @@ def test_generate_to_cache_capacity(setup):
         assert rel(got, O.last_logits(m, ids[:pos + 1])) <= 1e-4, pos
     with pytest.raises(ValueError):
         model(ids[:2], 1023)  # past the cache: refused on the host
+
+
+def test_capture_with_collectable_models(setup):
+    """Regression: models hold their compiled function and it holds them back, so only the cycle collector frees
+    them, and a collection during a graph capture destroyed their captured graphs mid-capture. Unreachable models
+    are left behind and the collector is made to run on (nearly) every allocation while a new model captures; the
+    capture must succeed and give the eager logits."""
+    import gc
+
+    G, O, sd, m = setup
+    for _ in range(2):
+        d = G.Gpt2Generator(sd)
+        d([5, 6, 7], 0)
+        d([8], 3)  # captures the decode graph
+        del d  # now only reachable through its own cycle
+    old = gc.get_threshold()
+    gc.set_threshold(1)
+    try:
+        a = G.Gpt2Generator(sd, graph=True)
+        a([5, 6, 7], 0)
+        la = a([8], 3)
+    finally:
+        gc.set_threshold(*old)
+    assert gc.isenabled()
+    b = G.Gpt2Generator(sd, graph=False)
+    b([5, 6, 7], 0)
+    assert np.array_equal(la, b([8], 3))
