@@ -820,8 +820,10 @@ static void launchGemm(GemmParams p, hipStream_t s, void* ws = nullptr, int64_t 
     else
       hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
   } else if (AM == lkd::A_ROWMAJOR && aligned) {
-    // few output tiles: K split over the waves of a workgroup; 32-column tiles when 64 would leave CUs idle
-    const bool wide = static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 192;
+    // few output tiles: K split over the waves of a workgroup; 32-column tiles unless the 64-column grid alone
+    // already gives every CU two workgroups (at M ~ 500, N = 2304 / 3072, 288-384 wide tiles left the last round
+    // of workgroups a fraction of the chip: 40.9 -> 32.7 us and 42.8 -> 34.2 us with 32 columns)
+    const bool wide = static_cast<int64_t>(ceilDiv(p.m, 64)) * ceilDiv(p.n, 64) >= 512;
     const int64_t tiles = static_cast<int64_t>(ceilDiv(p.n, wide ? 64 : 32)) * ceilDiv(p.m, 64);
     // and across workgroups when the grid still leaves CUs idle and K is long: 64-aligned K ranges of at least
     // 256, partial tiles in the workspace past its 64 KiB counter area, summed by gemmSplitReduceKernel
