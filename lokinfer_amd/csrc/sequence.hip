@@ -95,6 +95,21 @@ __global__ void lstmClearKernel(unsigned long long* xbuf, int n) {
   if (i < n) xbuf[i] = 0ull;
 }
 
+// Row r (lanes 16 r .. 16 r + 15) of a wave holds gate r of 16 units; returns in row 0 the four gates of each
+// unit. v_permlane16_swap(v, v) exchanges the odd rows of its first operand with the even rows of its second, so
+// its second result holds rows {1, 1, 3, 3}; v_permlane32_swap(v, v) exchanges the halves the same way, its second
+// result holding rows {2, 3, 2, 3}. Three VALU ops instead of LDS permutes.
+__device__ __forceinline__ void gatherGates(float v, float& i, float& f, float& g, float& o) {
+  const unsigned u = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const auto p3 = __builtin_amdgcn_permlane16_swap(p32[1], p32[1], false, false);
+  i = v;
+  f = __uint_as_float(p16[1]);
+  g = __uint_as_float(p32[1]);
+  o = __uint_as_float(p3[1]);
+}
+
 __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float* __restrict__ g,
                                                                     const float* __restrict__ whhT,
                                                                     float* __restrict__ out,
@@ -111,6 +126,10 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
   float w[64];
 #pragma unroll
   for (int i = 0; i < 64; ++i) w[i] = whhT[static_cast<int64_t>(64 * wave + i) * ld + col];
+  // every weight in registers before the loop (the empty asm redefines each one), so the step's products carry
+  // no per-load waits
+#pragma unroll
+  for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(w[i]));
   reinterpret_cast<float*>(hsw[wave])[lane] = 0.0f;
   unsigned long long* xdir = xbuf + dir * 2 * H;  // [parity][H]
   float c = 0.0f;
@@ -142,8 +161,8 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       const float x = gv + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
       const float sg = sigmoidHw(gate == 2 ? 2.0f * x : x);
       const float act = gate == 2 ? fmaf(2.0f, sg, -1.0f) : sg;
-      const float ig = __shfl(act, unit, 64), fg = __shfl(act, 16 + unit, 64);
-      const float gg = __shfl(act, 32 + unit, 64), og = __shfl(act, 48 + unit, 64);
+      float ig, fg, gg, og;
+      gatherGates(act, ig, fg, gg, og);
       if (lane < kLstmUnits) {
         c = fg * c + ig * gg;
         const float hv = ok ? og * tanhHw(c) : __builtin_nanf("");
