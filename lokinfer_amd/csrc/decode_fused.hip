@@ -32,9 +32,23 @@ constexpr int kPartStride = kDecHd + 2;
 // rows per wave of the partial GEMV: 16 for K <= 1024, else 64 (12 slices at K = 768 and at K = 3072)
 inline int64_t gemvRowsPerWave(int64_t k) { return k <= 1024 ? 16 : 64; }
 
-// Workgroup = 4 waves over 256 columns (64 lanes x float4) and 4 * RPW rows; wave w sums rows
-// r0 + w RPW .. + RPW - 1, the four wave sums combine in LDS as (w0 + w1) + (w2 + w3), and the workgroup writes
-// slice blockIdx.y. The workgroup's slice of x is first formed in LDS according to XMODE.
+#ifndef LK_GEMV_MIN_WGS
+#define LK_GEMV_MIN_WGS 256
+#endif
+// Column block of the partial GEMV: the widest of 256 / 128 / 64 columns whose grid still has LK_GEMV_MIN_WGS
+// workgroups, else 64.
+inline int gemvColBlock(int64_t n, int64_t slices) {
+  for (int cb = 256; cb > 64; cb /= 2)
+    if (lkh::ceilDiv(n, cb) * slices >= LK_GEMV_MIN_WGS) return cb;
+  return 64;
+}
+
+// Workgroup = 4 waves over CB columns and 4 * RPW rows; wave w owns rows r0 + w RPW .. + RPW - 1. A wave row of
+// CB / 4 lanes (float4 each) spans the CB columns, so a wave holds RS = 256 / CB such rows: lane subgroup q sums
+// rows q, q + RS, q + 2 RS, ... of the wave's RPW. The subgroups combine by permlane swaps ((q0 + q1) + (q2 + q3)),
+// the four wave sums in LDS as (w0 + w1) + (w2 + w3), and the workgroup writes slice blockIdx.y. Narrow column
+// blocks multiply the workgroups of a small-N GEMV (N = 768: 36 at CB = 256, 144 at CB = 64) without adding row
+// slices for the consumer to sum. The workgroup's slice of x is first formed in LDS according to XMODE.
 struct LnIn {  // mode 3: x = LayerNorm(sum of xpart slices + xbias + res), workgroup (0, 0) writes the sum
   const float* res;
   const float* gamma;
@@ -43,14 +57,32 @@ struct LnIn {  // mode 3: x = LayerNorm(sum of xpart slices + xbias + res), work
   float eps;
 };
 
-template <int XMODE, int RPW>
+// Sum of v over the RS lane subgroups of a wave (subgroup = 64 / RS consecutive lanes), in every subgroup.
+template <int RS>
+__device__ __forceinline__ float subgroupSum(float v) {
+  if constexpr (RS == 1) {
+    return v;
+  } else {
+    float r = v;
+    if constexpr (RS == 4) {
+      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+      r = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+    return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  }
+}
+
+template <int XMODE, int RPW, int CB>
 __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__ x, const float* __restrict__ xpart,
                                                       const float* __restrict__ xbias, int64_t xslices, int chunks,
                                                       LnIn ln, const float* __restrict__ w, float* __restrict__ part,
                                                       int64_t n, int64_t k) {
   constexpr int ROWS = 4 * RPW;
   __shared__ float xs[ROWS];
-  __shared__ f4v wsum[4][64];
+  constexpr int RS = 256 / CB, CL = CB / 4, LPW = RPW / RS;  // row subgroups, lanes per row, loads per lane
+  static_assert(RPW % RS == 0, "rows per wave must split over the lane subgroups");
+  __shared__ f4v wsum[4][CL];
   __shared__ float mrg[4][kDecHd];
   __shared__ float cw[64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -58,14 +90,16 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
   const int64_t rBase = static_cast<int64_t>(blockIdx.y) * ROWS;
   // The weight loads do not depend on x: the first batch is issued before x is formed, so its latency overlaps
   // the prologue's own loads and reductions.
-  constexpr int B0 = RPW < 32 ? RPW : 32;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + 4 * lane;
-  const int64_t r0 = rBase + static_cast<int64_t>(wv) * RPW;
+  constexpr int B0 = LPW < 32 ? LPW : 32;
+  const int cl = lane % CL, q = lane / CL;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + 4 * cl;
+  const int64_t r0 = rBase + static_cast<int64_t>(wv) * RPW + q;  // this lane's rows r0 + RS i
   const int64_t colc = min<int64_t>(col, n - 4);  // columns past N compute on a valid column, never stored
   f4v wr[B0];
 #pragma unroll
   for (int i = 0; i < B0; ++i)
-    wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + i, k - 1) * n + colc));
+    wr[i] = __builtin_nontemporal_load(
+        reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + RS * i, k - 1) * n + colc));
   if constexpr (XMODE == 0) {
     for (int t = tid; t < ROWS; t += 256) xs[t] = rBase + t < k ? x[rBase + t] : 0.0f;
   } else if constexpr (XMODE == 1) {
@@ -153,21 +187,25 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
   __syncthreads();
   f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < B0; ++i) acc += xs[wv * RPW + i] * wr[i];  // xs is 0 past K
+  for (int i = 0; i < B0; ++i) acc += xs[wv * RPW + q + RS * i] * wr[i];  // xs is 0 past K
 #pragma unroll
-  for (int b = B0; b < RPW; b += 32) {
+  for (int b = B0; b < LPW; b += 32) {
 #pragma unroll
     for (int i = 0; i < 32; ++i)
       wr[i] = __builtin_nontemporal_load(
-          reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + b + i, k - 1) * n + colc));
+          reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + RS * (b + i), k - 1) * n + colc));
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc += xs[wv * RPW + b + i] * wr[i];
+    for (int i = 0; i < 32; ++i) acc += xs[wv * RPW + q + RS * (b + i)] * wr[i];
   }
-  wsum[wv][lane] = acc;
+  acc.x = subgroupSum<RS>(acc.x);
+  acc.y = subgroupSum<RS>(acc.y);
+  acc.z = subgroupSum<RS>(acc.z);
+  acc.w = subgroupSum<RS>(acc.w);
+  if (q == 0) wsum[wv][cl] = acc;
   __syncthreads();
-  if (wv == 0 && col < n)
+  if (wv == 0 && q == 0 && col < n)
     *reinterpret_cast<f4v*>(part + static_cast<int64_t>(blockIdx.y) * n + col) =
-        (wsum[0][lane] + wsum[1][lane]) + (wsum[2][lane] + wsum[3][lane]);
+        (wsum[0][cl] + wsum[1][cl]) + (wsum[2][cl] + wsum[3][cl]);
 }
 
 // One wave per (head, 64-key chunk), as the split decode kernel, but q / k / v of this step are the fixed-order
@@ -360,11 +398,19 @@ int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const
   const lkd::LnIn ln{res, gamma, beta, sum_out, eps};
   if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(part)) & 15) != 0) return 1;
   const int64_t rpw = lkd::gemvRowsPerWave(k);
-  const dim3 grid(lkh::ceilDiv(n, 256), static_cast<unsigned>((k + 4 * rpw - 1) / (4 * rpw)));
+  const int64_t slices = (k + 4 * rpw - 1) / (4 * rpw);
+  const int cb = lkd::gemvColBlock(n, slices);
+  const dim3 grid(lkh::ceilDiv(n, cb), static_cast<unsigned>(slices));
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define LK_GP(MODE, R) \
-  hipLaunchKernelGGL((lkd::gemvPartXKernel<MODE, R>), grid, dim3(256), 0, s, x, xpart, xbias, xslices, chunks, ln, w, \
-                     part, n, k)
+#define LK_GP_CB(MODE, R, CB) \
+  hipLaunchKernelGGL((lkd::gemvPartXKernel<MODE, R, CB>), grid, dim3(256), 0, s, x, xpart, xbias, xslices, chunks, ln, \
+                     w, part, n, k)
+#define LK_GP(MODE, R)                    \
+  do {                                    \
+    if (cb == 256) LK_GP_CB(MODE, R, 256); \
+    else if (cb == 128) LK_GP_CB(MODE, R, 128); \
+    else LK_GP_CB(MODE, R, 64);           \
+  } while (0)
   if (xmode == 0) {
     if (rpw == 16) LK_GP(0, 16);
     else LK_GP(0, 64);
@@ -381,6 +427,7 @@ int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const
     return 1;
   }
 #undef LK_GP
+#undef LK_GP_CB
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
