@@ -116,8 +116,11 @@ struct WinoMmArgs {
   float scale;
 };
 
+// Three workgroups per CU for M = 4 (168 VGPRs; the few spills the bound costs sit before the step loop and in the
+// epilogue): a third wave per SIMD keeps the matrix pipe fed through the other waves' barriers and LDS stores
+// (K = 11 roofline launch 0.574 -> 0.599 of peak).
 template <int M, int A, int N>
-__global__ __launch_bounds__(256, 2) void winoMmKernel(WinoMmArgs p) {
+__global__ __launch_bounds__(256, M == 4 ? 3 : 2) void winoMmKernel(WinoMmArgs p) {
   constexpr int TT = 64;              // tiles per workgroup
   constexpr int ROWS = TT + N - 1;    // staged V rows (group shift)
   constexpr int LDB = 64 + 8;         // k-major U rows: the two lane halves read 4 rows = 32 banks apart
