@@ -187,8 +187,10 @@ __device__ __forceinline__ void storeTile(const GemmParams& p, v16f (&acc)[TM][T
     }
 }
 
+// The general form (FAST = false) is held to 168 VGPRs, three waves per SIMD (10 spills, outside the K loop's
+// MFMA body): 162 -> 123 us on the Kokoro decoder's im2col conv GEMM. The FAST form fits 168 by itself.
 template <int BM, int BN, int AM, int BMODE, bool FAST = false>
-__global__ __launch_bounds__(NT, 2) void gemmMfmaKernel(GemmParams p) {
+__global__ __launch_bounds__(NT, FAST ? 2 : 3) void gemmMfmaKernel(GemmParams p) {
   constexpr int WTM = BM / 2, WTN = BN / 2;    // wave tile
   constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
   constexpr int PADA = 4, PADB = 4;
@@ -569,8 +571,10 @@ struct TapCfg {
 };
 
 template <int BM, int BN>
-// At most 168 VGPRs: three waves per SIMD (12 per CU) keep the MFMA pipe fed through the barriers.
-__global__ __launch_bounds__(NT, 3) void convTapKernel(GemmParams p, int taps, int halo) {
+// 64 x 64: at most 168 VGPRs, three waves per SIMD (12 per CU) keep the MFMA pipe fed through the barriers.
+// 128 x 128 needs 254 VGPRs: bounded to three waves it spilled 77 of them and ran 222 vs 159 us on the Kokoro
+// decoder's conv, so it runs two.
+__global__ __launch_bounds__(NT, BM == 128 ? 2 : 3) void convTapKernel(GemmParams p, int taps, int halo) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int MAXH = TapCfg<BM>::maxHalo;
