@@ -116,11 +116,12 @@ struct WinoMmArgs {
   float scale;
 };
 
-// Three workgroups per CU for M = 4 (168 VGPRs; the few spills the bound costs sit before the step loop and in the
-// epilogue): a third wave per SIMD keeps the matrix pipe fed through the other waves' barriers and LDS stores
-// (K = 11 roofline launch 0.574 -> 0.599 of peak).
-template <int M, int A, int N>
-__global__ __launch_bounds__(256, M == 4 ? 3 : 2) void winoMmKernel(WinoMmArgs p) {
+// OCC workgroups per CU. M = 4 at OCC = 3 fits 168 VGPRs (the few spills the bound costs sit before the step loop
+// and in the epilogue): on grids of more than two workgroups per CU a third wave per SIMD keeps the matrix pipe fed
+// through the other waves' barriers and LDS stores (K = 11 roofline launch 0.574 -> 0.599 of peak); smaller grids
+// leave the third slot empty and run the unconstrained OCC = 2 form (176 VGPRs), which is 0.5% faster there.
+template <int M, int A, int N, int OCC = 2>
+__global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   constexpr int TT = 64;              // tiles per workgroup
   constexpr int ROWS = TT + N - 1;    // staged V rows (group shift)
   constexpr int LDB = 64 + 8;         // k-major U rows: the two lane halves read 4 rows = 32 banks apart
@@ -405,12 +406,19 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
   const dim3 grid(static_cast<unsigned>(co / 64), static_cast<unsigned>((tiles + 63) / 64),
                   static_cast<unsigned>(dilation * split));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool occ3 = static_cast<int64_t>(grid.x) * grid.y * grid.z > 2 * 256;  // more than two per CU
   if (a == 4)
     hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1>), grid, dim3(256), 0, s, p);
+  else if (a == 6 && occ3)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3>), grid, dim3(256), 0, s, p);
   else if (a == 6)
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1>), grid, dim3(256), 0, s, p);
+  else if (groups == 2 && occ3)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2, 3>), grid, dim3(256), 0, s, p);
   else if (groups == 2)
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2>), grid, dim3(256), 0, s, p);
+  else if (occ3)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3, 3>), grid, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3>), grid, dim3(256), 0, s, p);
   if (split > 1) {
