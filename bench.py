@@ -191,7 +191,7 @@ def wino_tiles(lo: int, d: int, m: int = 4) -> int:
 
 
 def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
-    """The dominant kernel of the Kokoro forward: the Winograd GEMM (winoMmKernel<4,7,3>, wino_mm_lc_f32_gpu) of a
+    """The dominant kernel of the Kokoro forward: the Winograd GEMM (winoMmKernel<4,7,3,3>, wino_mm_lc_f32_gpu) of a
     generator stage-1 resblock conv (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11 as 3 nested
     F(4,4) tap groups, d = 5). Its algorithm is A = 7 point GEMMs over (group, channel): 2 A T (N Ci) Co FLOPs
     per launch for T output tiles of 4 rows. The whole conv (input transform + GEMM, snake prologue) is timed
@@ -233,7 +233,7 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
     a = W.alpha_of(k)
     flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c
     direct = 2.0 * l * c * c * k
-    return {"kernel": "winoMmKernel<4,7,3> (wino_mm_lc_f32_gpu: K = 11 Winograd GEMM, generator stage 1)",
+    return {"kernel": "winoMmKernel<4,7,3,3> (wino_mm_lc_f32_gpu: K = 11 Winograd GEMM, generator stage 1)",
             "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
             "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops,
