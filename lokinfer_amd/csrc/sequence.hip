@@ -70,14 +70,14 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 }
 
 // Persistent LSTM recurrence: 16 workgroups per direction, each owning 16 hidden units, i.e. 64 gate rows of
-// W_hh held in registers for the whole sequence. Wave w of a workgroup owns k = 64 w .. 64 w + 63 and lane r
-// the gate row r = gate * 16 + unit, so a lane keeps 64 weights and the wave needs only the 64 values of h(t-1)
-// that its own lanes polled: they pass through a wave-private LDS slice (no workgroup barrier before the dot
-// products). The four waves' partial sums meet at one barrier; then wave 0 applies one activation per lane (its
-// gate row), combines the four gates of each unit with lane shuffles, updates the cell and publishes h(t) as
-// 64-bit words {tag = step + 1, value} with agent-scope atomic stores. Every wave then polls its 64 words of h(t)
-// until the tags match. No fences, no counters: the tag orders each value on its own. The gate pre-activations
-// of the next step are loaded while wave 0 polls.
+// W_hh held in registers for the whole sequence. Wave w of a workgroup owns k = KW w .. KW w + KW - 1 (KW = H /
+// kLstmWaves) and lane r the gate row r = gate * 16 + unit, so a lane keeps KW weights and the wave needs only the
+// KW values of h(t-1) that its own lanes polled: they pass through a wave-private LDS slice (no workgroup barrier
+// before the dot products). The waves' partial sums meet at one barrier; then wave 0 applies one activation per
+// lane (its gate row), gathers the four gates of each unit into row 0 with permlane swaps, updates the cell and
+// publishes h(t) as 64-bit words {tag = step + 1, value} with agent-scope atomic stores. Every wave then polls its
+// KW words of h(t) until the tags match. No fences, no counters: the tag orders each value on its own. The gate
+// pre-activations of the next step are loaded while wave 0 polls.
 // The words are double-buffered by step parity: a writer can be one step ahead of a reader (it only needs the
 // reader's h of the current step, which the reader publishes before it gathers), so with a single buffer its
 // step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
@@ -87,7 +87,10 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 // co-resident) ends the kernel instead of hanging it.
 constexpr int kLstmWgs = 16;         // workgroups per direction
 constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
-constexpr int kLstmThreads = 256;    // 4 waves x 64 k
+// waves per workgroup, each over H / kLstmWaves of k: 8 waves of 32 k run a step in 1.18 us, 4 of 64 k in 1.23 us,
+// 16 of 16 k in 1.23 us (the 16-partial sum and the wider barrier cost what the shorter dot products save)
+constexpr int kLstmWaves = 8;
+constexpr int kLstmThreads = 64 * kLstmWaves;
 constexpr long long kLstmSpinLimit = 1LL << 22;
 
 __global__ void lstmClearKernel(unsigned long long* xbuf, int n) {
@@ -116,21 +119,22 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
                                                                     unsigned long long* xbuf, int* failed,
                                                                     int64_t t) {
   constexpr int H = 256;
-  __shared__ float4 hsw[4][16];   // wave w: h(t-1)[64 w .. 64 w + 63]
-  __shared__ float part[4][64];   // wave w's partial dot product of each gate row
+  constexpr int KW = H / kLstmWaves;  // k per wave
+  __shared__ float4 hsw[kLstmWaves][KW / 4];  // wave w: h(t-1)[KW w .. KW w + KW - 1]
+  __shared__ float part[kLstmWaves][64];      // wave w's partial dot product of each gate row
   const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ld = 8 * H;
   const int gate = lane >> 4, unit = lane & 15;
   const int64_t col = dir * 4 * H + gate * H + b * kLstmUnits + unit;  // this lane's gate row in g / W_hh^T
-  float w[64];
+  float w[KW];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) w[i] = whhT[static_cast<int64_t>(64 * wave + i) * ld + col];
+  for (int i = 0; i < KW; ++i) w[i] = whhT[static_cast<int64_t>(KW * wave + i) * ld + col];
   // every weight in registers before the loop (the empty asm redefines each one), so the step's products carry
   // no per-load waits
 #pragma unroll
-  for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(w[i]));
-  reinterpret_cast<float*>(hsw[wave])[lane] = 0.0f;
+  for (int i = 0; i < KW; ++i) asm volatile("" : "+v"(w[i]));
+  reinterpret_cast<float*>(hsw[wave])[lane % KW] = 0.0f;
   unsigned long long* xdir = xbuf + dir * 2 * H;  // [parity][H]
   float c = 0.0f;
   bool ok = true;
@@ -140,13 +144,13 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
     const int64_t tt = dir == 0 ? step : t - 1 - step;
     __builtin_amdgcn_wave_barrier();
     // all 16 broadcast reads in flight before the first product
-    float4 hv[16];
+    float4 hv[KW / 4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) hv[i] = hsw[wave][i];
+    for (int i = 0; i < KW / 4; ++i) hv[i] = hsw[wave][i];
     __builtin_amdgcn_sched_barrier(0);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < KW / 4; ++i) {
       const float4 h = hv[i];
       a0 = fmaf(w[4 * i], h.x, a0);
       a1 = fmaf(w[4 * i + 1], h.y, a1);
@@ -158,7 +162,14 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
     const unsigned tag = static_cast<unsigned>(step + 1);
     unsigned long long* xb = xdir + (step & 1) * H;
     if (wave == 0) {
-      const float x = gv + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+      float pv[kLstmWaves];  // the waves' partials summed as a pairwise tree: ((p0 + p1) + (p2 + p3)) + ...
+#pragma unroll
+      for (int i = 0; i < kLstmWaves; ++i) pv[i] = part[i][lane];
+#pragma unroll
+      for (int n = kLstmWaves; n > 1; n /= 2)
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) pv[i] = pv[2 * i] + pv[2 * i + 1];
+      const float x = gv + pv[0];
       const float sg = sigmoidHw(gate == 2 ? 2.0f * x : x);
       const float act = gate == 2 ? fmaf(2.0f, sg, -1.0f) : sg;
       float ig, fg, gg, og;
@@ -172,12 +183,13 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       }
       if (step + 1 < t) gv = g[(dir == 0 ? step + 1 : t - 2 - step) * ld + col];
     }
-    // gather this wave's 64 values of h(t): lane polls word 64 w + lane
+    // gather this wave's KW values of h(t): lane polls word KW w + lane % KW (with KW = 32 both wave halves poll
+    // the same words and store the same values)
     {
       unsigned long long word = 0ull;
       long long spins = 0;
       while (ok) {
-        word = __hip_atomic_load(xb + 64 * wave + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        word = __hip_atomic_load(xb + KW * wave + lane % KW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (static_cast<unsigned>(word >> 32) == tag) break;
         if (++spins > kLstmSpinLimit) {
           ok = false;
@@ -186,7 +198,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       }
       // A lane that timed out keeps stepping (so every wave reaches the end) but stops waiting; its NaN
       // reaches every gate row through the next step's dot products.
-      reinterpret_cast<float*>(hsw[wave])[lane] =
+      reinterpret_cast<float*>(hsw[wave])[lane % KW] =
           ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
   }
