@@ -281,13 +281,16 @@ class KokoroGpu:
         with ctx.branch(self.streams[0], 1):
             t_en = self.text_encoder(ids)
             asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
+            self._keep("t_en", t_en)
         bert = self.albert(ids)
+        self._keep("bert", bert)
         d_en = ops.gemm_bias_f32_gpu(bert, self.g("bert_encoder.weight", _t), self.g("bert_encoder.bias"))
         x = ops.concat_bcast_f32_gpu(d_en, sp_vec)
         for i in range(3):
             x = self.lstm(x, f"predictor.text_encoder.lstms.{2 * i}")
             x = ops.adalayernorm_f32_gpu(x, self.style(bank_p, f"predictor.text_encoder.lstms.{2 * i + 1}.fc"))
             x = ops.concat_bcast_f32_gpu(x, sp_vec)
+        self._keep("d", x)
         en = ops.repeat_interleave_f32_gpu(x, dur, frames)  # [F, 640]
         sh = self.lstm(en, "predictor.shared")  # [F, 512]
 

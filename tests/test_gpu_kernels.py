@@ -383,3 +383,23 @@ def test_gemv_partial_res_ln(gpu):
     part2, x2 = lk.ops.gemv_partial_ln_f32_gpu(G(lk, res), G(lk, g), G(lk, b), G(lk, w), 1e-5)
     close(x2, res.astype(np.float32), 0)
     close(part2.numpy().sum(0)[None], K.gemm(K.layernorm(res, g, b, 1e-5), w), 2e-5)
+
+
+# At least 256 output tiles of 128 x 128: the only shapes that select convTapKernel<128, 128>, whose epilogue
+# writes the 128-row channel statistics itself (the Kokoro-487 decoder and generator sizes).
+@pytest.mark.parametrize("l,ci,co,k,dil,act", [(5000, 1104, 1024, 3, 1, "leaky"), (40000, 128, 128, 7, 3, "snake"),
+                                               (33000, 128, 128, 11, 5, "none")])
+def test_conv1d_tap128_stats(gpu, l, ci, co, k, dil, act):
+    lk = gpu
+    assert -(-l // 128) * -(-co // 128) >= 256
+    x, w, b = rng.standard_normal((l, ci)), rng.standard_normal((co, k, ci)) / np.sqrt(k * ci), rng.standard_normal(co)
+    af = np.stack([rng.standard_normal(ci) * 0.1, np.abs(rng.standard_normal(ci)) + 0.5, rng.standard_normal(ci) * 0.1])
+    alpha = np.abs(rng.standard_normal(ci)) + 0.2
+    pad = dil * (k - 1) // 2
+    res = rng.standard_normal((l, co))
+    ref = K.conv1d_lc(K.affine_act(x, af, alpha, act, 0.2), w, b, padding=pad, dilation=dil, residual=res,
+                      out_scale=0.7071)
+    y, st = lk.ops.conv1d_act_lc_f32_gpu(G(lk, x), G(lk, w), G(lk, b), G(lk, af), G(lk, alpha), act=act, slope=0.2,
+                                         residual=G(lk, res), out_scale=0.7071, padding=pad, dilation=dil, stats=True)
+    close(y, ref, 1e-4)
+    np.testing.assert_allclose(st.numpy(), K.channel_stats_lc(y.numpy()), rtol=1e-4, atol=1e-4)

@@ -29,9 +29,26 @@ def model(gpu):
     return gpu, KW, sd, KokoroGpu(sd)
 
 
-@pytest.mark.parametrize("tokens", [12, 59])
+# Stage outputs compared at the hidden-state bar (max rel err 1e-4): (GPU name, oracle name, GPU -> oracle layout).
+# The GPU keeps frame-rate tensors channel-last [L, C] (channels padded to 16); the oracle is channel-first [C, L].
+STAGES = [("bert", "bert", None), ("d", "d", None), ("t_en", "t_en", None), ("dec", "dec", "lc"),
+          ("stage0", "stage0", "lc"), ("stage1", "stage1", "lc")]
+
+
+def _as_oracle(a, kind, ref_shape):
+    if kind == "lc":
+        a = a[:, :ref_shape[0]].T
+    return a
+
+
+@pytest.mark.parametrize("tokens", [12, 59, 487])
 def test_forward_matches_oracle(model, tokens):
+    """Graph replay vs the oracle at the benchmark sizes. 487 tokens (2444 frames) is the headline config: it is
+    the only size whose generator convs select the three-per-CU Winograd GEMMs and the 128 x 128 tap conv with
+    its statistics epilogue. An eager run of the same graph supplies the stage outputs; the replayed graph must
+    reproduce its audio bit for bit."""
     lk, KW, sd, m = model
+    from lokinfer_amd.kokoro import KokoroGpu
     from oracle.kokoro import Oracle
 
     ids, ref_s, dur, noise = KW.inputs(tokens)
@@ -39,14 +56,24 @@ def test_forward_matches_oracle(model, tokens):
     audio, f0, n, post = (t.numpy() for t in m.forward(ids, ref_s, dur, noise))
     assert not post[:, 22:].any()  # logit columns past the 22 are zero padding
     post = post[:, :22]
+    eager = KokoroGpu(sd, graph=False)
+    eager.debug = {}
+    audio_e = eager.forward(ids, ref_s, dur, noise)[0].numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(audio, audio_e), "graph replay differs from the eager run of the same graph"
+    kept = {k: v.numpy() for k, v in eager.debug.items()}
+    del eager
     o = Oracle(sd)
     st = o.forward(ids, ref_s, dur, noise, f0_override=f0, stages=True)
     assert audio.shape == (600 * frames,) == tuple(st["audio"].shape)
     e = {"F0": rel(f0, st["F0"].numpy()), "N": rel(n, st["N"].numpy()),
          "post": rel(post.T, st["post"].numpy()), "audio": rel(audio, st["audio"].numpy())}
+    for gname, oname, kind in STAGES:
+        ref = st[oname].numpy()
+        e[gname] = rel(_as_oracle(kept[gname], kind, ref.shape), ref)
     print(f"tokens={tokens} frames={frames} max rel err: " + ", ".join(f"{k} {v:.2e}" for k, v in e.items()))
-    assert e["F0"] <= 1e-4 and e["N"] <= 1e-4
-    assert e["post"] <= 1e-3 and e["audio"] <= 1e-3
+    for k, v in e.items():
+        assert v <= (1e-3 if k == "audio" else 1e-4), (k, v)
 
 
 def test_graph_replay_is_stable(model):

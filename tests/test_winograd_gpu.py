@@ -188,3 +188,38 @@ def test_wino_split_ops_and_rejects(gpu):
         lk.ops.conv1d_wino_lc_f32_gpu(G(lk, x), G(lk, u), G(lk, b), G(lk, tr), 7, padding=8, dilation=3)
     with pytest.raises(ValueError):  # U for another kernel size
         lk.ops.conv1d_wino_lc_f32_gpu(G(lk, x), G(lk, u), G(lk, b), G(lk, tr), 3, padding=3, dilation=3)
+
+
+def _mm_workgroups(lo, co, d, tile):
+    """Workgroups of one wino_mm launch (csrc/winograd.hip lk_hip_wino_mm_lc_f32, no split): 64 output channels x
+    64 tiles of one residue class each. Above 512 (two per CU) the three-per-CU instantiations run."""
+    tiles = -(-(-(-lo // d)) // tile)
+    return (co // 64) * (-(-tiles // 64)) * d
+
+
+# Grids above 512 workgroups: the only shapes that select winoMmKernel<4,6,1,3>, <4,7,2,3> and <4,7,3,3> (the
+# Kokoro-487 generator's convs). Each runs with the fused affine + Snake, the residual and the stats epilogue,
+# as the generator's resblocks do.
+LARGE = [(128, 128, 80000, 11, 5), (256, 256, 48880, 7, 3), (128, 128, 70000, 3, 1), (128, 128, 80000, 3, 5)]
+
+
+@pytest.mark.parametrize("ci,co,l,k,d", LARGE)
+def test_wino_large_grid_instantiations(gpu, ci, co, l, k, d):
+    lk = gpu
+    r, x, w, b = _case(l + 3 * k + d, l, ci, co, k)
+    pad = _pad(k, d)
+    assert _mm_workgroups(l, co, d, 4) > 512
+    af, alpha = _affine(r, ci), r.uniform(0.2, 3.0, ci).astype(np.float32)
+    rr = r.standard_normal((l, co)).astype(np.float32)
+    u, tr = W.wino_weights(w)
+    y, st = lk.ops.conv1d_wino_lc_f32_gpu(G(lk, x), G(lk, u), G(lk, b), G(lk, tr), k, residual=G(lk, rr),
+                                          padding=pad, dilation=d, affine=G(lk, af), alpha=G(lk, alpha), stats=True)
+    ref = _direct(K.affine_act(x, af, alpha, "snake"), w, b, pad, d, rr)
+    close(y, ref, 2e-4)
+    yn = y.numpy()
+    assert st.shape == (W.stats_chunks(l, d) * d, co, 2)
+    if d == 1:
+        np.testing.assert_allclose(st.numpy(), K.channel_stats_lc(yn), rtol=1e-4, atol=1e-4)
+    gb = (r.standard_normal(2 * co) * 0.3).astype(np.float32)
+    af2 = lk.ops.wino_adain_affine_lc_f32_gpu(st, G(lk, gb), l, dilation=d).numpy()
+    _check_affine(af2, yn, gb, co)
