@@ -27,10 +27,19 @@ class Oracle:
         self.dt = dtype
         self.w = {k: torch.from_numpy(v).to(dtype) for k, v in sd.items()}
         self.sd = sd
+        # set to [] to record every module call as (module name, type, input shape, output shape), the layout of
+        # the reference's module-shape logs (bench/research/kokoro/shapes_*.json, written by forward hooks on
+        # the Kokoro package's modules); None records nothing
+        self.trace: list | None = None
+
+    def _rec(self, name, kind, x, y):
+        if self.trace is not None:
+            self.trace.append((name, kind, list(x.shape), list(y.shape)))
+        return y
 
     # ---- building blocks -----------------------------------------------------------------------------------
     def linear(self, x, p):
-        return F.linear(x, self.w[p + ".weight"], self.w[p + ".bias"])
+        return self._rec(p, "Linear", x, F.linear(x, self.w[p + ".weight"], self.w[p + ".bias"]))
 
     def lstm(self, x, p):
         """1-layer bidirectional nn.LSTM, x [T, I] -> [T, 2H] (reference lstm_bidir_f32_cpu, ops/kokoro.py:88-98)."""
@@ -41,31 +50,32 @@ class Oracle:
             for sfx in ("", "_reverse"):
                 for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh"):
                     getattr(m, f"{n}_l0{sfx}").copy_(w[f"{p}.{n}_l0{sfx}"])
-            return m(x[None])[0][0]
+            return self._rec(p, "LSTM", x, m(x[None])[0][0])
 
     def adain(self, x, s, p):
         """AdaIN1d on channel-first x [C, L]: (1 + g) * instance_norm(x) + b, (g, b) = fc(s)."""
-        h = F.linear(s, self.w[p + ".fc.weight"], self.w[p + ".fc.bias"])
+        h = self._rec(p + ".fc", "Linear", s, F.linear(s, self.w[p + ".fc.weight"], self.w[p + ".fc.bias"]))
         c = x.shape[0]
         g, b = h[:c], h[c:]
         return (1 + g[:, None]) * F.instance_norm(x[None], eps=1e-5)[0] + b[:, None]
 
     def conv(self, x, p, **kw):
         b = self.w.get(p + ".bias")
-        return F.conv1d(x[None], self.w[p + ".weight"], b, **kw)[0]
+        return self._rec(p, "Conv1d", x, F.conv1d(x[None], self.w[p + ".weight"], b, **kw)[0])
 
     def resblk(self, x, s, p, upsample):
         """AdainResBlk1d (StyleTTS2), channel-first [C, L] (reference adain_resblk, model.py:141-157)."""
         r = F.leaky_relu(self.adain(x, s, p + ".norm1"), 0.2)
         if upsample:
-            r = F.conv_transpose1d(r[None], self.w[p + ".pool.weight"], self.w[p + ".pool.bias"], stride=2, padding=1,
-                                   output_padding=1, groups=r.shape[0])[0]
+            r = self._rec(p + ".pool", "ConvTranspose1d", r, F.conv_transpose1d(
+                r[None], self.w[p + ".pool.weight"], self.w[p + ".pool.bias"], stride=2, padding=1, output_padding=1,
+                groups=r.shape[0])[0])
         r = self.conv(r, p + ".conv1", padding=1)
         r = F.leaky_relu(self.adain(r, s, p + ".norm2"), 0.2)
         r = self.conv(r, p + ".conv2", padding=1)
         sc = F.interpolate(x[None], scale_factor=2, mode="nearest")[0] if upsample else x
         if p + ".conv1x1.weight" in self.w:
-            sc = F.conv1d(sc[None], self.w[p + ".conv1x1.weight"])[0]
+            sc = self.conv(sc, p + ".conv1x1")  # no bias
         return (r + sc) * SQRT1_2
 
     def resblock1(self, x, s, p, k):
@@ -110,8 +120,7 @@ class Oracle:
         x = torch.cat([d_en, sp], 1)
         for i in range(3):
             x = self.lstm(x, f"predictor.text_encoder.lstms.{2 * i}")
-            h = F.linear(s_p, self.w[f"predictor.text_encoder.lstms.{2 * i + 1}.fc.weight"],
-                         self.w[f"predictor.text_encoder.lstms.{2 * i + 1}.fc.bias"])
+            h = self.linear(s_p, f"predictor.text_encoder.lstms.{2 * i + 1}.fc")
             c = x.shape[1]
             x = (1 + h[:c]) * F.layer_norm(x, (c,), eps=1e-5) + h[c:]
             x = torch.cat([x, sp], 1)
@@ -151,7 +160,10 @@ class Oracle:
     def harmonic_source(self, f0, noise):
         w = self.sd["decoder.generator.m_source.l_linear.weight"].reshape(9)
         b = self.sd["decoder.generator.m_source.l_linear.bias"]
-        return torch.from_numpy(harmonic_source(f0.detach().numpy().astype(np.float32), noise.numpy(), w, b)).to(self.dt)
+        y = torch.from_numpy(harmonic_source(f0.detach().numpy().astype(np.float32), noise.numpy(), w, b)).to(self.dt)
+        # the 9-harmonic merge inside is the source module's l_linear (9 -> 1), applied per sample
+        self._rec("decoder.generator.m_source.l_linear", "Linear", noise, y[:, None])
+        return y
 
     def stft(self, x):
         """TorchSTFT.transform as the reference computes it in f32 (stft_magphase, below) -> [22, frames]."""
@@ -178,8 +190,9 @@ class Oracle:
             xs = self.resblock1(xs, s_d, f"{G}noise_res.{i}", k_noise)
             if keep is not None:
                 keep[f"xs{i}"] = xs
-            x = F.conv_transpose1d(x[None], self.w[G + f"ups.{i}.weight"], self.w[G + f"ups.{i}.bias"], stride=u,
-                                   padding=(k_up - u) // 2)[0]
+            x = self._rec(G + f"ups.{i}", "ConvTranspose1d", x, F.conv_transpose1d(
+                x[None], self.w[G + f"ups.{i}.weight"], self.w[G + f"ups.{i}.bias"], stride=u,
+                padding=(k_up - u) // 2)[0])
             if i == 1:
                 x = F.pad(x[None], (1, 0), mode="reflect")[0]
             x = x + xs

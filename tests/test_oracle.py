@@ -241,3 +241,128 @@ def test_kokoro_harmonic_source_restatement_matches_torch_sinegen():
     # voiced: the f64 phase is exact; the f32 one drifts by O(ulp(phase)) -> compare at early samples only
     early = (np.arange(300 * n) >= 3000) & (np.arange(300 * n) < 3600)
     np.testing.assert_allclose(got[early], ref[early], atol=2e-3)
+
+
+# ---- Kokoro oracle: whole-model composition ---------------------------------------------------------------------
+# The reference's module-shape logs (bench/research/kokoro/shapes_510.json and shapes_128.json in lariaus/lokinfer,
+# copied to tests/golden/) list every Conv1d / ConvTranspose1d / Linear / LSTM call of the Kokoro package's forward,
+# in call order, with input and output shapes: T = 512 ids (F = 1127 frames) and T = 130 (F = 334). Three calls of
+# that list are not in the forced-duration parity graph and are dropped from it: ALBERT's pooler (its output is
+# unused) and the duration predictor (predictor.lstm + duration_proj), which forced durations replace
+# (models/kokoro/model.py:671-677).
+NOT_IN_FORCED_GRAPH = {"bert.pooler", "predictor.lstm", "predictor.duration_proj.linear_layer"}
+
+
+def _norm_shape(s):
+    s = list(s)
+    while len(s) > 1 and s[0] == 1:  # the logs keep the batch dim; the oracle runs unbatched
+        s = s[1:]
+    return s
+
+
+def _durations(t, frames, seed):
+    r = np.random.default_rng(seed)
+    dur = np.full(t, frames // t, np.int64)
+    dur[r.choice(t, frames - int(dur.sum()), replace=False)] += 1
+    return dur
+
+
+@pytest.mark.parametrize("fixture,tokens,frames", [("kokoro_module_shapes_128.json", 130, 334),
+                                                   ("kokoro_module_shapes_510.json", 512, 1127)])
+def test_kokoro_oracle_module_sequence_matches_reference_log(fixture, tokens, frames):
+    """Order, names, types and shapes of every module call of Oracle.forward equal the reference's log: a wrong
+    kernel size, padding, stride, dilation, channel count, upsampling factor, block order or a skipped / extra
+    block changes an entry."""
+    import json
+    import os
+
+    from lokinfer_amd import kokoro_weights as KW
+    from oracle.kokoro import Oracle
+
+    path = os.path.join(os.path.dirname(__file__), "golden", fixture)
+    want = [(n, k, _norm_shape(i), _norm_shape(o)) for n, k, i, o in json.load(open(path))
+            if n not in NOT_IN_FORCED_GRAPH]
+    ids, ref_s, _, _ = KW.inputs(tokens)
+    dur = _durations(tokens, frames, tokens)
+    noise = np.random.default_rng(1).standard_normal((600 * frames, 9)).astype(np.float32)
+    o = Oracle(KW.random_weights())
+    o.trace = []
+    o.forward(ids, ref_s, dur, noise)
+    got = [(n, k, _norm_shape(i), _norm_shape(x)) for n, k, i, x in o.trace]
+    assert len(got) == len(want)
+    for j, (g, w) in enumerate(zip(got, want)):
+        assert g == w, (j, g, w)
+
+
+def test_kokoro_oracle_albert_equals_transformers_albert():
+    """Oracle.albert in float64 equals transformers' AlbertModel (built locally: hidden 768, 12 heads, FFN 2048,
+    embedding 128, 12 passes of one shared layer, gelu_new) loaded with the same weights."""
+    from transformers import AlbertConfig, AlbertModel
+
+    from lokinfer_amd import kokoro_weights as KW
+    from oracle.kokoro import Oracle
+
+    sd = KW.random_weights()
+    cfg = AlbertConfig(vocab_size=KW.N_TOKENS, embedding_size=128, hidden_size=768, num_hidden_layers=12,
+                       num_attention_heads=12, intermediate_size=2048, hidden_act="gelu_new",
+                       max_position_embeddings=512, layer_norm_eps=1e-12, hidden_dropout_prob=0.0,
+                       attention_probs_dropout_prob=0.0)
+    m = AlbertModel(cfg, add_pooling_layer=False).double().eval()
+    own = {k[len("bert."):]: torch.from_numpy(v).double() for k, v in sd.items() if k.startswith("bert.")}
+    missing, unexpected = m.load_state_dict(own, strict=False)
+    assert not unexpected, unexpected
+    assert all("position_ids" in k or "token_type_ids" in k for k in missing), missing
+    ids = np.random.default_rng(3).integers(0, KW.N_TOKENS, 97)
+    with torch.no_grad():
+        ref = m(torch.from_numpy(ids)[None]).last_hidden_state[0].numpy()
+        got = Oracle(sd, dtype=torch.float64).albert(torch.from_numpy(ids)).numpy()
+    assert np.abs(got - ref).max() <= 1e-10 * np.abs(ref).max()
+
+
+def _fc(sd, p, s):
+    return sd[p + ".fc.weight"].astype(np.float64) @ s + sd[p + ".fc.bias"]
+
+
+def _adain_lc(sd, p, x, s):
+    return K.adain_affine_lc(K.channel_stats_lc(x), _fc(sd, p, s), x.shape[0])
+
+
+def _w_lc(w):  # torch conv weight [Co, Ci, K] -> [Co, K, Ci]
+    return np.transpose(w, (0, 2, 1))
+
+
+def test_kokoro_oracle_blocks_equal_the_channel_last_kernel_composition():
+    """Oracle.resblock1 (AdaINResBlock1 + Snake) and Oracle.resblk (AdainResBlk1d with upsampling) in float64 equal
+    the same blocks assembled from the channel-last kernel oracle (chunked statistics -> AdaIN affine -> fused
+    activation -> conv1d_lc / dwconvt_lc), a second implementation whose parts are pinned above against torch."""
+    from lokinfer_amd import kokoro_weights as KW
+    from oracle.kokoro import SQRT1_2, Oracle
+
+    sd = {k: v.astype(np.float64) for k, v in KW.random_weights().items()}
+    o = Oracle(sd, dtype=torch.float64)
+    s = rng.standard_normal(128)
+    # generator resblock 4 (128 channels, K = 7, dilations 1, 3, 5)
+    p, k = "decoder.generator.resblocks.4", 7
+    x = rng.standard_normal((300, 128))
+    want = o.resblock1(torch.from_numpy(x.T.copy()), torch.from_numpy(s), p, k).numpy().T
+    h = x
+    for j, d in enumerate((1, 3, 5)):
+        a1, a2 = sd[f"{p}.alpha1.{j}"].reshape(-1), sd[f"{p}.alpha2.{j}"].reshape(-1)
+        t = K.affine_act(h, _adain_lc(sd, f"{p}.adain1.{j}", h, s), a1, "snake")
+        t = K.conv1d_lc(t, _w_lc(sd[f"{p}.convs1.{j}.weight"]), sd[f"{p}.convs1.{j}.bias"], padding=d * (k - 1) // 2,
+                        dilation=d)
+        t = K.affine_act(t, _adain_lc(sd, f"{p}.adain2.{j}", t, s), a2, "snake")
+        t = K.conv1d_lc(t, _w_lc(sd[f"{p}.convs2.{j}.weight"]), sd[f"{p}.convs2.{j}.bias"], padding=(k - 1) // 2)
+        h = t + h
+    np.testing.assert_allclose(want, h, rtol=1e-10, atol=1e-10)
+    # predictor F0 block 1 (512 -> 256, depthwise ConvTranspose x2 on the residual path, nearest x2 + 1x1 shortcut)
+    p = "predictor.F0.1"
+    x = rng.standard_normal((40, 512))
+    want = o.resblk(torch.from_numpy(x.T.copy()), torch.from_numpy(s), p, True).numpy().T
+    r = K.affine_act(x, _adain_lc(sd, p + ".norm1", x, s), act="leaky", slope=0.2)
+    r = K.dwconvt_lc(r, sd[p + ".pool.weight"][:, 0, :], sd[p + ".pool.bias"], stride=2, padding=1)
+    r = K.conv1d_lc(r, _w_lc(sd[p + ".conv1.weight"]), sd[p + ".conv1.bias"], padding=1)
+    r = K.affine_act(r, _adain_lc(sd, p + ".norm2", r, s), act="leaky", slope=0.2)
+    r = K.conv1d_lc(r, _w_lc(sd[p + ".conv2.weight"]), sd[p + ".conv2.bias"], padding=1)
+    sc = K.conv1d_lc(np.repeat(x, 2, axis=0), _w_lc(sd[p + ".conv1x1.weight"]))
+    np.testing.assert_allclose(want, (r + sc) * SQRT1_2, rtol=1e-10, atol=1e-10)
