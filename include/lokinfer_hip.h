@@ -81,6 +81,15 @@ int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap);
 int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
                                 float* out, int64_t cap, int heads, int64_t max_keys, int write_kv, void* workspace,
                                 int64_t workspace_bytes, void* stream);
+/* Allocation-free variant of lk_hip_attention_decode_f32 (no counterpart in the reference): for callers that
+ * cannot allocate device memory (HIP graph capture of a serving loop, harnesses that forbid hipMalloc). The chunk
+ * partials go to a fixed 2 MiB device array the library holds on each GPU for the life of the process
+ * (lk_hip_attention_decode_noalloc_max_floats() floats: heads * ceil(max_keys / 64) * 66 must fit), so it calls no
+ * hipMalloc. Returns 4 when the call does not fit. Calls that overlap on one GPU race on that array. */
+int64_t lk_hip_attention_decode_noalloc_max_floats(void);
+int lk_hip_attention_decode_f32_noalloc(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
+                                        float* out, int64_t cap, int heads, int64_t max_keys, int write_kv,
+                                        void* stream);
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
                         void* stream);
 /* chunked prefill / generate (reference kv_write_rows_f32_gpu, attention_cache[_sg]_f32_gpu,

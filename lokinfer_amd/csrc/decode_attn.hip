@@ -12,6 +12,8 @@
 // twice (K rows, V rows) instead of once per key.
 #include "common.h"
 
+#include <mutex>
+
 namespace lkd {
 
 constexpr int kHd = 64;
@@ -190,6 +192,55 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
   hipLaunchKernelGGL(lkd::decodeMergeKernel, dim3(static_cast<unsigned>(heads)), dim3(64), 0, s, p.partial, out, pos,
                      cap, p.chunks);
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"
+
+// ---- allocation-free variant --------------------------------------------------------------------------------
+// The chunk partials live in a fixed device array instead of a caller workspace, for callers that cannot allocate
+// (HIP graph capture of a serving loop, harnesses that forbid hipMalloc). Each GPU holds its own copy of the array
+// for the life of the process; its device address is looked up once per device and kept. The merge reads only
+// partials the chunk launch of the same call wrote, so nothing needs clearing between calls, but two calls that
+// overlap on one GPU (different streams) race on the array.
+namespace {
+
+constexpr int64_t kNoAllocScratchFloats = 512 * 1024;  // 2 MiB: heads x ceil(max_keys / 64) x 66 floats
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex gScratchMu;
+float* gScratchPtr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr on failure).
+float* scratchOnCurrentDevice() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(gScratchMu);
+  if (!gScratchPtr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    gScratchPtr[dev] = static_cast<float*>(ptr);
+  }
+  return gScratchPtr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t lk_hip_attention_decode_noalloc_max_floats(void) { return kNoAllocScratchFloats; }
+
+int lk_hip_attention_decode_f32_noalloc(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
+                                        float* out, int64_t cap, int heads, int64_t maxKeys, int writeKv,
+                                        void* stream) {
+  if (heads <= 0 || cap <= 0) return 1;
+  const int64_t keys = maxKeys <= 0 || maxKeys > cap ? cap : maxKeys;
+  const int64_t need = static_cast<int64_t>(heads) * ((keys + lkd::kChunk - 1) / lkd::kChunk) * (lkd::kHd + 2);
+  if (need > kNoAllocScratchFloats) return 4;  // beyond the fixed scratch array
+  float* ptr = scratchOnCurrentDevice();
+  if (!ptr) return 2;
+  return lk_hip_attention_decode_f32(qkv, kc, vc, pos, bias, out, cap, heads, maxKeys, writeKv, ptr,
+                                     kNoAllocScratchFloats * 4, stream);
 }
 
 }  // extern "C"
