@@ -12,6 +12,7 @@ f32 CPU path timed on this host on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import statistics
@@ -26,6 +27,18 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def mfma_probe():
+    """The bench-only MFMA-ceiling probe library (lokinfer_amd/bench/libmfma_probe.so, built by build())."""
+    from lokinfer_amd.build import PROBE_LIB
+
+    if not PROBE_LIB.exists():
+        raise RuntimeError(f"{PROBE_LIB} is not built: python -m lokinfer_amd.build")
+    lib = C.CDLL(str(PROBE_LIB))
+    lib.lk_hip_mfma_f32_probe.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    lib.lk_hip_mfma_f32_probe.restype = C.c_int
+    return lib
 
 
 def event_times(fn, n: int) -> list[float]:
@@ -227,8 +240,16 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
         torch.cuda.synchronize()
     # the register-only f32 MFMA rate of this GPU under a chip-wide load (what the clock allows)
     pit, pwg = 512, 1024
-    lk.ops.mfma_probe_f32_gpu(pit, pwg)
-    probe_ms = statistics.median(event_times(lambda: lk.ops.mfma_probe_f32_gpu(pit, pwg), 5))
+    probe = mfma_probe()
+    probe_out = torch.empty(pwg * 256, device="cuda")
+
+    def run_probe():
+        rc = probe.lk_hip_mfma_f32_probe(C.c_void_p(probe_out.data_ptr()), pit, pwg,
+                                         C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+
+    run_probe()
+    probe_ms = statistics.median(event_times(run_probe, 5))
     ceiling = pwg * 4 * pit * 8 * 4096 / (probe_ms * 1e-3) / 1e12
     a = W.alpha_of(k)
     flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c

@@ -41,6 +41,21 @@ int lk_run_kernel(const lk_kernel* k, void* const* ptrs, uint32_t num_ptrs, cons
                   void* stream);
 const char* lk_last_error(void);
 
+/* ---- device error record (reference: GpuContext::takeGpuError at sync, src/runtime/executable.cpp:850-852) ----
+ * Kernels that find invalid data mid-graph (a position outside the cache, an id out of range, a persistent kernel
+ * whose exchange timed out) write a neutral value and record the first error per GPU. lk_take_device_error waits
+ * for the current device (hipDeviceSynchronize), returns the recorded code (0: none, -1: the read failed) with its
+ * detail (the offending position / id / step), and clears the record. */
+enum {
+  LK_DEVERR_EXCHANGE_TIMEOUT = 1,
+  LK_DEVERR_POSITION = 2,
+  LK_DEVERR_INDEX = 3,
+  LK_DEVERR_DURATIONS = 4,
+  LK_DEVERR_AUDIO_ROWS = 5
+};
+int lk_take_device_error(int64_t* detail);
+const char* lk_device_error_message(int code);
+
 /* ---- GEMM / conv (reference: gemm_f32_gpu_mps mps.mm:41-84; gemm_bias[_relu]_f32_gpu kokoro_lc.cpp:460-581;
  *      gemm_steel* kokoro_lc.cpp:391-409; conv1d_lc[_res]_f32_gpu kokoro_lc.cpp:81-109) ---- */
 /* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu.
@@ -91,7 +106,7 @@ int lk_hip_attention_decode_f32_noalloc(const float* qkv, float* kc, float* vc, 
                                         float* out, int64_t cap, int heads, int64_t max_keys, int write_kv,
                                         void* stream);
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
-                        void* stream);
+                        int64_t cap, void* stream);
 /* chunked prefill / generate (reference kv_write_rows_f32_gpu, attention_cache[_sg]_f32_gpu,
  * python/lokinfer/ops/transformer.py:239-268, 348-351; kernels/gpu/kokoro_lc.cpp:887-965): the T rows of qkv sit at
  * positions pos..pos+T-1 (pos a device i64[1]). kv_write_rows writes k, v (+ bias) there (rows >= cap dropped);
@@ -255,10 +270,6 @@ int lk_hip_f16_scatter_audio(const void* x, const int64_t* ids, const void* audi
 int lk_hip_f16_elementwise(const void* a, const void* b, void* out, int64_t n, int op, void* stream);
 /* weight packing: W f16[K, N] -> W^T f16[N, K] */
 int lk_hip_f16_transpose(const void* w, void* wt, int64_t k, int64_t n, void* stream);
-
-/* ---- measurement (no counterpart in the reference): register-only f32 MFMA loop, out f32[workgroups * 256];
- *      FLOPs = workgroups * 4 * iters * 8 * 4096 */
-int lk_hip_mfma_f32_probe(float* out, int iters, int workgroups, void* stream);
 
 #ifdef __cplusplus
 }

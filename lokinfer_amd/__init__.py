@@ -8,7 +8,8 @@ from .tensor import DType, Tensor, empty, f16, f32, from_numpy, from_torch, i32,
 from . import ops  # noqa: F401
 from . import f16_gpu as _f16_gpu
 from ._lib import LokinferError, registered_kernels  # noqa: F401
-from .compiler import CompiledModel, compile  # noqa: F401
+from .compiler import CapturedModel, CompiledModel, capture, compile, compile_ir, load  # noqa: F401
+from .graph import BufferType, Dim, ScalarType, Sym, TensorType  # noqa: F401
 
 ops.f16_gpu = _f16_gpu  # lk.ops.f16_gpu.<name>_f16_gpu, as in the reference
 

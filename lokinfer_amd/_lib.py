@@ -40,9 +40,27 @@ def lib():
                                 C.c_uint64, vp]
     L.lk_run_kernel.restype = i32
     L.lk_last_error.restype = C.c_char_p
+    L.lk_take_device_error.argtypes = [C.POINTER(i64)]
+    L.lk_take_device_error.restype = i32
+    L.lk_device_error_message.argtypes = [i32]
+    L.lk_device_error_message.restype = C.c_char_p
     L.lk_init()
     _lib = L
     return L
+
+
+def check_device_errors() -> None:
+    """Waits for the current GPU and raises LokinferError if a kernel recorded a data error since the last check
+    (a position outside a KV cache, an id out of range, a persistent kernel whose exchange timed out); clears it.
+    The reference reports GPU failures the same way, at its next synchronisation (takeGpuError,
+    src/runtime/executable.cpp:850-852 in lariaus/lokinfer)."""
+    L = lib()
+    detail = C.c_int64(0)
+    code = L.lk_take_device_error(C.byref(detail))
+    if code < 0:
+        raise LokinferError("could not read the device error record")
+    if code:
+        raise LokinferError(f"device error {code}: {L.lk_device_error_message(code).decode()} (detail {detail.value})")
 
 
 def registered_kernels() -> list[str]:

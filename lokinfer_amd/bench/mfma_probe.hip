@@ -1,10 +1,11 @@
-// Measurement kernels (no counterpart in the reference): the register-only f32 MFMA rate of this GPU under load, the
+// Bench-only measurement kernel, built into its own library (lokinfer_amd/bench/libmfma_probe.so), not into the
+// product library or its registry. No counterpart in the reference: the register-only f32 MFMA rate of this GPU under load, the
 // ceiling the roofline fraction of an MFMA-bound kernel is read against (the published peak assumes the full
 // 2.4 GHz clock, which a chip-wide MFMA load does not hold).
 //
 //   lk_hip_mfma_f32_probe   each wave runs `iters` rounds of 8 independent 32x32x2 f32 MFMA chains on register data
 //                           (8 x 4096 FLOP per round), then writes one sum per lane so nothing is eliminated
-#include "common.h"
+#include <hip/hip_runtime.h>
 
 namespace lkd {
 
@@ -43,21 +44,3 @@ int lk_hip_mfma_f32_probe(float* out, int iters, int workgroups, void* stream) {
 }
 
 }  // extern "C"
-
-namespace lkh {
-
-namespace {
-
-// mfma_probe_f32_gpu (MI355X backend, measurement): -> f32[workgroups * 256]; attrs iters, workgroups
-void runMfmaProbe(ExecCtx& ctx, const KernelArgs& a) {
-  Ints it(a);
-  it.skip(1);
-  const int iters = static_cast<int>(it.next()), wgs = static_cast<int>(it.next());
-  status(ctx, lk_hip_mfma_f32_probe(P<float>(a, 0), iters, wgs, ctx.stream), "mfma_probe: launch failed");
-}
-
-}  // namespace
-
-void registerProbeKernels() { registerKernel({"mfma_probe_f32_gpu", Device::Gpu, runMfmaProbe, 0, 1}); }
-
-}  // namespace lkh

@@ -18,6 +18,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "liblokinfer_hip.so"
+PROBE_SRC = PKG / "bench" / "mfma_probe.hip"
+PROBE_LIB = PKG / "bench" / "libmfma_probe.so"  # bench-only measurement kernel, not part of the product library
 ARCH = "gfx950"
 
 
@@ -39,7 +41,7 @@ def common_flags() -> list[str]:
 
 
 def _compile(src: Path) -> Path:
-    obj = BUILD / (src.name + ".o")
+    obj = BUILD / (src.parent.name + "_" + src.name + ".o")
     cmd = [hipcc(), *common_flags(), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd = [hipcc(), *common_flags(), "-x", "hip", "-c", str(src), "-o", str(obj)]
@@ -51,7 +53,7 @@ def _compile(src: Path) -> Path:
 
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
-    srcs = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+    srcs = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list((CSRC / "rt").glob("*.cpp")))
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, srcs))
@@ -61,6 +63,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the bench's MFMA-ceiling probe: its own library
+    pobj = _compile(PROBE_SRC)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    r = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(pobj)],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed (probe)\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
     return LIB

@@ -1,14 +1,13 @@
-"""`lk.compile`: turns a function of tensors into a replayable HIP graph per input-shape signature.
+"""Compiling a function (the reference's lk.compile / lk.load / compile_ir, python/lokinfer/compiler.py:94-231 in
+lariaus/lokinfer), two ways:
 
-The reference traces the function into text IR and runs a 4-pass compiler plus an instruction interpreter
-(python/lokinfer/compiler.py:94-231, src/runtime/executable.cpp:567-1144 in lariaus/lokinfer). On MI355X the
-equivalent of "compile once, run many" is stream capture: the first call with a new shape signature runs the
-function eagerly (binding the symbolic sizes, uploading captured constants, warming the kernels), then runs it
-again under hipStreamBeginCapture; later calls copy the inputs into the captured input buffers and replay the
-hipGraph (one launch for the whole forward, no per-kernel host work). All intermediates live in the graph's
-private memory pool, which plays the role of the reference's planned arena (plan-memory pass).
-
-Functions must be capturable: GPU work only between inputs and outputs (no host reads of device data).
+- `compile(fn, inputs=... | input_types=...)`: traces `fn` on symbolic values into the reference's text IR
+  (lokinfer_amd.graph), runs the compiler passes in the C++ runtime and builds an executable: constants in one
+  device arena, init run once, statically shaped calls captured into hipGraphs. The result saves to / loads from
+  .lkm v2 files (`CompiledModel.save`, `load`).
+- `capture(fn)`: runs `fn` eagerly once per input-shape signature, then captures it with torch's stream capture
+  and replays that hipGraph. It keeps the concurrent branches a function opens on side streams (the Kokoro
+  forward's), which the single-stream executable runs one after the other.
 """
 from __future__ import annotations
 
@@ -16,8 +15,9 @@ import gc
 
 import torch
 
+from .graph import BufferType, ScalarType, TensorType, Value, Dim, Sym, tracing, Graph
 from .runtime import GpuContext
-from .tensor import Tensor
+from .tensor import Tensor, f32, from_numpy, i64
 
 
 def _sig(args) -> tuple:
@@ -73,8 +73,8 @@ class _Entry:
         return outs
 
 
-class CompiledModel:
-    """Callable compiled function (reference CompiledModel, python/lokinfer/compiler.py:94-184)."""
+class CapturedModel:
+    """A function replayed from torch stream capture, one graph per input-shape signature (see `capture`)."""
 
     def __init__(self, fn, use_graph: bool = True, mutable: tuple = ()):
         self.fn = fn
@@ -103,11 +103,178 @@ class CompiledModel:
         return res[0] if len(res) == 1 else tuple(res)
 
 
-def compile(fn, inputs=None, input_types=None, graph: bool = True, mutable: tuple = ()) -> CompiledModel:
-    """Compiles `fn` (reference lk.compile, python/lokinfer/compiler.py:187-212). `inputs` / `input_types` are
-    accepted for API compatibility; shapes are bound per call signature. `mutable`: indices of the inputs that the
-    function writes in place (the reference's lk.MutableType inputs): bound by reference, one entry per buffer."""
-    m = CompiledModel(fn, use_graph=graph, mutable=mutable)
+def capture(fn, inputs=None, graph: bool = True, mutable: tuple = ()) -> CapturedModel:
+    """Stream-captured `fn`: shapes are bound per call signature. `mutable`: indices of the inputs that the function
+    writes in place (the reference's lk.MutableType inputs): bound by reference, one entry per buffer."""
+    m = CapturedModel(fn, use_graph=graph, mutable=mutable)
     if inputs is not None:
         m._entry(list(inputs))
     return m
+
+
+# ---- traced compilation through the C++ runtime -----------------------------------------------------------------
+
+class Pending:
+    """Handle of an asynchronous call (`CompiledModel.submit`); `wait()` returns what the call returns."""
+
+    __slots__ = ("_future",)
+
+    def __init__(self, future):
+        self._future = future
+
+    def done(self) -> bool:
+        return self._future.done()
+
+    def wait(self, timeout: float | None = None):
+        return self._future.result(timeout)
+
+
+class CompiledModel:
+    """A compiled model on the GPU (reference CompiledModel, python/lokinfer/compiler.py:94-184): `model(*inputs)`
+    returns fresh output tensors, `run_inplace` the executable's own output buffers (overwritten by its next
+    call); `save` writes a self-contained .lkm."""
+
+    def __init__(self, exe, model, text: str, input_types: list, single: bool, externals: dict | None = None):
+        self._exe = exe
+        self._model = model
+        self._externals = dict(externals or {})
+        self.source_ir = text
+        self.input_types = input_types
+        self._single = single
+        self._worker = None
+
+    @property
+    def uses_gpu(self) -> bool:
+        return True
+
+    def ir_text(self) -> str:
+        """The IR after the compiler pipeline."""
+        return self._model.text()
+
+    @property
+    def num_external_constants(self) -> int:
+        return len(self._externals)
+
+    def stats(self) -> dict:
+        return self._exe.stats()
+
+    def internalize(self) -> "CompiledModel":
+        """Copies the captured tensors (external constants) into the model, so later writes to them no longer
+        reach it (reference CompiledModel.internalize). The executable is re-created."""
+        self._drain()
+        if self._externals:
+            from .rt import Executable
+
+            self._model.internalize(self._externals)
+            self._externals = {}
+            self._exe = Executable(self._model, {})
+        return self
+
+    def save(self, path: str) -> None:
+        """Writes a self-contained .lkm v2 (captured weights internalized)."""
+        self._drain()
+        if self._externals:
+            self._model.internalize(self._externals)  # the executable keeps its bound device copies
+            self._externals = {}
+        self._model.save(path)
+
+    def _call(self, args, copy: bool):
+        outs = self._exe.run(list(args))
+        if copy:
+            outs = [Tensor(o.t.clone()) for o in outs]
+        return outs[0] if self._single else tuple(outs)
+
+    def __call__(self, *args):
+        if self._worker is not None:
+            return self.submit(*args).wait()
+        return self._call(args, True)
+
+    def run_inplace(self, *args):
+        """Outputs over the executable's own memory, no copy (valid until the next call)."""
+        return self._call(args, False)
+
+    def submit(self, *args) -> Pending:
+        """Runs the call on the model's worker thread (calls of one model run in submit order)."""
+        if self._worker is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            self._worker = ThreadPoolExecutor(max_workers=1, thread_name_prefix="lokinfer-model")
+        return Pending(self._worker.submit(self._call, args, True))
+
+    def _drain(self):
+        if self._worker is not None:
+            self._worker.submit(lambda: None).result()
+
+
+def _input_type(x, i: int, dynamic: bool):
+    if isinstance(x, (TensorType, ScalarType)):
+        return x
+    if hasattr(x, "shape") and hasattr(x, "dtype") and not isinstance(x, Tensor):
+        import numpy as np
+
+        x = from_numpy(np.ascontiguousarray(x))
+    if isinstance(x, Tensor):
+        shape = [Sym(f"D{i}_{j}") for j in range(x.ndim)] if dynamic else list(x.shape)
+        return TensorType(x.dtype, shape)
+    if isinstance(x, float):
+        return ScalarType(f32)
+    if isinstance(x, int):
+        return ScalarType(i64)
+    raise TypeError(f"unsupported input {type(x).__name__}")
+
+
+def compile(fn, inputs=None, *, dynamic: bool = False, input_types=None, pipeline=None,
+            graphs: bool = True) -> CompiledModel:
+    """Traces `fn` on symbolic values and compiles it (reference lk.compile).
+
+    inputs       example tensors / arrays / scalars (static shapes unless dynamic=True)
+    dynamic      every input dim becomes its own symbol
+    input_types  explicit TensorType / BufferType (mutable) / ScalarType list, e.g. [TensorType(f32, [Sym("N"), 4])]
+    pipeline     the compiler passes (default: dce, bufferize, plan-memory, hoist-init)
+    graphs       capture statically shaped calls into hipGraphs
+    """
+    from .rt import Executable, Model
+
+    if input_types is None:
+        if inputs is None:
+            raise ValueError("give inputs or input_types")
+        input_types = [_input_type(x, i, dynamic) for i, x in enumerate(inputs)]
+    g = Graph()
+    args = [g.arg(t, f"in{i}_") for i, t in enumerate(input_types)]
+    with tracing(g):
+        out = fn(*args)
+    single = isinstance(out, Value)
+    outs = [out] if single else list(out)
+    if not all(isinstance(o, Value) for o in outs):
+        raise TypeError("the traced function must return traced values")
+    text = g.to_text(outs)
+    model = Model.parse(text).run_passes(pipeline if pipeline is not None else "pipeline")
+    exe = Executable(model, g.externals, graphs=graphs)
+    return CompiledModel(exe, model, text, input_types, single, g.externals)
+
+
+def load(path: str, graphs: bool = True) -> CompiledModel:
+    """Loads a .lkm written by CompiledModel.save (or by the reference's writeModelFile): mmapped, constants
+    uploaded once."""
+    from .rt import Executable, Model
+
+    model = Model.load(path)
+    exe = Executable(model, {}, graphs=graphs)
+    return CompiledModel(exe, model, model.text(), [], model.num_outputs == 1)
+
+
+def compile_ir(text: str, *, externals: dict | None = None, internals: dict | None = None, pipeline=None,
+               single: bool = True, graphs: bool = True) -> CompiledModel:
+    """Compiles text IR directly: const.external data by name (lk.Tensors, bound by reference) and const.internal
+    data by name (arrays, copied) (reference compile_ir)."""
+    import numpy as np
+
+    from .rt import Executable, Model
+
+    model = Model.parse(text)
+    for name, arr in (internals or {}).items():
+        model.set_constant(name, np.ascontiguousarray(arr))
+    model.run_passes(pipeline if pipeline is not None else "pipeline")
+    ext = {k: (v if isinstance(v, Tensor) else from_numpy(np.ascontiguousarray(v))) for k, v in (externals or {}).items()}
+    exe = Executable(model, ext, graphs=graphs)
+    return CompiledModel(exe, model, text, [], single, ext)

@@ -10,8 +10,9 @@
 
 #include <hip/hip_runtime.h>
 
-#include <cstdint>
 #include <cstddef>
+#include <cstdint>
+#include <string>
 
 namespace lkh {
 
@@ -57,6 +58,12 @@ struct KernelEntry {
 };
 
 void registerKernel(const KernelEntry& e);
+// nullptr when no kernel has this name
+const KernelEntry* findKernel(const std::string& name);
+// sets the message lk_last_error() returns on this thread
+void setLastError(std::string msg);
+// device address of the current GPU's error record {code, detail} (nullptr if it cannot be resolved)
+unsigned long long* deviceErrorRecord();
 
 // Each kernel family registers its entries from one of these (explicit, no
 // static constructors).
@@ -69,7 +76,6 @@ void registerSignalKernels();
 void registerDecodeFusedKernels();
 void registerWinogradKernels();
 void registerF16Kernels();
-void registerProbeKernels();
 
 inline unsigned ceilDiv(int64_t a, int64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
@@ -115,6 +121,12 @@ inline void status(ExecCtx& ctx, int rc, const char* what) {
 
 // ---- device helpers ---------------------------------------------------------------------------------------
 namespace lkd {
+
+// Records a data error in the GPU's error record (lkh::deviceErrorRecord); the first error of a run is kept.
+__device__ __forceinline__ void raiseDeviceError(unsigned long long* rec, unsigned code, long long detail) {
+  if (rec && atomicCAS(rec, 0ull, static_cast<unsigned long long>(code)) == 0ull)
+    rec[1] = static_cast<unsigned long long>(detail);
+}
 
 __device__ __forceinline__ float waveSum(float v) {
 #pragma unroll

@@ -11,6 +11,7 @@
 // chunk order (flash-decoding). Every load of a chunk is issued before its first use, so a wave waits on HBM
 // twice (K rows, V rows) instead of once per key.
 #include "common.h"
+#include "lokinfer_hip.h"
 
 #include <mutex>
 
@@ -31,13 +32,15 @@ struct DecodeParams {
   int heads;
   int chunks;
   int writeKv;
+  unsigned long long* err;  // the GPU's error record
 };
 
 __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   const int h = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
   const int64_t D = static_cast<int64_t>(p.heads) * kHd;
   const int64_t pos = *p.pos;
-  if (pos < 0 || pos >= p.cap) {  // out-of-range position: no cache write; the merge writes NaN
+  if (pos < 0 || pos >= p.cap) {  // out-of-range position: no cache write, recorded; the merge writes NaN
+    if (h == 0 && s == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, pos);
     return;
   }
   const int64_t kb = static_cast<int64_t>(s) * kChunk;
@@ -167,7 +170,7 @@ int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap) {
 
 // qkv [1, 3D] (before bias), kc / vc [cap, D] (rows 0..pos-1 valid; row pos written when writeKv), pos device
 // i64[1], bias [3D] -> out [1, D], D = 64 heads. The grid covers max_keys (<= cap) keys; chunks past pos exit
-// early. pos outside [0, cap) writes nothing and yields NaN.
+// early. pos outside [0, cap) writes nothing, yields NaN and is recorded as LK_DEVERR_POSITION.
 int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
                                 float* out, int64_t cap, int heads, int64_t maxKeys, int writeKv, void* workspace,
                                 int64_t workspaceBytes, void* stream) {
@@ -183,6 +186,7 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
   p.cap = cap;
   p.heads = heads;
   p.writeKv = writeKv;
+  p.err = lkh::deviceErrorRecord();
   p.chunks = static_cast<int>((maxKeys + lkd::kChunk - 1) / lkd::kChunk);
   if (!workspace || workspaceBytes < static_cast<int64_t>(heads) * p.chunks * (lkd::kHd + 2) * 4) return 3;
   p.partial = static_cast<float*>(workspace);
@@ -218,7 +222,10 @@ float* scratchOnCurrentDevice() {
   std::lock_guard<std::mutex> lock(gScratchMu);
   if (!gScratchPtr[dev]) {
     void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
+      (void)hipGetLastError();  // do not leave the failure for a later launch check
+      return nullptr;
+    }
     gScratchPtr[dev] = static_cast<float*>(ptr);
   }
   return gScratchPtr[dev];

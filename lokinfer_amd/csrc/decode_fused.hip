@@ -209,17 +209,20 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
 }
 
 // One wave per (head, 64-key chunk), as the split decode kernel, but q / k / v of this step are the fixed-order
-// sums of `slices` GEMV partial rows (+ bias). An invalid position writes NaN partials (no cache write).
+// sums of `slices` GEMV partial rows (+ bias). An invalid position writes NaN partials (no cache write) and is
+// recorded in the GPU's error record.
 __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restrict__ qpart, int64_t slices,
                                                            float* kc, float* vc, const int64_t* pos,
                                                            const float* __restrict__ bias, float* __restrict__ cpart,
-                                                           int64_t cap, int heads, int chunks) {
+                                                           int64_t cap, int heads, int chunks,
+                                                           unsigned long long* err) {
   __shared__ float qs[kDecHd], vs[kDecHd];
   const int h = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
   const int64_t D = static_cast<int64_t>(heads) * kDecHd, ld = 3 * D;
   float* part = cpart + (static_cast<int64_t>(h) * chunks + s) * kPartStride;
   const int64_t ps = *pos;
   if (ps < 0 || ps >= cap) {
+    if (h == 0 && s == 0 && lane == 0) raiseDeviceError(err, LK_DEVERR_POSITION, ps);
     if (lane == 0) {
       part[0] = __builtin_nanf("");
       part[1] = 1.0f;
@@ -437,7 +440,7 @@ int lk_hip_attention_decode_part_f32(const float* qkv_part, int64_t slices, floa
   const int chunks = static_cast<int>((cap + lkd::kDecChunk - 1) / lkd::kDecChunk);
   hipLaunchKernelGGL(lkd::decodeChunkPartKernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(chunks)),
                      dim3(64), 0, static_cast<hipStream_t>(stream), qkv_part, slices, kc, vc, pos, bias, chunk_part,
-                     cap, heads, chunks);
+                     cap, heads, chunks, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -27,6 +27,7 @@
 #include <cmath>
 
 #include "common.h"
+#include "lokinfer_hip.h"
 
 // No fp contraction in this file (every intended fma below is an explicit fmaf).
 #pragma clang fp contract(off)
@@ -502,6 +503,7 @@ struct GqaParams {
   int64_t t, cap;
   int qh, kvh, chunks;
   float scale;  // 1 / sqrt(128)
+  unsigned long long* err;  // the GPU's error record: positions outside the cache
 };
 
 __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
@@ -622,6 +624,9 @@ __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
   const float inv = 1.0f / wsum;
   const int64_t qrow = q0 + q;
   const bool noRow = p0 + qrow >= p.cap || p0 < 0;
+  // recorded once, by the thread of head 0 that owns the first query without a cache row
+  if (noRow && qrow < p.t && d0 == 0 && blockIdx.y == 0 && qrow == (p0 < 0 ? 0 : p.cap - p0))
+    raiseDeviceError(p.err, LK_DEVERR_POSITION, p0 + qrow);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
 #pragma unroll
@@ -693,6 +698,7 @@ __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
   const int64_t p0 = *p.pos;
   float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
+  if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int64_t kb = static_cast<int64_t>(ch) * DCH;
   if (kb >= nk) {
     if (lane == 0) {
@@ -758,6 +764,7 @@ __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
   h16* o = p.out + static_cast<int64_t>(h) * QHD + d;
   if (p0 < 0 || p0 >= p.cap) {
     *o = static_cast<h16>(__builtin_nanf(""));
+    if (h == 0 && d == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
     return;
   }
   *o = mergeDim(part, static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH)), d);
@@ -784,6 +791,7 @@ struct GqaDecParams {
   int qh, kvh, chunks;
   float scale, eps;
   RopeTable tab;
+  unsigned long long* err;  // the GPU's error record: positions outside the cache
 };
 
 __device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, int lane) {
@@ -816,6 +824,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   const int64_t p0 = *p.pos;
   float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
+  if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int64_t kb = static_cast<int64_t>(ch) * DCH;
   if (kb >= nk) {
     if (lane == 0) {
@@ -951,7 +960,8 @@ __global__ void kvWriteF16Kernel(h16* __restrict__ kc, h16* __restrict__ vc, con
 __global__ __launch_bounds__(256) void embedScatterF16Kernel(const h16* __restrict__ table, const int64_t* __restrict__ ids,
                                                              const h16* __restrict__ x, const h16* __restrict__ audio,
                                                              h16* __restrict__ out, int64_t vocab, int64_t d,
-                                                             int64_t na, int64_t padId, int mode) {
+                                                             int64_t na, int64_t padId, int mode,
+                                                             unsigned long long* err) {
   __shared__ int cnt[4];
   const int64_t i = blockIdx.x;
   const int64_t id = ids[i];
@@ -972,6 +982,8 @@ __global__ __launch_bounds__(256) void embedScatterF16Kernel(const h16* __restri
     }
   }
   h16* o = out + i * d;
+  if (!src && threadIdx.x == 0)
+    raiseDeviceError(err, mode == 0 ? LK_DEVERR_INDEX : LK_DEVERR_AUDIO_ROWS, mode == 0 ? id : i);
   for (int64_t c = threadIdx.x; c < d; c += 256) o[c] = src ? src[c] : static_cast<h16>(__builtin_nanf(""));
 }
 
@@ -1174,7 +1186,7 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
   const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
   GqaParams p{static_cast<const h16*>(q), static_cast<const h16*>(kc), static_cast<const h16*>(vc), pos,
               static_cast<h16*>(out), static_cast<float*>(workspace), t, cap, qh, kvh, chunks,
-              1.0f / std::sqrt(static_cast<float>(QHD))};
+              1.0f / std::sqrt(static_cast<float>(QHD)), lkh::deviceErrorRecord()};
   if (t == 1) {
     if (!workspace || workspace_bytes < lk_hip_f16_attention_workspace_bytes(qh, cap)) return 3;
     hipLaunchKernelGGL(gqaDecodeChunkKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64),
@@ -1202,7 +1214,8 @@ int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void*
   const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
   GqaDecParams p{static_cast<const h16*>(qkv), static_cast<const h16*>(qg), static_cast<const h16*>(kg), pos,
                  static_cast<h16*>(kc), static_cast<h16*>(vc), static_cast<float*>(workspace), static_cast<h16*>(out),
-                 counters, cap, qh, kvh, chunks, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta)};
+                 counters, cap, qh, kvh, chunks, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta),
+                 lkh::deviceErrorRecord()};
   hipLaunchKernelGGL(gqaDecodeQkrKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), p);
   return launched();
@@ -1228,7 +1241,7 @@ int lk_hip_f16_embedding(const int64_t* ids, const void* table, void* out, int64
   if (t == 0) return 0;
   hipLaunchKernelGGL(embedScatterF16Kernel, dim3(static_cast<unsigned>(t)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const h16*>(table), ids, nullptr, nullptr,
-                     static_cast<h16*>(out), vocab, d, int64_t{0}, int64_t{0}, 0);
+                     static_cast<h16*>(out), vocab, d, int64_t{0}, int64_t{0}, 0, lkh::deviceErrorRecord());
   return launched();
 }
 
@@ -1239,7 +1252,8 @@ int lk_hip_f16_scatter_audio(const void* x, const int64_t* ids, const void* audi
   if (t == 0) return 0;
   hipLaunchKernelGGL(embedScatterF16Kernel, dim3(static_cast<unsigned>(t)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), nullptr, ids, static_cast<const h16*>(x),
-                     static_cast<const h16*>(audio), static_cast<h16*>(out), int64_t{0}, d, na, pad_id, 1);
+                     static_cast<const h16*>(audio), static_cast<h16*>(out), int64_t{0}, d, na, pad_id, 1,
+                     lkh::deviceErrorRecord());
   return launched();
 }
 

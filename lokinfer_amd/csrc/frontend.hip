@@ -2,26 +2,33 @@
 // (embedding_f32_cpu, kernels/cpu/kokoro_norm.cpp; argmax in Python, models/gpt2.py:348-359); here they stay
 // on the device so that a decode step or a forward is one captured graph with no host round trips.
 //
-//   lk_hip_embedding_f32   out[i] = table[ids[i]] (+ table2[ids2[i]])   ids out of range -> row of NaN
+//   lk_hip_embedding_f32   out[i] = table[ids[i]] (+ table2[ids2[i]])   ids out of range -> row of NaN, and the
+//                          GPU's error record gets LK_DEVERR_INDEX with the id
 //   lk_hip_argmax_f32      per row: index of the first maximum (int64)
 //   lk_hip_arange_offset_i64  out[i] = pos[0] + i (position ids of a chunk of new tokens; reference host kernel
 //                          arange_offset_i64_cpu, kernels/cpu/decode.cpp:221, python/lokinfer/ops/transformer.py:272-282)
 #include "common.h"
+#include "lokinfer_hip.h"
 
 namespace lkd {
 
 __global__ void embeddingKernel(const float* __restrict__ table, const int64_t* __restrict__ ids,
                                 const float* __restrict__ table2, const int64_t* __restrict__ ids2,
-                                float* __restrict__ out, int64_t n, int64_t d, int64_t rows, int64_t rows2) {
+                                float* __restrict__ out, int64_t n, int64_t d, int64_t rows, int64_t rows2,
+                                unsigned long long* err) {
   const int64_t total = n * d;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t r = i / d, c = i - r * d;
     const int64_t id = ids[r];
-    float v = (id >= 0 && id < rows) ? table[id * d + c] : __builtin_nanf("");
+    const bool ok = id >= 0 && id < rows;
+    float v = ok ? table[id * d + c] : __builtin_nanf("");
+    if (!ok && c == 0) raiseDeviceError(err, LK_DEVERR_INDEX, id);
     if (table2) {
       const int64_t id2 = ids2[r];
-      v += (id2 >= 0 && id2 < rows2) ? table2[id2 * d + c] : __builtin_nanf("");
+      const bool ok2 = id2 >= 0 && id2 < rows2;
+      v += ok2 ? table2[id2 * d + c] : __builtin_nanf("");
+      if (!ok2 && c == 0) raiseDeviceError(err, LK_DEVERR_INDEX, id2);
     }
     out[i] = v;
   }
@@ -102,7 +109,8 @@ int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* ta
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(lkd::embeddingKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), table, ids, table2, ids2, out, n, d, rows, rows2);
+                     static_cast<hipStream_t>(stream), table, ids, table2, ids2, out, n, d, rows, rows2,
+                     lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

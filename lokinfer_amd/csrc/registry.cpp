@@ -37,6 +37,8 @@ thread_local std::string tlsError;
 
 }  // namespace
 
+void setLastError(std::string msg) { tlsError = std::move(msg); }
+
 void registerKernel(const KernelEntry& e) {
   auto& t = table();
   if (t.find(e.name) == t.end()) names().push_back(e.name);
@@ -271,10 +273,9 @@ void runAttnDecode(ExecCtx& ctx, const KernelArgs& a) {
 // kv_write_f32_gpu (inout kc, vc): kc[cap, D], vc[cap, D], qkv[1, 3D], pos[1], bias[3D]; no outs
 void runKvWrite(ExecCtx& ctx, const KernelArgs& a) {
   Ints it(a);
-  it.skip(1);
-  const int64_t d = it.next();
+  const int64_t cap = it.next(), d = it.next();
   status(ctx, lk_hip_kv_write_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3), P<float>(a, 4),
-                                  d, ctx.stream),
+                                  d, cap, ctx.stream),
          "kv_write: launch failed");
 }
 
@@ -593,11 +594,18 @@ static void registerAll() {
     registerDecodeFusedKernels();
     registerWinogradKernels();
     registerF16Kernels();
-    registerProbeKernels();
     std::sort(names().begin(), names().end());
   });
 }
 
+}  // namespace lkh
+
+namespace lkh {
+const KernelEntry* findKernel(const std::string& name) {
+  registerAll();
+  auto it = table().find(name);
+  return it == table().end() ? nullptr : &it->second;
+}
 }  // namespace lkh
 
 // ---- C-ABI --------------------------------------------------------------------------------------------------
@@ -644,15 +652,26 @@ int lk_run_kernel(const lk_kernel* k, void* const* ptrs, uint32_t numPtrs, const
     return 1;
   }
   const auto* e = reinterpret_cast<const lkh::KernelEntry*>(k);
-  lkh::KernelArgs args{ptrs, nullptr, ints, floats, nullptr, numPtrs, numInts, numFloats};
-  lkh::ExecCtx ctx;
-  ctx.stream = static_cast<hipStream_t>(stream);
-  ctx.workspace = workspace;
-  ctx.workspaceBytes = workspaceBytes;
   if (e->numOperands >= 0 && numPtrs != static_cast<uint32_t>(e->numOperands + e->numOuts)) {
     lkh::tlsError = std::string(e->name) + ": wrong number of operands";
     return 1;
   }
+  // Runners index ints / floats by position. A caller's short arrays are copied into zero-padded ones, so a
+  // missing dim or attribute reads as 0 (which every runner's shape checks reject) instead of past the array.
+  constexpr uint32_t kMaxInts = 256, kMaxFloats = 32;
+  if (numInts > kMaxInts || numFloats > kMaxFloats || (numInts && !ints) || (numFloats && !floats)) {
+    lkh::tlsError = std::string(e->name) + ": too many (or missing) int / float arguments";
+    return 1;
+  }
+  int64_t iv[kMaxInts] = {};
+  double fv[kMaxFloats] = {};
+  if (numInts) std::memcpy(iv, ints, numInts * sizeof(int64_t));
+  if (numFloats) std::memcpy(fv, floats, numFloats * sizeof(double));
+  lkh::KernelArgs args{ptrs, nullptr, iv, fv, nullptr, numPtrs, numInts, numFloats};
+  lkh::ExecCtx ctx;
+  ctx.stream = static_cast<hipStream_t>(stream);
+  ctx.workspace = workspace;
+  ctx.workspaceBytes = workspaceBytes;
   e->run(ctx, args);
   if (ctx.error) {
     lkh::tlsError = std::string(e->name) + ": " + ctx.error;

@@ -1,0 +1,659 @@
+// The MI355X executable (see executable.h). Instruction lowering follows the reference's argument convention
+// (include/lokinfer/runtime/kernel.h:3-11, src/runtime/executable.cpp:406-447): a kernel gets its operands then
+// its outs as pointers; ints = every operand's dims, every out's dims, then the non-structural int / bool /
+// int-list / dim attrs in name order; floats = the float attrs in name order.
+#include "executable.h"
+
+#include <algorithm>
+#include <climits>
+#include <cstring>
+
+#include "lokinfer_hip.h"
+
+namespace lkrt {
+
+namespace {
+
+constexpr int64_t kUnbound = INT64_MIN;
+constexpr size_t kAlign = 256;
+constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+
+size_t alignUp(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+Status hipStatus(hipError_t e, const char* what) {
+  if (e == hipSuccess) return Status();
+  (void)hipGetLastError();
+  return Status::error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+Status deviceErrors() {
+  int64_t detail = 0;
+  const int code = lk_take_device_error(&detail);
+  if (code == 0) return Status();
+  if (code < 0) return Status::error("could not read the device error record");
+  return Status::error("device error " + std::to_string(code) + ": " + lk_device_error_message(code) + " (detail " +
+                       std::to_string(detail) + ")");
+}
+
+}  // namespace
+
+struct Executable::Instr {
+  OpKind kind;
+  const Op* op;
+  const lkh::KernelEntry* kernel = nullptr;
+  std::vector<ValueId> args;  // kernel: operands then outs
+  std::vector<int64_t> ints;  // static ints; dynInts patch the symbolic ones per call
+  std::vector<std::pair<uint32_t, Dim>> dynInts;
+  std::vector<double> floats;
+  mutable std::vector<void*> ptrBuf;
+  mutable std::vector<int64_t> intBuf;
+};
+
+Executable::Memory::~Memory() {
+  if (p) (void)hipFree(p);
+}
+
+Executable::~Executable() {
+  for (auto& [k, g] : graphs_) {
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+  }
+  if (captureStream_) (void)hipStreamDestroy(captureStream_);
+  if (pinned_) (void)hipHostFree(pinned_);
+}
+
+char* Executable::Bump::alloc(size_t bytes, Status& st) {
+  bytes = alignUp(std::max<size_t>(bytes, 1));
+  if (!blocks.empty() && used + bytes <= blocks.back()->n) {
+    char* p = static_cast<char*>(blocks.back()->p) + used;
+    used += bytes;
+    return p;
+  }
+  auto m = std::make_unique<Memory>();
+  m->n = std::max({bytes, 2 * capacity(), size_t(1) << 20});
+  if (hipError_t e = hipMalloc(&m->p, m->n); e != hipSuccess) {
+    st = hipStatus(e, "hipMalloc (call arena)");
+    return nullptr;
+  }
+  blocks.push_back(std::move(m));
+  used = bytes;
+  return static_cast<char*>(blocks.back()->p);
+}
+
+size_t Executable::Bump::capacity() const {
+  size_t n = 0;
+  for (const auto& b : blocks) n += b->n;
+  return n;
+}
+
+size_t Executable::callArenaBytes() const {
+  size_t n = eager_.capacity();
+  for (const auto& [k, g] : graphs_) n += g->mem ? g->mem->n : 0;
+  return n;
+}
+
+std::string Executable::strategy() const {
+  if (dynamic_) return "eager (data-dependent shapes or host scalar inputs)";
+  return graphs_on_ ? "hipGraph per input-shape binding" : "eager";
+}
+
+Status Executable::lower(const Region& r, std::vector<Instr>& out) {
+  const Model& m = *model_;
+  for (const Op& op : r.ops) {
+    Instr in;
+    in.kind = op.kind;
+    in.op = &op;
+    if (op.kind == OpKind::Kernel) {
+      if (!op.results.empty()) return Status::error("kernel '" + op.name + "' still has results (run bufferize)");
+      in.kernel = lkh::findKernel(op.name);
+      if (!in.kernel) {
+        return Status::error(isGpuKernelName(op.name)
+                                 ? "unknown kernel '" + op.name + "'"
+                                 : "kernel '" + op.name + "' is a host kernel: this runtime runs GPU kernels only");
+      }
+      if ((in.kernel->device == lkh::Device::Gpu) != isGpuKernelName(op.name))
+        return Status::error("kernel '" + op.name + "' is registered on a device its name doesn't say");
+      in.args = op.operands;
+      in.args.insert(in.args.end(), op.outs.begin(), op.outs.end());
+      if (in.kernel->numOperands >= 0 &&
+          (op.operands.size() != static_cast<size_t>(in.kernel->numOperands) ||
+           op.outs.size() != static_cast<size_t>(in.kernel->numOuts)))
+        return Status::error("kernel '" + op.name + "' takes " + std::to_string(in.kernel->numOperands) +
+                             " operands and " + std::to_string(in.kernel->numOuts) + " outs");
+      auto addDim = [&](Dim d) {
+        if (!d->isConst()) in.dynInts.emplace_back(static_cast<uint32_t>(in.ints.size()), d);
+        in.ints.push_back(d->isConst() ? d->value : 0);
+      };
+      for (ValueId v : in.args)
+        for (Dim d : m.typeOf(v)->shape) addDim(d);
+      for (const NamedAttr& a : op.attrs) {
+        if (isStructuralAttr(a.name)) continue;
+        switch (a.value.index()) {
+          case 0: in.ints.push_back(std::get<bool>(a.value) ? 1 : 0); break;
+          case 1: in.ints.push_back(std::get<int64_t>(a.value)); break;
+          case 2: in.floats.push_back(std::get<double>(a.value)); break;
+          case 3: break;  // string attrs carry no kernel argument
+          case 4: {
+            const Ints& v = std::get<Ints>(a.value);
+            in.ints.insert(in.ints.end(), v.begin(), v.end());
+            break;
+          }
+          case 5: {
+            const Floats& v = std::get<Floats>(a.value);
+            in.floats.insert(in.floats.end(), v.begin(), v.end());
+            break;
+          }
+          default: addDim(std::get<Dim>(a.value));
+        }
+      }
+      if (in.ints.size() > 256 || in.floats.size() > 32)
+        return Status::error("kernel '" + op.name + "': too many int / float arguments");
+      in.ptrBuf.resize(in.args.size());
+      in.intBuf = in.ints;
+    } else if (op.kind == OpKind::MemPlan && r.args.empty() && &r == &model_->init) {
+      return Status::error("mem.plan in init is not supported");
+    }
+    out.push_back(std::move(in));
+  }
+  return Status();
+}
+
+// Binds every symbol the exec inputs' shapes define: a dim that is (a sum of bound terms plus) k * S with S the
+// one unbound symbol binds S; every other dim is checked against the input's extent.
+Status Executable::bindInputs(const std::vector<TensorIn>& in, std::vector<int64_t>& sv) const {
+  const Model& m = *model_;
+  const Region& ex = m.exec;
+  if (in.size() != ex.args.size())
+    return Status::error("expected " + std::to_string(ex.args.size()) + " inputs, got " + std::to_string(in.size()));
+  sv.assign(m.dims().numSymbols(), kUnbound);
+  for (size_t i = 0; i < in.size(); ++i) {
+    Type t = m.typeOf(ex.args[i]);
+    if (in[i].dtype != t->dtype)
+      return Status::error("input " + std::to_string(i) + ": expected dtype " + dtypeName(t->dtype) + ", got " +
+                           dtypeName(in[i].dtype));
+    if (in[i].shape.size() != t->shape.size())
+      return Status::error("input " + std::to_string(i) + ": expected rank " + std::to_string(t->shape.size()) +
+                           ", got " + std::to_string(in[i].shape.size()));
+    if (!in[i].data && !t->isScalar()) return Status::error("input " + std::to_string(i) + " has no data");
+  }
+  const DimPool& dp = m.dims();
+  // linear form k * S + b of d in one unbound symbol S (b evaluable now)
+  auto linear = [&](Dim d, int64_t& sym, int64_t& k, int64_t& b) {
+    auto term = [&](Dim t, int64_t& s, int64_t& c) {
+      if (t->kind == DimKind::Sym && sv[static_cast<size_t>(t->value)] == kUnbound) {
+        s = t->value;
+        c = 1;
+        return true;
+      }
+      if (t->kind == DimKind::Mul && t->args.size() == 2 && t->args[0]->isConst() && t->args[1]->kind == DimKind::Sym &&
+          sv[static_cast<size_t>(t->args[1]->value)] == kUnbound) {
+        s = t->args[1]->value;
+        c = t->args[0]->value;
+        return true;
+      }
+      return false;
+    };
+    if (term(d, sym, k)) {
+      b = 0;
+      return true;
+    }
+    if (d->kind != DimKind::Add) return false;
+    bool found = false;
+    b = 0;
+    for (Dim t : d->args) {
+      int64_t s, c;
+      if (auto v = dp.eval(t, sv, kUnbound)) {
+        b += *v;
+      } else if (!found && term(t, s, c)) {
+        found = true;
+        sym = s;
+        k = c;
+      } else {
+        return false;
+      }
+    }
+    return found;
+  };
+  for (int pass = 0;; ++pass) {
+    bool progress = false, pending = false;
+    for (size_t i = 0; i < in.size(); ++i) {
+      Type t = m.typeOf(ex.args[i]);
+      for (size_t j = 0; j < t->shape.size(); ++j) {
+        const int64_t actual = in[i].shape[j];
+        if (dp.eval(t->shape[j], sv, kUnbound)) continue;
+        int64_t sym = 0, k = 0, b = 0;
+        if (linear(t->shape[j], sym, k, b) && k != 0 && (actual - b) % k == 0) {
+          sv[static_cast<size_t>(sym)] = (actual - b) / k;
+          progress = true;
+        } else {
+          pending = true;
+        }
+      }
+    }
+    if (!pending) break;
+    if (!progress) return Status::error("cannot bind the symbols of the input shapes");
+  }
+  for (size_t i = 0; i < in.size(); ++i) {
+    Type t = m.typeOf(ex.args[i]);
+    for (size_t j = 0; j < t->shape.size(); ++j) {
+      const int64_t want = *dp.eval(t->shape[j], sv, kUnbound);
+      if (want != in[i].shape[j] || want < 0)
+        return Status::error("input " + std::to_string(i) + " dim " + std::to_string(j) + " is " +
+                             std::to_string(in[i].shape[j]) + ", the model's shape " + m.types().str(t) + " needs " +
+                             std::to_string(want));
+    }
+  }
+  return Status();
+}
+
+Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv,
+                             Bump& mem, hipStream_t s, std::vector<TensorOut>* outs) {
+  const Model& m = *model_;
+  const DimPool& dp = m.dims();
+  auto eval = [&](Dim d, int64_t& v) -> bool {
+    auto r = dp.eval(d, sv, kUnbound);
+    if (!r) return false;
+    v = *r;
+    return true;
+  };
+  auto bytesOf = [&](Type t, int64_t& n) -> bool {
+    n = static_cast<int64_t>(dtypeSize(t->dtype));
+    for (Dim d : t->shape) {
+      int64_t v;
+      if (!eval(d, v) || v < 0) return false;
+      n *= v;
+    }
+    return true;
+  };
+  for (const Instr& in : code) {
+    const Op& op = *in.op;
+    switch (in.kind) {
+      case OpKind::Kernel: {
+        for (size_t k = 0; k < in.args.size(); ++k) {
+          const ValueId v = in.args[k];
+          if (m.typeOf(v)->isScalar()) {
+            in.ptrBuf[k] = &scalars_[v];
+          } else {
+            if (!slot[v]) return Status::error("kernel '" + op.name + "': an argument has no memory");
+            in.ptrBuf[k] = slot[v];
+          }
+        }
+        for (const auto& [idx, d] : in.dynInts)
+          if (!eval(d, in.intBuf[idx])) return Status::error("kernel '" + op.name + "': unbound symbol in its shapes");
+        lkh::KernelArgs a{in.ptrBuf.data(), nullptr, in.intBuf.data(), in.floats.data(), nullptr,
+                          static_cast<uint32_t>(in.ptrBuf.size()), static_cast<uint32_t>(in.intBuf.size()),
+                          static_cast<uint32_t>(in.floats.size())};
+        lkh::ExecCtx ctx;
+        ctx.stream = s;
+        ctx.workspace = workspace_;
+        ctx.workspaceBytes = workspaceBytes_;
+        in.kernel->run(ctx, a);
+        if (ctx.error) return Status::error("kernel '" + op.name + "': " + ctx.error);
+        break;
+      }
+      case OpKind::View: {
+        int64_t off;
+        if (!eval(op.dims[0], off)) return Status::error("view: unbound symbol in its offset");
+        Type src = m.typeOf(op.operands[0]), dst = m.typeOf(op.results[0]);
+        const int64_t es = static_cast<int64_t>(dtypeSize(dst->dtype));
+        int64_t sb, db;
+        if (bytesOf(src, sb) && bytesOf(dst, db) && (off < 0 || off * es + db > sb))
+          return Status::error("view out of bounds of its source (" + std::to_string(off * es + db) + " > " +
+                               std::to_string(sb) + " bytes)");
+        slot[op.results[0]] = slot[op.operands[0]] ? slot[op.operands[0]] + off * es : nullptr;
+        break;
+      }
+      case OpKind::BufferAlloc: {
+        const ValueId v = op.results[0];
+        if (fixed_[v]) {
+          slot[v] = fixed_[v];
+          break;
+        }
+        int64_t n;
+        if (!bytesOf(m.typeOf(v), n)) return Status::error("buffer.alloc: unbound symbol in its shape");
+        Status st;
+        slot[v] = mem.alloc(static_cast<size_t>(n), st);
+        if (!slot[v]) return st;
+        break;
+      }
+      case OpKind::MemPlan: {
+        std::vector<PlanItem> items;
+        for (size_t k = 0; k < op.dims.size(); ++k) {
+          int64_t n;
+          if (!eval(op.dims[k], n)) return Status::error("mem.plan: unbound symbol in a size");
+          items.push_back({n, op.ints[2 * k], op.ints[2 * k + 1]});
+        }
+        std::vector<int64_t> offs;
+        const int64_t total = planOffsets(items, op.ints.back(), offs);
+        const Ints* elem = op.attr("elem") ? std::get_if<Ints>(op.attr("elem")) : nullptr;
+        sv[static_cast<size_t>(op.symbols[0])] = total;
+        for (size_t k = 0; k < offs.size(); ++k)
+          sv[static_cast<size_t>(op.symbols[k + 1])] = offs[k] / (elem ? (*elem)[k] : 1);
+        Status st;
+        slot[op.results[0]] = mem.alloc(static_cast<size_t>(total), st);
+        if (!slot[op.results[0]]) return st;
+        break;
+      }
+      case OpKind::DimRead: {
+        const ValueId v = op.operands[0];
+        const size_t es = dtypeSize(m.typeOf(v)->dtype);
+        LKRT_TRY(hipStatus(hipMemcpyAsync(pinned_, slot[v] + op.ints[0] * static_cast<int64_t>(es), es,
+                                          hipMemcpyDeviceToHost, s),
+                           "dim.read"));
+        LKRT_TRY(hipStatus(hipStreamSynchronize(s), "dim.read"));
+        int64_t val;
+        if (es == 8) {
+          val = *pinned_;
+        } else {
+          int32_t x;
+          std::memcpy(&x, pinned_, 4);
+          val = x;
+        }
+        if (val < 0) return Status::error("dim.read: negative value " + std::to_string(val));
+        sv[static_cast<size_t>(op.symbols[0])] = val;
+        break;
+      }
+      case OpKind::Sync:
+        if (!op.results.empty()) slot[op.results[0]] = slot[op.operands[0]];  // one address space on the device
+        break;
+      case OpKind::ConstInline:
+      case OpKind::ConstInternal:
+      case OpKind::ConstExternal:
+        slot[op.results[0]] = fixed_[op.results[0]];
+        break;
+      case OpKind::BufferFree:
+        break;
+      case OpKind::Return:
+        if (outs) {
+          outs->clear();
+          for (ValueId v : op.operands) {
+            TensorOut o{slot[v], {}, m.typeOf(v)->dtype};
+            for (Dim d : m.typeOf(v)->shape) {
+              int64_t x;
+              if (!eval(d, x)) return Status::error("return: unbound symbol in an output shape");
+              o.shape.push_back(x);
+            }
+            outs->push_back(std::move(o));
+          }
+        }
+        break;
+    }
+  }
+  return Status();
+}
+
+Status Executable::callBytes(std::vector<int64_t> sv, size_t& bytes) const {
+  const Model& m = *model_;
+  bytes = 0;
+  for (const Instr& in : exec_) {
+    const Op& op = *in.op;
+    if (in.kind == OpKind::BufferAlloc && !fixed_[op.results[0]]) {
+      int64_t n = static_cast<int64_t>(dtypeSize(m.typeOf(op.results[0])->dtype));
+      for (Dim d : m.typeOf(op.results[0])->shape) {
+        auto v = m.dims().eval(d, sv, kUnbound);
+        if (!v) return Status::error("buffer.alloc: unbound symbol");
+        n *= *v;
+      }
+      bytes += alignUp(static_cast<size_t>(std::max<int64_t>(n, 1)));
+    } else if (in.kind == OpKind::MemPlan) {
+      std::vector<PlanItem> items;
+      for (size_t k = 0; k < op.dims.size(); ++k) {
+        auto v = m.dims().eval(op.dims[k], sv, kUnbound);
+        if (!v) return Status::error("mem.plan: unbound symbol");
+        items.push_back({*v, op.ints[2 * k], op.ints[2 * k + 1]});
+      }
+      std::vector<int64_t> offs;
+      const int64_t total = planOffsets(items, op.ints.back(), offs);
+      const Ints* elem = op.attr("elem") ? std::get_if<Ints>(op.attr("elem")) : nullptr;
+      sv[static_cast<size_t>(op.symbols[0])] = total;
+      for (size_t k = 0; k < offs.size(); ++k)
+        sv[static_cast<size_t>(op.symbols[k + 1])] = offs[k] / (elem ? (*elem)[k] : 1);
+      bytes += alignUp(static_cast<size_t>(std::max<int64_t>(total, 1)));
+    }
+  }
+  return Status();
+}
+
+std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> model, const std::vector<ExternalPtr>& ext,
+                                               hipStream_t stream, bool useGraphs, Status& st) {
+  std::unique_ptr<Executable> x(new Executable());
+  x->model_ = std::move(model);
+  const Model& m = *x->model_;
+  auto fail = [&](Status s) {
+    st = std::move(s);
+    return nullptr;
+  };
+  if (Status v = verifyModel(m); !v) return fail(v);
+  for (ValueId v = 0; v < m.numValues(); ++v)
+    if (m.typeOf(v)->isTensor()) return fail(Status::error("the model is not in buffer form (run bufferize)"));
+  if (Status s = x->lower(m.init, x->init_); !s) return fail(s);
+  if (Status s = x->lower(m.exec, x->exec_); !s) return fail(s);
+  for (const Op& op : m.exec.ops) x->dynamic_ = x->dynamic_ || op.kind == OpKind::DimRead;
+  for (ValueId v : m.exec.args) x->dynamic_ = x->dynamic_ || m.typeOf(v)->isScalar();
+  x->graphs_on_ = useGraphs;
+
+  // Model arena: every constant, init allocation, persistent buffer, then the workspace.
+  const size_t nv = m.numValues();
+  std::vector<int64_t> offset(nv, -1);
+  struct Upload {
+    ValueId v;
+    const void* src;
+    size_t bytes;
+  };
+  std::vector<Upload> uploads;
+  std::vector<std::pair<ValueId, void*>> deviceExternals;
+  size_t off = 0;
+  auto take = [&](ValueId v, size_t bytes) {
+    offset[v] = static_cast<int64_t>(off);
+    off += alignUp(std::max<size_t>(bytes, 1));
+  };
+  auto staticBytes = [&](Type t, size_t& n) {
+    n = dtypeSize(t->dtype);
+    for (Dim d : t->shape) {
+      if (!d->isConst() || d->value < 0) return false;
+      n *= static_cast<size_t>(d->value);
+    }
+    return true;
+  };
+  for (const Region* r : {&m.init, &m.exec}) {
+    const bool init = r == &m.init;
+    for (const Op& op : r->ops) {
+      switch (op.kind) {
+        case OpKind::ConstInline:
+          take(op.results[0], op.data.size());
+          uploads.push_back({op.results[0], op.data.data(), op.data.size()});
+          break;
+        case OpKind::ConstInternal: {
+          const Constant* c = m.findConstant(op.name);
+          size_t n;
+          if (!staticBytes(m.typeOf(op.results[0]), n)) return fail(Status::error("constant '" + op.name + "' has a symbolic shape"));
+          if (!c || (!c->bytes && n)) return fail(Status::error("constant '" + op.name + "' has no data"));
+          if (c->size != n) return fail(Status::error("constant '" + op.name + "' size doesn't match its type"));
+          take(op.results[0], n);
+          uploads.push_back({op.results[0], c->bytes, n});
+          break;
+        }
+        case OpKind::ConstExternal: {
+          const ExternalPtr* e = nullptr;
+          for (const ExternalPtr& q : ext)
+            if (q.name == op.name) e = &q;
+          size_t n;
+          if (!staticBytes(m.typeOf(op.results[0]), n)) return fail(Status::error("external '" + op.name + "' has a symbolic shape"));
+          if (!e) return fail(Status::error("no data bound for external constant '" + op.name + "'"));
+          if (e->bytes != n) return fail(Status::error("external '" + op.name + "' has " + std::to_string(e->bytes) +
+                                                       " bytes, its type " + std::to_string(n)));
+          if (e->onDevice) {
+            deviceExternals.emplace_back(op.results[0], e->ptr);
+          } else {
+            take(op.results[0], n);
+            uploads.push_back({op.results[0], e->ptr, n});
+          }
+          break;
+        }
+        case OpKind::BufferAlloc: {
+          if (!init && !op.flag("persistent")) break;  // per-call memory
+          size_t n;
+          if (!staticBytes(m.typeOf(op.results[0]), n))
+            return fail(Status::error("a model-lifetime buffer has a symbolic shape"));
+          take(op.results[0], n);
+          break;
+        }
+        case OpKind::DimRead:
+          if (init) return fail(Status::error("dim.read in init is not supported"));
+          break;
+        default:
+          break;
+      }
+    }
+  }
+  const size_t wsOff = off;
+  off += kWorkspaceBytes;
+  x->modelArena_ = std::make_unique<Memory>();
+  x->modelArena_->n = off;
+  if (Status s = hipStatus(hipMalloc(&x->modelArena_->p, off), "hipMalloc (model arena)"); !s) return fail(s);
+  x->modelBytes_ = off;
+  char* base = static_cast<char*>(x->modelArena_->p);
+  if (Status s = hipStatus(hipMemsetAsync(base, 0, off, stream), "hipMemsetAsync"); !s) return fail(s);
+  x->workspace_ = base + wsOff;
+  x->workspaceBytes_ = kWorkspaceBytes;
+  x->fixed_.assign(nv, nullptr);
+  for (ValueId v = 0; v < nv; ++v)
+    if (offset[v] >= 0) x->fixed_[v] = base + offset[v];
+  for (auto& [v, p] : deviceExternals) x->fixed_[v] = static_cast<char*>(p);
+  for (const Upload& u : uploads)
+    if (u.bytes)
+      if (Status s = hipStatus(hipMemcpyAsync(x->fixed_[u.v], u.src, u.bytes, hipMemcpyHostToDevice, stream),
+                               "upload");
+          !s)
+        return fail(s);
+  x->scalars_.assign(nv, 0);
+  if (Status s = hipStatus(hipHostMalloc(reinterpret_cast<void**>(&x->pinned_), 8), "hipHostMalloc"); !s) return fail(s);
+  if (Status s = hipStatus(hipStreamCreateWithFlags(&x->captureStream_, hipStreamNonBlocking), "hipStreamCreate"); !s)
+    return fail(s);
+
+  // init: model-lifetime results become the exec state
+  std::vector<char*> slot(x->fixed_);
+  std::vector<int64_t> sv(m.dims().numSymbols(), kUnbound);
+  std::vector<TensorOut> initOut;
+  Bump none;
+  if (Status s = x->interpret(x->init_, slot, sv, none, stream, &initOut); !s) return fail(Status::error("init: " + s.message()));
+  if (!none.blocks.empty()) return fail(Status::error("init allocated per-call memory"));
+  for (size_t i = 0; i < m.exec.state.size(); ++i) x->fixed_[m.exec.state[i]] = static_cast<char*>(initOut[i].data);
+  if (Status s = hipStatus(hipStreamSynchronize(stream), "init"); !s) return fail(s);
+  if (Status s = deviceErrors(); !s) return fail(Status::error("init: " + s.message()));
+  st = Status();
+  return x;
+}
+
+Status Executable::run(const std::vector<TensorIn>& inputs, std::vector<TensorOut>& outputs, hipStream_t stream,
+                       bool sync) {
+  const Model& m = *model_;
+  const Region& ex = m.exec;
+  std::vector<int64_t> sv;
+  LKRT_TRY(bindInputs(inputs, sv));
+  std::vector<char*> slot(fixed_);
+  for (size_t i = 0; i < inputs.size(); ++i) {
+    const ValueId v = ex.args[i];
+    if (m.typeOf(v)->isScalar()) std::memcpy(&scalars_[v], inputs[i].data, 8);
+    else slot[v] = static_cast<char*>(inputs[i].data);
+  }
+  bool eager = !graphs_on_ || dynamic_;
+  std::vector<int64_t> key;
+  if (!eager) {
+    key = sv;
+    for (size_t i = 0; i < inputs.size(); ++i)
+      if (ex.isMutable(i)) key.push_back(reinterpret_cast<int64_t>(inputs[i].data));
+    auto it = graphs_.find(key);
+    eager = it != graphs_.end() && !it->second->exec;  // a binding whose capture failed runs eagerly
+  }
+  if (eager) {
+    if (eager_.blocks.size() > 1) {  // coalesce last call's overflow blocks into one
+      LKRT_TRY(hipStatus(hipDeviceSynchronize(), "call arena"));
+      const size_t cap = eager_.capacity();
+      eager_.blocks.clear();
+      Status st;
+      if (!eager_.alloc(cap, st)) return st;
+    }
+    eager_.used = 0;
+    LKRT_TRY(interpret(exec_, slot, sv, eager_, stream, &outputs));
+  } else {
+    auto it = graphs_.find(key);
+    if (it == graphs_.end()) {
+      auto g = std::make_unique<Graph>();
+      size_t callB = 0, inB = 0;
+      LKRT_TRY(callBytes(sv, callB));
+      std::vector<size_t> inSize(inputs.size(), 0);
+      for (size_t i = 0; i < inputs.size(); ++i) {
+        if (ex.isMutable(i)) continue;
+        size_t n = dtypeSize(inputs[i].dtype);
+        for (int64_t d : inputs[i].shape) n *= static_cast<size_t>(d);
+        inSize[i] = n;
+        inB += alignUp(std::max<size_t>(n, 1));
+      }
+      g->mem = std::make_unique<Memory>();
+      g->mem->n = inB + callB;
+      LKRT_TRY(hipStatus(hipMalloc(&g->mem->p, std::max<size_t>(g->mem->n, 1)), "hipMalloc (call block)"));
+      char* p = static_cast<char*>(g->mem->p);
+      g->inputs.assign(inputs.size(), nullptr);
+      for (size_t i = 0; i < inputs.size(); ++i) {
+        if (ex.isMutable(i)) continue;
+        g->inputs[i] = p;
+        slot[ex.args[i]] = p;
+        if (inSize[i])
+          LKRT_TRY(hipStatus(hipMemcpyAsync(p, inputs[i].data, inSize[i], hipMemcpyDeviceToDevice, stream), "input copy"));
+        p += alignUp(std::max<size_t>(inSize[i], 1));
+      }
+      // A non-owning view of the block's call region: the warm-up run and the capture walk allocate the same
+      // addresses.
+      Bump view;
+      auto region = std::make_unique<Memory>();
+      region->p = p;
+      region->n = callB;
+      view.blocks.push_back(std::move(region));
+      std::vector<char*> warmSlot(slot);
+      std::vector<int64_t> warmSv(sv);
+      Status ws = interpret(exec_, warmSlot, warmSv, view, stream, &g->outputs);
+      if (ws && view.blocks.size() == 1) {
+        view.used = 0;
+        std::vector<char*> capSlot(slot);
+        std::vector<int64_t> capSv(sv);
+        std::vector<TensorOut> capOut;
+        LKRT_TRY(hipStatus(hipStreamBeginCapture(captureStream_, hipStreamCaptureModeThreadLocal), "capture"));
+        Status cs = interpret(exec_, capSlot, capSv, view, captureStream_, &capOut);
+        hipGraph_t graph = nullptr;
+        const hipError_t ee = hipStreamEndCapture(captureStream_, &graph);
+        if (cs && ee == hipSuccess) {
+          g->graph = graph;
+          LKRT_TRY(hipStatus(hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate"));
+        } else {
+          if (graph) (void)hipGraphDestroy(graph);
+          (void)hipGetLastError();
+          if (!cs) ws = cs;
+        }
+      }
+      view.blocks[0]->p = nullptr;  // not owned
+      LKRT_TRY(ws);
+      outputs = g->outputs;
+      graphs_[key] = std::move(g);
+    } else {
+      Graph& g = *it->second;
+      for (size_t i = 0; i < inputs.size(); ++i) {
+        if (!g.inputs[i]) continue;
+        size_t n = dtypeSize(inputs[i].dtype);
+        for (int64_t d : inputs[i].shape) n *= static_cast<size_t>(d);
+        if (n)
+          LKRT_TRY(hipStatus(hipMemcpyAsync(g.inputs[i], inputs[i].data, n, hipMemcpyDeviceToDevice, stream),
+                             "input copy"));
+      }
+      LKRT_TRY(hipStatus(hipGraphLaunch(g.exec, stream), "hipGraphLaunch"));
+      outputs = g.outputs;
+    }
+  }
+  if (sync) {
+    LKRT_TRY(hipStatus(hipStreamSynchronize(stream), "run"));
+    LKRT_TRY(deviceErrors());
+  }
+  return Status();
+}
+
+}  // namespace lkrt

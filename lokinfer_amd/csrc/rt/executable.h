@@ -1,0 +1,111 @@
+// The MI355X executable: runs a compiled (buffer-form) model on one HIP stream.
+//
+// Replaces the reference's Executable (lariaus/lokinfer include/lokinfer/runtime/runtime.h:84-124,
+// src/runtime/executable.cpp:567-1144) and its Metal GpuContext (src/runtime/gpu_internal.h:53-290):
+//  - one hipMalloc'd model arena per executable holds every constant (internal constants uploaded once at create),
+//    init's allocations, persistent state and the kernel workspace, zeroed once;
+//  - per call, memory comes from a call arena that grows by whole hipMallocs and is reused: a statically shaped
+//    call (no dim.read, no host scalar inputs) runs from one exactly sized block per input-shape binding, and after
+//    its first (eager) run is captured into a hipGraph that later calls replay after copying the inputs into the
+//    block's input buffers;
+//  - kernels are the registry's (lkh::findKernel), called with the reference's argument convention;
+//  - a kernel's ExecCtx::error becomes the call's Status, and so does a data error a kernel recorded on the device
+//    (read at the call's synchronisation, the reference's takeGpuError).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "ir.h"
+
+namespace lkrt {
+
+struct ExternalPtr {
+  std::string name;
+  void* ptr;
+  size_t bytes;
+  bool onDevice;  // false: host memory, uploaded into the model arena at create
+};
+
+struct TensorIn {
+  void* data;  // device pointer (host pointer to 8 bytes for a scalar)
+  std::vector<int64_t> shape;
+  DType dtype;
+};
+
+struct TensorOut {
+  void* data;  // device memory owned by the executable, valid until its next call
+  std::vector<int64_t> shape;
+  DType dtype;
+};
+
+class Executable {
+ public:
+  ~Executable();
+  // `model` must be in buffer form (after bufferize). Uploads constants and runs init on `stream`.
+  static std::unique_ptr<Executable> create(std::shared_ptr<const Model> model, const std::vector<ExternalPtr>& ext,
+                                            hipStream_t stream, bool useGraphs, Status& st);
+  // Enqueues one call on `stream`. With `sync`, waits for it and reports device-side data errors.
+  Status run(const std::vector<TensorIn>& inputs, std::vector<TensorOut>& outputs, hipStream_t stream, bool sync);
+
+  const Model& model() const { return *model_; }
+  size_t modelArenaBytes() const { return modelBytes_; }
+  size_t callArenaBytes() const;
+  int graphsCaptured() const { return static_cast<int>(graphs_.size()); }
+  std::string strategy() const;
+
+  struct Instr;
+
+ private:
+  Executable() = default;
+  struct Memory {
+    void* p = nullptr;
+    size_t n = 0;
+    Memory() = default;
+    Memory(const Memory&) = delete;
+    Memory& operator=(const Memory&) = delete;
+    ~Memory();
+  };
+  struct Bump {  // a bump allocator over one or more blocks; reset per call
+    std::vector<std::unique_ptr<Memory>> blocks;
+    size_t used = 0;
+    char* alloc(size_t bytes, Status& st);
+    size_t capacity() const;
+  };
+  struct Graph {
+    std::unique_ptr<Memory> mem;  // inputs, then the call's memory
+    std::vector<char*> inputs;    // staging buffer of each non-mutable input
+    std::vector<TensorOut> outputs;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+  };
+
+  Status lower(const Region& r, std::vector<Instr>& out);
+  Status bindInputs(const std::vector<TensorIn>& in, std::vector<int64_t>& sv) const;
+  Status interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv, Bump& mem,
+                   hipStream_t s, std::vector<TensorOut>* outs);
+  // bytes the exec region allocates for a binding (statically shaped calls only)
+  Status callBytes(std::vector<int64_t> sv, size_t& bytes) const;
+
+  std::shared_ptr<const Model> model_;
+  std::vector<Instr> init_, exec_;
+  std::unique_ptr<Memory> modelArena_;
+  size_t modelBytes_ = 0;
+  void* workspace_ = nullptr;
+  size_t workspaceBytes_ = 0;
+  std::vector<char*> fixed_;          // value -> model-lifetime address (constants, state, persistent buffers)
+  std::vector<int64_t> scalars_;      // host slots of scalar exec inputs
+  bool graphs_on_ = false;
+  bool dynamic_ = false;              // exec has dim.read or scalar inputs: always eager
+  Bump eager_;
+  std::map<std::vector<int64_t>, std::unique_ptr<Graph>> graphs_;
+  hipStream_t captureStream_ = nullptr;
+  int64_t* pinned_ = nullptr;         // dim.read landing slot
+};
+
+}  // namespace lkrt

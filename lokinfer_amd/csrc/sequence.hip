@@ -83,8 +83,9 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 // step s+1 word could replace the step s word the reader has not read yet. With two buffers the step s+1 word
 // replaces the step s-1 word, and every reader is past step s-1 once the writer holds all h(s).
 // The exchange words are cleared by a fill kernel before every launch. Every poll is bounded: after
-// kLstmSpinLimit polls the lane stops, writes NaN (which every later h inherits) and records the failure, so a missing peer (e.g. not
-// co-resident) ends the kernel instead of hanging it.
+// kLstmSpinLimit polls the lane stops, writes NaN (which every later h inherits) and records the step in the GPU's
+// error record (LK_DEVERR_EXCHANGE_TIMEOUT), so a missing peer (e.g. not co-resident) ends the kernel instead of
+// hanging it, and the host reports it at the next synchronisation.
 constexpr int kLstmWgs = 16;         // workgroups per direction
 constexpr int kLstmUnits = 16;       // hidden units per workgroup (H = 256)
 // waves per workgroup, each over H / kLstmWaves of k: 8 waves of 32 k run a step in 1.18 us, 4 of 64 k in 1.23 us,
@@ -116,12 +117,14 @@ __device__ __forceinline__ void gatherGates(float v, float& i, float& f, float& 
 __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float* __restrict__ g,
                                                                     const float* __restrict__ whhT,
                                                                     float* __restrict__ out,
-                                                                    unsigned long long* xbuf, int* failed,
-                                                                    int64_t t) {
+                                                                    unsigned long long* xbuf,
+                                                                    unsigned long long* err, int64_t t) {
   constexpr int H = 256;
   constexpr int KW = H / kLstmWaves;  // k per wave
   __shared__ float4 hsw[kLstmWaves][KW / 4];  // wave w: h(t-1)[KW w .. KW w + KW - 1]
-  __shared__ float part[kLstmWaves][64];      // wave w's partial dot product of each gate row
+  // wave w's partial dot product of each gate row, double-buffered by step parity: a wave w >= 1 may finish step
+  // s (it polls other workgroups' words only) and write step s + 1's partials before wave 0 has read step s's
+  __shared__ float part[2][kLstmWaves][64];
   const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ld = 8 * H;
@@ -157,14 +160,14 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       a2 = fmaf(w[4 * i + 2], h.z, a2);
       a3 = fmaf(w[4 * i + 3], h.w, a3);
     }
-    part[wave][lane] = (a0 + a1) + (a2 + a3);
+    part[step & 1][wave][lane] = (a0 + a1) + (a2 + a3);
     __syncthreads();
     const unsigned tag = static_cast<unsigned>(step + 1);
     unsigned long long* xb = xdir + (step & 1) * H;
     if (wave == 0) {
       float pv[kLstmWaves];  // the waves' partials summed as a pairwise tree: ((p0 + p1) + (p2 + p3)) + ...
 #pragma unroll
-      for (int i = 0; i < kLstmWaves; ++i) pv[i] = part[i][lane];
+      for (int i = 0; i < kLstmWaves; ++i) pv[i] = part[step & 1][i][lane];
 #pragma unroll
       for (int n = kLstmWaves; n > 1; n /= 2)
 #pragma unroll
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
         if (static_cast<unsigned>(word >> 32) == tag) break;
         if (++spins > kLstmSpinLimit) {
           ok = false;
-          atomicExch(failed, 1);
+          lkd::raiseDeviceError(err, LK_DEVERR_EXCHANGE_TIMEOUT, step);
         }
       }
       // A lane that timed out keeps stepping (so every wave reaches the end) but stops waiting; its NaN
@@ -208,7 +211,8 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
 // the first i with cum[i] > f.
 __global__ __launch_bounds__(256) void repeatInterleaveKernel(const float* __restrict__ x,
                                                              const int64_t* __restrict__ dur, float* __restrict__ out,
-                                                             int64_t t, int64_t c, int64_t frames) {
+                                                             int64_t t, int64_t c, int64_t frames,
+                                                             unsigned long long* err) {
   __shared__ int64_t cum[8192];
   __shared__ int64_t part[256];
   const int tid = threadIdx.x;
@@ -236,6 +240,7 @@ __global__ __launch_bounds__(256) void repeatInterleaveKernel(const float* __res
       else lo = mid + 1;
     }
     const bool ok = lo < t;
+    if (!ok && tid == 0) raiseDeviceError(err, LK_DEVERR_DURATIONS, f);
     for (int64_t j = tid; j < c; j += 256) out[f * c + j] = ok ? x[lo * c + j] : __builtin_nanf("");
   }
 }
@@ -294,13 +299,12 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;
-  const int64_t xBytes = 4 * 256 * 8 + 256;  // [direction][parity][256] words + failure flag
+  const int64_t xBytes = 4 * 256 * 8;  // [direction][parity][256] exchange words
   if (h == 256 && workspaceBytes >= gBytes + xBytes) {
     auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
-    int* failed = reinterpret_cast<int*>(static_cast<char*>(workspace) + gBytes + 4 * 256 * 8);
     hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(4), dim3(256), 0, s, xbuf, 4 * 256);
     hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), 0, s, g, whhT,
-                       out, xbuf, failed, t);
+                       out, xbuf, lkh::deviceErrorRecord(), t);
   } else {
     hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0, s, g, whhT, out,
                        t, static_cast<int>(h));
@@ -314,7 +318,7 @@ int lk_hip_repeat_interleave_f32(const float* x, const int64_t* dur, float* out,
   if (frames == 0) return 0;
   const int64_t blocks = std::min<int64_t>(frames, 1024);
   hipLaunchKernelGGL(lkd::repeatInterleaveKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, dur, out, t, c, frames);
+                     static_cast<hipStream_t>(stream), x, dur, out, t, c, frames, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

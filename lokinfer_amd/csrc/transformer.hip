@@ -18,6 +18,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "lokinfer_hip.h"
 
 namespace lkd {
 
@@ -96,7 +97,8 @@ template <bool CACHE>
 __global__ __launch_bounds__(256) void attnMfmaKernel(const float* __restrict__ qkv, const float* __restrict__ bias,
                                                       const float* __restrict__ kc, const float* __restrict__ vc,
                                                       const int64_t* __restrict__ pos, int64_t cap,
-                                                      float* __restrict__ out, int64_t t, int heads, int causal) {
+                                                      float* __restrict__ out, int64_t t, int heads, int causal,
+                                                      unsigned long long* err) {
   constexpr int HD = 64, KT = 32;
   __shared__ float mS[4][32], lS[4][32];
   __shared__ float oS[4][32][HD + 1];
@@ -230,22 +232,32 @@ __global__ __launch_bounds__(256) void attnMfmaKernel(const float* __restrict__ 
     for (int w = 0; w < 4; ++w) acc += sc[w] * oS[w][q][d];
     o[d] = noRow ? __builtin_nanf("") : CACHE ? acc * inv : acc * inv + bv[d];
   }
+  // recorded once, by the thread of head 0 that owns the first query without a cache row
+  if (noRow && d0 == 0 && h == 0 && qrow == (p0 < 0 ? 0 : cap - p0)) raiseDeviceError(err, LK_DEVERR_POSITION, p0 + qrow);
 }
 
+// a position outside [0, cap) writes nothing and is recorded in the GPU's error record
 __global__ void kvWriteKernel(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias,
-                              int64_t d) {
+                              int64_t d, int64_t cap, unsigned long long* err) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= d) return;
   const int64_t p = *pos;
+  if (p < 0 || p >= cap) {
+    if (i == 0) raiseDeviceError(err, LK_DEVERR_POSITION, p);
+    return;
+  }
   kc[p * d + i] = qkv[d + i] + bias[d + i];
   vc[p * d + i] = qkv[2 * d + i] + bias[2 * d + i];
 }
 
-// rows pos..pos+T-1 of the caches = k / v of qkv [T, 3D] + bias, float4 per thread; rows past cap are dropped
+// rows pos..pos+T-1 of the caches = k / v of qkv [T, 3D] + bias, float4 per thread; rows outside the cache are
+// dropped and recorded in the GPU's error record
 __global__ void kvWriteRowsKernel(float* __restrict__ kc, float* __restrict__ vc, const float* __restrict__ qkv,
                                   const int64_t* __restrict__ pos, const float* __restrict__ bias, int64_t t,
-                                  int64_t d, int64_t cap) {
+                                  int64_t d, int64_t cap, unsigned long long* err) {
   const int64_t p0 = *pos, d4 = d / 4, total = t * d4;
+  if ((p0 < 0 || p0 + t > cap) && blockIdx.x == 0 && threadIdx.x == 0)
+    raiseDeviceError(err, LK_DEVERR_POSITION, p0 < 0 ? p0 : p0 + t - 1);
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t r = i / d4, c = (i - r * d4) * 4, row = p0 + r;
@@ -298,7 +310,7 @@ int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, in
   if (t <= 0) return t == 0 ? 0 : 1;
   dim3 grid(lkh::ceilDiv(t, 32), static_cast<unsigned>(heads));
   hipLaunchKernelGGL(lkd::attnMfmaKernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), qkv, bias,
-                     nullptr, nullptr, nullptr, int64_t{0}, out, t, heads, causal);
+                     nullptr, nullptr, nullptr, int64_t{0}, out, t, heads, causal, nullptr);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -307,7 +319,7 @@ int lk_hip_attention_cache_f32(const float* qkv, const float* kc, const float* v
   if (t <= 0 || heads <= 0 || cap <= 0) return t == 0 ? 0 : 1;
   dim3 grid(lkh::ceilDiv(t, 32), static_cast<unsigned>(heads));
   hipLaunchKernelGGL(lkd::attnMfmaKernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), qkv, bias, kc,
-                     vc, pos, cap, out, t, heads, 1);
+                     vc, pos, cap, out, t, heads, 1, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -320,14 +332,15 @@ int lk_hip_kv_write_rows_f32(float* kc, float* vc, const float* qkv, const int64
     return 1;
   const int64_t blocks = std::min<int64_t>((total / 4 + 255) / 256, 4096);
   hipLaunchKernelGGL(lkd::kvWriteRowsKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), kc, vc, qkv, pos, bias, t, d, cap);
+                     static_cast<hipStream_t>(stream), kc, vc, qkv, pos, bias, t, d, cap, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 int lk_hip_kv_write_f32(float* kc, float* vc, const float* qkv, const int64_t* pos, const float* bias, int64_t d,
-                        void* stream) {
+                        int64_t cap, void* stream) {
+  if (d <= 0 || cap <= 0) return 1;
   hipLaunchKernelGGL(lkd::kvWriteKernel, dim3(lkh::ceilDiv(d, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), kc, vc, qkv, pos, bias, d);
+                     static_cast<hipStream_t>(stream), kc, vc, qkv, pos, bias, d, cap, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

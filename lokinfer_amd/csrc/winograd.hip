@@ -383,6 +383,7 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
                           int64_t workspace_bytes, void* stream) {
   const int a = tile == 2 ? 4 : kernel == 3 ? 6 : 7;
   if (ci % 16 != 0 || co % 64 != 0 || dilation < 1 || groups < 1 || groups > 3 || lo < 1) return 1;
+  if (v_rows % (static_cast<int64_t>(dilation) * a) != 0) return 1;  // V holds whole (residue, point) row blocks
   if ((tile == 2 && groups != 1) || (a == 6 && groups != 1) || (a == 7 && groups < 2)) return 1;
   const int64_t rmax = v_rows / (static_cast<int64_t>(dilation) * a);
   const int m = tile;
@@ -475,6 +476,10 @@ void runWinoMm(ExecCtx& ctx, const KernelArgs& a) {
   const int d = static_cast<int>(a.ints[at]), groups = static_cast<int>(a.ints[at + 1]);
   const int k = static_cast<int>(a.ints[at + 2]), tile = static_cast<int>(a.ints[at + 4]);
   LK_REQUIRE(ctx, a.ints[o + 1] == co && a.ints[3] == groups * ci, "wino_mm: u must be f32[A, N Ci, Co]");
+  const int64_t alpha = tile == 2 ? 4 : k == 3 ? 6 : 7;  // transform points of this kernel size and tile
+  LK_REQUIRE(ctx, a.ints[2] == alpha, "wino_mm: u's leading dim must be the transform's point count");
+  LK_REQUIRE(ctx, d >= 1 && vr % (static_cast<int64_t>(d) * alpha) == 0,
+             "wino_mm: v rows must be a multiple of dilation * points");
   const int outp = RES ? 6 : 5;
   const float scale = RES && a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1.0f;
   if (lk_hip_wino_mm_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), RES ? P<float>(a, 5) : nullptr,

@@ -225,7 +225,7 @@ def kv_write_f16_gpu(kc, vc, k, v, pos):
     check(tuple(kc.shape) == tuple(vc.shape) and tuple(k.shape) == tuple(v.shape) and k.shape[1] == kc.shape[1],
           "caches f16[cap, D], k / v f16[T, D]")
     check(kc.shape[1] % 8 == 0, "D must be a multiple of 8")
-    return _launch("kv_write_f16_gpu", [kc, vc, k, v, pos], [], outs=[])
+    return _launch("kv_write_f16_gpu", [kc, vc, k, v, pos], [], outs=[], inout=[0, 1])
 
 
 def _gqa_rule(q, kc, vc, pos, q_heads, kv_heads):
@@ -263,7 +263,7 @@ def qknorm_rope_kv_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, eps=1e-6, theta=1e6):
     dq = qkv.shape[1] - 2 * kc.shape[1]
     check(dq > 0 and dq % 128 == 0, "qkv must be f16[T, Dq + 2 Dk] with whole heads")
     return _launch("qknorm_rope_kv_opt_f16_gpu", [qkv, qg, kg, pos, kc, vc], [(qkv.shape[0], dq)],
-                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f16])
+                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f16], inout=[4, 5])
 
 
 # ---- decode-step fusions (MI355X backend) -------------------------------------------------------------------
@@ -283,7 +283,7 @@ def attention_decode_qkr_opt_f16_gpu(qkv, qg, kg, pos, kc, vc, counters, eps=1e-
     check(isinstance(counters, Tensor) and counters.dtype == i32 and tuple(counters.shape) == (dq // 128,),
           "counters must be i32[q heads]")
     return _launch("attention_decode_qkr_opt_f16_gpu", [qkv, qg, kg, pos, kc, vc, counters], [(1, dq)],
-                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f16])
+                   dict(eps=float(eps), theta=float(theta)), out_dtypes=[f16], inout=[4, 5, 6])
 
 
 def rmsnorm_lm_head_last_opt_f16_gpu(x, g, table, eps=1e-6):

@@ -27,7 +27,7 @@ import numpy as np
 import torch
 
 from . import ops
-from .compiler import compile as lk_compile
+from .compiler import capture as lk_capture
 from .tensor import Tensor, from_numpy
 
 N_LAYER, D, HEADS, N_POS, VOCAB, FFN = 12, 768, 12, 1024, 50257, 3072
@@ -69,7 +69,7 @@ class Gpt2Decoder:
         self.caches = [(Tensor(torch.zeros(N_POS, D, device=dev)), Tensor(torch.zeros(N_POS, D, device=dev)))
                        for _ in range(N_LAYER)]
         self.fused = fused
-        self.step_model = lk_compile(self._step, graph=graph)
+        self.step_model = lk_capture(self._step, graph=graph)
 
     def _step(self, tok: Tensor, pos: Tensor):
         w = self.w
@@ -138,7 +138,7 @@ class Gpt2Generator(Gpt2Decoder):
         self.sk = tuple(sk)
         dev = self.w["transformer.wte.weight"].t.device
         self.positions = torch.arange(N_POS, dtype=torch.int64, device=dev)  # device pos views, no host copies
-        self.chunk_model = lk_compile(self._chunk, graph=chunk_graph)
+        self.chunk_model = lk_capture(self._chunk, graph=chunk_graph)
 
     def _chunk(self, ids: Tensor, pos: Tensor):
         w = self.w

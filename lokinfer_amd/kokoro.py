@@ -31,7 +31,7 @@ import numpy as np
 import torch
 
 from . import ops, winograd
-from .compiler import compile as lk_compile
+from .compiler import capture as lk_capture
 from .runtime import GpuContext
 from .tensor import Tensor, from_numpy
 
@@ -71,7 +71,7 @@ class KokoroGpu:
         self.banks = {root: self._bank(root) for root in ("predictor", "decoder")}
         # side streams for the graph's concurrent branches (default priority)
         self.streams = [torch.cuda.Stream() for _ in range(4)]
-        self.model = lk_compile(self._forward, graph=graph)
+        self.model = lk_capture(self._forward, graph=graph)
         self.debug: dict | None = None  # set to {} to keep named intermediates (eager runs only)
 
     def _keep(self, name: str, t: Tensor) -> None:

@@ -7,13 +7,17 @@ launches the kernel on the current stream. Attributes are passed in attribute-na
 Python floats as floats (the reference ABI, include/lokinfer/runtime/kernel.h:3-11).
 
 Ops that are not in the reference are marked "(MI355X backend)" in their docstring.
+
+While `lk.compile` traces a function (lokinfer_amd.graph), the same ops record IR instead of launching: operands
+are traced values (or captured lk.Tensors), shapes may hold symbolic dims, and the result is a traced value.
 """
 from __future__ import annotations
 
 import torch
 
-from .runtime import GpuContext
 from . import winograd as _wino
+from .graph import TensorType, Value, current_graph
+from .runtime import GpuContext
 from .tensor import Tensor, f32, i64
 
 STAT_CHUNK = 128
@@ -30,6 +34,8 @@ def check(cond: bool, msg: str = "invalid operands") -> None:
 
 def _gpu(*xs: Tensor) -> None:
     for x in xs:
+        if isinstance(x, Value):
+            continue
         if not isinstance(x, Tensor):
             raise TypeError(f"expected lk.Tensor, got {type(x).__name__}")
         if x.device != "gpu":
@@ -44,9 +50,23 @@ def _f32(*xs: Tensor, rank: int | None = None) -> None:
 
 
 def _launch(name: str, operands: list[Tensor], out_shapes: list[tuple], attrs: dict | None = None,
-           out_dtypes: list | None = None, outs: list[Tensor] | None = None):
-    """Allocates outputs (unless given) and runs registry kernel `name` with the reference argument layout."""
+           out_dtypes: list | None = None, outs: list[Tensor] | None = None, inout: list[int] | None = None):
+    """Allocates outputs (unless given) and runs registry kernel `name` with the reference argument layout.
+    `inout`: operand indices the kernel writes in place (a KV cache), recorded as the kernel's `inout` attr when
+    tracing. While tracing, records the kernel and returns its traced results instead."""
     _gpu(*operands)
+    g = current_graph()
+    if g is not None:
+        if outs:
+            raise OpError(f"{name}: writing into a given output cannot be traced; use the op's result")
+        kattrs = dict(attrs or {})
+        if inout:
+            kattrs["inout"] = list(inout)
+        out_dtypes = out_dtypes or [f32] * len(out_shapes)
+        res = g.kernel(name, list(operands), kattrs, [TensorType(d, s) for s, d in zip(out_shapes, out_dtypes)])
+        if not res:
+            return None
+        return res[0] if len(res) == 1 else tuple(res)
     ctx = GpuContext.shared()
     if outs is None:
         out_dtypes = out_dtypes or [f32] * len(out_shapes)
@@ -75,21 +95,35 @@ def _launch(name: str, operands: list[Tensor], out_shapes: list[tuple], attrs: d
 # ---- device sync (reference ops/device.py:13-25; on discrete HBM these are real copies) ----------------------
 
 def to_gpu(x: Tensor) -> Tensor:
+    """Device boundary (reference ops/device.py:13-25). Traced: `sync cpu_to_gpu`, an alias on this runtime (all of
+    a model's memory is HBM); eager: a host-to-device copy."""
+    g = current_graph()
+    if g is not None:
+        return g.sync(x, "cpu_to_gpu")
     out = Tensor(x.t.to(GpuContext.shared().device, non_blocking=False))
     return out
 
 
 def to_cpu(x: Tensor) -> Tensor:
+    g = current_graph()
+    if g is not None:
+        return g.sync(x, "gpu_to_cpu")
     return Tensor(x.t.to("cpu"))
 
 
 def reshape(x: Tensor, shape) -> Tensor:
     """Zero-cost view with a new shape (same element count)."""
+    g = current_graph()
+    if g is not None:
+        return g.view(x, TensorType(x.dtype, shape), 0)
     return Tensor(x.t.view(*[int(s) for s in shape]))
 
 
 def view(x: Tensor, shape, offset: int = 0) -> Tensor:
     """Zero-cost view of `shape` starting `offset` elements into x (reference models/kokoro/model.py:109-114)."""
+    g = current_graph()
+    if g is not None:
+        return g.view(x, TensorType(x.dtype, shape), offset)
     n = 1
     for s in shape:
         n *= int(s)
@@ -431,7 +465,7 @@ def attention_decode_split_f32_gpu(qkv, kcache, vcache, pos, bias, heads, splits
     (reference ops/transformer.py:323-337). pos is a device i64[1]; the caller guarantees pos < cache rows."""
     s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
     return _launch("attention_decode_split_f32_gpu", [qkv, kcache, vcache, pos, bias], [s],
-                  dict(heads=int(heads), nsg=int(nsg), single=int(single), splits=int(splits)))
+                  dict(heads=int(heads), nsg=int(nsg), single=int(single), splits=int(splits)), inout=[1, 2])
 
 
 # ---- fused decode step (backend ops; they replace one layer's gemv4 / attention_decode_split /
@@ -505,7 +539,7 @@ def attention_decode_part_f32_gpu(qkv_part, kcache, vcache, pos, bias, heads):
     check(tuple(bias.shape) == (3 * d,), "bias must be f32[3D]")
     chunks = -(-kcache.shape[0] // 64)
     return _launch("attention_decode_part_f32_gpu", [qkv_part, kcache, vcache, pos, bias], [(heads, chunks, 66)],
-                   dict(heads=int(heads)))
+                   dict(heads=int(heads)), inout=[1, 2])
 
 
 def reduce_bias_res_ln2_f32_gpu(part, bias, res, gamma, beta, eps=1e-5):
@@ -521,7 +555,8 @@ def reduce_bias_res_ln2_f32_gpu(part, bias, res, gamma, beta, eps=1e-5):
 
 def attention_decode_kvw_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
     s = _decode_check(qkv, kcache, vcache, pos, bias, heads)
-    return _launch("attention_decode_kvw_f32_gpu", [qkv, kcache, vcache, pos, bias], [s], dict(heads=int(heads)))
+    return _launch("attention_decode_kvw_f32_gpu", [qkv, kcache, vcache, pos, bias], [s], dict(heads=int(heads)),
+                   inout=[1, 2])
 
 
 def attention_decode_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
@@ -531,7 +566,7 @@ def attention_decode_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
 
 def kv_write_f32_gpu(kcache, vcache, qkv, pos, bias):
     _decode_check(qkv, kcache, vcache, pos, bias, kcache.shape[1] // 64)
-    return _launch("kv_write_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[])
+    return _launch("kv_write_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[], inout=[0, 1])
 
 
 # ---- chunked prefill / generate (reference python/lokinfer/ops/transformer.py:220-282, 348-351, 441-517) ------
@@ -551,13 +586,15 @@ def kv_write_rows_f32_gpu(kcache, vcache, qkv, pos, bias):
     device i64[1]; rows at or past the cache's end are dropped (the reference reports an error on the host)."""
     _rows_check(kcache, vcache, qkv, pos, bias)
     check(kcache.shape[1] % 4 == 0, "D must be a multiple of 4")
-    return _launch("kv_write_rows_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[])
+    return _launch("kv_write_rows_f32_gpu", [kcache, vcache, qkv, pos, bias], [], outs=[], inout=[0, 1])
 
 
 def _cache_attn(name, qkv, kcache, vcache, pos, bias, heads, attrs):
     _rows_check(kcache, vcache, qkv, pos, bias)
     check(kcache.shape[1] == 64 * int(heads), "head_dim must be 64")
-    return _launch(name, [qkv, kcache, vcache, pos, bias], [(qkv.shape[0], kcache.shape[1])], attrs)
+    writes = name.startswith("attention_gen")  # the gen ops write the chunk's rows into the caches
+    return _launch(name, [qkv, kcache, vcache, pos, bias], [(qkv.shape[0], kcache.shape[1])], attrs,
+                   inout=[1, 2] if writes else None)
 
 
 def attention_cache_f32_gpu(qkv, kcache, vcache, pos, bias, heads):
@@ -850,10 +887,3 @@ def conv1d_1ch_f32_gpu(x, w, b, stride=1, padding=0, out=None):
         check(out.dtype == f32 and tuple(out.shape) == (lo,), "out must be f32[Lo]")
     return _launch("conv1d_1ch_f32_gpu", [x, w, b], [(lo,)], dict(padding=int(padding), stride=int(stride)),
                    outs=None if out is None else [out])
-
-
-def mfma_probe_f32_gpu(iters: int = 512, workgroups: int = 1024):
-    """(MI355X backend, measurement) register-only f32 MFMA loop: workgroups x 4 waves x iters x 8 x 4096 FLOPs."""
-    check(iters > 0 and workgroups > 0, "iters and workgroups must be positive")
-    return _launch("mfma_probe_f32_gpu", [], [(workgroups * 256,)], dict(iters=int(iters), workgroups=int(workgroups)))
-

@@ -27,7 +27,7 @@ import torch
 
 from . import ops
 from . import f16_gpu as F
-from .compiler import compile as lk_compile
+from .compiler import capture as lk_capture
 from .runtime import GpuContext
 from .tensor import Tensor, f16
 
@@ -125,7 +125,7 @@ class Qwen3Lm:
             self.layers.append(L)
         self.positions = torch.arange(1 << 16, dtype=torch.int64, device=dev)  # device pos views, no host copies
         self.counters = Tensor(torch.zeros(cfg.qh, dtype=torch.int32, device=dev))  # decode attention merge counters
-        self.model = lk_compile(self._fn, graph=graph, mutable=(3,))  # kv: the caller's cache, written in place
+        self.model = lk_capture(self._fn, graph=graph, mutable=(3,))  # kv: the caller's cache, written in place
 
     def kv_cache(self, capacity: int) -> Tensor:
         """A zeroed cache for `capacity` positions: f16[L, 2, capacity, kvh 128] on the device (reference kv_cache,

@@ -11,7 +11,7 @@ import ctypes as C
 
 import torch
 
-from ._lib import LokinferError, lib
+from ._lib import LokinferError, check_device_errors, lib
 
 WORKSPACE_BYTES = 64 << 20
 
@@ -95,4 +95,6 @@ class GpuContext:
 
 
 def synchronize() -> None:
+    """Waits for the GPU and raises LokinferError for a data error a kernel recorded (check_device_errors)."""
     torch.cuda.synchronize()
+    check_device_errors()

@@ -74,6 +74,12 @@ class Tensor:
         return self.t.data_ptr()
 
     def numpy(self) -> np.ndarray:
+        """Host copy. For a GPU tensor this is a synchronisation point: a data error a kernel recorded on the
+        device (lokinfer_amd._lib.check_device_errors) is raised here as LokinferError."""
+        if self.t.is_cuda:
+            from ._lib import check_device_errors
+
+            check_device_errors()
         return self.t.detach().cpu().numpy()
 
     def torch(self, device: str = "cpu") -> torch.Tensor:

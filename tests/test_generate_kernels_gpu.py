@@ -70,18 +70,26 @@ def test_attention_gen(gpu, pos, t):
 
 
 def test_rows_past_the_cache_are_dropped(gpu):
-    """pos + T > cap: the device cannot raise, so rows past the end are not written and their queries give NaN;
-    the rows that fit are exact."""
+    """pos + T > cap: rows past the end are not written and their queries give NaN, the rows that fit are exact,
+    and both kernels record LK_DEVERR_POSITION, raised at the next synchronisation (the reference's host kernel
+    reports "pos + T exceeds the cache")."""
+    from lokinfer_amd._lib import LokinferError, check_device_errors
+
     lk = gpu
     pos, t, fit = 1020, 8, 4
     kc, vc, qkv, bias = _case(t)
     KC, VC = G(lk, kc), G(lk, vc)
     P, Q, B = G(lk, [pos], np.int64), G(lk, qkv), G(lk, bias)
     lk.ops.kv_write_rows_f32_gpu(KC, VC, Q, P, B)
+    with pytest.raises(LokinferError, match="device error 2: a position is outside the KV cache.*detail 1027"):
+        check_device_errors()
     rk, rv = K.kv_write_rows(kc, vc, qkv[:fit], pos, bias)
     close(KC, rk, 1e-6)
     close(VC, rv, 1e-6)
-    got = lk.ops.attention_cache_f32_gpu(Q, KC, VC, P, B, HEADS).numpy()
+    out = lk.ops.attention_cache_f32_gpu(Q, KC, VC, P, B, HEADS)
+    with pytest.raises(LokinferError, match="device error 2"):
+        check_device_errors()
+    got = out.numpy()
     close(got[:fit], K.attention_cache(qkv[:fit], rk, rv, pos, bias, HEADS), 3e-5)
     assert np.isnan(got[fit:]).all()
 

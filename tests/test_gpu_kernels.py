@@ -289,7 +289,7 @@ def test_graph_replay_matches_eager(gpu):
 
     A, B, BI, W2 = G(lk, a), G(lk, b), G(lk, bias), G(lk, w2)
     e1, e2 = (t.numpy() for t in fn(A, B, BI, W2))
-    m = lk.compile(fn)
+    m = lk.capture(fn)
     for _ in range(3):
         g1, g2 = (t.numpy() for t in m(A, B, BI, W2))
         torch.cuda.synchronize()

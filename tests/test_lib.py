@@ -35,7 +35,7 @@ def test_registry_names_follow_the_device_convention():
 
 def test_every_python_op_kernel_is_registered():
     src = (ROOT / "lokinfer_amd" / "ops.py").read_text()
-    launched = set(re.findall(r'"(\w+_gpu(?:_mps)?)"', src))
+    launched = set(re.findall(r'_launch\(\s*f?"(\w+_gpu(?:_mps)?)"', src))
     names = set(lk.registered_kernels())
     assert launched <= names, sorted(launched - names)
 
@@ -56,3 +56,74 @@ def test_ops_reject_cpu_operands():
     x = lk.zeros(2, 2)
     with pytest.raises(ops.OpError):
         ops.add_f32_gpu(x, x)
+
+
+def test_device_error_messages_and_codes():
+    """Every code include/lokinfer_hip.h declares has its own message in the library (no GPU call)."""
+    text = (ROOT / "include" / "lokinfer_hip.h").read_text()
+    codes = dict((n, int(v)) for n, v in re.findall(r"\b(LK_DEVERR_\w+)\s*=\s*(\d+)", text))
+    assert sorted(codes.values()) == [1, 2, 3, 4, 5]
+    L = _lib.lib()
+    msgs = {c: L.lk_device_error_message(c).decode() for c in codes.values()}
+    assert len(set(msgs.values())) == len(msgs) and all("unknown" not in m for m in msgs.values())
+    assert L.lk_device_error_message(0).decode() == "no error"
+    assert "unknown" in L.lk_device_error_message(99).decode()
+
+
+def test_check_device_errors_raises_the_recorded_error(monkeypatch):
+    """check_device_errors turns the record lk_take_device_error returns into LokinferError with the message and
+    detail, and returns quietly for code 0 (the library is replaced by a stand-in that returns fixed records)."""
+    import ctypes as C
+
+    import pytest
+
+    real = _lib.lib()
+
+    class Fake:
+        def __init__(self, code, detail):
+            self.code, self.detail = code, detail
+
+        def lk_take_device_error(self, p):
+            C.cast(p, C.POINTER(C.c_int64))[0] = self.detail
+            return self.code
+
+        def lk_device_error_message(self, code):
+            return real.lk_device_error_message(code)
+
+    monkeypatch.setattr(_lib, "lib", lambda: Fake(0, 0))
+    _lib.check_device_errors()
+    monkeypatch.setattr(_lib, "lib", lambda: Fake(1, 77))
+    with pytest.raises(_lib.LokinferError, match=r"device error 1: a persistent kernel.*timed out.*detail 77"):
+        _lib.check_device_errors()
+    monkeypatch.setattr(_lib, "lib", lambda: Fake(-1, 0))
+    with pytest.raises(_lib.LokinferError, match="could not read"):
+        _lib.check_device_errors()
+
+
+def test_registry_rejects_bad_shapes_before_any_launch():
+    """Shape checks run on the host before a launch (null device pointers, no GPU needed): a U whose point count
+    does not match the kernel size, V rows that are not whole (residue, point) blocks, and a short ints array
+    (read as zeros, never past its end)."""
+    import ctypes as C
+
+    L = _lib.lib()
+    k = L.lk_find_kernel(b"wino_mm_lc_f32_gpu")
+    nop, nout = C.c_int(), C.c_int()
+    L.lk_kernel_arity(k, C.byref(nop), C.byref(nout))
+    n = nop.value + nout.value
+    ptrs = (C.c_void_p * n)()
+
+    def run(ints):
+        arr = (C.c_int64 * len(ints))(*ints)
+        return L.lk_run_kernel(k, ptrs, n, arr, len(ints), None, 0, None, 0, None), L.lk_last_error().decode()
+
+    # v [rows, Ci], u [A, Ci, Co], b [Co], tr [n], x [L, Ci], out [Lo, Co]; attrs dilation, groups, kernel, padding,
+    # tile (K = 3, tile 4: A = 6)
+    v_rows, ci, co, lo = 6 * 130, 64, 64, 500
+    good = [v_rows, ci, 6, ci, co, co, 60, lo, ci, lo, co, 1, 1, 3, 1, 4]
+    rc, msg = run([v_rows, ci, 7] + good[3:])
+    assert rc == 1 and "point count" in msg
+    rc, msg = run([v_rows + 1, ci] + good[2:])
+    assert rc == 1 and "multiple of dilation" in msg
+    rc, msg = run(good[:5])
+    assert rc == 1 and "wino_mm" in msg

@@ -15,6 +15,8 @@ import numpy as np
 import pytest
 import torch
 
+from lokinfer_amd._lib import LokinferError, check_device_errors
+
 from oracle import qwen3 as Q
 
 pytestmark = pytest.mark.gpu
@@ -192,11 +194,15 @@ def test_rows_past_the_cache(gpu):
     k, v = h16(t, 1024), h16(t, 1024)
     kc, vc = G(lk, np.zeros((cap, 1024), np.float16)), G(lk, np.zeros((cap, 1024), np.float16))
     F.kv_write_f16_gpu(kc, vc, G(lk, k), G(lk, v), P(lk, pos))
+    check_device_errors()  # the cache write drops the rows past the end without recording an error
     np.testing.assert_array_equal(kc.numpy()[pos:], k[:cap - pos])
     np.testing.assert_array_equal(vc.numpy()[pos:], v[:cap - pos])
     assert not kc.numpy()[:pos].any()
     q = h16(t, 2048)
-    got = F.attention_gqa_opt_f16_gpu(G(lk, q), kc, vc, P(lk, pos)).numpy().astype(np.float64)
+    out = F.attention_gqa_opt_f16_gpu(G(lk, q), kc, vc, P(lk, pos))
+    with pytest.raises(LokinferError, match="device error 2.*detail 64"):  # the first query without a cache row
+        check_device_errors()
+    got = out.numpy().astype(np.float64)
     ref = X.attention_gqa(q[:cap - pos], kc.numpy(), vc.numpy(), pos, 16, 8)
     check(got[:cap - pos], ref, 2.0 ** -22 * (8 + 8) * np.abs(v).max(), "fitting rows")
     assert np.isnan(got[cap - pos:]).all()
@@ -214,9 +220,15 @@ def test_embedding_scatter_elementwise(gpu):
     np.testing.assert_array_equal(e.numpy(), tab[ids])
     s = F.scatter_audio_f16_gpu(e, I, G(lk, audio)).numpy()
     np.testing.assert_array_equal(s, O.scatter_audio(tab[ids], ids, audio).astype(np.float16))
-    s3 = F.scatter_audio_f16_gpu(e, I, G(lk, audio[:3])).numpy()  # a pad row without an audio row: NaN
+    s3 = F.scatter_audio_f16_gpu(e, I, G(lk, audio[:3]))  # a pad row without an audio row: NaN, and recorded
+    with pytest.raises(LokinferError, match="device error 5.*detail 49"):
+        check_device_errors()
+    s3 = s3.numpy()
     assert np.isnan(s3[49]).all() and np.array_equal(s3[:49], s[:49])
-    bad = F.embedding_f16_gpu(G(lk, np.array([5, -1, 151936], np.int64)), G(lk, tab)).numpy()
+    bad = F.embedding_f16_gpu(G(lk, np.array([5, -1, 151936], np.int64)), G(lk, tab))
+    with pytest.raises(LokinferError, match="device error 3"):
+        check_device_errors()
+    bad = bad.numpy()
     assert np.array_equal(bad[0], tab[5]) and np.isnan(bad[1:]).all()
     a, b = h16(33, 70, scale=4.0), h16(33, 70, scale=4.0)
     check(F.add_f16_gpu(G(lk, a), G(lk, b)), X.add(a, b), 2.0 ** -20 * np.abs(O.c(a) + O.c(b)), "add")
@@ -243,8 +255,12 @@ def test_decode_fusions_equal_compositions(gpu, pos, cap):
         Pp = P(lk, p)
         ka, va, kb, vb = G(lk, kc0), G(lk, vc0), G(lk, kc0), G(lk, vc0)
         q = F.qknorm_rope_kv_opt_f16_gpu(G(lk, qkv), G(lk, qg), G(lk, kg), Pp, ka, va)
-        ref = F.attention_gqa_opt_f16_gpu(q, ka, va, Pp).numpy()
-        got = F.attention_decode_qkr_opt_f16_gpu(G(lk, qkv), G(lk, qg), G(lk, kg), Pp, kb, vb, counters).numpy()
+        ref = F.attention_gqa_opt_f16_gpu(q, ka, va, Pp)
+        got = F.attention_decode_qkr_opt_f16_gpu(G(lk, qkv), G(lk, qg), G(lk, kg), Pp, kb, vb, counters)
+        if p < 0:  # an invalid position: NaN outputs and no cache write on both sides, recorded on the device
+            with pytest.raises(LokinferError, match="device error 2.*detail -1"):
+                check_device_errors()
+        ref, got = ref.numpy(), got.numpy()
         np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
         np.testing.assert_array_equal(kb.numpy().view(np.uint16), ka.numpy().view(np.uint16))
         np.testing.assert_array_equal(vb.numpy().view(np.uint16), va.numpy().view(np.uint16))
