@@ -1,0 +1,164 @@
+"""The compiled-model runtime on the GPU (lk.compile / lk.load / compile_ir over include/lokinfer_rt.h): traced
+models against the same ops run eagerly, bit for bit (same kernels, same order); .lkm save / load round trips;
+symbolic shapes bound per call (one captured hipGraph per binding); data-dependent shapes (dim.read); persistent
+state written in place; errors from kernels, shapes and the device error record."""
+import numpy as np
+import pytest
+import torch
+
+from lokinfer_amd._lib import LokinferError
+
+pytestmark = pytest.mark.gpu
+
+rng = np.random.default_rng(11)
+
+
+def G(lk, a, dt=np.float32):
+    return lk.from_numpy(np.ascontiguousarray(a, dt), device="gpu", copy=True)
+
+
+def mlp_params(lk):
+    from oracle import mnist
+
+    x, (w1, b1, w2, b2) = mnist.mlp_inputs(1)
+    return x, [G(lk, p) for p in (w1, b1, w2, b2)], (w1, b1, w2, b2)
+
+
+def test_mnist_mlp_compiled_equals_eager_and_oracle(gpu, tmp_path):
+    lk = gpu
+    from oracle import mnist
+
+    x, (W1, B1, W2, B2), params = mlp_params(lk)
+
+    def mlp(xx):
+        return lk.ops.gemm_bias_f32_gpu(lk.ops.gemm_bias_relu_f32_gpu(xx, W1, B1), W2, B2)
+
+    X = G(lk, x)
+    eager = mlp(X).numpy()
+    m = lk.compile(mlp, inputs=[X])
+    assert 'kernel "gemm_bias_relu_f32_gpu"' in m.source_ir and m.num_external_constants == 4
+    for _ in range(3):  # first call eager in the call block, later calls replay the captured graph
+        assert np.array_equal(m(X).numpy(), eager)
+    assert m.stats()["graphs"] == 1
+    ref = mnist.mlp_forward(x, params)
+    assert np.abs(eager - ref).max() <= 1e-4 * np.abs(ref).max()
+    path = tmp_path / "mlp.lkm"
+    m.save(path)
+    m2 = lk.load(path)
+    assert np.array_equal(m2(X).numpy(), eager)
+    assert 'const.internal @"ext0"' in m2.ir_text()
+
+
+def test_symbolic_rows_one_graph_per_binding(gpu):
+    lk = gpu
+    D = 256
+    gamma, beta = G(lk, 1 + 0.1 * rng.standard_normal(D)), G(lk, 0.1 * rng.standard_normal(D))
+    w = G(lk, rng.standard_normal((D, 3 * D)) / 16)
+
+    def f(x):
+        h = lk.ops.layernorm_f32_gpu(x, gamma, beta)
+        y = lk.ops.gemm_f32_gpu_mps(h, w)
+        return lk.ops.view(y, [x.shape[0], D], 0), y  # a view of the first D columns' worth of elements
+
+    T = lk.Sym("T")
+    m = lk.compile(f, input_types=[lk.TensorType(lk.f32, [T, D])])
+    assert "exec(%in0_1: buffer<f32[T, 256]>)" in m.ir_text()
+    for t in (5, 37, 5, 128):
+        X = G(lk, rng.standard_normal((t, D)))
+        v, y = m(X)
+        ye = lk.ops.gemm_f32_gpu_mps(lk.ops.layernorm_f32_gpu(X, gamma, beta), w).numpy()
+        assert y.shape == (t, 3 * D) and np.array_equal(y.numpy(), ye)
+        assert np.array_equal(v.numpy(), ye.reshape(-1)[: t * D].reshape(t, D))
+    assert m.stats()["graphs"] == 3
+
+
+def test_data_dependent_shape_dim_read(gpu):
+    """F = argmax of a row (read on the host with dim.read), then a GEMM over the first F rows: an eager call
+    whose shapes are bound mid-call."""
+    lk = gpu
+    w = G(lk, rng.standard_normal((64, 32)))
+
+    def f(scores, rows):
+        idx = lk.ops.argmax_f32_gpu(scores)  # i64[1]
+        F = lk.graph.current_graph().dim_read(lk.ops.to_cpu(idx), 0, "F")
+        head = lk.ops.view(rows, [F, 64], 0)
+        return lk.ops.gemm_f32_gpu_mps(head, w)
+
+    m = lk.compile(f, input_types=[lk.TensorType(lk.f32, [1, 100]), lk.TensorType(lk.f32, [100, 64])])
+    assert "dim.read" in m.ir_text()
+    for k in (7, 63, 1):
+        s = np.zeros((1, 100), np.float32)
+        s[0, k] = 1
+        rows = rng.standard_normal((100, 64)).astype(np.float32)
+        got = m(G(lk, s), G(lk, rows)).numpy()
+        assert got.shape == (k, 32)
+        assert np.array_equal(got, lk.ops.gemm_f32_gpu_mps(G(lk, rows[:k]), w).numpy())
+    assert m.stats()["graphs"] == 0
+
+
+def test_persistent_kv_cache_written_in_place(gpu):
+    """A decode step over persistent caches (model state, hoisted into init, zeroed at create) equals the same
+    ops over caller caches, step after step."""
+    lk = gpu
+    from lokinfer_amd.graph import TensorType
+
+    heads, cap, D = 4, 64, 256
+    bias = G(lk, 0.1 * rng.standard_normal(3 * D))
+
+    def step(qkv, pos):
+        g = lk.graph.current_graph()
+        kc = g.persistent(TensorType(lk.f32, [cap, D]))
+        vc = g.persistent(TensorType(lk.f32, [cap, D]))
+        return lk.ops.attention_decode_f32_gpu(qkv, kc, vc, pos, bias, heads)
+
+    m = lk.compile(step, input_types=[TensorType(lk.f32, [1, 3 * D]), TensorType(lk.i64, [1])])
+    assert "persistent = true" in m.ir_text()
+    KC, VC = G(lk, np.zeros((cap, D))), G(lk, np.zeros((cap, D)))
+    for p in range(6):
+        q = G(lk, rng.standard_normal((1, 3 * D)))
+        P = G(lk, [p], np.int64)
+        got = m(q, P).numpy()
+        want = lk.ops.attention_decode_f32_gpu(q, KC, VC, P, bias, heads).numpy()
+        assert np.array_equal(got, want)
+
+
+def test_runtime_errors(gpu):
+    lk = gpu
+    ir = """model {
+  init {
+    return
+  }
+  exec(%a: tensor<f32[4, 8]>, %b: tensor<f32[9, 4]>) {
+    %c = kernel "gemm_f32_gpu_mps"(%a, %b) : tensor<f32[4, 4]>
+    return %c
+  }
+}
+"""
+    m = lk.compile_ir(ir)
+    with pytest.raises(LokinferError, match="gemm"):  # the kernel's own shape check, as a call error
+        m(G(lk, np.zeros((4, 8))), G(lk, np.zeros((9, 4))))
+    with pytest.raises(LokinferError, match="dim 0"):
+        m(G(lk, np.zeros((5, 8))), G(lk, np.zeros((9, 4))))
+    with pytest.raises(LokinferError, match="unknown kernel"):
+        lk.compile_ir(ir.replace("gemm_f32_gpu_mps", "nope_f32_gpu"))
+    with pytest.raises(LokinferError, match="host kernel"):
+        lk.compile_ir(ir.replace("gemm_f32_gpu_mps", "gemm_f32_cpu"))
+
+
+def test_device_error_surfaces_at_a_synchronised_call(gpu):
+    lk = gpu
+    heads, cap, D = 2, 16, 128
+    bias = G(lk, np.zeros(3 * D))
+
+    def step(q, p):
+        g = lk.graph.current_graph()
+        kc, vc = (g.persistent(lk.TensorType(lk.f32, [cap, D])) for _ in range(2))
+        return lk.ops.attention_decode_f32_gpu(q, kc, vc, p, bias, heads)
+
+    m = lk.compile(step, input_types=[lk.TensorType(lk.f32, [1, 3 * D]), lk.TensorType(lk.i64, [1])])
+    exe = m._exe
+    q = G(lk, rng.standard_normal((1, 3 * D)))
+    exe.run([q, G(lk, [3], np.int64)], sync=True)
+    with pytest.raises(LokinferError, match="device error 2.*detail 16"):
+        exe.run([q, G(lk, [cap], np.int64)], sync=True)
+    exe.run([q, G(lk, [4], np.int64)], sync=True)  # the record was cleared
