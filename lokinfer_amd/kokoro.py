@@ -64,7 +64,16 @@ def _vec_pad(a: np.ndarray, n: int) -> np.ndarray:
 
 
 class KokoroGpu:
-    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True):
+    """The Kokoro forward on the GPU. runtime="capture" replays a torch stream capture of the function with its
+    concurrent side-stream branches; runtime="compiled" traces it into the runtime's IR (lk.compile) per (T, F)
+    signature and runs it from the C++ executable on one stream (save() writes that model as a .lkm). The conv
+    dispatch (Winograd or tap conv) depends on the lengths, so the traced model is specialized per signature."""
+
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, runtime: str = "capture"):
+        if runtime not in ("capture", "compiled"):
+            raise ValueError("runtime must be 'capture' or 'compiled'")
+        self.runtime = runtime
+        self._compiled: dict[tuple, object] = {}
         self.sd = sd
         self._g: dict[str, Tensor] = {}
         self._per_t: dict[tuple, Tensor] = {}
@@ -325,12 +334,11 @@ class KokoroGpu:
         ctx.join(self.streams[1])
         ctx.join(self.streams[0])
         # decoder
-        fn_cf = Tensor(torch.empty((2, frames), dtype=torch.float32, device=asr.t.device))
-        ops.conv1d_1ch_f32_gpu(f0, self.g("decoder.F0_conv.weight", _flat), self.g("decoder.F0_conv.bias"), stride=2,
-                               padding=1, out=ops.view(fn_cf, [frames], 0))
-        ops.conv1d_1ch_f32_gpu(n_curve, self.g("decoder.N_conv.weight", _flat), self.g("decoder.N_conv.bias"),
-                               stride=2, padding=1, out=ops.view(fn_cf, [frames], frames))
-        fn_lc = ops.transpose_f32_gpu(fn_cf)  # [F, 2]
+        f0d = ops.conv1d_1ch_f32_gpu(f0, self.g("decoder.F0_conv.weight", _flat), self.g("decoder.F0_conv.bias"),
+                                     stride=2, padding=1)
+        nd = ops.conv1d_1ch_f32_gpu(n_curve, self.g("decoder.N_conv.weight", _flat), self.g("decoder.N_conv.bias"),
+                                    stride=2, padding=1)
+        fn_lc = ops.concat_pad_lc_f32_gpu(ops.reshape(f0d, [frames, 1]), ops.reshape(nd, [frames, 1]), cout=2)  # [F, 2]
         asr_res = ops.conv1d_lc_f32_gpu(asr, self.g("decoder.asr_res.0.weight", _w_lc), self.g("decoder.asr_res.0.bias"))
         extra = ops.concat_pad_lc_f32_gpu(asr_res, fn_lc, cout=66)  # [F, 66]
         x = self.resblk(ops.concat_pad_lc_f32_gpu(asr, fn_lc), bank_d, "decoder.encode", 514, 1024, False)
@@ -374,7 +382,19 @@ class KokoroGpu:
             raise ValueError(f"durations sum to {int(dur_h.sum())} frames but the noise holds {noise_rows / 600} frames")
         args = [a if isinstance(a, Tensor) else from_numpy(np.ascontiguousarray(a), device="gpu", copy=True)
                 for a in (ids, ref_s, dur, noise)]
-        return self.model.run_inplace(*args) if inplace else self.model(*args)
+        m = self.model if self.runtime == "capture" else self.compiled(args)
+        return m.run_inplace(*args) if inplace else m(*args)
+
+    def compiled(self, args):
+        """The traced, compiled model of this input signature (built on first use)."""
+        from .compiler import compile as lk_compile
+
+        key = tuple(tuple(a.shape) for a in args)
+        m = self._compiled.get(key)
+        if m is None:
+            m = lk_compile(self._forward, inputs=list(args))
+            self._compiled[key] = m
+        return m
 
 
 def _t(a):

@@ -90,3 +90,28 @@ def test_duration_mismatch_is_an_error(model):
     ids, ref_s, dur, noise = KW.inputs(12)
     with pytest.raises(ValueError):
         m.forward(ids, ref_s, dur + 1, noise)
+
+
+def test_compiled_runtime_equals_capture(model, tmp_path):
+    """The forward traced into the runtime's IR and run by the C++ executable (one stream, one arena) gives the
+    capture path's outputs bit for bit (the same kernels in a different interleaving); its .lkm loads and runs
+    to the same bits."""
+    lk, KW, sd, m = model
+    from lokinfer_amd.kokoro import KokoroGpu
+
+    ids, ref_s, dur, noise = KW.inputs(59)
+    want = [t.numpy() for t in m.forward(ids, ref_s, dur, noise)]
+    c = KokoroGpu(sd, runtime="compiled")
+    for _ in range(2):  # the first call runs eagerly in the call block, the second replays its hipGraph
+        got = [t.numpy() for t in c.forward(ids, ref_s, dur, noise)]
+        for g, w in zip(got, want):
+            assert np.array_equal(g, w)
+    cm = next(iter(c._compiled.values()))
+    assert cm.stats()["graphs"] == 1
+    path = tmp_path / "kokoro59.lkm"
+    cm.save(path)
+    loaded = lk.load(path)
+    args = [lk.from_numpy(np.ascontiguousarray(a), device="gpu", copy=True) for a in (ids, ref_s, dur, noise)]
+    got = [t.numpy() for t in loaded(*args)]
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
