@@ -56,15 +56,16 @@ char* lk_dim_canonical(const char* text);
  * create: the model must be in buffer form (after bufferize). Externals are bound by name: device pointers
  * (on_device != 0, borrowed: they must outlive the executable) or host bytes (uploaded once). Uploads every
  * constant into one device arena and runs init on `stream`. flags: bit 0 = capture statically shaped calls into
- * hipGraphs. The executable keeps the model alive. */
+ * hipGraphs; bits 8-11 = the most HIP streams a statically shaped call may use (0 or 1: one stream). Kernels are
+ * assigned to streams from their data dependencies. The executable keeps the model alive. */
 lk_exe* lk_exe_create(lk_model* m, int n_ext, const char* const* names, void* const* ptrs, const uint64_t* sizes,
                       const int* on_device, void* stream, int flags);
 /* run: enqueues one call on `stream`; outputs point into memory the executable owns, valid until its next call.
  * flags: bit 0 = synchronize and report device-side data errors. Calls of one executable must be stream-ordered. */
 int lk_exe_run(lk_exe* e, int n_in, const lk_tensor* inputs, int max_out, lk_tensor* outputs, int* n_out,
                void* stream, int flags);
-/* model arena bytes, call arena bytes, captured graphs */
-int lk_exe_stats(const lk_exe* e, uint64_t* model_bytes, uint64_t* call_bytes, int* graphs);
+/* model arena bytes (incl. the re-placed temporaries), call arena bytes, captured graphs, streams in use */
+int lk_exe_stats(const lk_exe* e, uint64_t* model_bytes, uint64_t* call_bytes, int* graphs, int* streams);
 void lk_exe_free(lk_exe* e);
 
 #ifdef __cplusplus

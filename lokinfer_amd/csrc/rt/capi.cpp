@@ -175,7 +175,9 @@ lk_exe* lk_exe_create(lk_model* m, int n_ext, const char* const* names, void* co
   std::vector<lkrt::ExternalPtr> ext;
   for (int i = 0; i < n_ext; ++i) ext.push_back({names[i], ptrs[i], sizes[i], on_device[i] != 0});
   lkrt::Status st;
-  auto e = lkrt::Executable::create(m->m, ext, static_cast<hipStream_t>(stream), (flags & 1) != 0, st);
+  const int streams = (flags >> 8) & 0xf;
+  auto e = lkrt::Executable::create(m->m, ext, static_cast<hipStream_t>(stream), (flags & 1) != 0, st,
+                                    streams ? streams : 1);
   if (!e) return failNull<lk_exe>(st);
   auto* w = new lk_exe;
   w->e = std::move(e);
@@ -207,8 +209,9 @@ int lk_exe_run(lk_exe* e, int n_in, const lk_tensor* inputs, int max_out, lk_ten
   return 0;
 }
 
-int lk_exe_stats(const lk_exe* e, uint64_t* model_bytes, uint64_t* call_bytes, int* graphs) {
+int lk_exe_stats(const lk_exe* e, uint64_t* model_bytes, uint64_t* call_bytes, int* graphs, int* streams) {
   if (!e) return fail(lkrt::Status::error("null executable"));
+  if (streams) *streams = e->e->streamsUsed();
   if (model_bytes) *model_bytes = e->e->modelArenaBytes();
   if (call_bytes) *call_bytes = e->e->callArenaBytes();
   if (graphs) *graphs = e->e->graphsCaptured();

@@ -5,6 +5,7 @@
 #include "executable.h"
 
 #include <algorithm>
+#include <array>
 #include <climits>
 #include <cstring>
 
@@ -47,6 +48,9 @@ struct Executable::Instr {
   std::vector<double> floats;
   mutable std::vector<void*> ptrBuf;
   mutable std::vector<int64_t> intBuf;
+  int stream = 0;          // 0: the call's stream, k: side stream k
+  std::vector<int> waits;  // instructions on other streams this one waits for (their events)
+  int event = -1;          // recorded after this kernel when another stream waits for it
 };
 
 Executable::Memory::~Memory() {
@@ -59,6 +63,8 @@ Executable::~Executable() {
     if (g->graph) (void)hipGraphDestroy(g->graph);
   }
   if (captureStream_) (void)hipStreamDestroy(captureStream_);
+  for (hipStream_t h : side_) (void)hipStreamDestroy(h);
+  for (hipEvent_t e : events_) (void)hipEventDestroy(e);
   if (pinned_) (void)hipHostFree(pinned_);
 }
 
@@ -250,6 +256,14 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
                              Bump& mem, hipStream_t s, std::vector<TensorOut>* outs) {
   const Model& m = *model_;
   const DimPool& dp = m.dims();
+  // streams: 0 is the call's; a side stream first waits for the call's work so far (fork) and the call's stream
+  // waits for every side stream at the end (join); events_[0] is the fork, events_[1 .. S-1] the joins
+  const bool multi = &code == &exec_ && numStreams_ > 1;
+  std::vector<uint8_t> forked(static_cast<size_t>(numStreams_), 0);
+  if (multi) LKRT_TRY(hipStatus(hipEventRecord(events_[0], s), "fork"));
+  auto streamOf = [&](const Instr& in) -> hipStream_t {
+    return in.stream == 0 || !multi ? s : side_[static_cast<size_t>(in.stream - 1)];
+  };
   auto eval = [&](Dim d, int64_t& v) -> bool {
     auto r = dp.eval(d, sv, kUnbound);
     if (!r) return false;
@@ -283,12 +297,20 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
         lkh::KernelArgs a{in.ptrBuf.data(), nullptr, in.intBuf.data(), in.floats.data(), nullptr,
                           static_cast<uint32_t>(in.ptrBuf.size()), static_cast<uint32_t>(in.intBuf.size()),
                           static_cast<uint32_t>(in.floats.size())};
+        hipStream_t ks = streamOf(in);
+        if (multi && in.stream > 0 && !forked[static_cast<size_t>(in.stream)]) {
+          LKRT_TRY(hipStatus(hipStreamWaitEvent(ks, events_[0], 0), "fork"));
+          forked[static_cast<size_t>(in.stream)] = 1;
+        }
+        if (multi)
+          for (int w : in.waits) LKRT_TRY(hipStatus(hipStreamWaitEvent(ks, events_[exec_[w].event], 0), "wait"));
         lkh::ExecCtx ctx;
-        ctx.stream = s;
-        ctx.workspace = workspace_;
+        ctx.stream = ks;
+        ctx.workspace = workspace_[multi ? static_cast<size_t>(in.stream) : 0];
         ctx.workspaceBytes = workspaceBytes_;
         in.kernel->run(ctx, a);
         if (ctx.error) return Status::error("kernel '" + op.name + "': " + ctx.error);
+        if (multi && in.event >= 0) LKRT_TRY(hipStatus(hipEventRecord(events_[in.event], ks), "record"));
         break;
       }
       case OpKind::View: {
@@ -305,7 +327,7 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
       }
       case OpKind::BufferAlloc: {
         const ValueId v = op.results[0];
-        if (fixed_[v]) {
+        if (fixed_[v] || skipAlloc_[v]) {  // model memory, or an arena whose temporaries were re-placed
           slot[v] = fixed_[v];
           break;
         }
@@ -364,6 +386,12 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
       case OpKind::BufferFree:
         break;
       case OpKind::Return:
+        if (multi)
+          for (int k = 1; k < numStreams_; ++k)
+            if (forked[static_cast<size_t>(k)]) {
+              LKRT_TRY(hipStatus(hipEventRecord(events_[static_cast<size_t>(k)], side_[static_cast<size_t>(k - 1)]), "join"));
+              LKRT_TRY(hipStatus(hipStreamWaitEvent(s, events_[static_cast<size_t>(k)], 0), "join"));
+            }
         if (outs) {
           outs->clear();
           for (ValueId v : op.operands) {
@@ -414,8 +442,200 @@ Status Executable::callBytes(std::vector<int64_t> sv, size_t& bytes) const {
   return Status();
 }
 
+// Stream schedule of a statically shaped exec region, and the re-placement of its per-call temporaries.
+//
+// Dependencies are per memory root (a value, seen through views and syncs): a kernel depends on the last writer of
+// every root it reads or writes and, for the roots it writes, on their readers since that write. In program order,
+// a kernel continues the stream whose last kernel is its latest predecessor; if no predecessor ends a stream it
+// takes an unused stream, else the stream whose last kernel is oldest. A dependency on another stream becomes an
+// event wait unless the vector clock of the waiting stream already covers it; the vector clocks then give
+// happens-before between any two kernels.
+//
+// The temporaries plan-memory put in a static arena (hoisted to init, reaching exec as state) were placed for one
+// stream. They are placed again here, largest first at the lowest fitting offset, where two of them conflict unless
+// every kernel touching one happens before the first kernel touching the other: concurrent branches never share
+// bytes, and the schedule needs no extra edges.
+Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
+  const Model& m = *model_;
+  const Region& ex = m.exec;
+  const size_t nv = m.numValues();
+  const int S = std::max(1, std::min(maxStreams, 8));
+  relocOffset_.assign(nv, -1);
+  skipAlloc_.assign(nv, 0);
+
+  // relocatable temporaries: exec state whose init value is a view of an init arena no init kernel touches
+  std::vector<ValueId> iroot(nv, kNoValue);
+  auto irootOf = [&](ValueId v) { return iroot[v] == kNoValue ? v : iroot[v]; };
+  std::vector<uint8_t> arena(nv, 0);
+  for (const Op& op : m.init.ops) {
+    if ((op.kind == OpKind::View || op.kind == OpKind::Sync) && !op.results.empty())
+      iroot[op.results[0]] = irootOf(op.operands[0]);
+    if (op.kind == OpKind::BufferAlloc && op.flag("arena")) arena[op.results[0]] = 1;
+  }
+  for (const Op& op : m.init.ops)
+    if (op.kind == OpKind::Kernel)
+      for (const auto* vs : {&op.operands, &op.outs})
+        for (ValueId v : *vs) arena[irootOf(v)] = 0;
+  const Op& initRet = m.init.ops.back();
+  std::vector<uint8_t> reloc(nv, 0);
+  for (size_t i = 0; i < ex.state.size(); ++i)
+    if (arena[irootOf(initRet.operands[i])]) reloc[ex.state[i]] = 1;
+  for (const Op& op : m.init.ops)
+    if (op.kind == OpKind::BufferAlloc && arena[op.results[0]]) skipAlloc_[op.results[0]] = 1;
+
+  // dependencies between exec kernels
+  std::vector<ValueId> root(nv, kNoValue);
+  auto rootOf = [&](ValueId v) { return root[v] == kNoValue ? v : root[v]; };
+  std::vector<int> lastWriter(nv, -1);
+  std::vector<std::vector<int>> readers(nv);
+  std::vector<std::vector<int>> preds(exec_.size());
+  std::vector<std::vector<int>> touching(nv);  // kernels touching each root
+  for (size_t j = 0; j < exec_.size(); ++j) {
+    const Op& op = *exec_[j].op;
+    if ((op.kind == OpKind::View || op.kind == OpKind::Sync) && !op.results.empty()) {
+      root[op.results[0]] = rootOf(op.operands[0]);
+      continue;
+    }
+    if (op.kind != OpKind::Kernel) continue;
+    std::vector<uint8_t> isInout(op.operands.size(), 0);
+    if (const AttrValue* io = op.attr("inout"))
+      if (const Ints* idx = std::get_if<Ints>(io))
+        for (int64_t k : *idx)
+          if (k >= 0 && static_cast<size_t>(k) < isInout.size()) isInout[static_cast<size_t>(k)] = 1;
+    std::vector<ValueId> rd, wr;
+    for (size_t k = 0; k < op.operands.size(); ++k) {
+      if (m.typeOf(op.operands[k])->isScalar()) continue;
+      (isInout[k] ? wr : rd).push_back(rootOf(op.operands[k]));
+    }
+    for (ValueId v : op.outs) wr.push_back(rootOf(v));
+    std::vector<int>& P = preds[j];
+    for (ValueId r : rd)
+      if (lastWriter[r] >= 0) P.push_back(lastWriter[r]);
+    for (ValueId w : wr) {
+      if (lastWriter[w] >= 0) P.push_back(lastWriter[w]);
+      P.insert(P.end(), readers[w].begin(), readers[w].end());
+    }
+    std::sort(P.begin(), P.end());
+    P.erase(std::unique(P.begin(), P.end()), P.end());
+    P.erase(std::remove(P.begin(), P.end(), static_cast<int>(j)), P.end());
+    for (ValueId r : rd) {
+      readers[r].push_back(static_cast<int>(j));
+      touching[r].push_back(static_cast<int>(j));
+    }
+    for (ValueId w : wr) {
+      lastWriter[w] = static_cast<int>(j);
+      readers[w].clear();
+      touching[w].push_back(static_cast<int>(j));
+    }
+  }
+
+  // streams and vector clocks
+  std::vector<std::array<int, 8>> vc(exec_.size());
+  std::vector<int> pos(exec_.size(), 0), tail(static_cast<size_t>(S), -1), count(static_cast<size_t>(S), 0);
+  int nextEvent = S;  // events 0 .. S-1: fork and joins
+  for (size_t j = 0; j < exec_.size(); ++j) {
+    Instr& in = exec_[j];
+    if (in.kind != OpKind::Kernel) continue;
+    const std::vector<int>& P = preds[j];
+    int best = -1;
+    for (int p : P)
+      if (tail[static_cast<size_t>(exec_[p].stream)] == p && p > best) best = p;
+    int st = 0;
+    if (best >= 0) {
+      st = exec_[best].stream;
+    } else {
+      int unused = -1, oldest = 0;
+      for (int k = 0; k < S; ++k) {
+        if (count[static_cast<size_t>(k)] == 0) {
+          unused = k;
+          break;
+        }
+        if (tail[static_cast<size_t>(k)] < tail[static_cast<size_t>(oldest)]) oldest = k;
+      }
+      st = j == 0 || tail[0] < 0 ? 0 : unused >= 0 ? unused : oldest;
+    }
+    std::array<int, 8> cur{};
+    if (tail[static_cast<size_t>(st)] >= 0) cur = vc[static_cast<size_t>(tail[static_cast<size_t>(st)])];
+    for (auto it = P.rbegin(); it != P.rend(); ++it) {  // latest first: its clock may cover the older ones
+      const int p = *it, sp = exec_[p].stream;
+      if (sp == st || cur[static_cast<size_t>(sp)] >= pos[static_cast<size_t>(p)]) continue;
+      in.waits.push_back(p);
+      if (exec_[p].event < 0) exec_[p].event = nextEvent++;
+      for (int k = 0; k < 8; ++k) cur[static_cast<size_t>(k)] = std::max(cur[static_cast<size_t>(k)], vc[static_cast<size_t>(p)][static_cast<size_t>(k)]);
+    }
+    in.stream = st;
+    pos[j] = ++count[static_cast<size_t>(st)];
+    cur[static_cast<size_t>(st)] = pos[j];
+    vc[j] = cur;
+    tail[static_cast<size_t>(st)] = static_cast<int>(j);
+  }
+  numStreams_ = 1;
+  for (int k = 0; k < S; ++k)
+    if (count[static_cast<size_t>(k)] > 0) numStreams_ = std::max(numStreams_, k + 1);
+  auto hb = [&](int a, int b) {  // kernel a happens before kernel b
+    return a == b || vc[static_cast<size_t>(b)][static_cast<size_t>(exec_[a].stream)] >= pos[static_cast<size_t>(a)];
+  };
+
+  // re-place the temporaries
+  struct Tmp {
+    ValueId v;
+    size_t bytes;
+    const std::vector<int>* users;
+  };
+  std::vector<Tmp> tmps;
+  for (ValueId v = 0; v < nv; ++v) {
+    if (!reloc[v]) continue;
+    size_t n = dtypeSize(m.typeOf(v)->dtype);
+    for (Dim d : m.typeOf(v)->shape) n *= static_cast<size_t>(d->value);
+    tmps.push_back({v, alignUp(std::max<size_t>(n, 1)), &touching[v]});
+  }
+  std::stable_sort(tmps.begin(), tmps.end(), [](const Tmp& a, const Tmp& b) { return a.bytes > b.bytes; });
+  auto before = [&](const Tmp& a, const Tmp& b) {  // every use of a happens before b's first use
+    if (a.users->empty() || b.users->empty()) return true;
+    const int first = b.users->front();
+    for (int u : *a.users)
+      if (!hb(u, first) || u == first) return false;
+    return true;
+  };
+  struct Placed {
+    size_t off, size, idx;
+  };
+  std::vector<Placed> placed;  // by offset
+  size_t total = 0;
+  for (size_t i = 0; i < tmps.size(); ++i) {
+    size_t best = SIZE_MAX, bestGap = SIZE_MAX, cursor = 0;
+    for (const Placed& p : placed) {
+      if (before(tmps[p.idx], tmps[i]) || before(tmps[i], tmps[p.idx])) continue;
+      if (p.off >= cursor) {
+        const size_t gap = p.off - cursor;
+        if (gap >= tmps[i].bytes && gap < bestGap) {
+          best = cursor;
+          bestGap = gap;
+        }
+      }
+      cursor = std::max(cursor, p.off + p.size);
+    }
+    if (best == SIZE_MAX) best = cursor;
+    relocOffset_[tmps[i].v] = static_cast<int64_t>(best);
+    total = std::max(total, best + tmps[i].bytes);
+    const Placed np{best, tmps[i].bytes, i};
+    placed.insert(std::upper_bound(placed.begin(), placed.end(), np,
+                                   [](const Placed& x, const Placed& y) { return x.off < y.off; }),
+                  np);
+  }
+  tempsBytes_ = total;
+  events_.assign(static_cast<size_t>(nextEvent), nullptr);
+  for (hipEvent_t& e : events_) LKRT_TRY(hipStatus(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate"));
+  for (int k = 1; k < numStreams_; ++k) {
+    hipStream_t h = nullptr;
+    LKRT_TRY(hipStatus(hipStreamCreateWithFlags(&h, hipStreamNonBlocking), "hipStreamCreate"));
+    side_.push_back(h);
+  }
+  return Status();
+}
+
 std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> model, const std::vector<ExternalPtr>& ext,
-                                               hipStream_t stream, bool useGraphs, Status& st) {
+                                               hipStream_t stream, bool useGraphs, Status& st, int maxStreams) {
   std::unique_ptr<Executable> x(new Executable());
   x->model_ = std::move(model);
   const Model& m = *x->model_;
@@ -431,6 +651,14 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
   for (const Op& op : m.exec.ops) x->dynamic_ = x->dynamic_ || op.kind == OpKind::DimRead;
   for (ValueId v : m.exec.args) x->dynamic_ = x->dynamic_ || m.typeOf(v)->isScalar();
   x->graphs_on_ = useGraphs;
+  x->relocOffset_.assign(m.numValues(), -1);
+  x->skipAlloc_.assign(m.numValues(), 0);
+  // Exec-region arenas (a mem.plan, an unhoisted static arena) were planned for one stream: such models keep one.
+  bool planned = false;
+  for (const Op& op : m.exec.ops)
+    planned = planned || op.kind == OpKind::MemPlan || (op.kind == OpKind::BufferAlloc && op.flag("arena"));
+  if (!x->dynamic_ && !planned && maxStreams > 1)
+    if (Status s = x->schedule(maxStreams, stream); !s) return fail(s);
 
   // Model arena: every constant, init allocation, persistent buffer, then the workspace.
   const size_t nv = m.numValues();
@@ -492,6 +720,7 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
         }
         case OpKind::BufferAlloc: {
           if (!init && !op.flag("persistent")) break;  // per-call memory
+          if (x->skipAlloc_[op.results[0]]) break;      // its temporaries were re-placed
           size_t n;
           if (!staticBytes(m.typeOf(op.results[0]), n))
             return fail(Status::error("a model-lifetime buffer has a symbolic shape"));
@@ -507,14 +736,14 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
     }
   }
   const size_t wsOff = off;
-  off += kWorkspaceBytes;
+  off += kWorkspaceBytes * static_cast<size_t>(x->numStreams_);
   x->modelArena_ = std::make_unique<Memory>();
   x->modelArena_->n = off;
   if (Status s = hipStatus(hipMalloc(&x->modelArena_->p, off), "hipMalloc (model arena)"); !s) return fail(s);
   x->modelBytes_ = off;
   char* base = static_cast<char*>(x->modelArena_->p);
   if (Status s = hipStatus(hipMemsetAsync(base, 0, off, stream), "hipMemsetAsync"); !s) return fail(s);
-  x->workspace_ = base + wsOff;
+  for (int k = 0; k < x->numStreams_; ++k) x->workspace_.push_back(base + wsOff + kWorkspaceBytes * static_cast<size_t>(k));
   x->workspaceBytes_ = kWorkspaceBytes;
   x->fixed_.assign(nv, nullptr);
   for (ValueId v = 0; v < nv; ++v)
@@ -539,6 +768,14 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
   if (Status s = x->interpret(x->init_, slot, sv, none, stream, &initOut); !s) return fail(Status::error("init: " + s.message()));
   if (!none.blocks.empty()) return fail(Status::error("init allocated per-call memory"));
   for (size_t i = 0; i < m.exec.state.size(); ++i) x->fixed_[m.exec.state[i]] = static_cast<char*>(initOut[i].data);
+  if (x->tempsBytes_) {
+    x->temps_ = std::make_unique<Memory>();
+    x->temps_->n = x->tempsBytes_;
+    if (Status s = hipStatus(hipMalloc(&x->temps_->p, x->tempsBytes_), "hipMalloc (temporaries)"); !s) return fail(s);
+    x->modelBytes_ += x->tempsBytes_;
+  }
+  for (ValueId v = 0; v < nv; ++v)
+    if (x->relocOffset_[v] >= 0) x->fixed_[v] = static_cast<char*>(x->temps_->p) + x->relocOffset_[v];
   if (Status s = hipStatus(hipStreamSynchronize(stream), "init"); !s) return fail(s);
   if (Status s = deviceErrors(); !s) return fail(Status::error("init: " + s.message()));
   st = Status();

@@ -9,6 +9,11 @@
 //    its first (eager) run is captured into a hipGraph that later calls replay after copying the inputs into the
 //    block's input buffers;
 //  - kernels are the registry's (lkh::findKernel), called with the reference's argument convention;
+//  - statically shaped exec regions run on up to kStreams HIP streams: kernels are assigned to streams from their
+//    data dependencies (a kernel continues the stream of its latest predecessor when it can, else takes an idle
+//    one), cross-stream dependencies become event waits, and the per-call temporaries the compiler placed in a
+//    static arena are re-placed so that two buffers share bytes only when every use of one happens before the
+//    other is written under that schedule;
 //  - a kernel's ExecCtx::error becomes the call's Status, and so does a data error a kernel recorded on the device
 //    (read at the call's synchronisation, the reference's takeGpuError).
 #pragma once
@@ -49,7 +54,7 @@ class Executable {
   ~Executable();
   // `model` must be in buffer form (after bufferize). Uploads constants and runs init on `stream`.
   static std::unique_ptr<Executable> create(std::shared_ptr<const Model> model, const std::vector<ExternalPtr>& ext,
-                                            hipStream_t stream, bool useGraphs, Status& st);
+                                            hipStream_t stream, bool useGraphs, Status& st, int maxStreams = 1);
   // Enqueues one call on `stream`. With `sync`, waits for it and reports device-side data errors.
   Status run(const std::vector<TensorIn>& inputs, std::vector<TensorOut>& outputs, hipStream_t stream, bool sync);
 
@@ -57,6 +62,7 @@ class Executable {
   size_t modelArenaBytes() const { return modelBytes_; }
   size_t callArenaBytes() const;
   int graphsCaptured() const { return static_cast<int>(graphs_.size()); }
+  int streamsUsed() const { return numStreams_; }
   std::string strategy() const;
 
   struct Instr;
@@ -86,6 +92,8 @@ class Executable {
   };
 
   Status lower(const Region& r, std::vector<Instr>& out);
+  // stream assignment + temporaries re-placement for a statically shaped exec region
+  Status schedule(int maxStreams, hipStream_t stream);
   Status bindInputs(const std::vector<TensorIn>& in, std::vector<int64_t>& sv) const;
   Status interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv, Bump& mem,
                    hipStream_t s, std::vector<TensorOut>* outs);
@@ -96,8 +104,15 @@ class Executable {
   std::vector<Instr> init_, exec_;
   std::unique_ptr<Memory> modelArena_;
   size_t modelBytes_ = 0;
-  void* workspace_ = nullptr;
+  std::vector<void*> workspace_;  // one per stream
   size_t workspaceBytes_ = 0;
+  int numStreams_ = 1;
+  std::vector<hipStream_t> side_;   // streams 1 .. numStreams_ - 1 (stream 0 is the caller's)
+  std::vector<hipEvent_t> events_;  // one per kernel another stream waits on, plus the call's fork / join events
+  std::unique_ptr<Memory> temps_;   // re-placed per-call temporaries
+  size_t tempsBytes_ = 0;
+  std::vector<int64_t> relocOffset_;  // exec state value -> offset in temps_ (-1: not re-placed)
+  std::vector<uint8_t> skipAlloc_;    // init arena allocs whose every byte was re-placed
   std::vector<char*> fixed_;          // value -> model-lifetime address (constants, state, persistent buffers)
   std::vector<int64_t> scalars_;      // host slots of scalar exec inputs
   bool graphs_on_ = false;

@@ -51,7 +51,7 @@ def _rt():
         "lk_dim_canonical": ([cp], vp),
         "lk_exe_create": ([vp, i32_, C.POINTER(cp), C.POINTER(vp), C.POINTER(u64), C.POINTER(i32_), vp, i32_], vp),
         "lk_exe_run": ([vp, i32_, C.POINTER(LkTensor), i32_, C.POINTER(LkTensor), C.POINTER(i32_), vp, i32_], i32_),
-        "lk_exe_stats": ([vp, C.POINTER(u64), C.POINTER(u64), C.POINTER(i32_)], i32_),
+        "lk_exe_stats": ([vp, C.POINTER(u64), C.POINTER(u64), C.POINTER(i32_), C.POINTER(i32_)], i32_),
         "lk_exe_free": ([vp], None),
     }
     for name, (args, res) in sig.items():
@@ -183,7 +183,7 @@ class Executable:
     init run, calls replayed from captured hipGraphs for statically shaped calls. `externals` maps
     const.external names to lk.Tensors bound by reference (device) or uploaded (host)."""
 
-    def __init__(self, model: Model, externals: dict | None = None, graphs: bool = True):
+    def __init__(self, model: Model, externals: dict | None = None, graphs: bool = True, streams: int = 1):
         L = _rt()
         externals = externals or {}
         self.model = model
@@ -195,7 +195,8 @@ class Executable:
         arr_p = (C.c_void_p * max(n, 1))(*[t.data_ptr() for t in ts])
         arr_s = (C.c_uint64 * max(n, 1))(*[t.nbytes for t in ts])
         arr_d = (C.c_int * max(n, 1))(*[1 if t.device == "gpu" else 0 for t in ts])
-        self._h = L.lk_exe_create(model._h, n, arr_n, arr_p, arr_s, arr_d, _stream(), 1 if graphs else 0)
+        flags = (1 if graphs else 0) | (max(1, min(int(streams), 8)) << 8)
+        self._h = L.lk_exe_create(model._h, n, arr_n, arr_p, arr_s, arr_d, _stream(), flags)
         if not self._h:
             raise LokinferError(L.lk_last_error().decode())
 
@@ -238,9 +239,9 @@ class Executable:
         return [_wrap_out(outs[k]) for k in range(n_out.value)]
 
     def stats(self) -> dict:
-        m, c, g = C.c_uint64(), C.c_uint64(), C.c_int()
-        _check(_rt().lk_exe_stats(self._h, C.byref(m), C.byref(c), C.byref(g)))
-        return {"model_arena_bytes": m.value, "call_arena_bytes": c.value, "graphs": g.value}
+        m, c, g, s = C.c_uint64(), C.c_uint64(), C.c_int(), C.c_int()
+        _check(_rt().lk_exe_stats(self._h, C.byref(m), C.byref(c), C.byref(g), C.byref(s)))
+        return {"model_arena_bytes": m.value, "call_arena_bytes": c.value, "graphs": g.value, "streams": s.value}
 
 
 def _wrap_out(o: LkTensor) -> Tensor:
