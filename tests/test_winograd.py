@@ -91,3 +91,33 @@ def test_row_counts():
     assert W.tiles_rows(300, 1, 1, 4, 3) == (3 * 32) * 6
     assert W.tiles_rows(300, 1, 1, 2, 3) == (3 * 64) * 4
     assert W.stats_chunks(1001, 5) == 2 and W.stats_chunks(128, 1) == 1 and W.stats_chunks(129, 1) == 2
+
+
+def test_tables_equal_the_committed_values():
+    """The exact tables equal tests/golden/winograd_tables.json, the values every Winograd GPU parity case and
+    every U / tr operand was built with (F(4, 3), F(4, 4), F(2, 3))."""
+    import json
+    from pathlib import Path
+
+    gold = json.loads((Path(__file__).resolve().parent / "golden" / "winograd_tables.json").read_text())
+    for name, (m, r, pts) in {"F(4,3)": (4, 3, None), "F(4,4)": (4, 4, None), "F(2,3)": (2, 3, W.POINTS_TILE2)}.items():
+        got = dict(zip(("AT", "G", "BT"), W.transforms_exact(m, r, pts)))
+        for key, mat in gold[name].items():
+            assert [[Fraction(v) for v in row] for row in mat] == got[key], (name, key)
+
+
+def test_wino_weights_sums_in_tap_order():
+    """U entries are the tap-order float64 sums of G x w rounded once to f32 (the same bits wherever U is built)."""
+    w = rng.standard_normal((8, 16, 7)).astype(np.float32)
+    u, _ = W.wino_weights(w)
+    r, n = W.variant(7)
+    g = W.transforms(4, r)[1]
+    for x in range(u.shape[0]):
+        for grp in range(n):
+            for i in (0, 5, 15):
+                for o in (0, 7):
+                    acc = 0.0
+                    for t in range(r):
+                        k = grp * 4 + t
+                        acc = acc + g[x, t] * (float(w[o, i, k]) if k < 7 else 0.0)
+                    assert u[x, grp * 16 + i, o] == np.float32(acc)
