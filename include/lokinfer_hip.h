@@ -141,6 +141,20 @@ int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const
  * chunk) partials chunk_part[heads, ceil(cap / 64), 66] = (max, sum, acc[64]); an invalid pos writes NaN. */
 int lk_hip_attention_decode_part_f32(const float* qkv_part, int64_t slices, float* kc, float* vc, const int64_t* pos,
                                      const float* bias, float* chunk_part, int64_t cap, int heads, void* stream);
+/* Layer-0 variant of xmode 3 whose sum is two embedding rows: sum = table[id[0]] + table2[id2[0]] (the GPT-2
+ * token + position lookups, which the reference does on the host, models/gpt2.py:189-190), written to sum_out;
+ * x = LayerNorm(sum). An id out of range records LK_DEVERR_INDEX and yields NaN. K <= 1024, K % 4 == 0. */
+int lk_hip_gemv_partial_embed_ln_f32(const float* table, const int64_t* id, const float* table2, const int64_t* id2,
+                                     int64_t rows, int64_t rows2, const float* gamma, const float* beta, float eps,
+                                     const float* w, float* part, float* sum_out, int64_t n, int64_t k, void* stream);
+/* Tied LM head + final LayerNorm + greedy argmax of a decode step (replaces add_bias_layernorm2_f32_gpu,
+ * gemm_nt_f32_gpu_mps and the Python argmax, models/gpt2.py:225, 243, 349-355): logits[r] = LayerNorm((slices of
+ * part) + bias + res) . table[r, :], argmax[0] = first index of the max logit. Two launches; workspace >= 16
+ * min(512, ceil(rows / 4)) bytes (3 when short). K <= 1024, K % 4 == 0. */
+int lk_hip_lm_head_ln_argmax_f32(const float* part, int64_t slices, const float* bias, const float* res,
+                                 const float* gamma, const float* beta, float eps, const float* table, float* logits,
+                                 int64_t* argmax, int64_t rows, int64_t k, void* workspace, int64_t workspaceBytes,
+                                 void* stream);
 /* sum = (slices of part[slices, N]) + bias + res; ln = LayerNorm(sum); one workgroup, N <= 1024 */
 int lk_hip_reduce_ln_f32(const float* part, int64_t slices, const float* bias, const float* res, const float* gamma,
                          const float* beta, float* sum_out, float* ln_out, int64_t n, float eps, void* stream);
@@ -169,6 +183,9 @@ int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* ta
                          int64_t n, int64_t d, int64_t rows, int64_t rows2, void* stream);
 /* out[i] = pos[0] + i (reference host kernel arange_offset_i64_cpu, kernels/cpu/decode.cpp:221) */
 int lk_hip_arange_offset_i64(const int64_t* pos, int64_t* out, int64_t n, void* stream);
+/* out[0] = indices[i] of the largest values[i] (ties: the smallest index), i < n: the last pass of an argmax whose
+ * first pass left (value, index) pairs */
+int lk_hip_argmax_pairs_f32(const float* values, const int64_t* indices, int64_t* out, int64_t n, void* stream);
 int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
                       int64_t workspace_bytes, void* stream);
 

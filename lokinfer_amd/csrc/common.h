@@ -140,6 +140,44 @@ __device__ __forceinline__ float waveMax(float v) {
   return v;
 }
 
+// Reductions over a row of 16 lanes by DPP moves (no LDS round trip): quad xor 1, quad xor 2, half-row mirror
+// (quads 0 <-> 1, 2 <-> 3), row mirror (half-rows). Each step adds a lane's value to its partner's, so every lane of
+// the row ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dppMov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rowSum16(float v) {
+  v += dppMov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dppMov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dppMov<0x141>(v);  // row_half_mirror
+  v += dppMov<0x140>(v);  // row_mirror
+  return v;
+}
+// Combines the 4 rows of a wave, (r0 + r1) + (r2 + r3) in every lane, by the permlane swaps of rows and halves.
+__device__ __forceinline__ float crossRowSum(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+__device__ __forceinline__ float crossRowMax(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+
+// Wave-wide sum / max with the same bits in every lane, by DPP and permlane swaps.
+__device__ __forceinline__ float waveSumDpp(float v) { return crossRowSum(rowSum16(v)); }
+__device__ __forceinline__ float waveMaxDpp(float v) {
+  v = fmaxf(v, dppMov<0xB1>(v));
+  v = fmaxf(v, dppMov<0x4E>(v));
+  v = fmaxf(v, dppMov<0x141>(v));
+  v = fmaxf(v, dppMov<0x140>(v));
+  return crossRowMax(v);
+}
+
 // sin(y)^2 for the Snake activation x + sin(a x)^2 / a. sin^2 has period pi, so y is reduced to
 // r = y - n pi, |r| <= pi / 2, by Cody-Waite with pi split into its nearest float and the remainder
 // (pi - 3.14159274f = -8.74227766e-8f), each product formed by one fma; sin(r) then comes from the hardware

@@ -19,6 +19,7 @@
 #include "common.h"
 #include "lokinfer_hip.h"
 
+#include <algorithm>
 #include <cstdint>
 
 namespace lkd {
@@ -28,6 +29,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kDecHd = 64;     // head dim
 constexpr int kDecChunk = 64;  // keys per decode chunk
 constexpr int kPartStride = kDecHd + 2;
+constexpr int kFastSlices = 12;  // partial-row slices whose loads are issued together
 
 // rows per wave of the partial GEMV: 16 for K <= 1024, else 64 (12 slices at K = 768 and at K = 3072)
 inline int64_t gemvRowsPerWave(int64_t k) { return k <= 1024 ? 16 : 64; }
@@ -55,6 +57,66 @@ struct LnIn {  // mode 3: x = LayerNorm(sum of xpart slices + xbias + res), work
   const float* beta;
   float* sumOut;
   float eps;
+  // mode 4 (embedding): the sum is res[id] + xbias[id2] (rows of two tables with `rows` / `rows2` rows)
+  const int64_t* id;
+  const int64_t* id2;
+  int64_t rows, rows2;
+  unsigned long long* err;
+};
+
+// LayerNorm prologue over one row of K <= 1024 columns, K % 4 == 0; thread t < K / 4 owns columns 4t .. 4t + 3.
+// The sum is ((slices of xpart, in order) + xbias) + res; load() issues every load, finish() (after the caller has
+// issued its own loads) forms the sum, writes it to sumOut if asked, and returns this thread's 4 LayerNorm outputs
+// (two-pass, biased variance; the workgroup is 4 waves). Threads past K / 4 return zeros.
+struct LnRow {
+  f4v pv[kFastSlices];
+  f4v xb, rs, ga, be;
+  int64_t c0;
+  bool live;
+  __device__ __forceinline__ void load(const float* xpart, int64_t xslices, const float* xbias, const float* res,
+                                       const float* gamma, const float* beta, int64_t k) {
+    c0 = 4 * static_cast<int64_t>(threadIdx.x);
+    live = c0 < k;
+    const int64_t cc = live ? c0 : 0;  // idle threads load column 0, never used
+    const f4v zero = {0.f, 0.f, 0.f, 0.f};
+    xb = zero;
+    if (xslices > 0) {
+#pragma unroll
+      for (int i = 0; i < kFastSlices; ++i)
+        pv[i] = *reinterpret_cast<const f4v*>(xpart + min<int64_t>(i, xslices - 1) * k + cc);
+    }
+    rs = *reinterpret_cast<const f4v*>(res + cc);
+    if (xbias) xb = *reinterpret_cast<const f4v*>(xbias + cc);
+    ga = *reinterpret_cast<const f4v*>(gamma + cc);
+    be = *reinterpret_cast<const f4v*>(beta + cc);
+  }
+  __device__ __forceinline__ f4v finish(const float* xpart, int64_t xslices, int64_t k, float eps, float* sumOut,
+                                        float (*scr)[4]) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const f4v zero = {0.f, 0.f, 0.f, 0.f};
+    f4v sp = zero;
+    if (xslices > 0) {
+#pragma unroll
+      for (int i = 0; i < kFastSlices; ++i)
+        if (i < xslices) sp += pv[i];
+      for (int64_t sl = kFastSlices; sl < xslices; ++sl)
+        sp += *reinterpret_cast<const f4v*>(xpart + sl * k + (live ? c0 : 0));
+    }
+    const f4v v = live ? (sp + xb) + rs : zero;
+    if (live && sumOut) *reinterpret_cast<f4v*>(sumOut + c0) = v;
+    const float s1 = waveSumDpp((v.x + v.y) + (v.z + v.w));
+    if (lane == 0) scr[0][wv] = s1;
+    __syncthreads();
+    const float mean = ((scr[0][0] + scr[0][1]) + (scr[0][2] + scr[0][3])) / static_cast<float>(k);
+    const f4v d = v - mean;
+    float s2 = live ? (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w) : 0.0f;
+    s2 = waveSumDpp(s2);
+    if (lane == 0) scr[1][wv] = s2;
+    __syncthreads();
+    const float var = ((scr[1][0] + scr[1][1]) + (scr[1][2] + scr[1][3])) / static_cast<float>(k);
+    const float rstd = 1.0f / sqrtf(var + eps);
+    return live ? d * rstd * ga + be : zero;
+  }
 };
 
 // Sum of v over the RS lane subgroups of a wave (subgroup = 64 / RS consecutive lanes), in every subgroup.
@@ -83,101 +145,105 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
   constexpr int RS = 256 / CB, CL = CB / 4, LPW = RPW / RS;  // row subgroups, lanes per row, loads per lane
   static_assert(RPW % RS == 0, "rows per wave must split over the lane subgroups");
   __shared__ f4v wsum[4][CL];
-  __shared__ float mrg[4][kDecHd];
-  __shared__ float cw[64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t rBase = static_cast<int64_t>(blockIdx.y) * ROWS;
-  // The weight loads do not depend on x: the first batch is issued before x is formed, so its latency overlaps
-  // the prologue's own loads and reductions.
   constexpr int B0 = LPW < 32 ? LPW : 32;
   const int cl = lane % CL, q = lane / CL;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + 4 * cl;
   const int64_t r0 = rBase + static_cast<int64_t>(wv) * RPW + q;  // this lane's rows r0 + RS i
   const int64_t colc = min<int64_t>(col, n - 4);  // columns past N compute on a valid column, never stored
   f4v wr[B0];
+  // Every load of the prologue is independent of the others and of the weights: all of them are issued at entry,
+  // the prologue's own operands first (they are waited for first), then the first batch of weights, so the whole
+  // prologue costs one memory round trip that overlaps the weight stream.
+  auto loadWeights = [&]() {
 #pragma unroll
-  for (int i = 0; i < B0; ++i)
-    wr[i] = __builtin_nontemporal_load(
-        reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + RS * i, k - 1) * n + colc));
+    for (int i = 0; i < B0; ++i)
+      wr[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const f4v*>(w + min<int64_t>(r0 + RS * i, k - 1) * n + colc));
+  };
   if constexpr (XMODE == 0) {
-    for (int t = tid; t < ROWS; t += 256) xs[t] = rBase + t < k ? x[rBase + t] : 0.0f;
+    const float xv = tid < ROWS && rBase + tid < k ? x[rBase + tid] : 0.0f;
+    loadWeights();
+    if (tid < ROWS) xs[tid] = xv;
   } else if constexpr (XMODE == 1) {
-    // x[r] = gelu(sum_s xpart[s, r] + xbias[r]), slices in order
-    for (int t = tid; t < ROWS; t += 256) {
-      const int64_t r = rBase + t;
-      float v = 0.0f;
-      if (r < k) {
-        float s = 0.0f;
-#pragma unroll 12
-        for (int64_t sl = 0; sl < xslices; ++sl) s += xpart[sl * k + r];
-        v = geluTanh(s + xbias[r]);
-      }
-      xs[t] = v;
-    }
-  } else if constexpr (XMODE == 3) {
-    // the whole row (K <= 1024): sum = slices in order + xbias + res, two-pass LayerNorm (biased variance)
-    __shared__ float lnrow[1024];
-    __shared__ float scr[4];
-    float v[4];
-    float s1 = 0.0f;
-    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+    // x[r] = gelu(sum_s xpart[s, r] + xbias[r]), slices in order; ROWS <= 256: thread t owns row rBase + t
+    static_assert(ROWS <= 256, "one row per thread");
+    const int64_t r = rBase + tid;
+    const bool live = tid < ROWS && r < k;
+    const int64_t rc = min<int64_t>(r, k - 1);  // rows past K load a valid row, never used
+    float pv[kFastSlices];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = tid + 256 * j;
-      float xv = 0.0f;
-      if (c < k) {
-        float sp = 0.0f;
-#pragma unroll 12
-        for (int64_t sl = 0; sl < xslices; ++sl) sp += xpart[sl * k + c];
-        xv = sp + (xbias ? xbias[c] : 0.0f) + ln.res[c];
-        if (writer) ln.sumOut[c] = xv;
-      }
-      v[j] = xv;
-      s1 += xv;
-    }
-    s1 = waveSum(s1);
-    if (lane == 0) scr[wv] = s1;
-    __syncthreads();
-    const float mean = ((scr[0] + scr[1]) + (scr[2] + scr[3])) / static_cast<float>(k);
-    __syncthreads();
-    float s2 = 0.0f;
+    for (int i = 0; i < kFastSlices; ++i) pv[i] = xpart[min<int64_t>(i, xslices - 1) * k + rc];
+    const float bv = xbias[rc];
+    loadWeights();
+    float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float d = v[j] - mean;
-      if (tid + 256 * j < k) s2 += d * d;
+    for (int i = 0; i < kFastSlices; ++i)
+      if (i < xslices) s += pv[i];
+    for (int64_t sl = kFastSlices; sl < xslices; ++sl) s += xpart[sl * k + rc];
+    if (tid < ROWS) xs[tid] = live ? geluTanh(s + bv) : 0.0f;
+  } else if constexpr (XMODE == 3 || XMODE == 4) {
+    // the whole row: sum = slices in order + xbias + res (mode 4: two table rows), then its LayerNorm, of which
+    // the workgroup keeps its own ROWS rows; workgroup (0, 0) writes the sum
+    __shared__ float scr[2][4];
+    const float* res = ln.res;
+    const float* xb = xbias;
+    bool bad = false;
+    if constexpr (XMODE == 4) {
+      const int64_t id = *ln.id, id2 = *ln.id2;
+      const bool ok = id >= 0 && id < ln.rows, ok2 = id2 >= 0 && id2 < ln.rows2;
+      bad = !ok || !ok2;
+      if (bad && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0)
+        raiseDeviceError(ln.err, LK_DEVERR_INDEX, ok ? id2 : id);
+      res = ln.res + (ok ? id : 0) * k;
+      xb = xbias + (ok2 ? id2 : 0) * k;
     }
-    s2 = waveSum(s2);
-    if (lane == 0) scr[wv] = s2;
-    __syncthreads();
-    const float var = ((scr[0] + scr[1]) + (scr[2] + scr[3])) / static_cast<float>(k);
-    const float rstd = 1.0f / sqrtf(var + ln.eps);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = tid + 256 * j;
-      if (c < k) lnrow[c] = (v[j] - mean) * rstd * ln.gamma[c] + ln.beta[c];
+    LnRow row;
+    row.load(xpart, xslices, xb, res, ln.gamma, ln.beta, k);
+    loadWeights();
+    if constexpr (XMODE == 4) {
+      if (bad) row.rs = f4v{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
     }
-    __syncthreads();
-    for (int t = tid; t < ROWS; t += 256) xs[t] = rBase + t < k ? lnrow[rBase + t] : 0.0f;
+    const f4v y = row.finish(xpart, xslices, k, ln.eps, blockIdx.x == 0 && blockIdx.y == 0 ? ln.sumOut : nullptr,
+                             scr);
+    // this thread's columns that fall in the workgroup's rows rBase .. rBase + ROWS - 1
+    if (row.live && row.c0 >= rBase && row.c0 < rBase + ROWS) *reinterpret_cast<f4v*>(&xs[row.c0 - rBase]) = y;
+    if (rBase + ROWS > k && tid < ROWS && rBase + tid >= k) xs[tid] = 0.0f;
   } else {
     // rows rBase .. rBase + 63 are head blockIdx.y: merge its chunk partials (m, l, acc) in chunk order,
     // M = max m_c, out[d] = sum_c e^{m_c - M} acc_c[d] / sum_c e^{m_c - M} l_c
     static_assert(XMODE != 2 || ROWS == kDecHd, "attention merge needs 64 rows per workgroup");
+    __shared__ float mrg[4][kDecHd];
+    __shared__ float cw[64];
     const float* base = xpart + static_cast<int64_t>(blockIdx.y) * chunks * kPartStride;
-    // chunk weights (chunks <= 64): lane c of wave 0 holds chunk c's (m, l)
+    // thread (d = lane, chunk group wv) owns chunks wv, wv + 4, ... (chunks <= 64); wave 0 lane c also holds
+    // chunk c's (m, l)
+    float av[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = wv + 4 * i;
+      av[i] = c < chunks ? base[c * kPartStride + 2 + lane] : 0.0f;
+    }
+    float mc = -INFINITY, lc = 0.0f;
+    if (wv == 0 && lane < chunks) {
+      mc = base[lane * kPartStride];
+      lc = base[lane * kPartStride + 1];
+    }
+    loadWeights();
     if (wv == 0) {
-      const float mc = lane < chunks ? base[lane * kPartStride] : -INFINITY;
-      const float lc = lane < chunks ? base[lane * kPartStride + 1] : 0.0f;
-      const float M = waveMax(mc);
+      const float M = waveMaxDpp(mc);
       const float wc = lc > 0.0f ? expf(mc - M) : 0.0f;
       cw[lane] = wc;
-      const float L = waveSum(lc * wc);
+      const float L = waveSumDpp(lc * wc);
       if (lane == 0) xs[0] = L;  // xs doubles as a scratch slot until the merge below
     }
     __syncthreads();
-    // thread (d = lane, chunk group wv) sums chunks wv, wv + 4, ... for dim d; groups combine in order
     float a = 0.0f;
-    for (int c = wv; c < chunks; c += 4) a += cw[c] * base[c * kPartStride + 2 + lane];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (wv + 4 * i < chunks) a += cw[wv + 4 * i] * av[i];
     mrg[wv][lane] = a;
     const float L = xs[0];
     __syncthreads();
@@ -211,110 +277,198 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
 // One wave per (head, 64-key chunk), as the split decode kernel, but q / k / v of this step are the fixed-order
 // sums of `slices` GEMV partial rows (+ bias). An invalid position writes NaN partials (no cache write) and is
 // recorded in the GPU's error record.
+//
+// Layout: lane (g = lane / 16, d4 = lane % 16) owns dims 4 d4 .. 4 d4 + 3 of keys kb + g + 4 i, i = 0..15, so each
+// load instruction reads 4 whole cache rows (coalesced), a score is a 16-lane row sum (DPP), and the softmax
+// weights of a lane's keys are already in the lane for P.V. Every load is issued before the first wait: the partial
+// rows of q / k / v first, then (once pos is known) the 16 key and 16 value rows of the chunk, unconditionally from
+// rows clamped into 0 .. pos (the row pos itself and the rows past it are replaced by selects, never used).
 __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restrict__ qpart, int64_t slices,
                                                            float* kc, float* vc, const int64_t* pos,
                                                            const float* __restrict__ bias, float* __restrict__ cpart,
                                                            int64_t cap, int heads, int chunks,
                                                            unsigned long long* err) {
-  __shared__ float qs[kDecHd], vs[kDecHd];
   const int h = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
+  const int g = lane >> 4, d4 = lane & 15;
   const int64_t D = static_cast<int64_t>(heads) * kDecHd, ld = 3 * D;
   float* part = cpart + (static_cast<int64_t>(h) * chunks + s) * kPartStride;
+  const int64_t c4 = h * kDecHd + 4 * d4;  // this lane's 4 dims in a row of q, k or v
+  // q / k / v partial rows (slices in order; 12 issued at once, more in a tail loop)
+  f4v pq[kFastSlices], pk[kFastSlices], pv[kFastSlices];
+#pragma unroll
+  for (int i = 0; i < kFastSlices; ++i) {
+    const float* row = qpart + min<int64_t>(i, slices - 1) * ld + c4;
+    pq[i] = *reinterpret_cast<const f4v*>(row);
+    pk[i] = *reinterpret_cast<const f4v*>(row + D);
+    pv[i] = *reinterpret_cast<const f4v*>(row + 2 * D);
+  }
+  const f4v bq = *reinterpret_cast<const f4v*>(bias + c4), bk = *reinterpret_cast<const f4v*>(bias + D + c4),
+            bv = *reinterpret_cast<const f4v*>(bias + 2 * D + c4);
+  // No early exit: a chunk past the live keys and an invalid position compute on clamped rows and store their
+  // fixed results at the end, so no load of the kernel waits behind a branch on pos.
   const int64_t ps = *pos;
-  if (ps < 0 || ps >= cap) {
-    if (h == 0 && s == 0 && lane == 0) raiseDeviceError(err, LK_DEVERR_POSITION, ps);
-    if (lane == 0) {
-      part[0] = __builtin_nanf("");
-      part[1] = 1.0f;
-    }
-    part[2 + lane] = __builtin_nanf("");
-    return;
-  }
+  const bool badPos = ps < 0 || ps >= cap;
+  if (badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(err, LK_DEVERR_POSITION, ps);
+  const int64_t psc = badPos ? 0 : ps;
   const int64_t kb = static_cast<int64_t>(s) * kDecChunk;
-  const int64_t ke = min<int64_t>(ps + 1, kb + kDecChunk);
-  if (kb >= ke) {  // chunk past the live keys
-    if (lane == 0) {
-      part[0] = -INFINITY;
-      part[1] = 0.0f;
-    }
-    part[2 + lane] = 0.0f;
-    return;
-  }
-  // this lane's dim of q, k, v: fixed-order sums of the partial rows
-  const int64_t cq = h * kDecHd + lane;
-  float sq = 0.0f, sk = 0.0f, sv = 0.0f;
-#pragma unroll 12
-  for (int64_t sl = 0; sl < slices; ++sl) {
-    const float* row = qpart + sl * ld;
-    sq += row[cq];
-    sk += row[D + cq];
-    sv += row[2 * D + cq];
-  }
-  const float qd = (sq + bias[cq]) * 0.125f;
-  const float knew = sk + bias[D + cq];
-  const float vnew = sv + bias[2 * D + cq];
-  if (ps >= kb && ps < kb + kDecChunk) {
-    kc[ps * D + cq] = knew;
-    vc[ps * D + cq] = vnew;
-  }
-  qs[lane] = qd;
-  vs[lane] = vnew;
-  const float snew = waveSum(qd * knew);
-  __syncthreads();
-  float q[kDecHd];
-#pragma unroll
-  for (int d = 0; d < kDecHd; ++d) q[d] = qs[d];
-
-  const int64_t j = kb + lane;
-  float sc = -INFINITY;
-  if (j < ke) {
-    if (j == ps) {
-      sc = snew;
-    } else {
-      const f4v* kr = reinterpret_cast<const f4v*>(kc + j * D + h * kDecHd);
-      f4v kv[kDecHd / 4];
-#pragma unroll
-      for (int d4 = 0; d4 < kDecHd / 4; ++d4) kv[d4] = kr[d4];
-      float dot = 0.0f;
-#pragma unroll
-      for (int d4 = 0; d4 < kDecHd / 4; ++d4)
-        dot += q[4 * d4] * kv[d4].x + q[4 * d4 + 1] * kv[d4].y + q[4 * d4 + 2] * kv[d4].z + q[4 * d4 + 3] * kv[d4].w;
-      sc = dot;
-    }
-  }
-  const float m = waveMax(sc);
-  const float pj = j < ke ? expf(sc - m) : 0.0f;
-  const float l = waveSum(pj);
-
-  // P.V: lane = (g, d4); keys kb + g + 4 i, i = 0..15
-  const int g = lane >> 4, d4 = lane & 15;
-  f4v vv[16];
+  const int64_t ke = min<int64_t>(psc + 1, kb + kDecChunk);
+  const bool dead = kb >= ke;  // chunk past the live keys (its rows clamp to row pos)
+  f4v kr[16], vr[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t row = kb + g + 4 * i;
-    if (row < ke && row != ps) {
-      vv[i] = reinterpret_cast<const f4v*>(vc + row * D + h * kDecHd)[d4];
-    } else if (row == ps) {
-      vv[i] = f4v{vs[4 * d4], vs[4 * d4 + 1], vs[4 * d4 + 2], vs[4 * d4 + 3]};
-    } else {
-      vv[i] = f4v{0.f, 0.f, 0.f, 0.f};
-    }
+    const int64_t row = min<int64_t>(kb + g + 4 * i, ke - 1);
+    kr[i] = *reinterpret_cast<const f4v*>(kc + row * D + c4);
+    vr[i] = *reinterpret_cast<const f4v*>(vc + row * D + c4);
   }
+  f4v sq = {0.f, 0.f, 0.f, 0.f}, sk = sq, sv = sq;
+#pragma unroll
+  for (int i = 0; i < kFastSlices; ++i)
+    if (i < slices) {
+      sq += pq[i];
+      sk += pk[i];
+      sv += pv[i];
+    }
+  for (int64_t sl = kFastSlices; sl < slices; ++sl) {
+    const float* row = qpart + sl * ld + c4;
+    sq += *reinterpret_cast<const f4v*>(row);
+    sk += *reinterpret_cast<const f4v*>(row + D);
+    sv += *reinterpret_cast<const f4v*>(row + 2 * D);
+  }
+  const f4v q = (sq + bq) * 0.125f;
+  const f4v knew = sk + bk;
+  const f4v vnew = sv + bv;
+  if (!badPos && g == 0 && ps >= kb && ps < kb + kDecChunk) {
+    *reinterpret_cast<f4v*>(kc + ps * D + c4) = knew;
+    *reinterpret_cast<f4v*>(vc + ps * D + c4) = vnew;
+  }
+  const float snew = rowSum16((q.x * knew.x + q.y * knew.y) + (q.z * knew.z + q.w * knew.w));
+  // scores of this lane's 16 keys (the same in the 16 lanes of a row), then the chunk softmax
+  float sc[16];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t key = kb + g + 4 * i;
+    const float dot = rowSum16((q.x * kr[i].x + q.y * kr[i].y) + (q.z * kr[i].z + q.w * kr[i].w));
+    sc[i] = key < ke ? (key == ps ? snew : dot) : -INFINITY;
+    m = fmaxf(m, sc[i]);
+  }
+  m = crossRowMax(m);
+  float l = 0.0f;
   f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc += __shfl(pj, g + 4 * i, 64) * vv[i];
-#pragma unroll
-  for (int o = 16; o < 64; o <<= 1) {
-    acc.x += __shfl_xor(acc.x, o, 64);
-    acc.y += __shfl_xor(acc.y, o, 64);
-    acc.z += __shfl_xor(acc.z, o, 64);
-    acc.w += __shfl_xor(acc.w, o, 64);
+  for (int i = 0; i < 16; ++i) {
+    const int64_t key = kb + g + 4 * i;
+    const float pj = key < ke ? expf(sc[i] - m) : 0.0f;
+    l += pj;
+    const f4v v = key < ke ? (key == ps ? vnew : vr[i]) : f4v{0.f, 0.f, 0.f, 0.f};
+    acc += pj * v;
+  }
+  l = crossRowSum(l);
+  acc.x = crossRowSum(acc.x);
+  acc.y = crossRowSum(acc.y);
+  acc.z = crossRowSum(acc.z);
+  acc.w = crossRowSum(acc.w);
+  const float nan = __builtin_nanf("");
+  if (badPos) {
+    m = nan;
+    l = 1.0f;
+    acc = f4v{nan, nan, nan, nan};
+  } else if (dead) {
+    m = -INFINITY;
+    l = 0.0f;
+    acc = f4v{0.f, 0.f, 0.f, 0.f};
   }
   if (lane == 0) {
     part[0] = m;
     part[1] = l;
   }
   if (g == 0) reinterpret_cast<f4v*>(part + 2)[d4] = acc;
+}
+
+// Tied LM head of a decode step with the final LayerNorm and the greedy argmax folded in: x = LayerNorm(slices of
+// part in order + bias + res) (every workgroup forms it in LDS from the partial rows), logits[r] = x . table[r, :]
+// for r < rows, and per workgroup the (max logit, first row) pair over its rows, which argmaxKernel reduces.
+// Wave w of workgroup b takes rows b * 4 + w + W i (W = 4 * grid waves), 8 rows per batch, the next batch loaded
+// while the current one is reduced; lane l holds columns 4 (l + 64 j), j < QPL (K <= 256 QPL).
+constexpr int kLmRowBatch = 8;
+constexpr int kLmGrid = 512;
+template <int QPL>
+__global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ part, int64_t slices,
+                                                     const float* __restrict__ bias, const float* __restrict__ res,
+                                                     const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                     float eps, const float* __restrict__ table,
+                                                     float* __restrict__ logits, float* __restrict__ bestV,
+                                                     int64_t* __restrict__ bestI, int64_t rows, int64_t k) {
+  __shared__ f4v xrow[256];
+  __shared__ float scr[2][4];
+  __shared__ float wbV[4];
+  __shared__ int64_t wbI[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t kq = k / 4;
+  const int64_t W = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wv;
+  LnRow row;
+  row.load(part, slices, bias, res, gamma, beta, k);
+  f4v wr[kLmRowBatch][QPL];
+  auto loadRows = [&](int64_t r0) {
+#pragma unroll
+    for (int b = 0; b < kLmRowBatch; ++b) {
+      const float* tr = table + min<int64_t>(r0 + W * b, rows - 1) * k;
+#pragma unroll
+      for (int j = 0; j < QPL; ++j)
+        wr[b][j] = __builtin_nontemporal_load(
+            reinterpret_cast<const f4v*>(tr + 4 * min<int64_t>(lane + 64 * j, kq - 1)));
+    }
+  };
+  loadRows(wave);
+  const f4v y = row.finish(part, slices, k, eps, nullptr, scr);
+  if (row.live) xrow[tid] = y;
+  __syncthreads();
+  f4v xv[QPL];
+#pragma unroll
+  for (int j = 0; j < QPL; ++j) xv[j] = lane + 64 * j < kq ? xrow[lane + 64 * j] : f4v{0.f, 0.f, 0.f, 0.f};
+  float best = -INFINITY;
+  int64_t bi = INT64_MAX;
+  for (int64_t r0 = wave; r0 < rows; r0 += W * kLmRowBatch) {
+    float d[kLmRowBatch];
+#pragma unroll
+    for (int b = 0; b < kLmRowBatch; ++b) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < QPL; ++j) {
+        const f4v t = xv[j] * wr[b][j];
+        acc += (t.x + t.y) + (t.z + t.w);
+      }
+      d[b] = acc;
+    }
+    if (r0 + W * kLmRowBatch < rows) loadRows(r0 + W * kLmRowBatch);
+#pragma unroll
+    for (int b = 0; b < kLmRowBatch; ++b) {
+      const int64_t r = r0 + W * b;
+      const float v = waveSumDpp(d[b]);
+      if (r < rows) {
+        if (lane == 0) logits[r] = v;
+        if (v > best || (!(v < best) && r < bi)) {
+          best = v;
+          bi = r;
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+    wbV[wv] = best;
+    wbI[wv] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (wbV[w] > best || (!(wbV[w] < best) && wbI[w] < bi)) {
+        best = wbV[w];
+        bi = wbI[w];
+      }
+    bestV[blockIdx.x] = best;
+    bestI[blockIdx.x] = bi;
+  }
 }
 
 constexpr int kRedMaxPerThread = 4;  // N <= 1024
@@ -394,11 +548,13 @@ int64_t lk_hip_gemv_partial_slices(int64_t k) {
   return (k + 4 * rpw - 1) / (4 * rpw);
 }
 
-int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const float* xbias, int64_t xslices,
-                            int chunks, const float* res, const float* gamma, const float* beta, float* sum_out,
-                            float eps, const float* w, float* part, int64_t n, int64_t k, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int launchGemvPartial(int xmode, const float* x, const float* xpart, const float* xbias, int64_t xslices, int chunks,
+                      const lkd::LnIn& ln, const float* w, float* part, int64_t n, int64_t k, void* stream) {
   if (n <= 0 || k <= 0 || n % 4 != 0) return 1;
-  const lkd::LnIn ln{res, gamma, beta, sum_out, eps};
   if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(part)) & 15) != 0) return 1;
   const int64_t rpw = lkd::gemvRowsPerWave(k);
   const int64_t slices = (k + 4 * rpw - 1) / (4 * rpw);
@@ -423,15 +579,42 @@ int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const
   } else if (xmode == 2) {
     if (rpw != 16 || k % lkd::kDecHd != 0 || chunks <= 0 || chunks > 64) return 1;
     LK_GP(2, 16);
-  } else if (xmode == 3) {
-    if (k > 1024 || !res || !gamma || !beta || !sum_out || (xslices > 0 && !xpart)) return 1;
-    LK_GP(3, 16);
+  } else if (xmode == 3 || xmode == 4) {
+    if (k > 1024 || k % 4 != 0 || !ln.res || !ln.gamma || !ln.beta || !ln.sumOut || (xslices > 0 && !xpart)) return 1;
+    if (xmode == 4 && (xslices != 0 || !xbias || !ln.id || !ln.id2 || ln.rows <= 0 || ln.rows2 <= 0)) return 1;
+    // the LayerNorm prologue reads and writes whole float4 columns
+    if (((reinterpret_cast<uintptr_t>(xpart) | reinterpret_cast<uintptr_t>(xbias) |
+          reinterpret_cast<uintptr_t>(ln.res) | reinterpret_cast<uintptr_t>(ln.gamma) |
+          reinterpret_cast<uintptr_t>(ln.beta) | reinterpret_cast<uintptr_t>(ln.sumOut)) & 15) != 0)
+      return 1;
+    if (xmode == 3) LK_GP(3, 16);
+    else LK_GP(4, 16);
   } else {
     return 1;
   }
 #undef LK_GP
 #undef LK_GP_CB
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lk_hip_gemv_partial_f32(int xmode, const float* x, const float* xpart, const float* xbias, int64_t xslices,
+                            int chunks, const float* res, const float* gamma, const float* beta, float* sum_out,
+                            float eps, const float* w, float* part, int64_t n, int64_t k, void* stream) {
+  if (xmode < 0 || xmode > 3) return 1;
+  const lkd::LnIn ln{res, gamma, beta, sum_out, eps, nullptr, nullptr, 0, 0, nullptr};
+  return launchGemvPartial(xmode, x, xpart, xbias, xslices, chunks, ln, w, part, n, k, stream);
+}
+
+int lk_hip_gemv_partial_embed_ln_f32(const float* table, const int64_t* id, const float* table2, const int64_t* id2,
+                                     int64_t rows, int64_t rows2, const float* gamma, const float* beta, float eps,
+                                     const float* w, float* part, float* sum_out, int64_t n, int64_t k,
+                                     void* stream) {
+  const lkd::LnIn ln{table, gamma, beta, sum_out, eps, id, id2, rows, rows2, lkh::deviceErrorRecord()};
+  return launchGemvPartial(4, nullptr, nullptr, table2, 0, 0, ln, w, part, n, k, stream);
 }
 
 int lk_hip_attention_decode_part_f32(const float* qkv_part, int64_t slices, float* kc, float* vc, const int64_t* pos,
@@ -442,6 +625,35 @@ int lk_hip_attention_decode_part_f32(const float* qkv_part, int64_t slices, floa
                      dim3(64), 0, static_cast<hipStream_t>(stream), qkv_part, slices, kc, vc, pos, bias, chunk_part,
                      cap, heads, chunks, lkh::deviceErrorRecord());
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int lk_hip_lm_head_ln_argmax_f32(const float* part, int64_t slices, const float* bias, const float* res,
+                                 const float* gamma, const float* beta, float eps, const float* table, float* logits,
+                                 int64_t* argmax, int64_t rows, int64_t k, void* workspace, int64_t workspaceBytes,
+                                 void* stream) {
+  if (rows <= 0 || k <= 0 || k > 1024 || k % 4 != 0 || slices < 0 || (slices > 0 && !part)) return 1;
+  if (((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(res) |
+        reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta) | reinterpret_cast<uintptr_t>(table)) &
+       15) != 0)
+    return 1;
+  const int64_t grid = std::min<int64_t>(lkd::kLmGrid, (rows + 3) / 4);
+  if (!workspace || workspaceBytes < grid * 16) return 3;
+  auto* bestI = static_cast<int64_t*>(workspace);
+  auto* bestV = reinterpret_cast<float*>(bestI + grid);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int qpl = static_cast<int>((k / 4 + 63) / 64);
+#define LK_LM(Q)                                                                                                   \
+  hipLaunchKernelGGL(lkd::lmHeadLnKernel<Q>, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, part, slices, bias, \
+                     res, gamma, beta, eps, table, logits, bestV, bestI, rows, k)
+  switch (qpl) {
+    case 1: LK_LM(1); break;
+    case 2: LK_LM(2); break;
+    case 3: LK_LM(3); break;
+    default: LK_LM(4); break;
+  }
+#undef LK_LM
+  if (hipGetLastError() != hipSuccess) return 2;
+  return lk_hip_argmax_pairs_f32(bestV, bestI, argmax, grid, stream);
 }
 
 int lk_hip_reduce_ln_f32(const float* part, int64_t slices, const float* bias, const float* res, const float* gamma,
@@ -500,7 +712,7 @@ void runGemvPartialResLn(ExecCtx& ctx, const KernelArgs& a) {
   const float eps = a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1e-5f;
   if (lk_hip_gemv_partial_f32(3, nullptr, P<float>(a, 0), P<float>(a, 1), sx, 0, P<float>(a, 2), P<float>(a, 3),
                               P<float>(a, 4), P<float>(a, 7), eps, P<float>(a, 5), P<float>(a, 6), n, k, ctx.stream))
-    ctx.error = "gemv_partial_res_ln: K > 1024, N % 4 != 0 or unaligned operands";
+    ctx.error = "gemv_partial_res_ln: K > 1024, K or N not a multiple of 4, or unaligned operands";
 }
 
 // gemv_partial_ln_f32_gpu(x[1, K], gamma[K], beta[K], w[K, N]; eps) -> (part[S, N], copy of x [1, K]); x' = LN(x)
@@ -513,7 +725,7 @@ void runGemvPartialLn(ExecCtx& ctx, const KernelArgs& a) {
   const float eps = a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1e-5f;
   if (lk_hip_gemv_partial_f32(3, nullptr, nullptr, nullptr, 0, 0, P<float>(a, 0), P<float>(a, 1), P<float>(a, 2),
                               P<float>(a, 5), eps, P<float>(a, 3), P<float>(a, 4), n, k, ctx.stream))
-    ctx.error = "gemv_partial_ln: K > 1024, N % 4 != 0 or unaligned operands";
+    ctx.error = "gemv_partial_ln: K > 1024, K or N not a multiple of 4, or unaligned operands";
 }
 
 // attention_decode_part_f32_gpu(qkv_part[S, 3D], kc[cap, D], vc[cap, D], pos[1], bias[3D]; heads)
@@ -527,6 +739,38 @@ void runAttnDecodePart(ExecCtx& ctx, const KernelArgs& a) {
   if (lk_hip_attention_decode_part_f32(P<float>(a, 0), s, P<float>(a, 1), P<float>(a, 2), P<int64_t>(a, 3),
                                        P<float>(a, 4), P<float>(a, 5), cap, heads, ctx.stream))
     ctx.error = "attention_decode_part: launch failed";
+}
+
+// gemv_partial_embed_ln_f32_gpu(table[V, K], id[1], table2[P, K], id2[1], gamma[K], beta[K], w[K, N]; eps)
+//   -> (part[S, N], sum[1, K]); sum = table[id] + table2[id2], x = LN(sum)
+void runGemvPartialEmbedLn(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t v = a.ints[0], k = a.ints[1], p = a.ints[3], n = a.ints[9];
+  LK_REQUIRE(ctx, a.ints[2] == 1 && a.ints[4] == k && a.ints[5] == 1 && a.ints[6] == k && a.ints[7] == k &&
+                      a.ints[8] == k && a.ints[10] == lk_hip_gemv_partial_slices(k) && a.ints[11] == n &&
+                      a.ints[12] == 1 && a.ints[13] == k,
+             "gemv_partial_embed_ln: expected table [V, K], id [1], table2 [P, K], id2 [1], gamma [K], beta [K], "
+             "w [K, N]");
+  const float eps = a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1e-5f;
+  if (lk_hip_gemv_partial_embed_ln_f32(P<float>(a, 0), P<int64_t>(a, 1), P<float>(a, 2), P<int64_t>(a, 3), v, p,
+                                       P<float>(a, 4), P<float>(a, 5), eps, P<float>(a, 6), P<float>(a, 7),
+                                       P<float>(a, 8), n, k, ctx.stream))
+    ctx.error = "gemv_partial_embed_ln: K > 1024, K or N not a multiple of 4, or unaligned operands";
+}
+
+// lm_head_ln_argmax_f32_gpu(part[S, K], bias[K], res[1, K], gamma[K], beta[K], table[V, K]; eps)
+//   -> (logits[1, V], argmax i64[1]); logits = LN(slices of part + bias + res) . table^T
+void runLmHeadLnArgmax(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t s = a.ints[0], k = a.ints[1], v = a.ints[7];
+  LK_REQUIRE(ctx, a.ints[2] == k && a.ints[3] == 1 && a.ints[4] == k && a.ints[5] == k && a.ints[6] == k &&
+                      a.ints[8] == k && a.ints[9] == 1 && a.ints[10] == v && a.ints[11] == 1,
+             "lm_head_ln_argmax: expected part [S, K], bias [K], res [1, K], gamma [K], beta [K], table [V, K]");
+  const float eps = a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1e-5f;
+  const int rc = lk_hip_lm_head_ln_argmax_f32(P<float>(a, 0), s, P<float>(a, 1), P<float>(a, 2), P<float>(a, 3),
+                                              P<float>(a, 4), eps, P<float>(a, 5), P<float>(a, 6), P<int64_t>(a, 7),
+                                              v, k, ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes),
+                                              ctx.stream);
+  status(ctx, rc, rc == 3 ? "lm_head_ln_argmax: workspace too small"
+                          : "lm_head_ln_argmax: K > 1024, K not a multiple of 4, or unaligned operands");
 }
 
 // reduce_bias_res_ln2_f32_gpu(part[S, N], bias[N], res[1, N], gamma[N], beta[N]; eps) -> (sum[1, N], ln[1, N])
@@ -551,6 +795,8 @@ void registerDecodeFusedKernels() {
   registerKernel({"gemv_partial_ln_f32_gpu", G, runGemvPartialLn, 4, 2});
   registerKernel({"attention_decode_part_f32_gpu", G, runAttnDecodePart, 5, 1});
   registerKernel({"reduce_bias_res_ln2_f32_gpu", G, runReduceLn, 5, 2});
+  registerKernel({"gemv_partial_embed_ln_f32_gpu", G, runGemvPartialEmbedLn, 7, 2});
+  registerKernel({"lm_head_ln_argmax_f32_gpu", G, runLmHeadLnArgmax, 6, 2});
 }
 
 }  // namespace lkh

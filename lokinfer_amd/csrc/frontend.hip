@@ -114,6 +114,13 @@ int lk_hip_embedding_f32(const float* table, const int64_t* ids, const float* ta
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
+int lk_hip_argmax_pairs_f32(const float* values, const int64_t* indices, int64_t* out, int64_t n, void* stream) {
+  if (n <= 0) return 1;
+  hipLaunchKernelGGL(lkd::argmaxKernel, dim3(1, 1), dim3(256), 0, static_cast<hipStream_t>(stream), values, indices,
+                     nullptr, nullptr, out, n, n);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
 int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, void* workspace,
                       int64_t workspaceBytes, void* stream) {
   if (rows <= 0 || n <= 0) return 1;

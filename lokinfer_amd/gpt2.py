@@ -19,7 +19,10 @@ projections into bias + residual + LayerNorm).
 By default (fused=True) each layer runs the same arithmetic in 5 launches instead of 13: the GEMVs write
 row-slice partial sums and the consumer of each GEMV sums the slices itself (the decode-attention chunk kernel
 for qkv; the next partial GEMV for the attention merge, for gelu(c_fc) and for bias + residual + LayerNorm, the
-new residual stream written by one of its workgroups). fused=False keeps the reference's op sequence.
+new residual stream written by one of its workgroups). The embedding lookups and LN_1 of layer 0 open the first
+partial GEMV, and ln_f, the LM head and the argmax are one op (a row-dot pass that also leaves per-workgroup
+(max, index) pairs, then a one-workgroup pass over the pairs): 62 launches per step. fused=False keeps the
+reference's op sequence.
 """
 from __future__ import annotations
 
@@ -74,13 +77,14 @@ class Gpt2Decoder:
     def _step(self, tok: Tensor, pos: Tensor):
         w = self.w
         P = "transformer."
-        h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos)
         if self.fused:
             # 5 launches per layer: each GEMV writes row-slice partial sums and its consumer reduces them (the
             # decode-attention chunk kernel for qkv, the next partial GEMV for the attention merge, for gelu(c_fc)
-            # and for bias + residual + LayerNorm)
-            qp, h = ops.gemv_partial_ln_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"],
-                                                w[P + "h.0.attn.c_attn.weight"], eps=LN_EPS)
+            # and for bias + residual + LayerNorm); the embedding lookups open the first GEMV, and the last
+            # LayerNorm and the argmax are folded into the LM head
+            qp, h = ops.gemv_partial_embed_ln_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos,
+                                                      w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"],
+                                                      w[P + "h.0.attn.c_attn.weight"], eps=LN_EPS)
             for i, (kc, vc) in enumerate(self.caches):
                 L = f"{P}h.{i}."
                 ch = ops.attention_decode_part_f32_gpu(qp, kc, vc, pos, w[L + "attn.c_attn.bias"], heads=HEADS)
@@ -94,10 +98,9 @@ class Gpt2Decoder:
                                                             w[N + "ln_1.bias"], w[N + "attn.c_attn.weight"],
                                                             eps=LN_EPS)
                 else:
-                    h, ln = ops.reduce_bias_res_ln2_f32_gpu(mp, w[L + "mlp.c_proj.bias"], h, w[P + "ln_f.weight"],
-                                                            w[P + "ln_f.bias"], eps=LN_EPS)
-            logits = ops.gemm_nt_f32_gpu_mps(ln, w[P + "wte.weight"])
-            return logits, ops.argmax_f32_gpu(logits)
+                    return ops.lm_head_ln_argmax_f32_gpu(mp, w[L + "mlp.c_proj.bias"], h, w[P + "ln_f.weight"],
+                                                         w[P + "ln_f.bias"], w[P + "wte.weight"], eps=LN_EPS)
+        h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos)
         ln = ops.layernorm_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"], eps=LN_EPS)
         for i, (kc, vc) in enumerate(self.caches):
             L = f"{P}h.{i}."

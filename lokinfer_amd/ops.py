@@ -509,8 +509,8 @@ def gemv_partial_res_ln_f32_gpu(xpart, xbias, res, gamma, beta, w, eps=1e-5):
     s is returned as the new residual stream."""
     _f32(xpart, res, w, rank=2)
     k = xpart.shape[1]
-    check(tuple(res.shape) == (1, k) and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024,
-          "expected res [1, K], w [K, N] with N % 4 == 0, K <= 1024")
+    check(tuple(res.shape) == (1, k) and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024 and k % 4 == 0,
+          "expected res [1, K], w [K, N] with N % 4 == 0, K % 4 == 0, K <= 1024")
     for v in (xbias, gamma, beta):
         _bias_ok(v, k)
     return _launch("gemv_partial_res_ln_f32_gpu", [xpart, xbias, res, gamma, beta, w],
@@ -521,12 +521,40 @@ def gemv_partial_ln_f32_gpu(x, gamma, beta, w, eps=1e-5):
     """(part, x'): partial GEMV of LN(x) for x f32[1, K], K <= 1024 (x' is a copy of x)."""
     _f32(x, w, rank=2)
     k = x.shape[1]
-    check(x.shape[0] == 1 and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024,
-          "expected x [1, K], w [K, N] with N % 4 == 0, K <= 1024")
+    check(x.shape[0] == 1 and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024 and k % 4 == 0,
+          "expected x [1, K], w [K, N] with N % 4 == 0, K % 4 == 0, K <= 1024")
     for v in (gamma, beta):
         _bias_ok(v, k)
     return _launch("gemv_partial_ln_f32_gpu", [x, gamma, beta, w], [(gemv_partial_slices(k), w.shape[1]), (1, k)],
                    dict(eps=float(eps)))
+
+
+def gemv_partial_embed_ln_f32_gpu(table, ids, table2, ids2, gamma, beta, w, eps=1e-5):
+    """(part, s): partial GEMV of LN(s) with s = table[ids] + table2[ids2] f32[1, K] (the layer-0 prologue of a
+    decode step: token + position embedding, LayerNorm, first GEMV); s is returned as the residual stream."""
+    _f32(table, table2, w, rank=2)
+    k = table.shape[1]
+    check(table2.shape[1] == k and w.shape[0] == k and w.shape[1] % 4 == 0 and k <= 1024 and k % 4 == 0,
+          "expected table [V, K], table2 [P, K], w [K, N] with N % 4 == 0, K % 4 == 0, K <= 1024")
+    for ix in (ids, ids2):
+        check(ix.dtype == i64 and tuple(ix.shape) == (1,), "ids must be i64[1]")
+    for v in (gamma, beta):
+        _bias_ok(v, k)
+    return _launch("gemv_partial_embed_ln_f32_gpu", [table, ids, table2, ids2, gamma, beta, w],
+                   [(gemv_partial_slices(k), w.shape[1]), (1, k)], dict(eps=float(eps)))
+
+
+def lm_head_ln_argmax_f32_gpu(part, bias, res, gamma, beta, table, eps=1e-5):
+    """(logits f32[1, V], argmax i64[1]): logits = LN(s) @ table^T with s = (slices of part f32[S, K]) + bias + res
+    (final LayerNorm + tied LM head + greedy argmax of a decode step); argmax is the first index of the maximum."""
+    _f32(part, res, table, rank=2)
+    k = part.shape[1]
+    check(tuple(res.shape) == (1, k) and table.shape[1] == k and k <= 1024 and k % 4 == 0,
+          "expected part [S, K], res [1, K], table [V, K], K % 4 == 0, K <= 1024")
+    for v in (bias, gamma, beta):
+        _bias_ok(v, k)
+    return _launch("lm_head_ln_argmax_f32_gpu", [part, bias, res, gamma, beta, table], [(1, table.shape[0]), (1,)],
+                   dict(eps=float(eps)), out_dtypes=[f32, i64])
 
 
 def attention_decode_part_f32_gpu(qkv_part, kcache, vcache, pos, bias, heads):

@@ -385,6 +385,53 @@ def test_gemv_partial_res_ln(gpu):
     close(part2.numpy().sum(0)[None], K.gemm(K.layernorm(res, g, b, 1e-5), w), 2e-5)
 
 
+def test_gemv_partial_embed_ln(gpu):
+    lk = gpu
+    v, p, k, n = 97, 40, 768, 2304
+    wte, wpe = rng.standard_normal((v, k)), rng.standard_normal((p, k))
+    g, b = rng.standard_normal(k), rng.standard_normal(k)
+    w = rng.standard_normal((k, n)) / np.sqrt(k)
+    WTE, WPE = G(lk, wte), G(lk, wpe)
+    ids = lambda i: lk.from_numpy(np.array([i], np.int64), device="gpu", copy=True)
+    for tok, pos in ((5, 0), (96, 39)):
+        part, s = lk.ops.gemv_partial_embed_ln_f32_gpu(WTE, ids(tok), WPE, ids(pos), G(lk, g), G(lk, b), G(lk, w),
+                                                       1e-5)
+        h = (wte[tok].astype(np.float32) + wpe[pos].astype(np.float32))[None]
+        close(s, h, 0)  # one f32 add per element: exact
+        close(part.numpy().sum(0)[None], K.gemm(K.layernorm(h, g, b, 1e-5), w), 2e-5)
+    part, s = lk.ops.gemv_partial_embed_ln_f32_gpu(WTE, ids(v), WPE, ids(0), G(lk, g), G(lk, b), G(lk, w), 1e-5)
+    with pytest.raises(lk.LokinferError, match="device error 3"):
+        s.numpy()
+
+
+@pytest.mark.parametrize("v", [50257, 10, 4099])
+def test_lm_head_ln_argmax(gpu, v):
+    lk = gpu
+    k = 768
+    x, w0 = rng.standard_normal((1, 3072)), rng.standard_normal((3072, k)) / 55
+    bias, res, g, b = rng.standard_normal(k), rng.standard_normal((1, k)), rng.standard_normal(k), rng.standard_normal(k)
+    table = rng.standard_normal((v, k)) * 0.02
+    xp = lk.ops.gemv_partial_f32_gpu(G(lk, x), G(lk, w0))
+    logits, am = lk.ops.lm_head_ln_argmax_f32_gpu(xp, G(lk, bias), G(lk, res), G(lk, g), G(lk, b), G(lk, table), 1e-5)
+    _, ln = K.add_bias_layernorm2(K.gemm(x, w0), bias, res, g, b, 1e-5)
+    ref = K.gemm(ln, table, nt=True)
+    close(logits, ref, 2e-5)
+    got = logits.numpy()
+    assert am.numpy().tolist() == [int(np.argmax(got[0]))]
+    assert int(am.numpy()[0]) == int(np.argmax(ref[0]))
+    if v > 3000:
+        # ties go to the first index: copy the winning row to a lower and a higher index
+        t2 = table.copy()
+        best = int(np.argmax(ref[0]))
+        t2[3] = t2[best]
+        t2[v - 1] = t2[best]
+        logits2, am2 = lk.ops.lm_head_ln_argmax_f32_gpu(xp, G(lk, bias), G(lk, res), G(lk, g), G(lk, b), G(lk, t2),
+                                                        1e-5)
+        l2 = logits2.numpy()[0]
+        assert l2[3] == l2[best] == l2[v - 1]
+        assert am2.numpy().tolist() == [3]
+
+
 # At least 256 output tiles of 128 x 128: the only shapes that select convTapKernel<128, 128>, whose epilogue
 # writes the 128-row channel statistics itself (the Kokoro-487 decoder and generator sizes).
 @pytest.mark.parametrize("l,ci,co,k,dil,act", [(5000, 1104, 1024, 3, 1, "leaky"), (40000, 128, 128, 7, 3, "snake"),
