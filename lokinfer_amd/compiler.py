@@ -76,19 +76,24 @@ class _Entry:
 class CapturedModel:
     """A function replayed from torch stream capture, one graph per input-shape signature (see `capture`)."""
 
-    def __init__(self, fn, use_graph: bool = True, mutable: tuple = ()):
+    MAX_ENTRIES = 16  # graphs kept per model (least recently used dropped first)
+
+    def __init__(self, fn, use_graph: bool = True, mutable: tuple = (), by_ref: tuple = ()):
         self.fn = fn
         self.use_graph = use_graph
-        self.mutable = tuple(mutable)
+        self.mutable = tuple(sorted(set(mutable) | set(by_ref)))
         self._entries: dict[tuple, _Entry] = {}
 
     def _entry(self, args) -> _Entry:
-        # a mutable input is part of the signature by address: the captured graph writes that buffer
+        # an input bound by reference is part of the signature by address: the captured graph reads (or writes)
+        # that buffer itself
         key = _sig(args) + tuple(args[i].t.data_ptr() for i in self.mutable)
-        e = self._entries.get(key)
+        e = self._entries.pop(key, None)
         if e is None:
+            if len(self._entries) >= self.MAX_ENTRIES:
+                self._entries.pop(next(iter(self._entries)))
             e = _Entry(self.fn, list(args), self.use_graph, self.mutable)
-            self._entries[key] = e
+        self._entries[key] = e  # most recently used last
         return e
 
     def run_inplace(self, *args):
@@ -103,10 +108,12 @@ class CapturedModel:
         return res[0] if len(res) == 1 else tuple(res)
 
 
-def capture(fn, inputs=None, graph: bool = True, mutable: tuple = ()) -> CapturedModel:
+def capture(fn, inputs=None, graph: bool = True, mutable: tuple = (), by_ref: tuple = ()) -> CapturedModel:
     """Stream-captured `fn`: shapes are bound per call signature. `mutable`: indices of the inputs that the function
-    writes in place (the reference's lk.MutableType inputs): bound by reference, one entry per buffer."""
-    m = CapturedModel(fn, use_graph=graph, mutable=mutable)
+    writes in place (the reference's lk.MutableType inputs): bound by reference, one entry per buffer. `by_ref`:
+    read-only inputs bound the same way, so that a call with the same buffers replays with no input copy (the
+    other inputs are copied into the graph's own buffers on every call)."""
+    m = CapturedModel(fn, use_graph=graph, mutable=mutable, by_ref=by_ref)
     if inputs is not None:
         m._entry(list(inputs))
     return m

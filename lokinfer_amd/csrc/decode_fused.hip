@@ -37,11 +37,17 @@ inline int64_t gemvRowsPerWave(int64_t k) { return k <= 1024 ? 16 : 64; }
 #ifndef LK_GEMV_MIN_WGS
 #define LK_GEMV_MIN_WGS 256
 #endif
-// Column block of the partial GEMV: the widest of 256 / 128 / 64 columns whose grid still has LK_GEMV_MIN_WGS
+// A LayerNorm prologue (modes 3, 4) makes every workgroup load all slices of the whole input row (48 KB at
+// K = 768), more than its share of the weights: those GEMVs take wider column blocks, hence fewer workgroups.
+// GPT-2 decode, ms per step by this floor: 256 -> 0.3145, 200 -> 0.306, 128 -> 0.298, 64 -> 0.3085.
+#ifndef LK_GEMV_MIN_WGS_LN
+#define LK_GEMV_MIN_WGS_LN 128
+#endif
+// Column block of the partial GEMV: the widest of 256 / 128 / 64 columns whose grid still has minWgs
 // workgroups, else 64.
-inline int gemvColBlock(int64_t n, int64_t slices) {
+inline int gemvColBlock(int64_t n, int64_t slices, int minWgs) {
   for (int cb = 256; cb > 64; cb /= 2)
-    if (lkh::ceilDiv(n, cb) * slices >= LK_GEMV_MIN_WGS) return cb;
+    if (lkh::ceilDiv(n, cb) * slices >= minWgs) return cb;
   return 64;
 }
 
@@ -293,11 +299,13 @@ __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restr
   const int64_t D = static_cast<int64_t>(heads) * kDecHd, ld = 3 * D;
   float* part = cpart + (static_cast<int64_t>(h) * chunks + s) * kPartStride;
   const int64_t c4 = h * kDecHd + 4 * d4;  // this lane's 4 dims in a row of q, k or v
-  // q / k / v partial rows (slices in order; 12 issued at once, more in a tail loop)
-  f4v pq[kFastSlices], pk[kFastSlices], pv[kFastSlices];
+  // q / k / v partial rows: row g of the wave loads slices g, g + 4, g + 8 (issued at once; more in a tail
+  // loop), the 4 row sums then combine as (r0 + r1) + (r2 + r3)
+  constexpr int kRowSlices = kFastSlices / 4;
+  f4v pq[kRowSlices], pk[kRowSlices], pv[kRowSlices];
 #pragma unroll
-  for (int i = 0; i < kFastSlices; ++i) {
-    const float* row = qpart + min<int64_t>(i, slices - 1) * ld + c4;
+  for (int i = 0; i < kRowSlices; ++i) {
+    const float* row = qpart + min<int64_t>(g + 4 * i, slices - 1) * ld + c4;
     pq[i] = *reinterpret_cast<const f4v*>(row);
     pk[i] = *reinterpret_cast<const f4v*>(row + D);
     pv[i] = *reinterpret_cast<const f4v*>(row + 2 * D);
@@ -322,18 +330,21 @@ __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restr
   }
   f4v sq = {0.f, 0.f, 0.f, 0.f}, sk = sq, sv = sq;
 #pragma unroll
-  for (int i = 0; i < kFastSlices; ++i)
-    if (i < slices) {
+  for (int i = 0; i < kRowSlices; ++i)
+    if (g + 4 * i < slices) {
       sq += pq[i];
       sk += pk[i];
       sv += pv[i];
     }
-  for (int64_t sl = kFastSlices; sl < slices; ++sl) {
+  for (int64_t sl = kFastSlices + g; sl < slices; sl += 4) {
     const float* row = qpart + sl * ld + c4;
     sq += *reinterpret_cast<const f4v*>(row);
     sk += *reinterpret_cast<const f4v*>(row + D);
     sv += *reinterpret_cast<const f4v*>(row + 2 * D);
   }
+  sq = f4v{crossRowSum(sq.x), crossRowSum(sq.y), crossRowSum(sq.z), crossRowSum(sq.w)};
+  sk = f4v{crossRowSum(sk.x), crossRowSum(sk.y), crossRowSum(sk.z), crossRowSum(sk.w)};
+  sv = f4v{crossRowSum(sv.x), crossRowSum(sv.y), crossRowSum(sv.z), crossRowSum(sv.w)};
   const f4v q = (sq + bq) * 0.125f;
   const f4v knew = sk + bk;
   const f4v vnew = sv + bv;
@@ -558,7 +569,7 @@ int launchGemvPartial(int xmode, const float* x, const float* xpart, const float
   if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(part)) & 15) != 0) return 1;
   const int64_t rpw = lkd::gemvRowsPerWave(k);
   const int64_t slices = (k + 4 * rpw - 1) / (4 * rpw);
-  const int cb = lkd::gemvColBlock(n, slices);
+  const int cb = lkd::gemvColBlock(n, slices, xmode >= 3 ? LK_GEMV_MIN_WGS_LN : LK_GEMV_MIN_WGS);
   const dim3 grid(lkh::ceilDiv(n, cb), static_cast<unsigned>(slices));
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define LK_GP_CB(MODE, R, CB) \

@@ -72,7 +72,11 @@ class Gpt2Decoder:
         self.caches = [(Tensor(torch.zeros(N_POS, D, device=dev)), Tensor(torch.zeros(N_POS, D, device=dev)))
                        for _ in range(N_LAYER)]
         self.fused = fused
-        self.step_model = lk_capture(self._step, graph=graph)
+        # the step graph reads tok and pos from these two buffers in place (a caller that writes them itself, as
+        # a serving loop does, replays with no input copy)
+        self.tok = Tensor(torch.zeros(1, dtype=torch.int64, device=dev))
+        self.pos = Tensor(torch.zeros(1, dtype=torch.int64, device=dev))
+        self.step_model = lk_capture(self._step, graph=graph, by_ref=(0, 1))
 
     def _step(self, tok: Tensor, pos: Tensor):
         w = self.w
@@ -119,8 +123,12 @@ class Gpt2Decoder:
 
     def step(self, tok: Tensor, pos: Tensor):
         """One decode step; returns (logits f32[1, 50257], argmax i64[1]) as the graph's output buffers
-        (overwritten by the next step)."""
-        return self.step_model.run_inplace(tok, pos)
+        (overwritten by the next step). tok and pos are copied into self.tok / self.pos unless they are those
+        buffers."""
+        for src, dst in ((tok, self.tok), (pos, self.pos)):
+            if src.t.data_ptr() != dst.t.data_ptr():
+                dst.t.copy_(src.t.reshape(1))
+        return self.step_model.run_inplace(self.tok, self.pos)
 
     def prefill(self, ids: np.ndarray) -> None:
         """Fills the caches by stepping the prompt tokens at positions 0..len-1."""
