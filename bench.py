@@ -26,6 +26,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes one GPT-2 decode step at pos 512 must read: per layer the 4 weight matrices, their biases and the two
+# LayerNorms; the tied LM head (wte); ln_f; the token and position rows; K and V rows 0..512 of 12 layers (f32)
+GPT2_STEP_BYTES = 4 * (12 * (768 * 2304 + 768 * 768 + 2 * 768 * 3072 + 2304 + 768 + 3072 + 768 + 4 * 768)
+                       + 50257 * 768 + 2 * 768 + 2 * 768 + 12 * 2 * 513 * 768)
 F32_MFMA_PEAK_TFLOPS = 157.3
 
 
@@ -86,25 +90,105 @@ def bench_gpt2(steps: int, warmup: int, cpu: bool = True) -> dict:
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     per = event_times(lambda: dec.step(tok, pos), max(steps, 20))
-    # dominant kernel: the tied LM head (gemm_nt at M = 1: one wave per wte row), 50257 x 768 f32 = 154.4 MB
-    ln = lk.from_numpy(np.random.default_rng(0).standard_normal((1, 768)).astype(np.float32), device="gpu")
+    # dominant kernel: the step's tail op (ln_f + tied LM head + argmax: lmHeadLnKernel, one wave per 4-row half
+    # over wte, then the one-workgroup pass over the per-workgroup (max, index) pairs); 50257 x 768 f32 = 154.4 MB
+    rng = np.random.default_rng(0)
+    part = lk.from_numpy(rng.standard_normal((12, 768)).astype(np.float32), device="gpu", copy=True)
+    vec = lambda: lk.from_numpy(rng.standard_normal(768).astype(np.float32), device="gpu", copy=True)  # noqa: E731
+    bias, gamma, beta = vec(), vec(), vec()
+    res = lk.from_numpy(rng.standard_normal((1, 768)).astype(np.float32), device="gpu", copy=True)
     wte = dec.w["transformer.wte.weight"]
-    lk.ops.gemm_nt_f32_gpu_mps(ln, wte)
-    kt = statistics.mean(event_times(lambda: lk.ops.gemm_nt_f32_gpu_mps(ln, wte), 50))
-    lm_bytes = 50257 * 768 * 4 + 768 * 4 + 50257 * 4
+    tables = [wte] + [lk.Tensor(wte.t.clone()) for _ in range(2)]  # 463 MB in turn: every call reads HBM
+    kt = graph_ms([lambda t=t: lk.ops.lm_head_ln_argmax_f32_gpu(part, bias, res, gamma, beta, t) for t in tables])
+    del tables
+    lm_bytes = 50257 * 768 * 4 + (12 + 5) * 768 * 4 + 50257 * 4
     res = {
         "median_ms": statistics.median(per), "wall_ms_per_step": wall_ms,
-        "roofline": {"kernel": "rowdotKernel<1> (gemm_nt_f32_gpu_mps, LM head)", "bound": "hbm",
+        "roofline": {"kernel": "lmHeadLnKernel<3> + argmax pass (lm_head_ln_argmax_f32_gpu: ln_f, tied LM head, "
+                               "argmax)", "bound": "hbm",
                      "achieved": lm_bytes / (kt * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": lm_bytes / (kt * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
                      "avg_launch_ms": kt, "bytes_per_launch": lm_bytes},
-        "step_bytes": 532.4e6,
+        "step_bytes": GPT2_STEP_BYTES,
         "prefill512_ms": statistics.median(pre),
         "prefill512_tflops": PREFILL512_FLOPS / (statistics.median(pre) * 1e-3) / 1e12,
     }
     if cpu:
         res["cpu_baseline"] = cpu_gpt2(sd, ids, nxt)
     return res
+
+
+def graph_ms(fn, n: int = 21, reps: int = 7) -> float:
+    """Milliseconds per call of fn() replayed n times from one captured graph (median over reps replays): the
+    device time per call, launch gaps included, without the host's per-call cost. fn may be a list of functions,
+    called in turn (operands rotated through more memory than the 256 MB last-level cache holds)."""
+    fns = fn if isinstance(fn, (list, tuple)) else [fn]
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        fns[0]()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(n):
+                fns[i % len(fns)]()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / n)
+    del g
+    return statistics.median(times)
+
+
+def bench_decode_attention() -> dict:
+    """Decode attention against its HBM roofline: bytes = the K and V rows read, 2 (pos + 1) D x element size,
+    over the per-call time of the kernel(s) replayed from a graph, with the calls rotated over enough cache copies
+    (> 400 MB) that every call reads HBM, as in a decode step whose weight stream evicts the caches. Cases: the
+    GPT-2 step's chunk kernel (attention_decode_part_f32_gpu: q / k / v from GEMV partials, 12 heads, 1024-row
+    caches) at pos 512 and 1023; the split decode attention (attention_decode_split_f32_gpu: chunk + merge
+    launches) on a 32768-row cache, where the K / V stream is long enough to be bandwidth-bound; Qwen3's f16 GQA
+    decode (attention_gqa_opt_f16_gpu, 16 / 8 heads x 128) at its config-5 position 416 and on a 32768-row cache."""
+    import lokinfer_amd as lk
+    from lokinfer_amd import f16_gpu as F
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    T = lambda *shape, dt=torch.float32: lk.Tensor(torch.randn(*shape, device=dev, generator=gen).to(dt))  # noqa
+    P = lambda v: lk.Tensor(torch.tensor([v], dtype=torch.int64, device=dev))  # noqa: E731
+    out = {}
+
+    def case(name, make, call, pos, cap, d, elem):
+        nbytes = 2 * (pos + 1) * d * elem
+        copies = max(1, -(-400_000_000 // (2 * cap * d * elem)))
+        caches = [make() for _ in range(copies)]
+        ms = graph_ms([lambda c=c: call(*c) for c in caches], n=max(21, copies))
+        del caches
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(ms * 1e3, 2), "bytes": nbytes, "achieved_gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    heads, d = 12, 768
+    qp, qkv, bias = T(12, 3 * d), T(1, 3 * d), T(3 * d)
+    for pos in (512, 1023):
+        pt = P(pos)
+        case(f"gpt2_step_chunk_pos{pos}", lambda: (T(1024, d), T(1024, d)),
+             lambda kc, vc, pt=pt: lk.ops.attention_decode_part_f32_gpu(qp, kc, vc, pt, bias, heads), pos, 1024, d, 4)
+    cap = 32768
+    pt = P(cap - 1)
+    case(f"split_f32_pos{cap - 1}", lambda: (T(cap, d), T(cap, d)),
+         lambda kc, vc: lk.ops.attention_decode_split_f32_gpu(qkv, kc, vc, pt, bias, heads), cap - 1, cap, d, 4)
+    q = T(1, 2048, dt=torch.float16)
+    for cap, pos in ((480, 416), (32768, 32767)):
+        pt = P(pos)
+        case(f"qwen3_gqa_f16_pos{pos}", lambda cap=cap: (T(cap, 1024, dt=torch.float16), T(cap, 1024, dt=torch.float16)),
+             lambda kc, vc, pt=pt: F.attention_gqa_opt_f16_gpu(q, kc, vc, pt, q_heads=16, kv_heads=8), pos, cap, 1024, 2)
+    return out
 
 
 def cpu_gpt2(sd, ids, nxt, budget_s: float = 15.0) -> dict:
@@ -318,7 +402,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["all", "kokoro487", "kokoro59", "gpt2", "qwen3"])
+    ap.add_argument("--workload", default="all", choices=["all", "kokoro487", "kokoro59", "gpt2", "qwen3", "decode_attn"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="launch only the roofline kernel (and the copy-calibration kernel), for rocprofv3 runs")
@@ -363,19 +447,28 @@ def main():
             "roofline_kernel": r["roofline"]["kernel"], "cpu_baseline": r.get("cpu_baseline"),
             "gpt2_prefill512_ms": round(r["prefill512_ms"], 4),
             "gpt2_prefill512_tflops": round(r["prefill512_tflops"], 2),
+            "gpt2_step_hbm_frac": round(GPT2_STEP_BYTES / (r["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "decode_attention_roofline": bench_decode_attention(),
         }
         print(json.dumps(line))
+        return
+    if wl == "decode_attn":  # the decode-attention leg alone (for rocprofv3 runs)
+        print(json.dumps({"decode_attention_roofline": bench_decode_attention()}))
         return
     tokens = 59 if wl == "kokoro59" else 487
     r = bench_kokoro(tokens, a.steps, a.warmup)
     extra = {}
     if wl == "all":
         r59 = bench_kokoro(59, a.steps, a.warmup)
-        g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=False)
+        g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=not a.no_cpu)
         extra = {"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
-                 "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_lm_head_roofline": g["roofline"],
+                 "kokoro59_cpu_baseline": None if a.no_cpu else cpu_kokoro(r59["sd"], r59["inputs"], budget_s=10.0),
+                 "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_decode_cpu_baseline": g.get("cpu_baseline"),
+                 "gpt2_step_hbm_frac": round(GPT2_STEP_BYTES / (g["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "gpt2_lm_head_roofline": g["roofline"],
                  "gpt2_prefill512_ms": round(g["prefill512_ms"], 4),
-                 "gpt2_prefill512_tflops": round(g["prefill512_tflops"], 2)}
+                 "gpt2_prefill512_tflops": round(g["prefill512_tflops"], 2),
+                 "decode_attention_roofline": bench_decode_attention()}
     roof = roofline_wino()
     cpu = None if a.no_cpu else cpu_kokoro(r["sd"], r["inputs"])
     line = {

@@ -91,7 +91,9 @@ int lk_hip_layernorm_f32(const float* a, const float* bias, const float* r, cons
 int lk_hip_bias_gelu_f32(const float* x, const float* bias, float* out, int64_t rows, int64_t cols, void* stream);
 int lk_hip_attention_qkv_f32(const float* qkv, const float* bias, float* out, int64_t t, int heads, int causal,
                              void* stream);
-/* split-key decode attention (64-key chunks + merge launch); pos is a device i64[1] */
+/* split-key decode attention (waves of 64-key chunks, then a merge launch); pos is a device i64[1]. Up to 8192
+ * keys each wave takes one chunk; beyond, each wave takes ceil(chunks / 128) chunks, combined online, so a head
+ * has at most 128 partials (workspace: heads * waves * 66 floats, lk_hip_attention_decode_workspace_bytes) */
 int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap);
 int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
                                 float* out, int64_t cap, int heads, int64_t max_keys, int write_kv, void* workspace,
@@ -99,7 +101,7 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
 /* Allocation-free variant of lk_hip_attention_decode_f32 (no counterpart in the reference): for callers that
  * cannot allocate device memory (HIP graph capture of a serving loop, harnesses that forbid hipMalloc). The chunk
  * partials go to a fixed 2 MiB device array the library holds on each GPU for the life of the process
- * (lk_hip_attention_decode_noalloc_max_floats() floats: heads * ceil(max_keys / 64) * 66 must fit), so it calls no
+ * (lk_hip_attention_decode_noalloc_max_floats() floats: heads * waves * 66 must fit, waves as above), so it calls no
  * hipMalloc. Returns 4 when the call does not fit. Calls that overlap on one GPU race on that array. */
 int64_t lk_hip_attention_decode_noalloc_max_floats(void);
 int lk_hip_attention_decode_f32_noalloc(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,

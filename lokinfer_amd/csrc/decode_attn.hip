@@ -2,15 +2,12 @@
 // attention_decode_kvw_f32_gpu, transformer_gpu.cpp:122-222, kokoro_tok.metal:637-876 in lariaus/lokinfer).
 //
 // One query (heads x 64) attends over cache rows 0..pos; row pos is k, v (+ bias) of this step and is written
-// into both caches. Keys are split into 64-key chunks, one wave per (head, chunk):
-//   scores  lane j owns key kb + j: a 64-float dot with q (16 independent float4 loads per lane)
-//   softmax chunk max / sum with wave64 shuffles (base-e, q pre-scaled by 1/8 = 1/sqrt(64))
-//   P.V     lane = (key group g in 0..3, dim quad d4 in 0..15): 16 keys per lane as float4 loads, then a 2-step
-//           shuffle reduction over g
-// Partials (m, l, acc[64]) go to the caller's workspace; a second launch merges the chunks of each head in
-// chunk order (flash-decoding). Every load of a chunk is issued before its first use, so a wave waits on HBM
-// twice (K rows, V rows) instead of once per key.
+// into both caches. Keys are split into 64-key chunks, one wave per (head, chunk) (DecodeChunk: coalesced row
+// loads, DPP row sums for the scores, base-e softmax on q / 8 = q / sqrt(64), P.V in registers). Partials
+// (m, l, acc[64]) go to the caller's workspace; a second launch merges the chunks of each head in chunk order
+// (flash-decoding).
 #include "common.h"
+#include "decode_chunk.h"
 #include "lokinfer_hip.h"
 
 #include <mutex>
@@ -30,7 +27,8 @@ struct DecodeParams {
   float* partial;  // [heads, chunks, 66]
   int64_t cap;
   int heads;
-  int chunks;
+  int chunks;  // partials per head: waves per head
+  int sub;     // 64-key chunks per wave
   int writeKv;
   unsigned long long* err;  // the GPU's error record
 };
@@ -38,125 +36,105 @@ struct DecodeParams {
 __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   const int h = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
   const int64_t D = static_cast<int64_t>(p.heads) * kHd;
+  const int64_t c4 = h * kHd + 4 * (lane & 15);  // this lane's 4 dims in a row of q, k or v
+  const float4 q4 = *reinterpret_cast<const float4*>(p.qkv + c4);
+  const float4 k4 = *reinterpret_cast<const float4*>(p.qkv + D + c4);
+  const float4 v4 = *reinterpret_cast<const float4*>(p.qkv + 2 * D + c4);
+  const float4 bq = *reinterpret_cast<const float4*>(p.bias + c4);
+  const float4 bk = *reinterpret_cast<const float4*>(p.bias + D + c4);
+  const float4 bv = *reinterpret_cast<const float4*>(p.bias + 2 * D + c4);
   const int64_t pos = *p.pos;
-  if (pos < 0 || pos >= p.cap) {  // out-of-range position: no cache write, recorded; the merge writes NaN
-    if (h == 0 && s == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, pos);
-    return;
+  DecodeChunk ch;
+  ch.load(p.kc, p.vc, pos, p.cap, s * p.sub, D, c4);
+  // an out-of-range position writes no cache row and NaN partials, and is recorded; the merge writes NaN
+  if (ch.badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, pos);
+  const decF4 q = decF4{q4.x + bq.x, q4.y + bq.y, q4.z + bq.z, q4.w + bq.w} * 0.125f;
+  const decF4 knew = {k4.x + bk.x, k4.y + bk.y, k4.z + bk.z, k4.w + bk.w};
+  const decF4 vnew = {v4.x + bv.x, v4.y + bv.y, v4.z + bv.z, v4.w + bv.w};
+  if (p.writeKv && ch.writesRow()) {
+    *reinterpret_cast<decF4*>(p.kc + pos * D + c4) = knew;
+    *reinterpret_cast<decF4*>(p.vc + pos * D + c4) = vnew;
   }
-  const int64_t kb = static_cast<int64_t>(s) * kChunk;
-  const int64_t ke = min<int64_t>(pos + 1, kb + kChunk);
-  float* part = p.partial + (static_cast<int64_t>(h) * p.chunks + s) * (kHd + 2);
-  const float* qrow = p.qkv + h * kHd;
-  const float* bq = p.bias + h * kHd;
-  const float* bk = p.bias + D + h * kHd;
-  const float* bv = p.bias + 2 * D + h * kHd;
-  if (kb >= ke) {  // chunk past the live keys
-    if (lane == 0) {
-      part[0] = -INFINITY;
-      part[1] = 0.0f;
+  DecodeChunk::Result r = ch.compute(q, knew, vnew);
+  // a long cache: this wave also takes the next sub - 1 64-key chunks, combined online (stops at pos)
+  for (int j = 1; j < p.sub && !ch.badPos && static_cast<int64_t>(s * p.sub + j) * kChunk <= pos; ++j) {
+    DecodeChunk nx;
+    nx.load(p.kc, p.vc, pos, p.cap, s * p.sub + j, D, c4);
+    if (p.writeKv && nx.writesRow()) {
+      *reinterpret_cast<decF4*>(p.kc + pos * D + c4) = knew;
+      *reinterpret_cast<decF4*>(p.vc + pos * D + c4) = vnew;
     }
-    part[2 + lane] = 0.0f;
-    return;
+    r = DecodeChunk::combine(r, nx.compute(q, knew, vnew));
   }
-  const float knew = p.qkv[D + h * kHd + lane] + bk[lane];
-  if (p.writeKv && pos >= kb && pos < kb + kChunk) {
-    p.kc[pos * D + h * kHd + lane] = knew;
-    p.vc[pos * D + h * kHd + lane] = p.qkv[2 * D + h * kHd + lane] + bv[lane];
-  }
-  const float snew = waveSum((qrow[lane] + bq[lane]) * 0.125f * knew);
-  float q[kHd];
-#pragma unroll
-  for (int d = 0; d < kHd; ++d) q[d] = (qrow[d] + bq[d]) * 0.125f;
-
-  // scores
-  const int64_t j = kb + lane;
-  float sc = -INFINITY;
-  if (j < ke) {
-    if (j == pos) {
-      sc = snew;
-    } else {
-      const float4* kr = reinterpret_cast<const float4*>(p.kc + j * D + h * kHd);
-      float4 kv[kHd / 4];
-#pragma unroll
-      for (int d4 = 0; d4 < kHd / 4; ++d4) kv[d4] = kr[d4];
-      float dot = 0.0f;
-#pragma unroll
-      for (int d4 = 0; d4 < kHd / 4; ++d4)
-        dot += q[4 * d4] * kv[d4].x + q[4 * d4 + 1] * kv[d4].y + q[4 * d4 + 2] * kv[d4].z + q[4 * d4 + 3] * kv[d4].w;
-      sc = dot;
-    }
-  }
-  const float m = waveMax(sc);
-  const float pj = j < ke ? expf(sc - m) : 0.0f;
-  const float l = waveSum(pj);
-
-  // P.V: lane = (g, d4); keys kb + g + 4 i, i = 0..15
-  const int g = lane >> 4, d4 = lane & 15;
-  float4 vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t row = kb + g + 4 * i;
-    if (row < ke && row != pos) {
-      vv[i] = reinterpret_cast<const float4*>(p.vc + row * D + h * kHd)[d4];
-    } else if (row == pos) {
-      const float* vq = p.qkv + 2 * D + h * kHd + 4 * d4;
-      vv[i] = make_float4(vq[0] + bv[4 * d4], vq[1] + bv[4 * d4 + 1], vq[2] + bv[4 * d4 + 2], vq[3] + bv[4 * d4 + 3]);
-    } else {
-      vv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float w = __shfl(pj, g + 4 * i, 64);
-    acc.x += w * vv[i].x;
-    acc.y += w * vv[i].y;
-    acc.z += w * vv[i].z;
-    acc.w += w * vv[i].w;
-  }
-#pragma unroll
-  for (int o = 16; o < 64; o <<= 1) {
-    acc.x += __shfl_xor(acc.x, o, 64);
-    acc.y += __shfl_xor(acc.y, o, 64);
-    acc.z += __shfl_xor(acc.z, o, 64);
-    acc.w += __shfl_xor(acc.w, o, 64);
-  }
-  if (lane == 0) {
-    part[0] = m;
-    part[1] = l;
-  }
-  if (g == 0) reinterpret_cast<float4*>(part + 2)[d4] = acc;
+  ch.store(r, p.partial + (static_cast<int64_t>(h) * p.chunks + s) * (kHd + 2));
 }
 
-// Merge of one head's chunks: lane c holds chunk c's (m, l) (chunks <= 64 per pass, looped beyond),
-// M = max m_c, w_c = e^{m_c - M}, out[d] = sum_c w_c acc_c[d] / sum_c w_c l_c, chunks in order.
-__global__ __launch_bounds__(64) void decodeMergeKernel(const float* __restrict__ partial, float* __restrict__ out,
-                                                        const int64_t* pos, int64_t cap, int chunks) {
-  const int h = blockIdx.x, lane = threadIdx.x;
+// Merge of one head's chunks (one workgroup of 16 waves per head): M = max m_c, w_c = e^{m_c - M},
+// out[d] = sum_c w_c acc_c[d] / sum_c w_c l_c. Wave w takes chunks w, w + 16, ... in order, their loads issued 8
+// chunks at a time; the 16 wave sums are added in wave order. A long cache (512 chunks at 32768 rows) then costs a
+// few memory round trips instead of one per chunk.
+constexpr int kMergeWaves = 16, kMergeBatch = 8;
+__global__ __launch_bounds__(64 * kMergeWaves) void decodeMergeKernel(const float* __restrict__ partial,
+                                                                      float* __restrict__ out, const int64_t* pos,
+                                                                      int64_t cap, int chunks) {
+  __shared__ float red[kMergeWaves][kHd];
+  __shared__ float sM[kMergeWaves], sL[kMergeWaves];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t ps = *pos;
   if (ps < 0 || ps >= cap) {
-    out[h * kHd + lane] = __builtin_nanf("");
+    if (wv == 0) out[h * kHd + lane] = __builtin_nanf("");
     return;
   }
   const float* base = partial + static_cast<int64_t>(h) * chunks * (kHd + 2);
-  float M = -INFINITY;
-  for (int c0 = 0; c0 < chunks; c0 += 64) {
-    const int c = c0 + lane;
-    M = fmaxf(M, waveMax(c < chunks ? base[c * (kHd + 2)] : -INFINITY));
-  }
-  float L = 0.0f, A = 0.0f;
-  for (int c0 = 0; c0 < chunks; c0 += 64) {
-    const int c = c0 + lane;
-    const float lc = c < chunks ? base[c * (kHd + 2) + 1] : 0.0f;
-    const float wc = lc > 0.0f ? expf(base[c * (kHd + 2)] - M) : 0.0f;
-    L += waveSum(lc * wc);
-    const int n = min(64, chunks - c0);
-    for (int i = 0; i < n; ++i) {
-      const float w = __shfl(wc, i, 64);
-      A += w * base[(c0 + i) * (kHd + 2) + 2 + lane];
+  float m = -INFINITY;
+  for (int c = tid; c < chunks; c += 64 * kMergeWaves) m = fmaxf(m, base[c * (kHd + 2)]);
+  m = waveMaxDpp(m);
+  if (lane == 0) sM[wv] = m;
+  __syncthreads();
+  float M = sM[0];
+#pragma unroll
+  for (int w = 1; w < kMergeWaves; ++w) M = fmaxf(M, sM[w]);
+  float a = 0.0f, l = 0.0f;
+  for (int c0 = wv; c0 < chunks; c0 += kMergeWaves * kMergeBatch) {
+    float mc[kMergeBatch], lc[kMergeBatch], ac[kMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const int c = min(c0 + kMergeWaves * i, chunks - 1);
+      mc[i] = base[c * (kHd + 2)];
+      lc[i] = base[c * (kHd + 2) + 1];
+      ac[i] = base[c * (kHd + 2) + 2 + lane];
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      if (c0 + kMergeWaves * i < chunks) {
+        const float w = lc[i] > 0.0f ? expf(mc[i] - M) : 0.0f;
+        l += w * lc[i];
+        a += w * ac[i];
+      }
     }
   }
-  out[h * kHd + lane] = A / L;
+  red[wv][lane] = a;
+  if (lane == 0) sL[wv] = l;
+  __syncthreads();
+  if (wv == 0) {
+    float A = red[0][lane], L = sL[0];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; ++w) {
+      A += red[w][lane];
+      L += sL[w];
+    }
+    out[h * kHd + lane] = A / L;
+  }
+}
+
+// Waves per head and 64-key chunks per wave for `keys` keys: one chunk per wave up to 128 chunks, beyond that
+// as many chunks per wave as keep the waves (and the partials the merge reads) at 128 or fewer per head.
+constexpr int64_t kMaxWavesPerHead = 128;
+inline void decodeSplit(int64_t keys, int* waves, int* sub) {
+  const int64_t c = (keys + kChunk - 1) / kChunk;
+  const int64_t sb = c > kMaxWavesPerHead ? (c + kMaxWavesPerHead - 1) / kMaxWavesPerHead : 1;
+  *sub = static_cast<int>(sb);
+  *waves = static_cast<int>((c + sb - 1) / sb);
 }
 
 }  // namespace lkd
@@ -164,13 +142,14 @@ __global__ __launch_bounds__(64) void decodeMergeKernel(const float* __restrict_
 extern "C" {
 
 int64_t lk_hip_attention_decode_workspace_bytes(int heads, int64_t cap) {
-  const int64_t chunks = (cap + lkd::kChunk - 1) / lkd::kChunk;
-  return static_cast<int64_t>(heads) * chunks * (lkd::kHd + 2) * 4;
+  int waves = 0, sub = 0;
+  lkd::decodeSplit(cap, &waves, &sub);
+  return static_cast<int64_t>(heads) * waves * (lkd::kHd + 2) * 4;
 }
 
 // qkv [1, 3D] (before bias), kc / vc [cap, D] (rows 0..pos-1 valid; row pos written when writeKv), pos device
-// i64[1], bias [3D] -> out [1, D], D = 64 heads. The grid covers max_keys (<= cap) keys; chunks past pos exit
-// early. pos outside [0, cap) writes nothing, yields NaN and is recorded as LK_DEVERR_POSITION.
+// i64[1], bias [3D] -> out [1, D], D = 64 heads. The grid covers max_keys (<= cap) keys; chunks past pos store
+// empty partials. pos outside [0, cap) writes nothing, yields NaN and is recorded as LK_DEVERR_POSITION.
 int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const int64_t* pos, const float* bias,
                                 float* out, int64_t cap, int heads, int64_t maxKeys, int writeKv, void* workspace,
                                 int64_t workspaceBytes, void* stream) {
@@ -187,14 +166,14 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
   p.heads = heads;
   p.writeKv = writeKv;
   p.err = lkh::deviceErrorRecord();
-  p.chunks = static_cast<int>((maxKeys + lkd::kChunk - 1) / lkd::kChunk);
+  lkd::decodeSplit(maxKeys, &p.chunks, &p.sub);
   if (!workspace || workspaceBytes < static_cast<int64_t>(heads) * p.chunks * (lkd::kHd + 2) * 4) return 3;
   p.partial = static_cast<float*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(lkd::decodeChunkKernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(p.chunks)),
                      dim3(64), 0, s, p);
-  hipLaunchKernelGGL(lkd::decodeMergeKernel, dim3(static_cast<unsigned>(heads)), dim3(64), 0, s, p.partial, out, pos,
-                     cap, p.chunks);
+  hipLaunchKernelGGL(lkd::decodeMergeKernel, dim3(static_cast<unsigned>(heads)), dim3(64 * lkd::kMergeWaves), 0, s,
+                     p.partial, out, pos, cap, p.chunks);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -208,7 +187,7 @@ int lk_hip_attention_decode_f32(const float* qkv, float* kc, float* vc, const in
 // overlap on one GPU (different streams) race on the array.
 namespace {
 
-constexpr int64_t kNoAllocScratchFloats = 512 * 1024;  // 2 MiB: heads x ceil(max_keys / 64) x 66 floats
+constexpr int64_t kNoAllocScratchFloats = 512 * 1024;  // 2 MiB: heads x (waves per head) x 66 floats
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 constexpr int kMaxDevices = 64;
@@ -242,7 +221,9 @@ int lk_hip_attention_decode_f32_noalloc(const float* qkv, float* kc, float* vc, 
                                         void* stream) {
   if (heads <= 0 || cap <= 0) return 1;
   const int64_t keys = maxKeys <= 0 || maxKeys > cap ? cap : maxKeys;
-  const int64_t need = static_cast<int64_t>(heads) * ((keys + lkd::kChunk - 1) / lkd::kChunk) * (lkd::kHd + 2);
+  int waves = 0, sub = 0;
+  lkd::decodeSplit(keys, &waves, &sub);
+  const int64_t need = static_cast<int64_t>(heads) * waves * (lkd::kHd + 2);
   if (need > kNoAllocScratchFloats) return 4;  // beyond the fixed scratch array
   float* ptr = scratchOnCurrentDevice();
   if (!ptr) return 2;

@@ -17,6 +17,7 @@
 // with the same arithmetic per element: the sums over K are split into row slices and added in a fixed order
 // (deterministic), softmax is base e on q / 8, LayerNorm is two-pass with the biased variance.
 #include "common.h"
+#include "decode_chunk.h"
 #include "lokinfer_hip.h"
 
 #include <algorithm>
@@ -280,15 +281,10 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
         (wsum[0][cl] + wsum[1][cl]) + (wsum[2][cl] + wsum[3][cl]);
 }
 
-// One wave per (head, 64-key chunk), as the split decode kernel, but q / k / v of this step are the fixed-order
-// sums of `slices` GEMV partial rows (+ bias). An invalid position writes NaN partials (no cache write) and is
-// recorded in the GPU's error record.
-//
-// Layout: lane (g = lane / 16, d4 = lane % 16) owns dims 4 d4 .. 4 d4 + 3 of keys kb + g + 4 i, i = 0..15, so each
-// load instruction reads 4 whole cache rows (coalesced), a score is a 16-lane row sum (DPP), and the softmax
-// weights of a lane's keys are already in the lane for P.V. Every load is issued before the first wait: the partial
-// rows of q / k / v first, then (once pos is known) the 16 key and 16 value rows of the chunk, unconditionally from
-// rows clamped into 0 .. pos (the row pos itself and the rows past it are replaced by selects, never used).
+// One wave per (head, 64-key chunk) (DecodeChunk), as the split decode kernel, but q / k / v of this step are
+// the fixed-order sums of `slices` GEMV partial rows (+ bias). Every load is issued before the first wait: the
+// partial rows first, then (once pos is known) the chunk's key and value rows. An invalid position writes NaN
+// partials (no cache write) and is recorded in the GPU's error record.
 __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restrict__ qpart, int64_t slices,
                                                            float* kc, float* vc, const int64_t* pos,
                                                            const float* __restrict__ bias, float* __restrict__ cpart,
@@ -312,22 +308,10 @@ __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restr
   }
   const f4v bq = *reinterpret_cast<const f4v*>(bias + c4), bk = *reinterpret_cast<const f4v*>(bias + D + c4),
             bv = *reinterpret_cast<const f4v*>(bias + 2 * D + c4);
-  // No early exit: a chunk past the live keys and an invalid position compute on clamped rows and store their
-  // fixed results at the end, so no load of the kernel waits behind a branch on pos.
   const int64_t ps = *pos;
-  const bool badPos = ps < 0 || ps >= cap;
-  if (badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(err, LK_DEVERR_POSITION, ps);
-  const int64_t psc = badPos ? 0 : ps;
-  const int64_t kb = static_cast<int64_t>(s) * kDecChunk;
-  const int64_t ke = min<int64_t>(psc + 1, kb + kDecChunk);
-  const bool dead = kb >= ke;  // chunk past the live keys (its rows clamp to row pos)
-  f4v kr[16], vr[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t row = min<int64_t>(kb + g + 4 * i, ke - 1);
-    kr[i] = *reinterpret_cast<const f4v*>(kc + row * D + c4);
-    vr[i] = *reinterpret_cast<const f4v*>(vc + row * D + c4);
-  }
+  DecodeChunk ch;
+  ch.load(kc, vc, ps, cap, s, D, c4);
+  if (ch.badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(err, LK_DEVERR_POSITION, ps);
   f4v sq = {0.f, 0.f, 0.f, 0.f}, sk = sq, sv = sq;
 #pragma unroll
   for (int i = 0; i < kRowSlices; ++i)
@@ -345,62 +329,19 @@ __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restr
   sq = f4v{crossRowSum(sq.x), crossRowSum(sq.y), crossRowSum(sq.z), crossRowSum(sq.w)};
   sk = f4v{crossRowSum(sk.x), crossRowSum(sk.y), crossRowSum(sk.z), crossRowSum(sk.w)};
   sv = f4v{crossRowSum(sv.x), crossRowSum(sv.y), crossRowSum(sv.z), crossRowSum(sv.w)};
-  const f4v q = (sq + bq) * 0.125f;
-  const f4v knew = sk + bk;
-  const f4v vnew = sv + bv;
-  if (!badPos && g == 0 && ps >= kb && ps < kb + kDecChunk) {
+  const f4v knew = sk + bk, vnew = sv + bv;
+  if (ch.writesRow()) {
     *reinterpret_cast<f4v*>(kc + ps * D + c4) = knew;
     *reinterpret_cast<f4v*>(vc + ps * D + c4) = vnew;
   }
-  const float snew = rowSum16((q.x * knew.x + q.y * knew.y) + (q.z * knew.z + q.w * knew.w));
-  // scores of this lane's 16 keys (the same in the 16 lanes of a row), then the chunk softmax
-  float sc[16];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t key = kb + g + 4 * i;
-    const float dot = rowSum16((q.x * kr[i].x + q.y * kr[i].y) + (q.z * kr[i].z + q.w * kr[i].w));
-    sc[i] = key < ke ? (key == ps ? snew : dot) : -INFINITY;
-    m = fmaxf(m, sc[i]);
-  }
-  m = crossRowMax(m);
-  float l = 0.0f;
-  f4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t key = kb + g + 4 * i;
-    const float pj = key < ke ? expf(sc[i] - m) : 0.0f;
-    l += pj;
-    const f4v v = key < ke ? (key == ps ? vnew : vr[i]) : f4v{0.f, 0.f, 0.f, 0.f};
-    acc += pj * v;
-  }
-  l = crossRowSum(l);
-  acc.x = crossRowSum(acc.x);
-  acc.y = crossRowSum(acc.y);
-  acc.z = crossRowSum(acc.z);
-  acc.w = crossRowSum(acc.w);
-  const float nan = __builtin_nanf("");
-  if (badPos) {
-    m = nan;
-    l = 1.0f;
-    acc = f4v{nan, nan, nan, nan};
-  } else if (dead) {
-    m = -INFINITY;
-    l = 0.0f;
-    acc = f4v{0.f, 0.f, 0.f, 0.f};
-  }
-  if (lane == 0) {
-    part[0] = m;
-    part[1] = l;
-  }
-  if (g == 0) reinterpret_cast<f4v*>(part + 2)[d4] = acc;
+  ch.finish((sq + bq) * 0.125f, knew, vnew, part);
 }
 
 // Tied LM head of a decode step with the final LayerNorm and the greedy argmax folded in: x = LayerNorm(slices of
 // part in order + bias + res) (every workgroup forms it in LDS from the partial rows), logits[r] = x . table[r, :]
 // for r < rows, and per workgroup the (max logit, first row) pair over its rows, which argmaxKernel reduces.
-// Wave w of workgroup b takes rows b * 4 + w + W i (W = 4 * grid waves), 8 rows per batch, the next batch loaded
-// while the current one is reduced; lane l holds columns 4 (l + 64 j), j < QPL (K <= 256 QPL).
+// Wave w of workgroup b takes rows b * 4 + w + W i (W = 4 * grid waves) in two alternating halves of 4 rows (one
+// reduced while the other loads); lane l holds columns 4 (l + 64 j), j < QPL (K <= 256 QPL).
 constexpr int kLmRowBatch = 8;
 constexpr int kLmGrid = 512;
 template <int QPL>
@@ -420,10 +361,12 @@ __global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ 
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wv;
   LnRow row;
   row.load(part, slices, bias, res, gamma, beta, k);
-  f4v wr[kLmRowBatch][QPL];
-  auto loadRows = [&](int64_t r0) {
+  // two halves of kLmRowBatch / 2 rows in ping-pong: while one half is reduced the other is in flight
+  constexpr int H = kLmRowBatch / 2;
+  f4v wa[H][QPL], wb[H][QPL];
+  auto loadHalf = [&](f4v (&wr)[H][QPL], int64_t r0) {
 #pragma unroll
-    for (int b = 0; b < kLmRowBatch; ++b) {
+    for (int b = 0; b < H; ++b) {
       const float* tr = table + min<int64_t>(r0 + W * b, rows - 1) * k;
 #pragma unroll
       for (int j = 0; j < QPL; ++j)
@@ -431,7 +374,8 @@ __global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ 
             reinterpret_cast<const f4v*>(tr + 4 * min<int64_t>(lane + 64 * j, kq - 1)));
     }
   };
-  loadRows(wave);
+  loadHalf(wa, wave);
+  loadHalf(wb, wave + W * H);
   const f4v y = row.finish(part, slices, k, eps, nullptr, scr);
   if (row.live) xrow[tid] = y;
   __syncthreads();
@@ -440,10 +384,11 @@ __global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ 
   for (int j = 0; j < QPL; ++j) xv[j] = lane + 64 * j < kq ? xrow[lane + 64 * j] : f4v{0.f, 0.f, 0.f, 0.f};
   float best = -INFINITY;
   int64_t bi = INT64_MAX;
-  for (int64_t r0 = wave; r0 < rows; r0 += W * kLmRowBatch) {
-    float d[kLmRowBatch];
+  // rows r0 + W b of one half: dot products, then (once the next loads of this half are issued) the row sums
+  auto consume = [&](f4v (&wr)[H][QPL], int64_t r0) {
+    float d[H];
 #pragma unroll
-    for (int b = 0; b < kLmRowBatch; ++b) {
+    for (int b = 0; b < H; ++b) {
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < QPL; ++j) {
@@ -452,9 +397,9 @@ __global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ 
       }
       d[b] = acc;
     }
-    if (r0 + W * kLmRowBatch < rows) loadRows(r0 + W * kLmRowBatch);
+    if (r0 + W * kLmRowBatch < rows) loadHalf(wr, r0 + W * kLmRowBatch);
 #pragma unroll
-    for (int b = 0; b < kLmRowBatch; ++b) {
+    for (int b = 0; b < H; ++b) {
       const int64_t r = r0 + W * b;
       const float v = waveSumDpp(d[b]);
       if (r < rows) {
@@ -465,6 +410,10 @@ __global__ __launch_bounds__(256) void lmHeadLnKernel(const float* __restrict__ 
         }
       }
     }
+  };
+  for (int64_t r0 = wave; r0 < rows; r0 += W * kLmRowBatch) {
+    consume(wa, r0);
+    if (r0 + W * H < rows) consume(wb, r0 + W * H);
   }
   if (lane == 0) {
     wbV[wv] = best;

@@ -169,6 +169,23 @@ def test_attention_decode_split(gpu, pos):
     close(VC, rv, 1e-6)
 
 
+# Caches past 128 chunks per head: each wave takes several 64-key chunks combined online (20000 rows: 3 chunks per
+# wave, 105 waves per head); positions in the first, a middle (partly live) and the last wave.
+@pytest.mark.parametrize("pos", [70, 8300, 19999])
+def test_attention_decode_split_long_cache(gpu, pos):
+    lk = gpu
+    heads, cap, d = 4, 20000, 256
+    kc, vc = rng.standard_normal((cap, d)), rng.standard_normal((cap, d))
+    qkv, bias = rng.standard_normal((1, 3 * d)) * 2, rng.standard_normal(3 * d) * 0.1
+    KC, VC = G(lk, kc), G(lk, vc)
+    P = lk.from_numpy(np.array([pos], np.int64), device="gpu", copy=True)
+    ref, rk, rv = K.attention_decode(qkv, kc, vc, pos, bias, heads)
+    got = lk.ops.attention_decode_split_f32_gpu(G(lk, qkv), KC, VC, P, G(lk, bias), heads)
+    close(got, ref, 3e-5)
+    close(KC.numpy()[pos], rk[pos], 1e-6)
+    close(VC.numpy()[pos], rv[pos], 1e-6)
+
+
 @pytest.mark.parametrize("l,c", [(1, 64), (127, 256), (300, 1024), (2435, 128), (1000, 528)])
 def test_stats_affine_act(gpu, l, c):
     lk = gpu
