@@ -52,6 +52,15 @@ void lk_model_free(lk_model* m);
 /* the canonical text of a dim expression ("2*(N + 1)" -> "2*N + 2"); NULL if it does not parse */
 char* lk_dim_canonical(const char* text);
 
+/* bake-init (reference: rt::bakeInit, runtime/bake_init.h:19-27): runs `m`'s init once with the externals bound
+ * (as lk_exe_create) and returns a new model in which every init result that is computed data (a plain
+ * buffer.alloc written by init kernels, or a view of one) is a const.internal holding that data, resident where the
+ * kernel that wrote it runs; init ops nothing needs any more are removed. Arena, persistent and output buffers,
+ * constants, and models whose init defines symbols (dim.read, mem.plan) are left alone. stats (may be NULL):
+ * [baked, baked bytes, init ops before, init ops after]. NULL on error (lk_last_error). */
+lk_model* lk_model_bake_init(const lk_model* m, int n_ext, const char* const* names, void* const* ptrs,
+                             const uint64_t* sizes, const int* on_device, void* stream, uint64_t* stats);
+
 /* ---- executables (reference: Executable::create / run, runtime.h:84-95) ----
  * create: the model must be in buffer form (after bufferize). Externals are bound by name: device pointers
  * (on_device != 0, borrowed: they must outlive the executable) or host bytes (uploaded once). Uploads every

@@ -177,13 +177,33 @@ class CompiledModel:
             self._exe = Executable(self._model, {})
         return self
 
-    def save(self, path: str) -> None:
-        """Writes a self-contained .lkm v2 (captured weights internalized)."""
+    def save(self, path: str, *, bake_init: bool = False) -> None:
+        """Writes a self-contained .lkm v2 (captured weights internalized). bake_init=True stores init's results
+        (e.g. transposed weights) instead of their inputs, so loading does no init work (reference
+        CompiledModel.save, compiler.py:112-117)."""
         self._drain()
+        if bake_init:
+            model, _ = self._model.bake_init(self._externals)
+            model.internalize(self._externals)
+            model.save(path)
+            return
         if self._externals:
             self._model.internalize(self._externals)  # the executable keeps its bound device copies
             self._externals = {}
         self._model.save(path)
+
+    def bake_init(self) -> dict:
+        """Runs init once and replaces its computed results (weights transformed by hoisted kernels) with constants;
+        init work nothing else needs is removed and the executable is re-created. Arenas, persistent state and
+        models whose init defines symbols are left alone. Returns statistics (baked, baked_bytes,
+        init_ops_before, init_ops_after) (reference CompiledModel.bake_init, compiler.py:119-127)."""
+        from .rt import Executable
+
+        self._drain()
+        model, stats = self._model.bake_init(self._externals)
+        self._exe = Executable(model, self._externals)
+        self._model = model
+        return stats
 
     def _call(self, args, copy: bool):
         outs = self._exe.run(list(args))

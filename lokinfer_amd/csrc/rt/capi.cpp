@@ -169,6 +169,24 @@ char* lk_dim_canonical(const char* text) {
   return dupString(pool.str(d));
 }
 
+lk_model* lk_model_bake_init(const lk_model* m, int n_ext, const char* const* names, void* const* ptrs,
+                             const uint64_t* sizes, const int* on_device, void* stream, uint64_t* stats) {
+  if (!m || n_ext < 0) return failNull<lk_model>(lkrt::Status::error("null argument"));
+  std::vector<lkrt::ExternalPtr> ext;
+  for (int i = 0; i < n_ext; ++i) ext.push_back({names[i], ptrs[i], sizes[i], on_device[i] != 0});
+  lkrt::Status st;
+  lkrt::BakeStats bs;
+  auto baked = lkrt::bakeInit(m->m, ext, static_cast<hipStream_t>(stream), &bs, st);
+  if (!baked) return failNull<lk_model>(st);
+  if (stats) {
+    stats[0] = bs.baked;
+    stats[1] = bs.bakedBytes;
+    stats[2] = bs.initOpsBefore;
+    stats[3] = bs.initOpsAfter;
+  }
+  return wrap(std::move(baked));
+}
+
 lk_exe* lk_exe_create(lk_model* m, int n_ext, const char* const* names, void* const* ptrs, const uint64_t* sizes,
                       const int* on_device, void* stream, int flags) {
   if (!m || n_ext < 0) return failNull<lk_exe>(lkrt::Status::error("null argument"));

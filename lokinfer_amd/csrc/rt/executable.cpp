@@ -768,6 +768,7 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
   if (Status s = x->interpret(x->init_, slot, sv, none, stream, &initOut); !s) return fail(Status::error("init: " + s.message()));
   if (!none.blocks.empty()) return fail(Status::error("init allocated per-call memory"));
   for (size_t i = 0; i < m.exec.state.size(); ++i) x->fixed_[m.exec.state[i]] = static_cast<char*>(initOut[i].data);
+  for (const TensorOut& o : initOut) x->state_.push_back(static_cast<char*>(o.data));
   if (x->tempsBytes_) {
     x->temps_ = std::make_unique<Memory>();
     x->temps_->n = x->tempsBytes_;

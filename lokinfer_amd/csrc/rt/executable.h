@@ -62,6 +62,8 @@ class Executable {
   size_t modelArenaBytes() const { return modelBytes_; }
   size_t callArenaBytes() const;
   int graphsCaptured() const { return static_cast<int>(graphs_.size()); }
+  // Address of init's i-th result (the exec state), in the model arena or an external's memory.
+  const void* stateData(size_t i) const { return i < state_.size() ? state_[i] : nullptr; }
   int streamsUsed() const { return numStreams_; }
   std::string strategy() const;
 
@@ -114,6 +116,7 @@ class Executable {
   std::vector<int64_t> relocOffset_;  // exec state value -> offset in temps_ (-1: not re-placed)
   std::vector<uint8_t> skipAlloc_;    // init arena allocs whose every byte was re-placed
   std::vector<char*> fixed_;          // value -> model-lifetime address (constants, state, persistent buffers)
+  std::vector<char*> state_;          // init's results as init wrote them
   std::vector<int64_t> scalars_;      // host slots of scalar exec inputs
   bool graphs_on_ = false;
   bool dynamic_ = false;              // exec has dim.read or scalar inputs: always eager
@@ -122,5 +125,16 @@ class Executable {
   hipStream_t captureStream_ = nullptr;
   int64_t* pinned_ = nullptr;         // dim.read landing slot
 };
+
+// bake-init (the reference's runtime/bake_init.h): runs `model`'s init once (externals bound) and returns a copy
+// in which every init result that is computed data (a plain buffer.alloc written by init kernels, or a view of one)
+// is a const.internal holding that data, on the device of the kernel that wrote it; init ops nothing needs any more
+// are removed. Left alone: arena / persistent / output buffers, constants, and the whole model when init defines
+// symbols (dim.read, mem.plan).
+struct BakeStats {
+  size_t baked = 0, bakedBytes = 0, initOpsBefore = 0, initOpsAfter = 0;
+};
+std::unique_ptr<Model> bakeInit(std::shared_ptr<const Model> model, const std::vector<ExternalPtr>& ext,
+                                hipStream_t stream, BakeStats* stats, Status& st);
 
 }  // namespace lkrt

@@ -47,6 +47,8 @@ def _rt():
         "lk_model_num_inputs": ([vp], i32_),
         "lk_model_num_outputs": ([vp], i32_),
         "lk_model_input_is_mutable": ([vp, i32_], i32_),
+        "lk_model_bake_init": ([vp, i32_, C.POINTER(cp), C.POINTER(vp), C.POINTER(u64), C.POINTER(i32_), vp,
+                                C.POINTER(u64)], vp),
         "lk_model_free": ([vp], None),
         "lk_dim_canonical": ([cp], vp),
         "lk_exe_create": ([vp, i32_, C.POINTER(cp), C.POINTER(vp), C.POINTER(u64), C.POINTER(i32_), vp, i32_], vp),
@@ -155,6 +157,17 @@ class Model:
         arr_s = (C.c_uint64 * len(names))(*[len(d) for d in data])
         _check(_rt().lk_model_internalize(self._h, len(names), arr_n, arr_p, arr_s))
 
+    def bake_init(self, externals: dict | None = None) -> tuple["Model", dict]:
+        """Runs init once (externals bound by name, as for an Executable) and returns (a new model whose computed
+        init results are const.internal data, statistics) (reference rt::bakeInit)."""
+        L = _rt()
+        arrs, _keep = _ext_arrays(externals or {})
+        st = (C.c_uint64 * 4)()
+        h = L.lk_model_bake_init(self._h, *arrs, _stream(), st)
+        if not h:
+            raise LokinferError(L.lk_last_error().decode())
+        return Model(h), {"baked": st[0], "baked_bytes": st[1], "init_ops_before": st[2], "init_ops_after": st[3]}
+
     @property
     def num_inputs(self) -> int:
         return _rt().lk_model_num_inputs(self._h)
@@ -178,6 +191,18 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+def _ext_arrays(externals: dict):
+    """(n, names, pointers, sizes, on_device) C arrays for externals bound by name, and the tensors to keep alive."""
+    names = list(externals)
+    ts = [externals[n] if isinstance(externals[n], Tensor) else Tensor(externals[n]) for n in names]
+    n = len(names)
+    arr_n = (C.c_char_p * max(n, 1))(*[x.encode() for x in names])
+    arr_p = (C.c_void_p * max(n, 1))(*[t.data_ptr() for t in ts])
+    arr_s = (C.c_uint64 * max(n, 1))(*[t.nbytes for t in ts])
+    arr_d = (C.c_int * max(n, 1))(*[1 if t.device == "gpu" else 0 for t in ts])
+    return (n, arr_n, arr_p, arr_s, arr_d), ts
+
+
 class Executable:
     """A model loaded onto the GPU (reference lk::rt::Executable): constants uploaded once into one device arena,
     init run, calls replayed from captured hipGraphs for statically shaped calls. `externals` maps
@@ -188,15 +213,9 @@ class Executable:
         externals = externals or {}
         self.model = model
         self._ext = dict(externals)  # keeps the bound tensors alive
-        names = list(externals)
-        ts = [externals[n] if isinstance(externals[n], Tensor) else Tensor(externals[n]) for n in names]
-        n = len(names)
-        arr_n = (C.c_char_p * max(n, 1))(*[x.encode() for x in names])
-        arr_p = (C.c_void_p * max(n, 1))(*[t.data_ptr() for t in ts])
-        arr_s = (C.c_uint64 * max(n, 1))(*[t.nbytes for t in ts])
-        arr_d = (C.c_int * max(n, 1))(*[1 if t.device == "gpu" else 0 for t in ts])
+        arrs, self._ts = _ext_arrays(externals)
         flags = (1 if graphs else 0) | (max(1, min(int(streams), 8)) << 8)
-        self._h = L.lk_exe_create(model._h, n, arr_n, arr_p, arr_s, arr_d, _stream(), flags)
+        self._h = L.lk_exe_create(model._h, *arrs, _stream(), flags)
         if not self._h:
             raise LokinferError(L.lk_last_error().decode())
 

@@ -162,3 +162,71 @@ def test_device_error_surfaces_at_a_synchronised_call(gpu):
     with pytest.raises(LokinferError, match="device error 2.*detail 16"):
         exe.run([q, G(lk, [cap], np.int64)], sync=True)
     exe.run([q, G(lk, [4], np.int64)], sync=True)  # the record was cleared
+
+
+# ---- bake-init (reference tests/unit/test_compiler.cpp:240-290, tests/python/test_call_api.py:195-220) ---------
+
+BAKE_SRC = """model {
+  init {
+    return
+  }
+  exec(%x: tensor<f32[4]>) {
+    %w = const.inline dense<[1.0, 2.0, 3.0, 4.0]> : tensor<f32[4]>
+    %w2 = kernel "add_f32_gpu"(%w, %w) : tensor<f32[4]>
+    %a = kernel "add_f32_gpu"(%x, %w2) : tensor<f32[4]>
+    %o = kernel "mul_f32_gpu"(%a, %x) : tensor<f32[4]>
+    return %o
+  }
+}
+"""
+
+
+def test_bake_init_text_model(gpu, tmp_path):
+    """2 w is hoisted into init (a kernel on a constant) and baked; the static arena (scratch for %a) is not."""
+    lk = gpu
+    m = lk.compile_ir(BAKE_SRC)
+    x = np.array([0.5, -1.0, 2.0, 3.0], np.float32)
+    ref = (x + 2 * np.arange(1, 5, dtype=np.float32)) * x
+    X = G(lk, x)
+    assert np.array_equal(m(X).numpy(), ref)
+    stats = m.bake_init()
+    assert stats["baked"] == 1 and stats["baked_bytes"] == 16
+    assert stats["init_ops_after"] < stats["init_ops_before"]
+    text = m.ir_text()
+    assert 'const.internal @"baked' in text
+    assert 'kernel "add_f32_gpu"(%w' not in text  # the init kernel is gone
+    assert "arena = true" in text                 # scratch memory stays an alloc
+    assert np.array_equal(m(X).numpy(), ref)
+    # the baked model survives the binary format
+    path = tmp_path / "baked.lkm"
+    m.save(path)
+    back = lk.load(path)
+    assert 'const.internal @"baked' in back.ir_text()
+    assert np.array_equal(back(X).numpy(), ref)
+
+
+def test_bake_init_stores_transformed_weights(gpu, tmp_path):
+    lk = gpu
+    w_np = np.random.default_rng(0).standard_normal((16, 24)).astype(np.float32)
+    w = G(lk, w_np)
+
+    def f(x):
+        return lk.ops.gemm_f32_gpu(x, lk.ops.transpose_f32_gpu(w))  # the transpose is hoisted into init
+
+    x = G(lk, np.random.default_rng(1).standard_normal((5, 24)))
+    model = lk.compile(f, inputs=[x])
+    ref = model(x).numpy().copy()
+    assert np.abs(ref - x.numpy() @ w_np.T).max() <= 1e-4 * np.abs(ref).max()
+    stats = model.bake_init()
+    assert stats["baked"] == 1 and stats["baked_bytes"] == 24 * 16 * 4
+    assert stats["init_ops_after"] < stats["init_ops_before"]
+    ir = model.ir_text()
+    assert "transpose_f32_gpu" not in ir and "baked" in ir
+    assert 'device = "gpu"' in ir  # resident where the init kernel wrote it
+    assert np.array_equal(model(x).numpy(), ref)
+    # export: the file holds w^T only (the original w is gone with the init work that read it)
+    path = tmp_path / "baked.lkm"
+    lk.compile(f, inputs=[x]).save(path, bake_init=True)
+    loaded = lk.load(path)
+    assert "transpose" not in loaded.ir_text()
+    assert np.array_equal(loaded(x).numpy(), ref)
