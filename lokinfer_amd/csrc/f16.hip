@@ -684,14 +684,94 @@ __device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
 }
 
 // ---- causal GQA, T = 1: one wave per (q head, 64-key chunk), partial (m, l, o[128]) to the workspace, then one
-// workgroup per q head merges the chunks in order. Scores: lane j owns key kb + j (16 x 16-byte loads of its K row,
-// q from LDS). P.V: lane (key group g = lane / 16, dim octet lane % 16) sums keys g, g + 4, ... of the chunk, then a
-// two-step shuffle reduction over g.
+// workgroup per q head merges the chunks in order.
 constexpr int DCH = 64;
 
+// One wave's chunk (GqaChunk, shared by the split and the fused decode kernels, so both give the same bits):
+// lane (g = lane / 16, d8 = lane % 16) owns dims 8 d8 .. 8 d8 + 7 of keys kb + g + 4 i, i < 16. A load instruction
+// reads 4 whole 256-byte head rows (coalesced); a score is the lane's 8-term dot summed over the 16 lanes of its row
+// by DPP (the same bits in every lane of the row); the chunk max / sum and P.V cross the 4 rows by permlane swaps.
+// Rows are loaded from rows clamped to 0 .. pos; the row pos itself takes this step's key / value when the caller
+// has them (its cache row may be written concurrently).
+struct GqaChunk {
+  half8 kr[16], vr[16];
+  int64_t kb, nk;
+  int g, d8;
+
+  __device__ __forceinline__ void load(const h16* kc, const h16* vc, int64_t nkeys, int ch, int64_t dk,
+                                       int64_t kvOff) {
+    const int lane = threadIdx.x & 63;
+    g = lane >> 4;
+    d8 = lane & 15;
+    kb = static_cast<int64_t>(ch) * DCH;
+    nk = nkeys;
+    const int64_t last = nk > 0 ? nk - 1 : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t row = min<int64_t>(kb + g + 4 * i, last);
+      kr[i] = ld8(kc + row * dk + kvOff + 8 * d8);
+      vr[i] = ld8(vc + row * dk + kvOff + 8 * d8);
+    }
+    // all 32 row loads in flight before the first use (left alone, the scheduler spreads them through the dots
+    // to save registers, and the chunk then waits on memory several times)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // q8: this lane's 8 query dims (f32). newKey: position whose key / value are knew / vnew (-1: none). Writes the
+  // chunk partial (m, l, o[128]) (scores in log2 units: dot * scale * log2 e).
+  __device__ __forceinline__ void finish(const float (&q8)[8], int64_t newKey, const half8& knew, const half8& vnew,
+                                         float scale, float* part) const {
+    const int lane = threadIdx.x & 63;
+    float sc[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t key = kb + g + 4 * i;
+      const half8 kk = key == newKey ? knew : kr[i];
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(q8[e], static_cast<float>(kk[e]), dot);
+      dot = rowSum16(dot);
+      sc[i] = key < nk ? dot * scale * kLog2e : -INFINITY;
+      m = fmaxf(m, sc[i]);
+    }
+    m = crossRowMax(m);
+    float l = 0.0f, acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t key = kb + g + 4 * i;
+      const float w = key < nk ? __builtin_amdgcn_exp2f(sc[i] - m) : 0.0f;
+      l += w;
+      const half8 vv = key == newKey ? vnew : vr[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, static_cast<float>(vv[e]), acc[e]);
+    }
+    l = crossRowSum(l);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = crossRowSum(acc[e]);
+    if (lane == 0) {
+      part[0] = m;
+      part[1] = l;
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[2 + 8 * d8 + e] = acc[e];
+    }
+  }
+};
+
+__device__ __forceinline__ void emptyChunk(float* part, int lane) {
+  if (lane == 0) {
+    part[0] = -INFINITY;
+    part[1] = 0.0f;
+  }
+  part[2 + lane] = 0.0f;
+  part[2 + 64 + lane] = 0.0f;
+}
+
 __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
-  __shared__ float qs[QHD];
-  __shared__ float ps[DCH];
   const int h = blockIdx.x, ch = blockIdx.y, lane = threadIdx.x;
   const int64_t dk = static_cast<int64_t>(p.kvh) * QHD;
   const int64_t kvOff = static_cast<int64_t>(h / (p.qh / p.kvh)) * QHD;
@@ -699,62 +779,18 @@ __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
   float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
   if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
-  const int64_t kb = static_cast<int64_t>(ch) * DCH;
-  if (kb >= nk) {
-    if (lane == 0) {
-      part[0] = -INFINITY;
-      part[1] = 0.0f;
-    }
-    part[2 + lane] = 0.0f;
-    part[2 + 64 + lane] = 0.0f;
+  if (static_cast<int64_t>(ch) * DCH >= nk) {
+    emptyChunk(part, lane);
     return;
   }
-  qs[lane] = static_cast<float>(p.q[h * QHD + lane]);
-  qs[64 + lane] = static_cast<float>(p.q[h * QHD + 64 + lane]);
-  const int64_t key = kb + lane;
-  const h16* kr = p.kc + min<int64_t>(key, nk - 1) * dk + kvOff;
-  half8 kv[16];
+  const half8 qh8 = ld8(p.q + h * QHD + 8 * (lane & 15));
+  GqaChunk c;
+  c.load(p.kc, p.vc, nk, ch, dk, kvOff);
+  float q8[8];
 #pragma unroll
-  for (int c = 0; c < 16; ++c) kv[c] = ld8(kr + 8 * c);
-  __syncthreads();
-  float dot = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 16; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dot = fmaf(qs[8 * c + e], static_cast<float>(kv[c][e]), dot);
-  const float s = key < nk ? dot * p.scale * kLog2e : -INFINITY;
-  const float mc = waveMax(s);
-  const float pv = __builtin_amdgcn_exp2f(s - mc);
-  const float lc = waveSum(pv);
-  ps[lane] = pv;
-  __syncthreads();
-  const int g = lane >> 4, oc = lane & 15;
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  half8 vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = ld8(p.vc + min<int64_t>(kb + g + 4 * i, nk - 1) * dk + kvOff + 8 * oc);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float w = ps[g + 4 * i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, static_cast<float>(vv[i][e]), acc[e]);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    acc[e] += __shfl_xor(acc[e], 16, 64);
-    acc[e] += __shfl_xor(acc[e], 32, 64);
-  }
-  if (lane == 0) {
-    part[0] = mc;
-    part[1] = lc;
-  }
-  if (g == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part[2 + 8 * oc + e] = acc[e];
-  }
+  for (int e = 0; e < 8; ++e) q8[e] = static_cast<float>(qh8[e]);
+  const half8 none = {};
+  c.finish(q8, -1, none, none, p.scale, part);
 }
 
 __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
@@ -814,7 +850,6 @@ __device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, 
 // wait for them alone), then the chunk's K and V rows.
 __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   __shared__ float qs[QHD];
-  __shared__ float ps[DCH];
   __shared__ __attribute__((aligned(16))) h16 kn[QHD];
   __shared__ __attribute__((aligned(16))) h16 vn[QHD];
   const int h = blockIdx.x, ch = blockIdx.y, lane = threadIdx.x;
@@ -827,12 +862,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int64_t kb = static_cast<int64_t>(ch) * DCH;
   if (kb >= nk) {
-    if (lane == 0) {
-      part[0] = -INFINITY;
-      part[1] = 0.0f;
-    }
-    part[2 + lane] = 0.0f;
-    part[2 + 64 + lane] = 0.0f;
+    emptyChunk(part, lane);
     decodeMergeIfLast(p, h, lane);
     return;
   }
@@ -854,16 +884,8 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     v0 = xv[lane];
     v1 = xv[lane + 64];
   }
-  const int64_t key = kb + lane;
-  const h16* kr = p.kc + min<int64_t>(key, nk - 1) * dk + kvOff;
-  half8 kv[16];
-#pragma unroll
-  for (int c = 0; c < 16; ++c) kv[c] = ld8(kr + 8 * c);
-  const int g = lane >> 4, oc = lane & 15;
-  half8 vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = ld8(p.vc + min<int64_t>(kb + g + 4 * i, nk - 1) * dk + kvOff + 8 * oc);
+  GqaChunk c;
+  c.load(p.kc, p.vc, nk, ch, dk, kvOff);
   auto headSumSq = [&](const half8& c8) {
     float sq = 0.0f;
     if (lane < 16) {
@@ -897,45 +919,12 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     }
   }
   __syncthreads();
-  if (key == p0) {
+  const int d8 = lane & 15;
+  float q8[8];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) kv[c] = ld8(kn + 8 * c);
-  }
-  float dot = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 16; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dot = fmaf(qs[8 * c + e], static_cast<float>(kv[c][e]), dot);
-  const float sc = key < nk ? dot * p.scale * kLog2e : -INFINITY;
-  const float mc = waveMax(sc);
-  const float pv = __builtin_amdgcn_exp2f(sc - mc);
-  const float lc = waveSum(pv);
-  ps[lane] = pv;
-  __syncthreads();
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  const half8 vnew = ld8(vn + 8 * oc);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (hasNew && kb + g + 4 * i == p0) vv[i] = vnew;
-    const float w = ps[g + 4 * i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, static_cast<float>(vv[i][e]), acc[e]);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    acc[e] += __shfl_xor(acc[e], 16, 64);
-    acc[e] += __shfl_xor(acc[e], 32, 64);
-  }
-  if (lane == 0) {
-    part[0] = mc;
-    part[1] = lc;
-  }
-  if (g == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part[2 + 8 * oc + e] = acc[e];
-  }
+  for (int e = 0; e < 8; ++e) q8[e] = qs[8 * d8 + e];
+  const half8 none = {};
+  c.finish(q8, hasNew ? p0 : -1, hasNew ? ld8(kn + 8 * d8) : none, hasNew ? ld8(vn + 8 * d8) : none, p.scale, part);
   decodeMergeIfLast(p, h, lane);
 }
 
