@@ -128,6 +128,8 @@ __device__ __forceinline__ void raiseDeviceError(unsigned long long* rec, unsign
     rec[1] = static_cast<unsigned long long>(detail);
 }
 
+constexpr float kLog2e = 1.44269504088896341f;
+
 __device__ __forceinline__ float waveSum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -3,7 +3,7 @@
 //
 // One query (heads x 64) attends over cache rows 0..pos; row pos is k, v (+ bias) of this step and is written
 // into both caches. Keys are split into 64-key chunks, one wave per (head, chunk) (DecodeChunk: coalesced row
-// loads, DPP row sums for the scores, base-e softmax on q / 8 = q / sqrt(64), P.V in registers). Partials
+// loads, DPP row sums for the scores, softmax of q / 8 = q / sqrt(64) in log2 units, P.V in registers). Partials
 // (m, l, acc[64]) go to the caller's workspace; a second launch merges the chunks of each head in chunk order
 // (flash-decoding).
 #include "common.h"
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   ch.load(p.kc, p.vc, pos, p.cap, s * p.sub, D, c4);
   // an out-of-range position writes no cache row and NaN partials, and is recorded; the merge writes NaN
   if (ch.badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, pos);
-  const decF4 q = decF4{q4.x + bq.x, q4.y + bq.y, q4.z + bq.z, q4.w + bq.w} * 0.125f;
+  const decF4 q = decF4{q4.x + bq.x, q4.y + bq.y, q4.z + bq.z, q4.w + bq.w} * (0.125f * kLog2e);
   const decF4 knew = {k4.x + bk.x, k4.y + bk.y, k4.z + bk.z, k4.w + bk.w};
   const decF4 vnew = {v4.x + bv.x, v4.y + bv.y, v4.z + bv.z, v4.w + bv.w};
   if (p.writeKv && ch.writesRow()) {
@@ -69,10 +69,11 @@ __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   ch.store(r, p.partial + (static_cast<int64_t>(h) * p.chunks + s) * (kHd + 2));
 }
 
-// Merge of one head's chunks (one workgroup of 16 waves per head): M = max m_c, w_c = e^{m_c - M},
-// out[d] = sum_c w_c acc_c[d] / sum_c w_c l_c. Wave w takes chunks w, w + 16, ... in order, their loads issued 8
-// chunks at a time; the 16 wave sums are added in wave order. A long cache (512 chunks at 32768 rows) then costs a
-// few memory round trips instead of one per chunk.
+// Merge of one head's chunks (one workgroup of 16 waves per head), one pass: wave w takes chunks w, w + 16, ... in
+// order, 8 chunks' loads at a time, keeping a running max M_w (log2 units) and sums rescaled to it,
+// L_w = sum_c 2^{m_c - M_w} l_c, A_w[d] = sum_c 2^{m_c - M_w} acc_c[d]; then out[d] = sum_w 2^{M_w - M} A_w[d] /
+// sum_w 2^{M_w - M} L_w with M = max M_w, the 16 waves in order. A long cache (128 chunks per head) costs one
+// memory round trip.
 constexpr int kMergeWaves = 16, kMergeBatch = 8;
 __global__ __launch_bounds__(64 * kMergeWaves) void decodeMergeKernel(const float* __restrict__ partial,
                                                                       float* __restrict__ out, const int64_t* pos,
@@ -86,15 +87,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decodeMergeKernel(const floa
     return;
   }
   const float* base = partial + static_cast<int64_t>(h) * chunks * (kHd + 2);
-  float m = -INFINITY;
-  for (int c = tid; c < chunks; c += 64 * kMergeWaves) m = fmaxf(m, base[c * (kHd + 2)]);
-  m = waveMaxDpp(m);
-  if (lane == 0) sM[wv] = m;
-  __syncthreads();
-  float M = sM[0];
-#pragma unroll
-  for (int w = 1; w < kMergeWaves; ++w) M = fmaxf(M, sM[w]);
-  float a = 0.0f, l = 0.0f;
+  float M = -INFINITY, a = 0.0f, l = 0.0f;  // M is the same in every lane of the wave (m, l are per chunk)
   for (int c0 = wv; c0 < chunks; c0 += kMergeWaves * kMergeBatch) {
     float mc[kMergeBatch], lc[kMergeBatch], ac[kMergeBatch];
 #pragma unroll
@@ -104,24 +97,41 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decodeMergeKernel(const floa
       lc[i] = base[c * (kHd + 2) + 1];
       ac[i] = base[c * (kHd + 2) + 2 + lane];
     }
+    float bm = M;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i)
+      if (c0 + kMergeWaves * i < chunks && lc[i] > 0.0f) bm = fmaxf(bm, mc[i]);
+    if (bm > M) {  // rescale the running sums to the new max
+      const float r = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - bm);
+      a *= r;
+      l *= r;
+      M = bm;
+    }
 #pragma unroll
     for (int i = 0; i < kMergeBatch; ++i) {
-      if (c0 + kMergeWaves * i < chunks) {
-        const float w = lc[i] > 0.0f ? expf(mc[i] - M) : 0.0f;
+      if (c0 + kMergeWaves * i < chunks && lc[i] > 0.0f) {
+        const float w = __builtin_amdgcn_exp2f(mc[i] - M);
         l += w * lc[i];
         a += w * ac[i];
       }
     }
   }
   red[wv][lane] = a;
-  if (lane == 0) sL[wv] = l;
+  if (lane == 0) {
+    sM[wv] = M;
+    sL[wv] = l;
+  }
   __syncthreads();
   if (wv == 0) {
-    float A = red[0][lane], L = sL[0];
+    float Mx = sM[0];
 #pragma unroll
-    for (int w = 1; w < kMergeWaves; ++w) {
-      A += red[w][lane];
-      L += sL[w];
+    for (int w = 1; w < kMergeWaves; ++w) Mx = fmaxf(Mx, sM[w]);
+    float A = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; ++w) {
+      const float r = sL[w] > 0.0f ? __builtin_amdgcn_exp2f(sM[w] - Mx) : 0.0f;
+      A += r * red[w][lane];
+      L += r * sL[w];
     }
     out[h * kHd + lane] = A / L;
   }

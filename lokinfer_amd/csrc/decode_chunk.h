@@ -1,7 +1,7 @@
 // One wave's share of batch-1 decode attention: head h, keys kb .. ke - 1 of a [cap, heads * 64] K / V cache
 // (a 64-key chunk), with this step's key / value (row pos) taken from registers instead of the cache. Used by the
 // split decode kernel (q, k, v from the qkv row) and by the fused decode-step kernel (q, k, v from GEMV partial
-// rows).
+// rows). Scores are in log2 units (the caller scales q by log2(e) / sqrt(64)), so each exponential is one exp2.
 //
 // Layout: lane (g = lane / 16, d4 = lane % 16) owns dims 4 d4 .. 4 d4 + 3 of keys kb + g + 4 i, i = 0..15, so
 // each load instruction reads 4 whole cache rows (coalesced), a score is a 16-lane row sum (DPP), and the softmax
@@ -42,14 +42,15 @@ struct DecodeChunk {
       kr[i] = *reinterpret_cast<const decF4*>(kc + row * D + c4);
       vr[i] = *reinterpret_cast<const decF4*>(vc + row * D + c4);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all 32 row loads issued here, not spread into the reduction
   }
 
   struct Result {
-    float m, l;  // chunk max and sum of e^{s - m} (-inf, 0 for a chunk past the live keys)
-    decF4 acc;   // sum of e^{s - m} v over the chunk, this lane's 4 dims (the same in every row of the wave)
+    float m, l;  // chunk max and sum of 2^{s - m} (-inf, 0 for a chunk past the live keys)
+    decF4 acc;   // sum of 2^{s - m} v over the chunk, this lane's 4 dims (the same in every row of the wave)
   };
 
-  // q (already scaled by 1 / sqrt(64)), knew, vnew: this lane's 4 dims.
+  // q (already scaled by log2(e) / sqrt(64)), knew, vnew: this lane's 4 dims.
   __device__ __forceinline__ Result compute(decF4 q, decF4 knew, decF4 vnew) const {
     const float snew = rowSum16((q.x * knew.x + q.y * knew.y) + (q.z * knew.z + q.w * knew.w));
     float sc[16];
@@ -67,7 +68,7 @@ struct DecodeChunk {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t key = kb + g + 4 * i;
-      const float pj = key < ke ? expf(sc[i] - m) : 0.0f;
+      const float pj = key < ke ? __builtin_amdgcn_exp2f(sc[i] - m) : 0.0f;
       l += pj;
       const decF4 v = key < ke ? (key == ps ? vnew : vr[i]) : decF4{0.f, 0.f, 0.f, 0.f};
       acc += pj * v;
@@ -102,8 +103,8 @@ struct DecodeChunk {
   // Online combination of two chunk results (the running one first): both rescaled to the larger max.
   __device__ __forceinline__ static Result combine(Result a, Result b) {
     const float m = fmaxf(a.m, b.m);
-    const float wa = a.l > 0.0f ? expf(a.m - m) : 0.0f;
-    const float wb = b.l > 0.0f ? expf(b.m - m) : 0.0f;
+    const float wa = a.l > 0.0f ? __builtin_amdgcn_exp2f(a.m - m) : 0.0f;
+    const float wb = b.l > 0.0f ? __builtin_amdgcn_exp2f(b.m - m) : 0.0f;
     return Result{m, a.l * wa + b.l * wb, a.acc * wa + b.acc * wb};
   }
 

@@ -15,7 +15,7 @@
 // They replace the reference's gemv4*_f32_gpu / attention_decode_split_f32_gpu / add_bias_layernorm2_f32_gpu
 // sequence (transformer_gpu.cpp:122-251, kokoro_tok.metal:36-117, 637-924 in lariaus/lokinfer) for one layer,
 // with the same arithmetic per element: the sums over K are split into row slices and added in a fixed order
-// (deterministic), softmax is base e on q / 8, LayerNorm is two-pass with the biased variance.
+// (deterministic), softmax is of q / 8 (taken in log2 units), LayerNorm is two-pass with the biased variance.
 #include "common.h"
 #include "decode_chunk.h"
 #include "lokinfer_hip.h"
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
     if (rBase + ROWS > k && tid < ROWS && rBase + tid >= k) xs[tid] = 0.0f;
   } else {
     // rows rBase .. rBase + 63 are head blockIdx.y: merge its chunk partials (m, l, acc) in chunk order,
-    // M = max m_c, out[d] = sum_c e^{m_c - M} acc_c[d] / sum_c e^{m_c - M} l_c
+    // M = max m_c, out[d] = sum_c 2^{m_c - M} acc_c[d] / sum_c 2^{m_c - M} l_c (log2 units)
     static_assert(XMODE != 2 || ROWS == kDecHd, "attention merge needs 64 rows per workgroup");
     __shared__ float mrg[4][kDecHd];
     __shared__ float cw[64];
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void gemvPartXKernel(const float* __restrict__
     loadWeights();
     if (wv == 0) {
       const float M = waveMaxDpp(mc);
-      const float wc = lc > 0.0f ? expf(mc - M) : 0.0f;
+      const float wc = lc > 0.0f ? __builtin_amdgcn_exp2f(mc - M) : 0.0f;
       cw[lane] = wc;
       const float L = waveSumDpp(lc * wc);
       if (lane == 0) xs[0] = L;  // xs doubles as a scratch slot until the merge below
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(64) void decodeChunkPartKernel(const float* __restr
     *reinterpret_cast<f4v*>(kc + ps * D + c4) = knew;
     *reinterpret_cast<f4v*>(vc + ps * D + c4) = vnew;
   }
-  ch.finish((sq + bq) * 0.125f, knew, vnew, part);
+  ch.finish((sq + bq) * (0.125f * kLog2e), knew, vnew, part);
 }
 
 // Tied LM head of a decode step with the final LayerNorm and the greedy argmax folded in: x = LayerNorm(slices of

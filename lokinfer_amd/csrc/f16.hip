@@ -38,7 +38,6 @@ typedef _Float16 h16;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr float kLog2e = 1.44269504088896341f;
 
 // The contract's output rounding: the f32 result, then f16. The empty asm makes the f32 value opaque, so the compiler
 // cannot fold the operation producing it and the conversion into one mixed-precision instruction (v_fma_mix*),
