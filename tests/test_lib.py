@@ -127,3 +127,39 @@ def test_registry_rejects_bad_shapes_before_any_launch():
     assert rc == 1 and "multiple of dilation" in msg
     rc, msg = run(good[:5])
     assert rc == 1 and "wino_mm" in msg
+
+
+def test_decode_step_ops_reject_bad_shapes_before_any_launch():
+    """The fused decode-step ops check their shapes (and K % 4, K <= 1024) on the host, before any launch."""
+    import ctypes as C
+
+    L = _lib.lib()
+
+    def run(name, ints, floats=(1e-5,)):
+        k = L.lk_find_kernel(name.encode())
+        assert k, name
+        nop, nout = C.c_int(), C.c_int()
+        L.lk_kernel_arity(k, C.byref(nop), C.byref(nout))
+        n = nop.value + nout.value
+        ptrs = (C.c_void_p * n)()
+        arr = (C.c_int64 * len(ints))(*ints)
+        fl = (C.c_double * len(floats))(*floats)
+        return L.lk_run_kernel(k, ptrs, n, arr, len(ints), fl, len(floats), None, 0, None), L.lk_last_error().decode()
+
+    # lm_head_ln_argmax: part [S, K], bias [K], res [1, K], gamma [K], beta [K], table [V, K] -> logits [1, V], i64 [1]
+    S, K, V = 12, 768, 100
+    good = [S, K, K, 1, K, K, K, V, K, 1, V, 1]
+    bad_table = [S, K, K, 1, K, K, K, V, K + 4, 1, V, 1]
+    rc, msg = run("lm_head_ln_argmax_f32_gpu", bad_table)
+    assert rc == 1 and "lm_head_ln_argmax" in msg
+    rc, msg = run("lm_head_ln_argmax_f32_gpu", good[:6])
+    assert rc == 1 and "lm_head_ln_argmax" in msg
+    # gemv_partial_embed_ln: table [V, K], id [1], table2 [P, K], id2 [1], gamma, beta [K], w [K, N]
+    #   -> part [slices(K), N], sum [1, K]
+    N, P = 2304, 1024
+    slices = 12
+    good = [V, K, 1, P, K, 1, K, K, K, N, slices, N, 1, K]
+    rc, msg = run("gemv_partial_embed_ln_f32_gpu", good[:9] + [N, slices + 1, N, 1, K])
+    assert rc == 1 and "gemv_partial_embed_ln" in msg
+    rc, msg = run("gemv_partial_embed_ln_f32_gpu", [V, K, 2] + good[3:])
+    assert rc == 1 and "gemv_partial_embed_ln" in msg
