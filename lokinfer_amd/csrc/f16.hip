@@ -458,6 +458,162 @@ __global__ __launch_bounds__(256, 2) void gemmF16Kernel(GemmF16Params p) {
   }
 }
 
+// Wide form (SwiGLU at M >= 256, any GEMM at M >= 1024): workgroup tile 128 (M) x 128 (B rows), 4 waves as 2 x 2,
+// each 64 rows x two 32-column blocks (2 x 2 MFMA blocks: every A and B fragment feeds two MFMAs), which halves the
+// global and LDS bytes per MFMA against the 64 x 128 tile. Staged K-major through unpadded, XOR-swizzled LDS rows
+// from two register sets; B row layout (SwiGLU: 64 gate rows, then the 64 matching up rows), split-K partials and
+// epilogues as gemmF16Kernel.
+constexpr int WBM = 128, WBN = 128;
+constexpr int WA = WBM * GBK / 8 / 256, WB = WBN * GBK / 8 / 256;  // 16-byte chunks per thread per stage
+
+template <bool SWIGLU, bool KTAIL>
+__global__ __launch_bounds__(256, 2) void gemmF16WideKernel(GemmF16Params p) {
+  // unpadded 64-half rows; 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7): a 16-lane store phase covers two
+  // whole rows (all 64 banks) and a fragment read (rows lr of a 32-row block, one chunk each) hits 16 distinct
+  // 4-bank groups per phase
+  __shared__ __attribute__((aligned(16))) h16 As[2][WBM * GBK];
+  __shared__ __attribute__((aligned(16))) h16 Bs[2][WBN * GBK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5, wr = wave >> 1, wc = wave & 1;
+  const GridItem gi = xcdOrder();
+  const int64_t m0 = static_cast<int64_t>(gi.y) * WBM;
+  const int64_t kb = p.split > 1 ? gi.z * p.kSplit : 0;
+  const int64_t ke = p.split > 1 ? min<int64_t>(kb + p.kSplit, p.k) : p.k;
+  constexpr int CPR = GBK / 8;
+  const int sc = (tid % CPR) * 8;
+  const h16* ap[WA];
+  const h16* bp[WB];
+#pragma unroll
+  for (int i = 0; i < WA; ++i) ap[i] = p.a + min<int64_t>(m0 + (tid + 256 * i) / CPR, p.m - 1) * p.lda;
+#pragma unroll
+  for (int i = 0; i < WB; ++i) {
+    const int r = (tid + 256 * i) / CPR;
+    int64_t row;
+    if constexpr (SWIGLU) {
+      const int64_t o = min<int64_t>(static_cast<int64_t>(gi.x) * 64 + (r & 63), p.n - 1);
+      row = r < 64 ? o : p.n + o;
+    } else {
+      row = min<int64_t>(static_cast<int64_t>(gi.x) * WBN + r, p.n - 1);
+    }
+    bp[i] = p.bt + row * p.k;
+  }
+  // LDS offset (halves) of this thread's i-th staged chunk
+  auto swz = [&](int i) {
+    const int r = (tid + 256 * i) / CPR, c = tid % CPR;
+    return r * GBK + 8 * (c ^ ((r >> 1) & 7));
+  };
+  // fragment reads: row 32 b + lr of a tile, chunk 2 q + lh -> slot (2 q + lh) ^ ((lr >> 1) & 7)
+  int fo[GBK / 16];
+#pragma unroll
+  for (int q = 0; q < GBK / 16; ++q) fo[q] = lr * GBK + 8 * ((2 * q + lh) ^ ((lr >> 1) & 7));
+  // two register sets: stage st + 2's tile is loaded while stage st's MFMAs run; it is stored after stage st + 1's
+  // (a deeper ring of four sets measured no faster: 254 VGPRs)
+  half8 ra[2][WA], rb[2][WB];
+  auto gload = [&](int64_t k0, int s) {
+    const int64_t kk = min<int64_t>(k0 + sc, ke - 8);
+#pragma unroll
+    for (int i = 0; i < WA; ++i) ra[s][i] = ld8(ap[i] + kk);
+#pragma unroll
+    for (int i = 0; i < WB; ++i) rb[s][i] = ld8(bp[i] + kk);
+  };
+  auto sstore = [&](int buf, int64_t k0, int s) {
+    const bool zero = KTAIL && k0 + sc >= ke;
+    const half8 z = {};
+#pragma unroll
+    for (int i = 0; i < WA; ++i) st8(&As[buf][swz(i)], zero ? z : ra[s][i]);
+#pragma unroll
+    for (int i = 0; i < WB; ++i) st8(&Bs[buf][swz(i)], zero ? z : rb[s][i]);
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int64_t stages = (ke - kb + GBK - 1) / GBK;
+  auto kOf = [&](int64_t st) { return kb + min<int64_t>(st, stages - 1) * GBK; };
+  // stage st: MFMAs on LDS buffer st & 1, k step by k step (each step's four fragments read just before its four
+  // MFMAs); loads stage st + 2 into set st & 1 (its stage st is in LDS already) and stores stage st + 1 from the
+  // other set into the other buffer. Loads past the last stage reload it (unconditional).
+  auto stage = [&](int64_t st, int buf, int sLoad, int sStore) {
+    constexpr int Q = GBK / 16;
+    gload(kOf(st + 2), sLoad);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      half8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = ld8(&As[buf][(64 * wr + 32 * i) * GBK + fo[q]]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = ld8(&Bs[buf][(64 * j + 32 * wc) * GBK + fo[q]]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    sstore(buf ^ 1, kOf(st + 1), sStore);
+    __syncthreads();
+  };
+  gload(kOf(0), 0);
+  gload(kOf(1), 1);
+  sstore(0, kb, 0);
+  __syncthreads();
+  // set roles alternate: stage st loads into set st & 1 and stores from set (st + 1) & 1
+  int64_t st = 0;
+  for (; st + 2 <= stages; st += 2) {
+    stage(st, 0, 0, 1);
+    stage(st + 1, 1, 1, 0);
+  }
+  if (st < stages) stage(st, 0, 0, 1);
+  // accumulator r of block (i, j): row 64 wr + 32 i + 8 (r / 4) + 4 lh + r % 4, column lr of B block j
+  const int64_t lastRow = p.m - 1;
+  if (p.split > 1) {
+    const int64_t w = SWIGLU ? 2 * p.n : p.n;
+    float* pp = p.part + static_cast<int64_t>(gi.z) * p.m * w;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gm = m0 + 64 * wr + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (gm > lastRow) continue;
+        if constexpr (SWIGLU) {
+          const int64_t gn = static_cast<int64_t>(gi.x) * 64 + 32 * wc + lr;
+          if (gn < p.n) {
+            pp[gm * w + gn] = acc[i][0][r];
+            pp[gm * w + p.n + gn] = acc[i][1][r];
+          }
+        } else {
+          const int64_t gn = static_cast<int64_t>(gi.x) * WBN + 32 * wc + lr;
+          if (gn < p.n) pp[gm * w + gn] = acc[i][0][r];
+          if (gn + 64 < p.n) pp[gm * w + gn + 64] = acc[i][1][r];
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t gm = m0 + 64 * wr + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+      if (gm > lastRow) continue;
+      if constexpr (SWIGLU) {
+        const int64_t gn = static_cast<int64_t>(gi.x) * 64 + 32 * wc + lr;
+        if (gn < p.n) p.c[gm * p.n + gn] = toH16(siluMul(acc[i][0][r], acc[i][1][r]));
+      } else {
+        const int64_t gn = static_cast<int64_t>(gi.x) * WBN + 32 * wc + lr;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int64_t col = gn + 64 * j;
+          if (col >= p.n) continue;
+          float y = acc[i][j][r];
+          if (p.bias) y += static_cast<float>(p.bias[col]);
+          if (p.res) y = static_cast<float>(p.res[gm * p.n + col]) + y;
+          p.c[gm * p.n + col] = toH16(y);
+        }
+      }
+    }
+}
+
 // split-K reduction: the partial planes summed in order, then the epilogue
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void gemmF16ReduceKernel(GemmF16Params p) {
@@ -1045,8 +1201,11 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
   }
   GemmF16Params p{static_cast<const h16*>(x), static_cast<const h16*>(wt), static_cast<const h16*>(bias),
                   static_cast<const h16*>(res), static_cast<h16*>(out), nullptr, m, n, k, k, k, 1};
+  // the wide tile where it measured faster: SwiGLU at M >= 256 (Qwen3's 416-row gate/up: 57 -> 49 us) and any
+  // M >= 1024 (4096^3: 471 -> 706 TFLOP/s); at M = 416 the plain shapes fill the chip better with 64-row tiles
+  const bool wide = swiglu ? m >= 256 : m >= 1024;
   const unsigned gx = static_cast<unsigned>(swiglu ? (n + 63) / 64 : (n + GBN - 1) / GBN);
-  const unsigned gy = static_cast<unsigned>((m + GBM - 1) / GBM);
+  const unsigned gy = static_cast<unsigned>(wide ? (m + WBM - 1) / WBM : (m + GBM - 1) / GBM);
   const int64_t tiles = static_cast<int64_t>(gx) * gy;
   int split = 1;
   if (workspace && tiles < 192 && k >= 1024) {
@@ -1061,7 +1220,13 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
   }
   const bool tail = (p.split > 1 ? p.kSplit : k) % GBK != 0 || k % GBK != 0;
   const dim3 grid(gx, gy, static_cast<unsigned>(split));
-  if (swiglu) {
+  if (wide && swiglu) {
+    if (tail) hipLaunchKernelGGL((gemmF16WideKernel<true, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemmF16WideKernel<true, false>), grid, dim3(256), 0, s, p);
+  } else if (wide) {
+    if (tail) hipLaunchKernelGGL((gemmF16WideKernel<false, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemmF16WideKernel<false, false>), grid, dim3(256), 0, s, p);
+  } else if (swiglu) {
     if (tail) hipLaunchKernelGGL((gemmF16Kernel<true, true>), grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL((gemmF16Kernel<true, false>), grid, dim3(256), 0, s, p);
   } else {

@@ -59,7 +59,9 @@ def gemm_term(x, w):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 2048, 4096), (44, 2048, 2048), (401, 2048, 1024), (416, 6144, 2048),
-                                   (3, 40, 24), (70, 200, 130), (1, 6144, 2048), (128, 2048, 4096)])
+                                   (3, 40, 24), (70, 200, 130), (1, 6144, 2048), (128, 2048, 4096),
+                                   # the 128-row tile (M >= 1024): split-K grid, K tail with ragged M and N, full grid
+                                   (1024, 2048, 1024), (1100, 200, 300), (1024, 2048, 4096)])
 def test_gemm(gpu, m, k, n):
     lk = gpu
     F = lk.ops.f16_gpu
@@ -75,7 +77,10 @@ def test_gemm(gpu, m, k, n):
           ft + 2.0 ** -23 * np.abs(O.c(x) @ O.c(w) + O.c(b)), "gemm_bias_opt")
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 2048, 6144), (44, 2048, 6144), (416, 2048, 6144), (5, 64, 40)])
+# M >= 256 runs the 128-row tile: (416, 2048, 6144) on a full grid, (300, 520, 200) with a K tail and ragged M and
+# N, (512, 2048, 512) split over K
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 6144), (44, 2048, 6144), (416, 2048, 6144), (5, 64, 40),
+                                   (300, 520, 200), (512, 2048, 512)])
 def test_gemm_swiglu(gpu, m, k, n):
     lk = gpu
     F = lk.ops.f16_gpu
