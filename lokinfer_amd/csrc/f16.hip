@@ -656,7 +656,8 @@ struct GqaParams {
   h16* out;
   float* part;
   int64_t t, cap;
-  int qh, kvh, chunks;
+  int qh, kvh;
+  int chunks, sub;  // T = 1: partials (waves) per head, each over sub consecutive 64-key chunks
   float scale;  // 1 / sqrt(128)
   unsigned long long* err;  // the GPU's error record: positions outside the cache
 };
@@ -801,39 +802,37 @@ __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
   }
 }
 
-// merged decode attention value d of one head from its chunk partials (m, l, o[128]), in chunk order:
-// M = max m_c, out = sum_c w_c o_c[d] / sum_c w_c l_c with w_c = 2^(m_c - M). The chunks go in blocks of 16 whose
-// loads are issued together (predicated), so a merge costs a few memory round trips instead of one per chunk.
+// merged decode attention value d of one head from its partials (m, l, o[128]), in partial order, one pass:
+// out = sum_c w_c o_c[d] / sum_c w_c l_c with w_c = 2^(m_c - M), M the running max (the sums rescaled when it
+// grows). The partials go in blocks of 16 whose loads are issued together (predicated), so a merge costs one memory
+// round trip per block (at most 8: a head has at most 128 partials).
 constexpr int MB = 16;
 __device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
-  float m = -INFINITY;
-  for (int c0 = 0; c0 < used; c0 += MB) {
-    float mc[MB];
-#pragma unroll
-    for (int c = 0; c < MB; ++c) mc[c] = c0 + c < used ? part[(c0 + c) * (QHD + 2)] : -INFINITY;
-#pragma unroll
-    for (int c = 0; c < MB; ++c)
-      if (c0 + c < used) m = fmaxf(m, mc[c]);
-  }
-  float l = 0.0f, acc = 0.0f;
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
   for (int c0 = 0; c0 < used; c0 += MB) {
     float mc[MB], lc[MB], oc[MB];
 #pragma unroll
     for (int c = 0; c < MB; ++c) {
       const bool in = c0 + c < used;
       const float* pc = part + (c0 + c) * (QHD + 2);
-      mc[c] = in ? pc[0] : 0.0f;
+      mc[c] = in ? pc[0] : -INFINITY;
       lc[c] = in ? pc[1] : 0.0f;
       oc[c] = in ? pc[2 + d] : 0.0f;
     }
+    float mb = m;
+#pragma unroll
+    for (int c = 0; c < MB; ++c) mb = fmaxf(mb, mc[c]);
+    if (mb == -INFINITY) continue;  // nothing live yet
+    const float r = __builtin_amdgcn_exp2f(m - mb);  // 0 while m is -inf
+    l *= r;
+    acc *= r;
 #pragma unroll
     for (int c = 0; c < MB; ++c) {
-      if (c0 + c < used) {
-        const float w = __builtin_amdgcn_exp2f(mc[c] - m);
-        l = fmaf(w, lc[c], l);
-        acc = fmaf(w, oc[c], acc);
-      }
+      const float w = lc[c] > 0.0f ? __builtin_amdgcn_exp2f(mc[c] - mb) : 0.0f;
+      l = fmaf(w, lc[c], l);
+      acc = fmaf(w, oc[c], acc);
     }
+    m = mb;
   }
   return toH16(acc / l);
 }
@@ -872,11 +871,15 @@ struct GqaChunk {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // q8: this lane's 8 query dims (f32). newKey: position whose key / value are knew / vnew (-1: none). Writes the
-  // chunk partial (m, l, o[128]) (scores in log2 units: dot * scale * log2 e).
-  __device__ __forceinline__ void finish(const float (&q8)[8], int64_t newKey, const half8& knew, const half8& vnew,
-                                         float scale, float* part) const {
-    const int lane = threadIdx.x & 63;
+  struct Result {
+    float m, l;     // chunk max and sum of 2^(s - m) (-inf, 0 for a chunk past the live keys)
+    float acc[8];   // sum of 2^(s - m) v over the chunk, this lane's 8 dims (the same in every row of the wave)
+  };
+
+  // q8: this lane's 8 query dims (f32). newKey: position whose key / value are knew / vnew (-1: none). Scores in
+  // log2 units: dot * scale * log2 e.
+  __device__ __forceinline__ Result compute(const float (&q8)[8], int64_t newKey, const half8& knew,
+                                            const half8& vnew, float scale) const {
     float sc[16];
     float m = -INFINITY;
 #pragma unroll
@@ -903,19 +906,49 @@ struct GqaChunk {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, static_cast<float>(vv[e]), acc[e]);
     }
-    l = crossRowSum(l);
+    Result r;
+    r.m = m;
+    r.l = crossRowSum(l);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = crossRowSum(acc[e]);
+    for (int e = 0; e < 8; ++e) r.acc[e] = crossRowSum(acc[e]);
+    return r;
+  }
+
+  // writes the partial (m, l, o[128]): lane 0 m and l, row 0 the 128 dims
+  __device__ __forceinline__ void store(const Result& r, float* part) const {
+    const int lane = threadIdx.x & 63;
     if (lane == 0) {
-      part[0] = m;
-      part[1] = l;
+      part[0] = r.m;
+      part[1] = r.l;
     }
     if (g == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part[2 + 8 * d8 + e] = acc[e];
+      for (int e = 0; e < 8; ++e) part[2 + 8 * d8 + e] = r.acc[e];
     }
   }
+
+  // online combination of two chunk results (the running one first), both rescaled to the larger max
+  __device__ __forceinline__ static Result combine(const Result& a, const Result& b) {
+    Result r;
+    r.m = fmaxf(a.m, b.m);
+    const float wa = a.l > 0.0f ? __builtin_amdgcn_exp2f(a.m - r.m) : 0.0f;
+    const float wb = b.l > 0.0f ? __builtin_amdgcn_exp2f(b.m - r.m) : 0.0f;
+    r.l = a.l * wa + b.l * wb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.acc[e] = a.acc[e] * wa + b.acc[e] * wb;
+    return r;
+  }
 };
+
+// caches of more than 128 chunks: a wave takes ceil(chunks / 128) consecutive chunks, so a head has at most 128
+// partials to merge
+constexpr int kGqaMaxWaves = 128;
+inline void gqaSplit(int64_t cap, int* waves, int* sub) {
+  const int64_t c = (cap + DCH - 1) / DCH;
+  const int64_t sb = c > kGqaMaxWaves ? (c + kGqaMaxWaves - 1) / kGqaMaxWaves : 1;
+  *sub = static_cast<int>(sb);
+  *waves = static_cast<int>((c + sb - 1) / sb);
+}
 
 __device__ __forceinline__ void emptyChunk(float* part, int lane) {
   if (lane == 0) {
@@ -927,25 +960,31 @@ __device__ __forceinline__ void emptyChunk(float* part, int lane) {
 }
 
 __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
-  const int h = blockIdx.x, ch = blockIdx.y, lane = threadIdx.x;
+  const int h = blockIdx.x, w = blockIdx.y, lane = threadIdx.x;
   const int64_t dk = static_cast<int64_t>(p.kvh) * QHD;
   const int64_t kvOff = static_cast<int64_t>(h / (p.qh / p.kvh)) * QHD;
   const int64_t p0 = *p.pos;
-  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
+  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + w) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
-  if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
-  if (static_cast<int64_t>(ch) * DCH >= nk) {
+  if (nk == 0 && h == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
+  const int ch0 = w * p.sub;
+  if (static_cast<int64_t>(ch0) * DCH >= nk) {
     emptyChunk(part, lane);
     return;
   }
   const half8 qh8 = ld8(p.q + h * QHD + 8 * (lane & 15));
   GqaChunk c;
-  c.load(p.kc, p.vc, nk, ch, dk, kvOff);
+  c.load(p.kc, p.vc, nk, ch0, dk, kvOff);
   float q8[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) q8[e] = static_cast<float>(qh8[e]);
   const half8 none = {};
-  c.finish(q8, -1, none, none, p.scale, part);
+  GqaChunk::Result r = c.compute(q8, -1, none, none, p.scale);
+  for (int j = 1; j < p.sub; ++j) {
+    c.load(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
+    r = GqaChunk::combine(r, c.compute(q8, -1, none, none, p.scale));
+  }
+  c.store(r, part);
 }
 
 __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
@@ -958,7 +997,8 @@ __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
     if (h == 0 && d == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
     return;
   }
-  *o = mergeDim(part, static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH)), d);
+  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per partial
+  *o = mergeDim(part, static_cast<int>(min<int64_t>(p.chunks, (p0 + span) / span)), d);
 }
 
 // ---- T = 1 with the QK-norm / RoPE / KV write and the merge folded in: a chunk wave normalizes and rotates its q
@@ -979,7 +1019,8 @@ struct GqaDecParams {
   h16* out;            // [1, qh 128]
   unsigned* counters;  // [qh], zero between launches
   int64_t cap;
-  int qh, kvh, chunks;
+  int qh, kvh;
+  int chunks, sub;  // partials (waves) per head, each over sub consecutive 64-key chunks
   float scale, eps;
   RopeTable tab;
   unsigned long long* err;  // the GPU's error record: positions outside the cache
@@ -993,7 +1034,8 @@ __device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, 
   if (!lastFlag) return;
   __threadfence();  // acquire: the other waves' partials (and no stale L1 lines) from here on
   const int64_t p0 = *p.pos;
-  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + DCH) / DCH));
+  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per partial
+  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + span) / span));
   const float* ph = p.part + static_cast<int64_t>(h) * p.chunks * (QHD + 2);
   h16* o = p.out + static_cast<int64_t>(h) * QHD;
   o[lane] = mergeDim(ph, used, lane);
@@ -1007,21 +1049,22 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   __shared__ float qs[QHD];
   __shared__ __attribute__((aligned(16))) h16 kn[QHD];
   __shared__ __attribute__((aligned(16))) h16 vn[QHD];
-  const int h = blockIdx.x, ch = blockIdx.y, lane = threadIdx.x;
+  const int h = blockIdx.x, w = blockIdx.y, lane = threadIdx.x;
   const int grp = p.qh / p.kvh;
   const int64_t dq = static_cast<int64_t>(p.qh) * QHD, dk = static_cast<int64_t>(p.kvh) * QHD;
   const int64_t kvOff = static_cast<int64_t>(h / grp) * QHD;
   const int64_t p0 = *p.pos;
-  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + ch) * (QHD + 2);
+  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + w) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
-  if (nk == 0 && h == 0 && ch == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
-  const int64_t kb = static_cast<int64_t>(ch) * DCH;
+  if (nk == 0 && h == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
+  const int ch0 = w * p.sub;
+  const int64_t kb = static_cast<int64_t>(ch0) * DCH;
   if (kb >= nk) {
     emptyChunk(part, lane);
     decodeMergeIfLast(p, h, lane);
     return;
   }
-  const bool hasNew = p0 < kb + DCH;  // this chunk holds key pos (kb <= pos here)
+  const bool hasNew = p0 < kb + static_cast<int64_t>(DCH) * p.sub;  // this wave's chunks hold key pos (kb <= pos)
   const int cl = lane & 15;           // rowSumSq's chunk of a 128-wide head (lanes 16.. add nothing)
   const h16* xq = p.qkv + h * QHD;
   const h16* xk = p.qkv + dq + kvOff;
@@ -1040,7 +1083,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     v1 = xv[lane + 64];
   }
   GqaChunk c;
-  c.load(p.kc, p.vc, nk, ch, dk, kvOff);
+  c.load(p.kc, p.vc, nk, ch0, dk, kvOff);
   auto headSumSq = [&](const half8& c8) {
     float sq = 0.0f;
     if (lane < 16) {
@@ -1079,7 +1122,14 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) q8[e] = qs[8 * d8 + e];
   const half8 none = {};
-  c.finish(q8, hasNew ? p0 : -1, hasNew ? ld8(kn + 8 * d8) : none, hasNew ? ld8(vn + 8 * d8) : none, p.scale, part);
+  const int64_t newKey = hasNew ? p0 : -1;
+  const half8 knew = hasNew ? ld8(kn + 8 * d8) : none, vnew = hasNew ? ld8(vn + 8 * d8) : none;
+  GqaChunk::Result r = c.compute(q8, newKey, knew, vnew, p.scale);
+  for (int j = 1; j < p.sub; ++j) {
+    c.load(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
+    r = GqaChunk::combine(r, c.compute(q8, newKey, knew, vnew, p.scale));
+  }
+  c.store(r, part);
   decodeMergeIfLast(p, h, lane);
 }
 
@@ -1324,7 +1374,9 @@ int lk_hip_f16_qknorm_rope_kv(const void* qkv, const void* qg, const void* kg, c
 }
 
 int64_t lk_hip_f16_attention_workspace_bytes(int qh, int64_t cap) {
-  return static_cast<int64_t>(qh) * ((cap + lkd::DCH - 1) / lkd::DCH) * (lkd::QHD + 2) * 4;
+  int waves = 0, sub = 0;
+  lkd::gqaSplit(cap, &waves, &sub);
+  return static_cast<int64_t>(qh) * waves * (lkd::QHD + 2) * 4;
 }
 
 // causal GQA: q f16[T, qh 128], caches f16[cap, kvh 128] holding rows 0..pos+T-1 -> out f16[T, qh 128].
@@ -1336,9 +1388,10 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
     return 1;
   if (t == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
+  int chunks = 0, sub = 0;
+  gqaSplit(cap, &chunks, &sub);
   GqaParams p{static_cast<const h16*>(q), static_cast<const h16*>(kc), static_cast<const h16*>(vc), pos,
-              static_cast<h16*>(out), static_cast<float*>(workspace), t, cap, qh, kvh, chunks,
+              static_cast<h16*>(out), static_cast<float*>(workspace), t, cap, qh, kvh, chunks, sub,
               1.0f / std::sqrt(static_cast<float>(QHD)), lkh::deviceErrorRecord()};
   if (t == 1) {
     if (!workspace || workspace_bytes < lk_hip_f16_attention_workspace_bytes(qh, cap)) return 3;
@@ -1364,10 +1417,11 @@ int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void*
       !aligned16(vc))
     return 1;
   if (!workspace || workspace_bytes < lk_hip_f16_attention_workspace_bytes(qh, cap)) return 3;
-  const int chunks = static_cast<int>((cap + DCH - 1) / DCH);
+  int chunks = 0, sub = 0;
+  gqaSplit(cap, &chunks, &sub);
   GqaDecParams p{static_cast<const h16*>(qkv), static_cast<const h16*>(qg), static_cast<const h16*>(kg), pos,
                  static_cast<h16*>(kc), static_cast<h16*>(vc), static_cast<float*>(workspace), static_cast<h16*>(out),
-                 counters, cap, qh, kvh, chunks, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta),
+                 counters, cap, qh, kvh, chunks, sub, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta),
                  lkh::deviceErrorRecord()};
   hipLaunchKernelGGL(gqaDecodeQkrKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), p);

@@ -167,8 +167,10 @@ def _attn_case(t, pos, qh, kvh, cap):
     return q, kc, vc
 
 
+# caches of more than 128 chunks (cap 20000: 313 chunks) run waves over 3 consecutive chunks each
 @pytest.mark.parametrize("t,pos,cap", [(1, 0, 64), (1, 415, 480), (1, 1999, 2048), (1, 64, 2048), (2, 0, 64),
-                                       (44, 0, 480), (416, 0, 480), (33, 100, 480), (70, 7, 300), (300, 1500, 2048)])
+                                       (44, 0, 480), (416, 0, 480), (33, 100, 480), (70, 7, 300), (300, 1500, 2048),
+                                       (1, 70, 20000), (1, 9000, 20000), (1, 19999, 20000)])
 def test_attention_gqa(gpu, t, pos, cap):
     lk = gpu
     F = lk.ops.f16_gpu
@@ -242,7 +244,7 @@ def test_embedding_scatter_elementwise(gpu):
 
 
 @pytest.mark.parametrize("pos,cap", [(0, 64), (63, 480), (64, 480), (415, 480), (1000, 1024), (1999, 2048),
-                                     (5000, 8192)])
+                                     (5000, 8192), (8300, 20000), (19999, 20000)])
 def test_decode_fusions_equal_compositions(gpu, pos, cap):
     """The decode-step fusions give the bits of the ops they replace: attention_decode_qkr vs qknorm_rope_kv +
     attention_gqa (output and both caches), twice in a row with the same counters (each call leaves them zero);
