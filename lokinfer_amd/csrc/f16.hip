@@ -950,6 +950,13 @@ inline void gqaSplit(int64_t cap, int* waves, int* sub) {
   *waves = static_cast<int>((c + sb - 1) / sb);
 }
 
+// two q heads of a kv group per wave (their K / V rows read once) on caches of 128 or more chunks, where the
+// kernels are bandwidth-bound (32768 rows: 65 -> 50 us); on short caches, which are latency-bound, the halved grid
+// and doubled per-wave work cost more (config 5 at pos 416: 7.7 -> 9.1 us)
+inline bool pairHeads(int qh, int kvh, int64_t cap) {
+  return (qh / kvh) % 2 == 0 && (cap + DCH - 1) / DCH >= kGqaMaxWaves;
+}
+
 __device__ __forceinline__ void emptyChunk(float* part, int lane) {
   if (lane == 0) {
     part[0] = -INFINITY;
@@ -959,32 +966,46 @@ __device__ __forceinline__ void emptyChunk(float* part, int lane) {
   part[2 + 64 + lane] = 0.0f;
 }
 
+// H q heads of one kv group per wave (H = 2 when the group size is even): the K / V rows are loaded once and each
+// head's partial is the single-head arithmetic on them, so H changes no bits.
+template <int H>
 __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
-  const int h = blockIdx.x, w = blockIdx.y, lane = threadIdx.x;
+  const int h0 = blockIdx.x * H, w = blockIdx.y, lane = threadIdx.x;
   const int64_t dk = static_cast<int64_t>(p.kvh) * QHD;
-  const int64_t kvOff = static_cast<int64_t>(h / (p.qh / p.kvh)) * QHD;
+  const int64_t kvOff = static_cast<int64_t>(h0 / (p.qh / p.kvh)) * QHD;
   const int64_t p0 = *p.pos;
-  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + w) * (QHD + 2);
+  float* part[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) part[k] = p.part + (static_cast<int64_t>(h0 + k) * p.chunks + w) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
-  if (nk == 0 && h == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
+  if (nk == 0 && h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int ch0 = w * p.sub;
   if (static_cast<int64_t>(ch0) * DCH >= nk) {
-    emptyChunk(part, lane);
+#pragma unroll
+    for (int k = 0; k < H; ++k) emptyChunk(part[k], lane);
     return;
   }
-  const half8 qh8 = ld8(p.q + h * QHD + 8 * (lane & 15));
+  half8 qh8[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) qh8[k] = ld8(p.q + (h0 + k) * QHD + 8 * (lane & 15));
   GqaChunk c;
   c.load(p.kc, p.vc, nk, ch0, dk, kvOff);
-  float q8[8];
+  float q8[H][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q8[e] = static_cast<float>(qh8[e]);
+  for (int k = 0; k < H; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q8[k][e] = static_cast<float>(qh8[k][e]);
   const half8 none = {};
-  GqaChunk::Result r = c.compute(q8, -1, none, none, p.scale);
+  GqaChunk::Result r[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) r[k] = c.compute(q8[k], -1, none, none, p.scale);
   for (int j = 1; j < p.sub; ++j) {
     c.load(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
-    r = GqaChunk::combine(r, c.compute(q8, -1, none, none, p.scale));
+#pragma unroll
+    for (int k = 0; k < H; ++k) r[k] = GqaChunk::combine(r[k], c.compute(q8[k], -1, none, none, p.scale));
   }
-  c.store(r, part);
+#pragma unroll
+  for (int k = 0; k < H; ++k) c.store(r[k], part[k]);
 }
 
 __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
@@ -1044,33 +1065,47 @@ __device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, 
 }
 
 // All loads are issued first, in the order the in-order memory counter needs: the raw q / k / v values (the norms
-// wait for them alone), then the chunk's K and V rows.
+// wait for them alone), then the chunk's K and V rows. H q heads of one kv group per wave, as in
+// gqaDecodeChunkKernel (each head's merge is run by the last wave counted on that head's counter).
+template <int H>
 __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
-  __shared__ float qs[QHD];
+  __shared__ float qs[H][QHD];
   __shared__ __attribute__((aligned(16))) h16 kn[QHD];
   __shared__ __attribute__((aligned(16))) h16 vn[QHD];
-  const int h = blockIdx.x, w = blockIdx.y, lane = threadIdx.x;
+  const int h0 = blockIdx.x * H, w = blockIdx.y, lane = threadIdx.x;
   const int grp = p.qh / p.kvh;
   const int64_t dq = static_cast<int64_t>(p.qh) * QHD, dk = static_cast<int64_t>(p.kvh) * QHD;
-  const int64_t kvOff = static_cast<int64_t>(h / grp) * QHD;
+  const int64_t kvOff = static_cast<int64_t>(h0 / grp) * QHD;
   const int64_t p0 = *p.pos;
-  float* part = p.part + (static_cast<int64_t>(h) * p.chunks + w) * (QHD + 2);
+  float* part[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) part[k] = p.part + (static_cast<int64_t>(h0 + k) * p.chunks + w) * (QHD + 2);
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
-  if (nk == 0 && h == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
+  if (nk == 0 && h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int ch0 = w * p.sub;
   const int64_t kb = static_cast<int64_t>(ch0) * DCH;
   if (kb >= nk) {
-    emptyChunk(part, lane);
-    decodeMergeIfLast(p, h, lane);
+#pragma unroll
+    for (int k = 0; k < H; ++k) {
+      emptyChunk(part[k], lane);
+      decodeMergeIfLast(p, h0 + k, lane);
+    }
     return;
   }
   const bool hasNew = p0 < kb + static_cast<int64_t>(DCH) * p.sub;  // this wave's chunks hold key pos (kb <= pos)
   const int cl = lane & 15;           // rowSumSq's chunk of a 128-wide head (lanes 16.. add nothing)
-  const h16* xq = p.qkv + h * QHD;
   const h16* xk = p.qkv + dq + kvOff;
   const h16* xv = p.qkv + dq + dk + kvOff;
-  const half8 qc = ld8(xq + 8 * cl);
-  const h16 q0 = xq[lane], q1 = xq[lane + 64], gq0 = p.qg[lane], gq1 = p.qg[lane + 64];
+  half8 qc[H];
+  h16 q0[H], q1[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) {
+    const h16* xq = p.qkv + (h0 + k) * QHD;
+    qc[k] = ld8(xq + 8 * cl);
+    q0[k] = xq[lane];
+    q1[k] = xq[lane + 64];
+  }
+  const h16 gq0 = p.qg[lane], gq1 = p.qg[lane + 64];
   half8 kc8 = {};
   h16 k0 = 0, k1 = 0, gk0 = 0, gk1 = 0, v0 = 0, v1 = 0;
   if (hasNew) {
@@ -1092,13 +1127,14 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     }
     return waveSum(sq);
   };
-  {
-    const float r = rmsFactor(headSumSq(qc), QHD, p.eps);
+#pragma unroll
+  for (int k = 0; k < H; ++k) {
+    const float r = rmsFactor(headSumSq(qc[k]), QHD, p.eps);
     h16 a, b;
-    ropePair(static_cast<float>(rmsElem(q0, gq0, r)), static_cast<float>(rmsElem(q1, gq1, r)), p0, p.tab.invf[lane],
-             a, b);
-    qs[lane] = static_cast<float>(a);
-    qs[lane + 64] = static_cast<float>(b);
+    ropePair(static_cast<float>(rmsElem(q0[k], gq0, r)), static_cast<float>(rmsElem(q1[k], gq1, r)), p0,
+             p.tab.invf[lane], a, b);
+    qs[k][lane] = static_cast<float>(a);
+    qs[k][lane + 64] = static_cast<float>(b);
   }
   if (hasNew) {
     const float r = rmsFactor(headSumSq(kc8), QHD, p.eps);
@@ -1109,7 +1145,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
     kn[lane + 64] = b;
     vn[lane] = v0;
     vn[lane + 64] = v1;
-    if (h % grp == 0) {  // one wave per kv head writes the new row to both caches
+    if (h0 % grp == 0) {  // one wave per kv head writes the new row to both caches
       p.kc[p0 * dk + kvOff + lane] = a;
       p.kc[p0 * dk + kvOff + lane + 64] = b;
       p.vc[p0 * dk + kvOff + lane] = v0;
@@ -1118,19 +1154,27 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   }
   __syncthreads();
   const int d8 = lane & 15;
-  float q8[8];
+  float q8[H][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q8[e] = qs[8 * d8 + e];
+  for (int k = 0; k < H; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q8[k][e] = qs[k][8 * d8 + e];
   const half8 none = {};
   const int64_t newKey = hasNew ? p0 : -1;
   const half8 knew = hasNew ? ld8(kn + 8 * d8) : none, vnew = hasNew ? ld8(vn + 8 * d8) : none;
-  GqaChunk::Result r = c.compute(q8, newKey, knew, vnew, p.scale);
+  GqaChunk::Result r[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) r[k] = c.compute(q8[k], newKey, knew, vnew, p.scale);
   for (int j = 1; j < p.sub; ++j) {
     c.load(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
-    r = GqaChunk::combine(r, c.compute(q8, newKey, knew, vnew, p.scale));
+#pragma unroll
+    for (int k = 0; k < H; ++k) r[k] = GqaChunk::combine(r[k], c.compute(q8[k], newKey, knew, vnew, p.scale));
   }
-  c.store(r, part);
-  decodeMergeIfLast(p, h, lane);
+#pragma unroll
+  for (int k = 0; k < H; ++k) {
+    c.store(r[k], part[k]);
+    decodeMergeIfLast(p, h0 + k, lane);
+  }
 }
 
 
@@ -1395,8 +1439,12 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
               1.0f / std::sqrt(static_cast<float>(QHD)), lkh::deviceErrorRecord()};
   if (t == 1) {
     if (!workspace || workspace_bytes < lk_hip_f16_attention_workspace_bytes(qh, cap)) return 3;
-    hipLaunchKernelGGL(gqaDecodeChunkKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64),
-                       0, s, p);
+    if (pairHeads(qh, kvh, cap))
+      hipLaunchKernelGGL(gqaDecodeChunkKernel<2>, dim3(static_cast<unsigned>(qh / 2), static_cast<unsigned>(chunks)),
+                         dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL(gqaDecodeChunkKernel<1>, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)),
+                         dim3(64), 0, s, p);
     hipLaunchKernelGGL(gqaDecodeMergeKernel, dim3(static_cast<unsigned>(qh)), dim3(128), 0, s, p);
     return launched();
   }
@@ -1423,8 +1471,13 @@ int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void*
                  static_cast<h16*>(kc), static_cast<h16*>(vc), static_cast<float*>(workspace), static_cast<h16*>(out),
                  counters, cap, qh, kvh, chunks, sub, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta),
                  lkh::deviceErrorRecord()};
-  hipLaunchKernelGGL(gqaDecodeQkrKernel, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pairHeads(qh, kvh, cap))
+    hipLaunchKernelGGL(gqaDecodeQkrKernel<2>, dim3(static_cast<unsigned>(qh / 2), static_cast<unsigned>(chunks)),
+                       dim3(64), 0, s, p);
+  else
+    hipLaunchKernelGGL(gqaDecodeQkrKernel<1>, dim3(static_cast<unsigned>(qh), static_cast<unsigned>(chunks)),
+                       dim3(64), 0, s, p);
   return launched();
 }
 

@@ -167,7 +167,8 @@ def _attn_case(t, pos, qh, kvh, cap):
     return q, kc, vc
 
 
-# caches of more than 128 chunks (cap 20000: 313 chunks) run waves over 3 consecutive chunks each
+# caches of 128 chunks or more take two q heads per wave; past 128 chunks (cap 20000: 313) a wave runs 3
+# consecutive chunks
 @pytest.mark.parametrize("t,pos,cap", [(1, 0, 64), (1, 415, 480), (1, 1999, 2048), (1, 64, 2048), (2, 0, 64),
                                        (44, 0, 480), (416, 0, 480), (33, 100, 480), (70, 7, 300), (300, 1500, 2048),
                                        (1, 70, 20000), (1, 9000, 20000), (1, 19999, 20000)])
