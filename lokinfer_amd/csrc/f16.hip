@@ -804,10 +804,12 @@ __global__ __launch_bounds__(256) void gqaFlashKernel(GqaParams p) {
 
 // merged decode attention value d of one head from its partials (m, l, o[128]), in partial order, one pass:
 // out = sum_c w_c o_c[d] / sum_c w_c l_c with w_c = 2^(m_c - M), M the running max (the sums rescaled when it
-// grows). The partials go in blocks of 16 whose loads are issued together (predicated), so a merge costs one memory
-// round trip per block (at most 8: a head has at most 128 partials).
-constexpr int MB = 16;
-__device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
+// grows). The partials go in blocks of MB whose loads are issued together (predicated), so a merge costs one memory
+// round trip per block: 16-wide blocks up to 16 partials (a short cache's one block), 64-wide beyond (a head has at
+// most 128 partials: two round trips; 16-wide blocks took 8 and 22 us at 32768 rows, 64-wide ones cost the short
+// case 0.6 us). The width depends only on the partial count, so every caller merges with the same bits.
+template <int MB>
+__device__ __forceinline__ h16 mergeDimBlocks(const float* part, int used, int d) {
   float m = -INFINITY, l = 0.0f, acc = 0.0f;
   for (int c0 = 0; c0 < used; c0 += MB) {
     float mc[MB], lc[MB], oc[MB];
@@ -835,6 +837,10 @@ __device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
     m = mb;
   }
   return toH16(acc / l);
+}
+
+__device__ __forceinline__ h16 mergeDim(const float* part, int used, int d) {
+  return used <= 16 ? mergeDimBlocks<16>(part, used, d) : mergeDimBlocks<64>(part, used, d);
 }
 
 // ---- causal GQA, T = 1: one wave per (q head, 64-key chunk), partial (m, l, o[128]) to the workspace, then one
