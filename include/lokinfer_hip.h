@@ -268,7 +268,8 @@ int lk_hip_f16_attention_gqa(const void* q, const void* kc, const void* vc, cons
 /* decode step (T = 1) fusions (backend ops; the reference runs qknorm_rope_kv_opt -> attention_gqa_opt and
  * rmsnorm -> lm_head_last_opt, model.py:393-401, 287-288): attention_decode_qkr_opt_f16_gpu goes from the raw qkv
  * projections f16[1, 128 (qh + 2 kvh)] to the attention output f16[1, 128 qh] in one launch (QK-norm, RoPE, row pos of
- * both caches, key-split chunks, and their merge by the last chunk of each head to finish; counters: qh unsigned
+ * both caches, key-split chunks (a wave takes ceil(chunks / 128) consecutive 64-key chunks, and two q heads of a kv
+ * group on caches of 128 chunks or more), and their merge by the last wave of each head to finish; counters: qh unsigned
  * ints, zero before the first call and left zero; workspace as lk_hip_f16_attention_workspace_bytes, 3 when short);
  * rmsnorm_lm_head_last_opt_f16_gpu normalizes the last row inside the LM-head GEMV. Each equals its composition bit
  * for bit. */
