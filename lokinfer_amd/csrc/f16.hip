@@ -963,15 +963,6 @@ inline bool pairHeads(int qh, int kvh, int64_t cap) {
   return (qh / kvh) % 2 == 0 && (cap + DCH - 1) / DCH >= kGqaMaxWaves;
 }
 
-__device__ __forceinline__ void emptyChunk(float* part, int lane) {
-  if (lane == 0) {
-    part[0] = -INFINITY;
-    part[1] = 0.0f;
-  }
-  part[2 + lane] = 0.0f;
-  part[2 + 64 + lane] = 0.0f;
-}
-
 // H q heads of one kv group per wave (H = 2 when the group size is even): the K / V rows are loaded once and each
 // head's partial is the single-head arithmetic on them, so H changes no bits.
 template <int H>
@@ -986,11 +977,7 @@ __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
   const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
   if (nk == 0 && h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int ch0 = w * p.sub;
-  if (static_cast<int64_t>(ch0) * DCH >= nk) {
-#pragma unroll
-    for (int k = 0; k < H; ++k) emptyChunk(part[k], lane);
-    return;
-  }
+  if (static_cast<int64_t>(ch0) * DCH >= nk) return;  // past the live keys: the merge reads no partial of it
   half8 qh8[H];
 #pragma unroll
   for (int k = 0; k < H; ++k) qh8[k] = ld8(p.q + (h0 + k) * QHD + 8 * (lane & 15));
@@ -1031,8 +1018,9 @@ __global__ __launch_bounds__(128) void gqaDecodeMergeKernel(GqaParams p) {
 // ---- T = 1 with the QK-norm / RoPE / KV write and the merge folded in: a chunk wave normalizes and rotates its q
 // head from the raw projections itself; the chunk holding pos takes the new key and value from them too (never
 // from the cache row being written), and the first q head of each kv group writes that row to both caches. Each
-// wave then writes its chunk partial, fences it and counts itself on its head's counter; the last wave of the head
-// to arrive (no wave ever waits) reads all the head's partials after an acquire fence, merges them as the merge
+// wave holding live keys then writes its chunk partial, fences it and counts itself on its head's counter (waves past
+// pos return at once: counting them only queued same-address atomics ahead of the merge); the last live wave of the
+// head to arrive (no wave ever waits) reads the head's partials after an acquire fence, merges them as the merge
 // kernel does (mergeDim) and resets the counter. Values and roundings are those of qkRopeKvKernel +
 // gqaDecodeChunkKernel + gqaDecodeMergeKernel (the same helpers), so the output is identical.
 struct GqaDecParams {
@@ -1053,16 +1041,15 @@ struct GqaDecParams {
   unsigned long long* err;  // the GPU's error record: positions outside the cache
 };
 
-__device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, int lane) {
+// live: the head's waves holding keys (only they count themselves; the others return at once)
+__device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, int lane, int live) {
   __shared__ unsigned lastFlag;
   __threadfence();  // release: this wave's partial is in L2 before it is counted
-  if (lane == 0) lastFlag = atomicAdd(&p.counters[h], 1u) == static_cast<unsigned>(p.chunks - 1);
+  if (lane == 0) lastFlag = atomicAdd(&p.counters[h], 1u) == static_cast<unsigned>(live - 1);
   __syncthreads();
   if (!lastFlag) return;
   __threadfence();  // acquire: the other waves' partials (and no stale L1 lines) from here on
-  const int64_t p0 = *p.pos;
-  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per partial
-  const int used = p0 < 0 ? 0 : static_cast<int>(min<int64_t>(p.chunks, (p0 + span) / span));
+  const int used = live;
   const float* ph = p.part + static_cast<int64_t>(h) * p.chunks * (QHD + 2);
   h16* o = p.out + static_cast<int64_t>(h) * QHD;
   o[lane] = mergeDim(ph, used, lane);
@@ -1090,14 +1077,18 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   if (nk == 0 && h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int ch0 = w * p.sub;
   const int64_t kb = static_cast<int64_t>(ch0) * DCH;
-  if (kb >= nk) {
+  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per wave
+  const int live = static_cast<int>((nk + span - 1) / span);
+  if (nk == 0) {  // a position outside the cache: NaN outputs, no cache write, recorded above
+    if (w == 0)
 #pragma unroll
-    for (int k = 0; k < H; ++k) {
-      emptyChunk(part[k], lane);
-      decodeMergeIfLast(p, h0 + k, lane);
-    }
+      for (int k = 0; k < H; ++k) {
+        p.out[static_cast<int64_t>(h0 + k) * QHD + lane] = static_cast<h16>(__builtin_nanf(""));
+        p.out[static_cast<int64_t>(h0 + k) * QHD + lane + 64] = static_cast<h16>(__builtin_nanf(""));
+      }
     return;
   }
+  if (kb >= nk) return;  // past the live keys: no partial, not counted
   const bool hasNew = p0 < kb + static_cast<int64_t>(DCH) * p.sub;  // this wave's chunks hold key pos (kb <= pos)
   const int cl = lane & 15;           // rowSumSq's chunk of a 128-wide head (lanes 16.. add nothing)
   const h16* xk = p.qkv + dq + kvOff;
@@ -1179,7 +1170,7 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
 #pragma unroll
   for (int k = 0; k < H; ++k) {
     c.store(r[k], part[k]);
-    decodeMergeIfLast(p, h0 + k, lane);
+    decodeMergeIfLast(p, h0 + k, lane, live);
   }
 }
 
