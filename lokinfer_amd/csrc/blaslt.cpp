@@ -1,4 +1,5 @@
-// Plain f32 GEMMs (optional per-column bias, nothing else fused) through hipBLASLt, the vendor library GEMM.
+// Plain GEMMs (f32, or f16 storage with f32 accumulation; optional per-column bias and residual, nothing else
+// fused) through hipBLASLt, the vendor library GEMM.
 //
 // The hand-written MFMA kernels (gemm.hip) keep every fused form: activations, residuals, output scales, split-K
 // partials for a consumer, the conv loaders. For a plain row-major A [M, K] times B ([K, N], or [N, K] with nt) at
@@ -8,8 +9,9 @@
 //
 // Row-major C = A B is the column-major product C^T [N, M] = B^T [N, K] A^T [K, M]: the row-major buffers are passed
 // unchanged as the column-major operands (B first), and the per-column bias becomes hipBLASLt's per-row bias of D.
-// f32 compute (HIPBLAS_COMPUTE_32F, no reduced-precision inner products). One handle per device and one plan
-// (descriptors + the heuristic's first algorithm) per shape, cached for the process.
+// A residual R [M, N] is the library's C operand with beta = 1 (D = A B + R + bias, one rounding at the output).
+// f32 compute (HIPBLAS_COMPUTE_32F, no reduced-precision inner products) for both storage types. One handle per
+// device and one plan (descriptors + the heuristic's first algorithm) per shape, cached for the process.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -30,7 +32,7 @@ struct Plan {
   bool ok = false;
 };
 
-using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, size_t>;
+using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, bool, size_t>;
 
 std::mutex gMu;
 std::map<Key, Plan> gPlans;
@@ -45,20 +47,25 @@ hipblasLtHandle_t handleFor(int dev) {
   return h;
 }
 
-Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, bool bias, size_t wsMax) {
+Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, bool bias, bool f16, size_t wsMax) {
   Plan p;
+  const hipDataType ty = f16 ? HIP_R_16F : HIP_R_32F;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
   const int32_t ta = nt ? HIPBLAS_OP_T : HIPBLAS_OP_N, tb = HIPBLAS_OP_N;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
   const uint32_t epi = bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
+  if (bias) {
+    const int32_t bty = ty;
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bty, sizeof(bty));
+  }
   // column-major operands: "A" = B^T [N, K] (stored [K, N] with ld N, or [N, K] with ld K read transposed),
   // "B" = A^T [K, M] with ld K, D = C^T [N, M] with ld N
-  if (nt) hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, static_cast<uint64_t>(k), static_cast<uint64_t>(n), k);
-  else hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, static_cast<uint64_t>(n), static_cast<uint64_t>(k), n);
-  hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, static_cast<uint64_t>(k), static_cast<uint64_t>(m), k);
-  hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, static_cast<uint64_t>(n), static_cast<uint64_t>(m), n);
+  if (nt) hipblasLtMatrixLayoutCreate(&p.la, ty, static_cast<uint64_t>(k), static_cast<uint64_t>(n), k);
+  else hipblasLtMatrixLayoutCreate(&p.la, ty, static_cast<uint64_t>(n), static_cast<uint64_t>(k), n);
+  hipblasLtMatrixLayoutCreate(&p.lb, ty, static_cast<uint64_t>(k), static_cast<uint64_t>(m), k);
+  hipblasLtMatrixLayoutCreate(&p.lc, ty, static_cast<uint64_t>(n), static_cast<uint64_t>(m), n);
   if (!p.la || !p.lb || !p.lc) return p;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
@@ -77,27 +84,28 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
 
 }  // namespace
 
-// C [M, N] = A [M, K] B (+ bias [N]); B [K, N], or [N, K] with nt. Returns false (nothing launched) when no library
-// algorithm fits the shape and the workspace.
-bool bltGemmF32(const float* a, const float* b, const float* bias, float* c, int64_t m, int64_t n, int64_t k, bool nt,
-                void* ws, size_t wsBytes, hipStream_t s) {
+// C [M, N] = A [M, K] B (+ bias [N]) (+ res [M, N]); B [K, N], or [N, K] with nt; f16: every operand is IEEE half.
+// Returns false (nothing launched) when no library algorithm fits the shape and the workspace.
+bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
+             bool nt, bool f16, void* ws, size_t wsBytes, hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
   // the bias pointer lives in the shared per-shape descriptor: set it and enqueue under the lock
   std::lock_guard<std::mutex> lock(gMu);
   hipblasLtHandle_t h = handleFor(dev);
   if (!h) return false;
-  const Key key{dev, m, n, k, nt, bias != nullptr, ws ? wsBytes : 0};
+  const size_t wsb = ws ? wsBytes : 0;
+  const Key key{dev, m, n, k, nt, bias != nullptr, f16, wsb};
   auto it = gPlans.find(key);
-  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, ws ? wsBytes : 0)).first;
+  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, f16, wsb)).first;
   const Plan& plan = it->second;
   if (!plan.ok) return false;
   if (bias && hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=
                   HIPBLAS_STATUS_SUCCESS)
     return false;
-  const float alpha = 1.0f, beta = 0.0f;
-  return hipblasLtMatmul(h, plan.desc, &alpha, b, plan.la, a, plan.lb, &beta, c, plan.lc, c, plan.lc, &plan.algo,
-                         plan.ws ? ws : nullptr, plan.ws, s) == HIPBLAS_STATUS_SUCCESS;
+  const float alpha = 1.0f, beta = res ? 1.0f : 0.0f;
+  return hipblasLtMatmul(h, plan.desc, &alpha, b, plan.la, a, plan.lb, &beta, res ? res : c, plan.lc, c, plan.lc,
+                         &plan.algo, plan.ws ? ws : nullptr, plan.ws, s) == HIPBLAS_STATUS_SUCCESS;
 }
 
 }  // namespace lkh

@@ -25,6 +25,7 @@
 // identical bits.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "common.h"
 #include "lokinfer_hip.h"
@@ -1262,6 +1263,11 @@ int launched() { return hipGetLastError() == hipSuccess ? 0 : 2; }
 
 }  // namespace
 
+namespace lkh {
+bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
+             bool nt, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
+}  // namespace lkh
+
 extern "C" {
 
 int lk_hip_f16_rms_lm_head(const void* x, const void* g, const void* table, float* out, int64_t t, int64_t d, int64_t v,
@@ -1290,6 +1296,11 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
     else launchGemvF16<EPI_PLAIN, false>(g, blocks, s);
     return launched();
   }
+  static const bool libOff = getenv("LK_BLASLT_OFF") != nullptr;  // A/B switch: hand-written kernels only
+  if (!swiglu && !libOff &&
+      lkh::bltGemm(x, wt, bias, res, out, m, n, k, true, true, workspace,
+                   workspace ? static_cast<size_t>(workspace_bytes) : 0, s))
+    return launched();  // plain GEMM (bias, residual): the library's f16 GEMM with f32 accumulation
   GemmF16Params p{static_cast<const h16*>(x), static_cast<const h16*>(wt), static_cast<const h16*>(bias),
                   static_cast<const h16*>(res), static_cast<h16*>(out), nullptr, m, n, k, k, k, 1};
   // the wide tile where it measured faster: SwiGLU at M >= 256 (Qwen3's 416-row gate/up: 57 -> 49 us) and any
