@@ -61,8 +61,9 @@ const char* lk_device_error_message(int code);
 /* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu.
  * workspace (optional, may be NULL): with few output tiles and a long K, K is split across workgroups whose
  * partial tiles (split * M * N floats past the first 64 KiB) a second kernel sums; calls sharing a workspace
- * must be stream-ordered. With act 0 and scale 1 the product runs as hipBLASLt's f32 GEMM (bias epilogue, res as
- * its C operand, its workspace past the first 64 KiB); the first call per shape builds its plan */
+ * must be stream-ordered. With scale 1 (and no res when act != 0) the product runs as hipBLASLt's f32 GEMM (bias /
+ * relu / gelu epilogues, res as its C operand, its workspace past the first 64 KiB); the first call per shape builds its
+ * plan */
 int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
                     int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
                     void* stream);

@@ -1,5 +1,5 @@
-// Plain GEMMs (f32, or f16 storage with f32 accumulation; optional per-column bias and residual, nothing else
-// fused) through hipBLASLt, the vendor library GEMM.
+// Plain GEMMs (f32, or f16 storage with f32 accumulation; optional per-column bias, ReLU / tanh-GELU, or a
+// residual) through hipBLASLt, the vendor library GEMM.
 //
 // The hand-written MFMA kernels (gemm.hip) keep every fused form: activations, residuals, output scales, split-K
 // partials for a consumer, the conv loaders. For a plain row-major A [M, K] times B ([K, N], or [N, K] with nt) at
@@ -32,7 +32,7 @@ struct Plan {
   bool ok = false;
 };
 
-using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, bool, size_t>;
+using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, int, bool, size_t>;
 
 std::mutex gMu;
 std::map<Key, Plan> gPlans;
@@ -47,14 +47,17 @@ hipblasLtHandle_t handleFor(int dev) {
   return h;
 }
 
-Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, bool bias, bool f16, size_t wsMax) {
+Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, bool bias, int act, bool f16,
+              size_t wsMax) {
   Plan p;
   const hipDataType ty = f16 ? HIP_R_16F : HIP_R_32F;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
   const int32_t ta = nt ? HIPBLAS_OP_T : HIPBLAS_OP_N, tb = HIPBLAS_OP_N;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
-  const uint32_t epi = bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
+  uint32_t epi = bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
+  if (act == 1) epi = bias ? HIPBLASLT_EPILOGUE_RELU_BIAS : HIPBLASLT_EPILOGUE_RELU;
+  if (act == 2) epi = bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
   if (bias) {
     const int32_t bty = ty;
@@ -84,10 +87,12 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
 
 }  // namespace
 
-// C [M, N] = A [M, K] B (+ bias [N]) (+ res [M, N]); B [K, N], or [N, K] with nt; f16: every operand is IEEE half.
-// Returns false (nothing launched) when no library algorithm fits the shape and the workspace.
+// C [M, N] = act(A [M, K] B (+ bias [N])) (+ res [M, N], only with act 0: the library's epilogue activation would
+// apply after the residual); act 0 none, 1 relu, 2 gelu (tanh form). B [K, N], or [N, K] with nt; f16: every operand
+// is IEEE half. Returns false (nothing launched) when no library algorithm fits the shape and the workspace.
 bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, bool f16, void* ws, size_t wsBytes, hipStream_t s) {
+             bool nt, int act, bool f16, void* ws, size_t wsBytes, hipStream_t s) {
+  if (act < 0 || act > 2 || (act != 0 && res)) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
   // the bias pointer lives in the shared per-shape descriptor: set it and enqueue under the lock
@@ -95,9 +100,9 @@ bool bltGemm(const void* a, const void* b, const void* bias, const void* res, vo
   hipblasLtHandle_t h = handleFor(dev);
   if (!h) return false;
   const size_t wsb = ws ? wsBytes : 0;
-  const Key key{dev, m, n, k, nt, bias != nullptr, f16, wsb};
+  const Key key{dev, m, n, k, nt, bias != nullptr, act, f16, wsb};
   auto it = gPlans.find(key);
-  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, f16, wsb)).first;
+  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, act, f16, wsb)).first;
   const Plan& plan = it->second;
   if (!plan.ok) return false;
   if (bias && hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=

@@ -1265,7 +1265,7 @@ int launched() { return hipGetLastError() == hipSuccess ? 0 : 2; }
 
 namespace lkh {
 bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
+             bool nt, int act, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
 }  // namespace lkh
 
 extern "C" {
@@ -1298,7 +1298,7 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
   }
   static const bool libOff = getenv("LK_BLASLT_OFF") != nullptr;  // A/B switch: hand-written kernels only
   if (!swiglu && !libOff &&
-      lkh::bltGemm(x, wt, bias, res, out, m, n, k, true, true, workspace,
+      lkh::bltGemm(x, wt, bias, res, out, m, n, k, true, 0, true, workspace,
                    workspace ? static_cast<size_t>(workspace_bytes) : 0, s))
     return launched();  // plain GEMM (bias, residual): the library's f16 GEMM with f32 accumulation
   GemmF16Params p{static_cast<const h16*>(x), static_cast<const h16*>(wt), static_cast<const h16*>(bias),

@@ -879,7 +879,7 @@ static GemmParams baseParams() {
 
 namespace lkh {
 bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
+             bool nt, int act, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
 }  // namespace lkh
 
 // ---- typed C-ABI launchers ---------------------------------------------------------------------------------
@@ -907,11 +907,11 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
   p.scale = scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
   static const bool libOff = getenv("LK_BLASLT_OFF") != nullptr;  // A/B switch: hand-written kernels only
-  if (act == lkd::ACT_NONE && scale == 1.0f && !libOff) {
-    // plain GEMM (bias and residual allowed): the library's, its workspace past the 64 KiB counter area
+  if (scale == 1.0f && (act == lkd::ACT_NONE || !res) && !libOff) {
+    // bias, then relu / gelu or a residual: the library's GEMM, its workspace past the 64 KiB counter area
     void* ws = workspace && workspace_bytes > 65536 ? static_cast<char*>(workspace) + 65536 : nullptr;
     const size_t wsb = ws ? static_cast<size_t>(workspace_bytes - 65536) : 0;
-    if (lkh::bltGemm(a, b, bias, res, out, m, n, k, nt != 0, false, ws, wsb, s))
+    if (lkh::bltGemm(a, b, bias, res, out, m, n, k, nt != 0, act, false, ws, wsb, s))
       return hipGetLastError() == hipSuccess ? 0 : 2;
   }
   if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s, workspace, workspace_bytes);
