@@ -922,15 +922,15 @@ struct GqaChunk {
   }
 
   // writes the partial (m, l, o[128]): lane 0 m and l, row 0 the 128 dims
-  __device__ __forceinline__ void store(const Result& r, float* part) const {
+  __device__ __forceinline__ static void store(const Result& r, float* part) {
     const int lane = threadIdx.x & 63;
     if (lane == 0) {
       part[0] = r.m;
       part[1] = r.l;
     }
-    if (g == 0) {
+    if ((lane >> 4) == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part[2 + 8 * d8 + e] = r.acc[e];
+      for (int e = 0; e < 8; ++e) part[2 + 8 * (lane & 15) + e] = r.acc[e];
     }
   }
 
@@ -1058,38 +1058,20 @@ __device__ __forceinline__ void decodeMergeIfLast(const GqaDecParams& p, int h, 
   if (lane == 0) p.counters[h] = 0u;
 }
 
-// All loads are issued first, in the order the in-order memory counter needs: the raw q / k / v values (the norms
-// wait for them alone), then the chunk's K and V rows. H q heads of one kv group per wave, as in
-// gqaDecodeChunkKernel (each head's merge is run by the last wave counted on that head's counter).
+// One wave's part of the fused T = 1 step: QK-norm + RoPE of its H q heads from the raw projections, the new key /
+// value when its chunks hold pos (written to both caches by the first q head of the kv group), then its chunks'
+// attention results r[H]. All loads are issued first, in the order the in-order memory counter needs: the raw q / k /
+// v values (the norms wait for them alone), then the chunk's K and V rows. qs, kn, vn: this wave's own LDS slices.
+// Requires kb = w sub 64 < nk.
 template <int H>
-__global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
-  __shared__ float qs[H][QHD];
-  __shared__ __attribute__((aligned(16))) h16 kn[QHD];
-  __shared__ __attribute__((aligned(16))) h16 vn[QHD];
-  const int h0 = blockIdx.x * H, w = blockIdx.y, lane = threadIdx.x;
+__device__ __forceinline__ void qkrWave(const GqaDecParams& p, int h0, int w, int64_t p0, int64_t nk, float (*qs)[QHD],
+                                        h16* kn, h16* vn, GqaChunk::Result (&r)[H]) {
+  const int lane = threadIdx.x & 63;
   const int grp = p.qh / p.kvh;
   const int64_t dq = static_cast<int64_t>(p.qh) * QHD, dk = static_cast<int64_t>(p.kvh) * QHD;
   const int64_t kvOff = static_cast<int64_t>(h0 / grp) * QHD;
-  const int64_t p0 = *p.pos;
-  float* part[H];
-#pragma unroll
-  for (int k = 0; k < H; ++k) part[k] = p.part + (static_cast<int64_t>(h0 + k) * p.chunks + w) * (QHD + 2);
-  const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
-  if (nk == 0 && h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
   const int ch0 = w * p.sub;
   const int64_t kb = static_cast<int64_t>(ch0) * DCH;
-  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per wave
-  const int live = static_cast<int>((nk + span - 1) / span);
-  if (nk == 0) {  // a position outside the cache: NaN outputs, no cache write, recorded above
-    if (w == 0)
-#pragma unroll
-      for (int k = 0; k < H; ++k) {
-        p.out[static_cast<int64_t>(h0 + k) * QHD + lane] = static_cast<h16>(__builtin_nanf(""));
-        p.out[static_cast<int64_t>(h0 + k) * QHD + lane + 64] = static_cast<h16>(__builtin_nanf(""));
-      }
-    return;
-  }
-  if (kb >= nk) return;  // past the live keys: no partial, not counted
   const bool hasNew = p0 < kb + static_cast<int64_t>(DCH) * p.sub;  // this wave's chunks hold key pos (kb <= pos)
   const int cl = lane & 15;           // rowSumSq's chunk of a 128-wide head (lanes 16.. add nothing)
   const h16* xk = p.qkv + dq + kvOff;
@@ -1127,17 +1109,17 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   };
 #pragma unroll
   for (int k = 0; k < H; ++k) {
-    const float r = rmsFactor(headSumSq(qc[k]), QHD, p.eps);
+    const float rf = rmsFactor(headSumSq(qc[k]), QHD, p.eps);
     h16 a, b;
-    ropePair(static_cast<float>(rmsElem(q0[k], gq0, r)), static_cast<float>(rmsElem(q1[k], gq1, r)), p0,
+    ropePair(static_cast<float>(rmsElem(q0[k], gq0, rf)), static_cast<float>(rmsElem(q1[k], gq1, rf)), p0,
              p.tab.invf[lane], a, b);
     qs[k][lane] = static_cast<float>(a);
     qs[k][lane + 64] = static_cast<float>(b);
   }
   if (hasNew) {
-    const float r = rmsFactor(headSumSq(kc8), QHD, p.eps);
+    const float rf = rmsFactor(headSumSq(kc8), QHD, p.eps);
     h16 a, b;
-    ropePair(static_cast<float>(rmsElem(k0, gk0, r)), static_cast<float>(rmsElem(k1, gk1, r)), p0, p.tab.invf[lane],
+    ropePair(static_cast<float>(rmsElem(k0, gk0, rf)), static_cast<float>(rmsElem(k1, gk1, rf)), p0, p.tab.invf[lane],
              a, b);
     kn[lane] = a;
     kn[lane + 64] = b;
@@ -1150,7 +1132,10 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
       p.vc[p0 * dk + kvOff + lane + 64] = v1;
     }
   }
-  __syncthreads();
+  // the slices are this wave's alone and a wave's LDS accesses complete in order: no workgroup barrier
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int d8 = lane & 15;
   float q8[H][8];
 #pragma unroll
@@ -1160,7 +1145,6 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
   const half8 none = {};
   const int64_t newKey = hasNew ? p0 : -1;
   const half8 knew = hasNew ? ld8(kn + 8 * d8) : none, vnew = hasNew ? ld8(vn + 8 * d8) : none;
-  GqaChunk::Result r[H];
 #pragma unroll
   for (int k = 0; k < H; ++k) r[k] = c.compute(q8[k], newKey, knew, vnew, p.scale);
   for (int j = 1; j < p.sub; ++j) {
@@ -1168,13 +1152,74 @@ __global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
 #pragma unroll
     for (int k = 0; k < H; ++k) r[k] = GqaChunk::combine(r[k], c.compute(q8[k], newKey, knew, vnew, p.scale));
   }
+}
+
+// A position outside the cache: NaN outputs for the H heads (written by their first wave), no cache write, the error
+// recorded once.
+template <int H>
+__device__ __forceinline__ void qkrBadPosition(const GqaDecParams& p, int h0, int w, int64_t p0) {
+  const int lane = threadIdx.x & 63;
+  if (h0 == 0 && w == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, p0);
+  if (w == 0)
+#pragma unroll
+    for (int k = 0; k < H; ++k) {
+      p.out[static_cast<int64_t>(h0 + k) * QHD + lane] = static_cast<h16>(__builtin_nanf(""));
+      p.out[static_cast<int64_t>(h0 + k) * QHD + lane + 64] = static_cast<h16>(__builtin_nanf(""));
+    }
+}
+
+// One wave per (H q heads of one kv group, sub-chunk range); each head's merge is run by the last wave counted on
+// that head's counter (decodeMergeIfLast).
+template <int H>
+__global__ __launch_bounds__(64) void gqaDecodeQkrKernel(GqaDecParams p) {
+  __shared__ float qs[H][QHD];
+  __shared__ __attribute__((aligned(16))) h16 kn[QHD];
+  __shared__ __attribute__((aligned(16))) h16 vn[QHD];
+  const int h0 = blockIdx.x * H, w = blockIdx.y, lane = threadIdx.x;
+  const int64_t p0 = *p.pos;
+  const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
+  if (nk == 0) {
+    qkrBadPosition<H>(p, h0, w, p0);
+    return;
+  }
+  const int64_t span = static_cast<int64_t>(DCH) * p.sub;  // keys per wave
+  const int live = static_cast<int>((nk + span - 1) / span);
+  if (static_cast<int64_t>(w) * span >= nk) return;  // past the live keys: no partial, not counted
+  GqaChunk::Result r[H];
+  qkrWave<H>(p, h0, w, p0, nk, qs, kn, vn, r);
 #pragma unroll
   for (int k = 0; k < H; ++k) {
-    c.store(r[k], part[k]);
+    GqaChunk::store(r[k], p.part + (static_cast<int64_t>(h0 + k) * p.chunks + w) * (QHD + 2));
     decodeMergeIfLast(p, h0 + k, lane, live);
   }
 }
 
+// Short caches (chunks <= kQkrWgWaves, sub = 1): one workgroup per q head, wave w on chunk w. The live waves leave
+// their partials in LDS and, after one workgroup barrier, the first 128 threads merge them (mergeDim, one dim each):
+// no workspace round trip, fence or counter. Same helpers, so the same bits as gqaDecodeQkrKernel<1>.
+constexpr int kQkrWgWaves = 8;  // 512 threads: the 256 VGPRs a chunk wave needs (220) without spills
+__global__ __launch_bounds__(64 * kQkrWgWaves) void gqaDecodeQkrWgKernel(GqaDecParams p) {
+  __shared__ float qs[kQkrWgWaves][1][QHD];
+  __shared__ __attribute__((aligned(16))) h16 kn[kQkrWgWaves][QHD];
+  __shared__ __attribute__((aligned(16))) h16 vn[kQkrWgWaves][QHD];
+  __shared__ float parts[kQkrWgWaves * (QHD + 2)];
+  const int h0 = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t p0 = *p.pos;
+  const int64_t nk = (p0 < 0 || p0 >= p.cap) ? 0 : p0 + 1;
+  if (nk == 0) {  // uniform over the workgroup: every wave returns before the barrier
+    qkrBadPosition<1>(p, h0, w, p0);
+    return;
+  }
+  const int live = static_cast<int>((nk + DCH - 1) / DCH);
+  if (static_cast<int64_t>(w) * DCH < nk) {
+    GqaChunk::Result r[1];
+    qkrWave<1>(p, h0, w, p0, nk, qs[w], kn[w], vn[w], r);
+    GqaChunk::store(r[0], parts + w * (QHD + 2));
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < QHD; d += blockDim.x)  // one wave (a one-chunk cache) merges both halves
+    p.out[static_cast<int64_t>(h0) * QHD + d] = mergeDim(parts, live, d);
+}
 
 // ---- row copies, gathers, elementwise -----------------------------------------------------------------------
 // kv_write: rows pos..pos+T-1 of both caches = k, v (8 halves per thread); rows past the cache are dropped
@@ -1480,7 +1525,10 @@ int lk_hip_f16_attention_decode_qkr(const void* qkv, const void* qg, const void*
                  counters, cap, qh, kvh, chunks, sub, 1.0f / std::sqrt(static_cast<float>(QHD)), eps, ropeTable(theta),
                  lkh::deviceErrorRecord()};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pairHeads(qh, kvh, cap))
+  if (sub == 1 && chunks <= kQkrWgWaves)
+    hipLaunchKernelGGL(gqaDecodeQkrWgKernel, dim3(static_cast<unsigned>(qh)), dim3(64 * static_cast<unsigned>(chunks)),
+                       0, s, p);
+  else if (pairHeads(qh, kvh, cap))
     hipLaunchKernelGGL(gqaDecodeQkrKernel<2>, dim3(static_cast<unsigned>(qh / 2), static_cast<unsigned>(chunks)),
                        dim3(64), 0, s, p);
   else

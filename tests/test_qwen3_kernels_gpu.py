@@ -244,7 +244,8 @@ def test_embedding_scatter_elementwise(gpu):
     check(F.silu_mul_f16_gpu(G(lk, a), G(lk, b)), sm, 2.0 ** -20 * np.abs(sm) + 2.0 ** -24, "silu_mul")
 
 
-@pytest.mark.parametrize("pos,cap", [(0, 64), (63, 480), (64, 480), (415, 480), (1000, 1024), (1999, 2048),
+@pytest.mark.parametrize("pos,cap", [(0, 64), (63, 480), (64, 480), (200, 300), (415, 480), (511, 512), (1000, 1024),
+                                     (1999, 2048),
                                      (5000, 8192), (8300, 20000), (19999, 20000)])
 def test_decode_fusions_equal_compositions(gpu, pos, cap):
     """The decode-step fusions give the bits of the ops they replace: attention_decode_qkr vs qknorm_rope_kv +
