@@ -22,22 +22,28 @@ namespace lkd {
 constexpr int kStatChunk = 128;
 
 // Block = 64 channels x 4 row groups of one 128-row chunk. Pass 1: mean; pass 2: centred M2 (the chunk's rows are
-// re-read from L2).
+// re-read from L2). Dilation d: the chunks of each residue class rho (rows rho + d i, i < ceil((L - rho) / d)), block
+// y = rho chunks + k over rows rho + d (128 k + i), written to st[(rho chunks + k) C + c] (the Winograd GEMM's
+// statistics layout; d = 1 is the plain 128-row layout). Chunks past a residue class's rows write nothing.
 __global__ __launch_bounds__(256) void statsKernel(const float* __restrict__ x, float* __restrict__ st, int64_t l,
-                                                  int64_t c) {
+                                                  int64_t c, int d, int64_t chunks) {
   __shared__ float part[4][64];
   const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * 64 + cl;
   const int64_t s = blockIdx.y;
-  const int64_t t0 = s * kStatChunk;
-  const int n = static_cast<int>(min<int64_t>(kStatChunk, l - t0));
+  const int64_t rho = s / chunks, k = s - rho * chunks;
+  const int64_t lor = rho < l ? (l - rho + d - 1) / d : 0;  // rows of this residue class
+  const int64_t t0 = k * kStatChunk;
+  const int n = static_cast<int>(min<int64_t>(kStatChunk, lor - t0));
+  if (n <= 0) return;  // uniform over the block
   const bool ok = ch < c;
   const int r0 = g * 32;
-  const float* col = x + t0 * c + (ok ? ch : 0);
+  const int64_t stride = static_cast<int64_t>(d) * c;
+  const float* col = x + (rho + t0 * d) * c + (ok ? ch : 0);
   // the thread's 32 rows are loaded once (independent loads in flight) and kept for both passes
   float v[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = (ok && r0 + i < n) ? col[static_cast<int64_t>(r0 + i) * c] : 0.0f;
+  for (int i = 0; i < 32; ++i) v[i] = (ok && r0 + i < n) ? col[static_cast<int64_t>(r0 + i) * stride] : 0.0f;
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) sum += v[i];
@@ -48,8 +54,8 @@ __global__ __launch_bounds__(256) void statsKernel(const float* __restrict__ x, 
   float m2 = 0.0f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
-    const float d = v[i] - mean;
-    if (r0 + i < n) m2 += d * d;
+    const float dv = v[i] - mean;
+    if (r0 + i < n) m2 += dv * dv;
   }
   part[g][cl] = m2;
   __syncthreads();
@@ -251,14 +257,26 @@ inline unsigned gridFor(int64_t n, int threads = 256) {
 
 }  // namespace lkd
 
+namespace lkh {
+// Statistics per residue class of dilation d in 128-row chunks (chunks = ceil(ceil(L / d) / 128) per class), the
+// Winograd GEMM's layout: the split-K path of the Winograd GEMM computes them from the summed output.
+int residueStats(const float* x, float* st, int64_t l, int64_t c, int d, int64_t chunks, hipStream_t s) {
+  if (l <= 0 || c <= 0 || d < 1 || chunks < 1) return 1;
+  dim3 grid(static_cast<unsigned>(ceilDiv(c, 64)), static_cast<unsigned>(d * chunks));
+  hipLaunchKernelGGL(lkd::statsKernel, grid, dim3(256), 0, s, x, st, l, c, d, chunks);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+}  // namespace lkh
+
 #define LK_RET return hipGetLastError() == hipSuccess ? 0 : 2
 
 extern "C" {
 
 int lk_hip_channel_stats_lc_f32(const float* x, float* st, int64_t l, int64_t c, void* stream) {
   if (l <= 0 || c <= 0) return 1;
-  dim3 grid(lkh::ceilDiv(c, 64), lkh::ceilDiv(l, lkd::kStatChunk));
-  hipLaunchKernelGGL(lkd::statsKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, st, l, c);
+  const int64_t chunks = lkh::ceilDiv(l, lkd::kStatChunk);
+  dim3 grid(lkh::ceilDiv(c, 64), chunks);
+  hipLaunchKernelGGL(lkd::statsKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, st, l, c, 1, chunks);
   LK_RET;
 }
 

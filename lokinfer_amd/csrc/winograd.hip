@@ -23,6 +23,10 @@
 #include <algorithm>
 #include <cstdint>
 
+namespace lkh {
+int residueStats(const float* x, float* st, int64_t l, int64_t c, int d, int64_t chunks, hipStream_t s);  // kokoro.hip
+}  // namespace lkh
+
 namespace lkd {
 
 typedef float v16w __attribute__((ext_vector_type(16)));
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   }
 }
 
-// Split-K reduction (dilation 1): out = (sum_s part[s] + bias [+ res]) * scale, the s sum in split order; one
+// Split-K reduction: out = (sum_s part[s] + bias [+ res]) * scale, the s sum in split order; one
 // float4 of one row per thread, grid-stride (Co % 64 == 0, so a float4 never straddles two rows).
 __global__ __launch_bounds__(256) void winoSplitReduceKernel(const float* __restrict__ part, int split,
                                                             const float* __restrict__ bias,
@@ -389,14 +393,14 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
   const int m = tile;
   const int64_t tiles = ((lo + dilation - 1) / dilation + m - 1) / m;  // residue class 0 is the longest
   if (rmax < tiles + groups - 1) return 1;  // V must hold every tile and its group shifts
-  // split-K when the grid is too small to fill the chip (two workgroups per CU): dilation 1 only (the reduction
-  // writes the plain 128-row statistics), at least 32 steps per split (fewer measured slower than no split on
-  // MI355X: the partial rows' round trip and the second launch outweigh the extra workgroups), partials in the
-  // workspace past its 64 KiB counter area
+  // split-K when the grid is too small to fill the chip (two workgroups per CU): at least 32 steps per split (fewer
+  // measured slower than no split on MI355X: the partial rows' round trip and the second launch outweigh the extra
+  // workgroups; so did splits up to three workgroups per CU at 16 steps), partials in the workspace past its 64 KiB
+  // counter area
   const int64_t base = (co / 64) * ((tiles + 63) / 64) * dilation;
   const int steps = a * static_cast<int>(ci / 16);
   int split = 1;
-  if (dilation == 1 && workspace && base < 512) {
+  if (workspace && base < 512) {
     split = static_cast<int>(std::min<int64_t>({8, 512 / base, steps / 32}));
     while (split > 1 && 65536 + static_cast<int64_t>(split) * lo * co * 4 > workspace_bytes) --split;
     split = std::max(split, 1);
@@ -426,8 +430,8 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
     hipLaunchKernelGGL(lkd::winoSplitReduceKernel,
                        dim3(static_cast<unsigned>(std::min<int64_t>((lo * co / 4 + 255) / 256, 8192))), dim3(256), 0,
                        s, part, split, bias, res, out, lo, co, scale);
-    // dilation 1: the statistics are the plain 128-row chunks of the output
-    if (stats && lk_hip_channel_stats_lc_f32(out, stats, lo, co, stream)) return 2;
+    // the statistics of the summed output, per residue class as the fused epilogue writes them
+    if (stats && lkh::residueStats(out, stats, lo, co, dilation, p.chunks, s)) return 2;
   }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }

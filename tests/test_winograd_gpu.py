@@ -113,7 +113,8 @@ def _check_affine(af, y, gb, co):
 
 
 @pytest.mark.parametrize("ci,co,l,k,d", [(128, 128, 1000, 11, 5), (128, 128, 777, 7, 3), (256, 256, 300, 3, 1),
-                                         (128, 128, 129, 3, 1), (128, 64, 5, 7, 3), (64, 64, 300, 12, 2)])
+                                         (128, 128, 129, 3, 1), (128, 64, 5, 7, 3), (64, 64, 300, 12, 2),
+                                         (256, 256, 700, 7, 3), (256, 128, 300, 11, 5)])  # split-K, dilated stats
 @pytest.mark.parametrize("res", [False, True])
 def test_wino_stats_epilogue_affine(gpu, ci, co, l, k, d, res):
     lk = gpu
