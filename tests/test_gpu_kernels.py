@@ -315,6 +315,43 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(e1b, e1)
 
 
+def test_library_gemms_replay_in_graphs(gpu):
+    """The plain / bias / relu / gelu / residual f32 GEMMs and the f16 bias / residual GEMMs run as the vendor
+    library's GEMM; captured together in one graph at the models' shapes and at skinny large-K shapes (where a
+    library may split K), every replay, with eager library GEMMs between replays, equals the eager results."""
+    lk = gpu
+    F = lk.ops.f16_gpu
+    f32 = [(59, 2048, 768, "none", True), (487, 768, 2304, "none", False), (487, 768, 2048, "gelu", False),
+           (64, 8192, 256, "none", True), (16, 4096, 4096, "relu", False), (512, 768, 3072, "gelu", False)]
+    ops32 = []
+    for m, k, n, act, res in f32:
+        ops32.append((G(lk, rng.standard_normal((m, k))), G(lk, rng.standard_normal((k, n)) / np.sqrt(k)),
+                      G(lk, rng.standard_normal(n)), G(lk, rng.standard_normal((m, n))) if res else None, act))
+    H = lambda a: lk.from_numpy(np.ascontiguousarray(a, dtype=np.float16), device="gpu", copy=True)
+    x16 = [H(rng.standard_normal((mm, kk)) * 0.5) for mm, kk in ((416, 2048), (40, 6144))]
+    w16 = [F.pack((rng.standard_normal((2048, 4096)) / 45).astype(np.float16)),
+           F.pack((rng.standard_normal((6144, 2048)) / 78).astype(np.float16))]
+    b16 = H(rng.standard_normal(4096))
+    r16 = H(rng.standard_normal((40, 2048)))
+
+    def fn():
+        outs = [lk.ops.gemm_steel_f32_gpu(a, b, bias, act=act, residual=res) for a, b, bias, res, act in ops32]
+        outs.append(F.gemm_bias_opt_f16_gpu(x16[0], w16[0], b16))
+        outs.append(F.gemm_add_opt_f16_gpu(x16[1], w16[1], r16))
+        return tuple(outs)
+
+    eager = [t.numpy() for t in fn()]
+    m = lk.capture(fn)
+    for _ in range(4):  # the first call runs eagerly while the graph is captured, the others replay it
+        got = [t.numpy() for t in m()]
+        torch.cuda.synchronize()
+        for i, (g, e) in enumerate(zip(got, eager)):
+            assert np.array_equal(g.view(np.uint8), e.view(np.uint8)), i
+        again = [t.numpy() for t in fn()]  # eager library work between replays
+        for i, (g, e) in enumerate(zip(again, eager)):
+            assert np.array_equal(g.view(np.uint8), e.view(np.uint8)), i
+
+
 @pytest.mark.parametrize("l,c,co,k,d,act", [(40001, 128, 128, 11, 5, "snake"), (33000, 128, 128, 3, 1, "snake"),
                                             (20000, 256, 256, 7, 3, "snake"), (30000, 128, 128, 7, 1, "leaky"),
                                             (32768, 512, 256, 3, 1, "none")])
