@@ -244,8 +244,9 @@ int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* 
  *      (lk_hip_f16_transpose); the reference fixes only the math and leaves the layout to the kernel. ---- */
 /* out f16[M, N] = x f16[M, K] @ W (+ bias f16[N]) (+ res f16[M, N]), or silu(x @ Wg) * (x @ Wu) with swiglu = 1
  * (W^T rows [gate | up], N' = 2N): gemm[_bias]_f16_gpu, gemm[_bias|_add|_swiglu]_opt_f16_gpu. K % 8 == 0, 16-byte
- * aligned x and W^T. M = 1 runs a GEMV; M > 1 without swiglu runs as hipBLASLt's f16 GEMM (f32 accumulation).
- * workspace (optional): split-K partials when the grid is small, or the library's workspace. */
+ * aligned x and W^T. M = 1 runs a GEMV; M > 1 runs as hipBLASLt's f16 GEMM (f32 accumulation; with swiglu its f32
+ * [gate | up] goes to the workspace and one pass applies silu(gate) * up). workspace (optional): that plane, the
+ * library's workspace, or split-K partials when the grid is small. */
 int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void* res, void* out, int64_t m, int64_t n,
                     int64_t k, int swiglu, void* workspace, int64_t workspace_bytes, void* stream);
 int64_t lk_hip_f16_gemm_workspace_bytes(int64_t m, int64_t n, int swiglu);

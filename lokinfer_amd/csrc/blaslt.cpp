@@ -32,7 +32,7 @@ struct Plan {
   bool ok = false;
 };
 
-using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, int, bool, size_t>;
+using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, int, bool, bool, size_t>;
 
 std::mutex gMu;
 std::map<Key, Plan> gPlans;
@@ -48,9 +48,9 @@ hipblasLtHandle_t handleFor(int dev) {
 }
 
 Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, bool bias, int act, bool f16,
-              size_t wsMax) {
+              bool f32out, size_t wsMax) {
   Plan p;
-  const hipDataType ty = f16 ? HIP_R_16F : HIP_R_32F;
+  const hipDataType ty = f16 ? HIP_R_16F : HIP_R_32F, tyc = f32out ? HIP_R_32F : ty;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
   const int32_t ta = nt ? HIPBLAS_OP_T : HIPBLAS_OP_N, tb = HIPBLAS_OP_N;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
@@ -60,7 +60,7 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
   if (act == 2) epi = bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
   if (bias) {
-    const int32_t bty = ty;
+    const int32_t bty = tyc;
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bty, sizeof(bty));
   }
   // column-major operands: "A" = B^T [N, K] (stored [K, N] with ld N, or [N, K] with ld K read transposed),
@@ -68,7 +68,7 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
   if (nt) hipblasLtMatrixLayoutCreate(&p.la, ty, static_cast<uint64_t>(k), static_cast<uint64_t>(n), k);
   else hipblasLtMatrixLayoutCreate(&p.la, ty, static_cast<uint64_t>(n), static_cast<uint64_t>(k), n);
   hipblasLtMatrixLayoutCreate(&p.lb, ty, static_cast<uint64_t>(k), static_cast<uint64_t>(m), k);
-  hipblasLtMatrixLayoutCreate(&p.lc, ty, static_cast<uint64_t>(n), static_cast<uint64_t>(m), n);
+  hipblasLtMatrixLayoutCreate(&p.lc, tyc, static_cast<uint64_t>(n), static_cast<uint64_t>(m), n);
   if (!p.la || !p.lb || !p.lc) return p;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
@@ -88,10 +88,11 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
 }  // namespace
 
 // C [M, N] = act(A [M, K] B (+ bias [N])) (+ res [M, N], only with act 0: the library's epilogue activation would
-// apply after the residual); act 0 none, 1 relu, 2 gelu (tanh form). B [K, N], or [N, K] with nt; f16: every operand
-// is IEEE half. Returns false (nothing launched) when no library algorithm fits the shape and the workspace.
+// apply after the residual); act 0 none, 1 relu, 2 gelu (tanh form). B [K, N], or [N, K] with nt; f16: A and B are
+// IEEE half, and so are bias, res and C unless f32out (then they are f32: the unrounded f32 accumulations). Returns
+// false (nothing launched) when no library algorithm fits the shape and the workspace.
 bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, int act, bool f16, void* ws, size_t wsBytes, hipStream_t s) {
+             bool nt, int act, bool f16, bool f32out, void* ws, size_t wsBytes, hipStream_t s) {
   if (act < 0 || act > 2 || (act != 0 && res)) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
@@ -100,9 +101,9 @@ bool bltGemm(const void* a, const void* b, const void* bias, const void* res, vo
   hipblasLtHandle_t h = handleFor(dev);
   if (!h) return false;
   const size_t wsb = ws ? wsBytes : 0;
-  const Key key{dev, m, n, k, nt, bias != nullptr, act, f16, wsb};
+  const Key key{dev, m, n, k, nt, bias != nullptr, act, f16, f32out && f16, wsb};
   auto it = gPlans.find(key);
-  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, act, f16, wsb)).first;
+  if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, act, f16, f32out && f16, wsb)).first;
   const Plan& plan = it->second;
   if (!plan.ok) return false;
   if (bias && hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=

@@ -879,7 +879,7 @@ static GemmParams baseParams() {
 
 namespace lkh {
 bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, int act, bool f16, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
+             bool nt, int act, bool f16, bool f32out, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
 }  // namespace lkh
 
 // ---- typed C-ABI launchers ---------------------------------------------------------------------------------
@@ -911,7 +911,7 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
     // bias, then relu / gelu or a residual: the library's GEMM, its workspace past the 64 KiB counter area
     void* ws = workspace && workspace_bytes > 65536 ? static_cast<char*>(workspace) + 65536 : nullptr;
     const size_t wsb = ws ? static_cast<size_t>(workspace_bytes - 65536) : 0;
-    if (lkh::bltGemm(a, b, bias, res, out, m, n, k, nt != 0, act, false, ws, wsb, s))
+    if (lkh::bltGemm(a, b, bias, res, out, m, n, k, nt != 0, act, false, false, ws, wsb, s))
       return hipGetLastError() == hipSuccess ? 0 : 2;
   }
   if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s, workspace, workspace_bytes);
