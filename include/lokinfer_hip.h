@@ -68,7 +68,8 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
                     int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
                     void* stream);
 /* channel-last conv1d: x [L, Ci] (Ci % 16 == 0), w [Co, K, Ci] -> out [Lo, Co] = (conv(pre(x)) + b + res) * scale;
- * pre = optional affine [3, Ci] (mean, scale, beta) then snake(alpha) (pre 1) / leaky(slope) (pre 2) */
+ * pre = optional affine [3, Ci] (mean, scale, beta) then snake(alpha) (pre 1) / leaky(slope) (pre 2). K = 1, stride 1,
+ * no padding and no prologue run as lk_hip_gemm_f32's NT form */
 int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, const float* res, float* out, int64_t l,
                          int64_t ci, int64_t co, int64_t kw, int stride, int padding, int dilation, float scale,
                          const float* affine, const float* alpha, int pre, float slope, float* stats, void* workspace,

@@ -970,6 +970,12 @@ int lk_hip_conv1d_lc_f32(const float* x, const float* w, const float* bias, cons
   if (ci % 16 != 0 || stride < 1 || dilation < 1 || padding < 0) return 1;
   const int64_t lo = (l + 2 * padding - static_cast<int64_t>(dilation) * (kw - 1) - 1) / stride + 1;
   if (lo <= 0 || co <= 0) return lo == 0 ? 0 : 1;
+  if (kw == 1 && stride == 1 && padding == 0 && pre == 0 && !affine) {
+    // one tap, no prologue: out = x W^T (+ bias, + res, * scale), the GEMM entry's NT form (W [Co, 1, Ci] = [Co, Ci])
+    const int rc = lk_hip_gemm_f32(x, w, bias, res, out, lo, co, ci, 1, 0, scale, workspace, workspace_bytes, stream);
+    if (rc || !stats) return rc;
+    return lk_hip_channel_stats_lc_f32(out, stats, lo, co, stream);
+  }
   lkd::GemmParams p = lkh::baseParams();
   p.a = x;
   p.b = w;

@@ -224,7 +224,8 @@ def test_snake_wide_range(gpu):
 
 
 @pytest.mark.parametrize("l,ci,co,k,pad,dil", [(295, 528, 1024, 3, 1, 1), (600, 256, 256, 7, 9, 3), (1000, 128, 128, 11, 25, 5),
-                                               (70, 1104, 512, 1, 0, 1), (33, 16, 64, 3, 1, 1), (5000, 128, 128, 3, 1, 1)])
+                                               (70, 1104, 512, 1, 0, 1), (33, 16, 64, 3, 1, 1), (5000, 128, 128, 3, 1, 1),
+                                               (4888, 1104, 512, 1, 0, 1)])
 def test_conv1d_lc(gpu, l, ci, co, k, pad, dil):
     lk = gpu
     x, w, b = rng.standard_normal((l, ci)), rng.standard_normal((co, k, ci)) / np.sqrt(k * ci), rng.standard_normal(co)
