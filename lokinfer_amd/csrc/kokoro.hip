@@ -15,6 +15,8 @@
 //
 // All element-wise kernels are grid-stride over float4 where the channel count allows; the reductions read
 // rows of 64 consecutive channels (256 B) per wave.
+#include <cmath>
+
 #include "common.h"
 
 namespace lkd {
@@ -191,10 +193,14 @@ __global__ void ewKernel(const float* __restrict__ a, const float* __restrict__ 
 // (its own plus nfft / hop halo frames) into LDS.
 constexpr int kIstftMaxN = 64;
 constexpr int kIstftFrames = 256;
+// NF > 0: nfft == NF at compile time, so a frame's 2 (NF / 2 + 1) logit loads are independent and in flight together
+// (a runtime-length loop waits for each load in turn: 136 us at 293281 frames).
+template <int NF>
 __global__ __launch_bounds__(256) void istftKernel(const float* __restrict__ x, float* __restrict__ out, int64_t l,
-                                                  int64_t cpad, int nfft, int hop) {
+                                                  int64_t cpad, int nfftArg, int hop) {
   extern __shared__ float smem[];
   __shared__ float tabRe[33 * kIstftMaxN], tabIm[33 * kIstftMaxN], win[kIstftMaxN];
+  const int nfft = NF > 0 ? NF : nfftArg;
   const int bins = nfft / 2 + 1, pad = nfft / 2;
   for (int i = threadIdx.x; i < bins * nfft; i += blockDim.x) {
     const int k = i / nfft, m = i % nfft;
@@ -220,17 +226,41 @@ __global__ __launch_bounds__(256) void istftKernel(const float* __restrict__ x, 
     const int64_t t = tFirst + f;
     if (t >= l) continue;
     const float* xt = x + t * cpad;
-    float re[33], im[33];
-    for (int k = 0; k < bins; ++k) {
-      const float mag = expf(xt[k]);
-      const float ph = sinf(xt[bins + k]);
-      re[k] = mag * cosf(ph);
-      im[k] = mag * sinf(ph);
-    }
-    for (int m = 0; m < nfft; ++m) {
-      float v = 0.0f;
-      for (int k = 0; k < bins; ++k) v += re[k] * tabRe[k * nfft + m] + im[k] * tabIm[k * nfft + m];
-      fr[f * nfft + m] = v;
+    if constexpr (NF > 0) {
+      constexpr int B = NF / 2 + 1;
+      float lm[B], lp[B], re[B], im[B];
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        lm[k] = xt[k];
+        lp[k] = xt[B + k];
+      }
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const float mag = expf(lm[k]);
+        const float ph = sinf(lp[k]);
+        re[k] = mag * cosf(ph);
+        im[k] = mag * sinf(ph);
+      }
+#pragma unroll
+      for (int m = 0; m < NF; ++m) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < B; ++k) v += re[k] * tabRe[k * NF + m] + im[k] * tabIm[k * NF + m];
+        fr[f * NF + m] = v;
+      }
+    } else {
+      float re[33], im[33];
+      for (int k = 0; k < bins; ++k) {
+        const float mag = expf(xt[k]);
+        const float ph = sinf(xt[bins + k]);
+        re[k] = mag * cosf(ph);
+        im[k] = mag * sinf(ph);
+      }
+      for (int m = 0; m < nfft; ++m) {
+        float v = 0.0f;
+        for (int k = 0; k < bins; ++k) v += re[k] * tabRe[k * nfft + m] + im[k] * tabIm[k * nfft + m];
+        fr[f * nfft + m] = v;
+      }
     }
   }
   __syncthreads();
@@ -244,6 +274,73 @@ __global__ __launch_bounds__(256) void istftKernel(const float* __restrict__ x, 
       const int m = static_cast<int>(p - t * hop);
       if (t < tFirst || t - tFirst >= nFrames) continue;  // unreachable by construction of nHalo
       y += fr[(t - tFirst) * nfft + m];
+      env += win[m] * win[m];
+    }
+    out[i] = y / env;
+  }
+}
+
+// n_fft = 20, hop = 5 (the model's): the same synthesis with a host-built table (the window-folded DFT and the
+// window, double cos / sin rounded to f32, as the kernel above builds them), the sizes as constants (the divisions
+// by hop become multiplies) and 32-bit indices (L hop < 2^31). A workgroup owns 249 hops of output, so it
+// synthesizes exactly 256 frames (its own and the 7 halo frames), one per thread, in one pass.
+struct IstftTable20 {
+  float re[11 * 20], im[11 * 20], win[20];
+};
+
+__global__ __launch_bounds__(256) void istft20Kernel(const float* __restrict__ x, float* __restrict__ out, int l,
+                                                    int cpad, IstftTable20 host) {
+  constexpr int NF = 20, HOP = 5, B = 11, PAD = 10;
+  constexpr int NHALO = (NF + HOP - 1) / HOP + 3;
+  constexpr int NFR = 256, FRAMES = NFR - NHALO;  // one synthesized frame per thread: FRAMES hops of output each
+  __shared__ float tabRe[B * NF], tabIm[B * NF], win[NF], fr[NFR * NF];
+  for (int i = threadIdx.x; i < B * NF; i += blockDim.x) {
+    tabRe[i] = host.re[i];
+    tabIm[i] = host.im[i];
+  }
+  if (threadIdx.x < NF) win[threadIdx.x] = host.win[threadIdx.x];
+  __syncthreads();
+  const int len = HOP * (l - 1);
+  const int i0 = blockIdx.x * FRAMES * HOP;
+  // Frames touched by samples [i0, i0 + FRAMES hop): t in [tFirst, tFirst + NFR).
+  const int p0 = i0 + PAD;
+  const int tFirst = p0 >= NF ? (p0 - NF) / HOP + 1 : 0;
+  for (int f = threadIdx.x; f < NFR; f += blockDim.x) {
+    const int t = tFirst + f;
+    if (t >= l) continue;
+    const float* xt = x + static_cast<int64_t>(t) * cpad;
+    float lm[B], lp[B], re[B], im[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      lm[k] = xt[k];
+      lp[k] = xt[B + k];
+    }
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const float mag = expf(lm[k]);
+      const float ph = sinf(lp[k]);
+      re[k] = mag * cosf(ph);
+      im[k] = mag * sinf(ph);
+    }
+#pragma unroll
+    for (int m = 0; m < NF; ++m) {
+      float v = 0.0f;
+#pragma unroll
+      for (int k = 0; k < B; ++k) v += re[k] * tabRe[k * NF + m] + im[k] * tabIm[k * NF + m];
+      fr[f * NF + m] = v;
+    }
+  }
+  __syncthreads();
+  const int iEnd = min(len, i0 + FRAMES * HOP);
+  for (int i = i0 + threadIdx.x; i < iEnd; i += blockDim.x) {
+    const int p = PAD + i;
+    const int tHi = min(l - 1, p / HOP);
+    const int tLo = p >= NF ? (p - NF) / HOP + 1 : 0;
+    float y = 0.0f, env = 0.0f;
+    for (int t = tLo; t <= tHi; ++t) {
+      const int m = p - t * HOP;
+      if (t < tFirst || t - tFirst >= NFR) continue;  // unreachable by construction of NHALO
+      y += fr[(t - tFirst) * NF + m];
       env += win[m] * win[m];
     }
     out[i] = y / env;
@@ -352,8 +449,31 @@ int lk_hip_istft_lc_f32(const float* x, float* out, int64_t l, int64_t cpad, int
   const unsigned blocks = lkh::ceilDiv(len, static_cast<int64_t>(lkd::kIstftFrames) * hop);
   const int nHalo = (nfft + hop - 1) / hop + 3;
   const size_t shm = static_cast<size_t>(lkd::kIstftFrames + nHalo) * nfft * sizeof(float);
-  hipLaunchKernelGGL(lkd::istftKernel, dim3(blocks), dim3(256), shm, static_cast<hipStream_t>(stream), x, out, l,
-                     cpad, nfft, hop);
+  if (nfft == 20 && hop == 5 && len < (int64_t{1} << 30)) {  // the model's n_fft and hop
+    static const lkd::IstftTable20 tab = [] {
+      lkd::IstftTable20 t{};
+      for (int i = 0; i < 11 * 20; ++i) {
+        const int k = i / 20, m = i % 20;
+        const bool edge = k == 0 || 2 * k == 20;
+        const double wm = 0.5 - 0.5 * std::cos(2.0 * M_PI * static_cast<double>(m) / 20.0);
+        const double ang = 2.0 * M_PI * static_cast<double>((k * m) % 20) / 20.0;
+        const double cc = (edge ? 1.0 : 2.0) * static_cast<double>(static_cast<float>(wm)) / 20.0;
+        t.re[i] = static_cast<float>(cc * std::cos(ang));
+        t.im[i] = edge ? 0.0f : static_cast<float>(-cc * std::sin(ang));
+      }
+      for (int m = 0; m < 20; ++m)
+        t.win[m] = static_cast<float>(0.5 - 0.5 * std::cos(2.0 * M_PI * static_cast<double>(m) / 20.0));
+      return t;
+    }();
+    const unsigned b20 = static_cast<unsigned>(lkh::ceilDiv(len, int64_t{(256 - 7) * 5}));
+    hipLaunchKernelGGL(lkd::istft20Kernel, dim3(b20), dim3(256), 0, static_cast<hipStream_t>(stream), x, out,
+                       static_cast<int>(l), static_cast<int>(cpad), tab);
+  } else if (nfft == 20) {
+    hipLaunchKernelGGL(lkd::istftKernel<20>, dim3(blocks), dim3(256), shm, static_cast<hipStream_t>(stream), x, out, l,
+                       cpad, nfft, hop);
+  } else
+    hipLaunchKernelGGL(lkd::istftKernel<0>, dim3(blocks), dim3(256), shm, static_cast<hipStream_t>(stream), x, out, l,
+                       cpad, nfft, hop);
   LK_RET;
 }
 

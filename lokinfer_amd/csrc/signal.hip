@@ -16,6 +16,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cmath>
 
 // Every fused multiply-add in this file is an explicit __builtin_fmaf; nothing else may be contracted.
 #pragma clang fp contract(off)
@@ -59,6 +60,44 @@ __global__ __launch_bounds__(64 * kHarm) void harmonicPhaseKernel(const float* _
   }
 }
 
+// The same phases for n <= kHarmLds frames: one workgroup per harmonic (so the nine scans run on nine CUs), f0
+// staged in LDS first; thread T walks the contiguous frames [T seg, (T + 1) seg), seg = ceil(n / 256): it sums its
+// increments in double, a workgroup scan of the 256 sums (wave scans, then the wave totals through LDS) gives each
+// thread its prefix, and the thread re-walks its frames with the running sum. The sums of f32 increments in [0, 1)
+// are exact in double, so this order gives the values of the frame-by-frame scan above. (That scan, all nine
+// harmonics in one workgroup, runs n / 64 dependent rounds of a global load and six shuffles: 57 us at n = 4888.)
+constexpr int kHarmLds = 16384;
+__global__ __launch_bounds__(256) void harmonicPhaseLdsKernel(const float* __restrict__ f0, float* __restrict__ p300,
+                                                              int n) {
+  __shared__ float f0s[kHarmLds];
+  __shared__ double waveTotal[4];
+  for (int j = threadIdx.x; j < n; j += blockDim.x) f0s[j] = f0[j];
+  __syncthreads();
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float hf = static_cast<float>(h + 1);
+  const int seg = (n + 255) / 256;
+  const int j0 = min(n, tid * seg), j1 = min(n, j0 + seg);
+  double sum = 0.0;
+  for (int j = j0; j < j1; ++j) sum += static_cast<double>(torchRemainder1(f0s[j] * hf / 24000.0f));
+  double pre = sum;  // inclusive scan within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double u = __shfl_up(pre, o, 64);
+    if (lane >= o) pre += u;
+  }
+  if (lane == 63) waveTotal[wave] = pre;
+  __syncthreads();
+  double acc = 0.0;  // this thread's exclusive prefix: the earlier waves' totals, then the left neighbour's scan
+  for (int w = 0; w < wave; ++w) acc += waveTotal[w];
+  const double left = __shfl_up(pre, 1, 64);
+  if (lane > 0) acc += left;
+  for (int j = j0; j < j1; ++j) {
+    acc += static_cast<double>(torchRemainder1(f0s[j] * hf / 24000.0f));
+    const float phase = (static_cast<float>(acc) * 2.0f) * 3.14159265358979323846f;
+    p300[static_cast<int64_t>(j) * kHarm + h] = phase * 300.0f;
+  }
+}
+
 __global__ void harmonicSourceKernel(const float* __restrict__ f0, const float* __restrict__ p300,
                                      const float* __restrict__ noise, const float* __restrict__ w,
                                      const float* __restrict__ b, float* __restrict__ out, int64_t n) {
@@ -91,45 +130,130 @@ __global__ void harmonicSourceKernel(const float* __restrict__ f0, const float* 
   }
 }
 
-// One thread per frame: reflect-padded frame (center = True), windowed DFT by a table built like the
-// reference's (double cos / sin, rounded to f32), accumulation over m in order, im = 0 at DC / Nyquist.
-constexpr int kStftMaxN = 64;
-__global__ __launch_bounds__(256) void stftKernel(const float* __restrict__ x, float* __restrict__ out, int64_t s,
-                                                 int64_t frames, int nfft, int hop, int64_t ldo) {
-  __shared__ float tabRe[33 * kStftMaxN], tabIm[33 * kStftMaxN];
-  const int bins = nfft / 2 + 1, pad = nfft / 2;
-  for (int i = threadIdx.x; i < bins * nfft; i += blockDim.x) {
-    const int k = i / nfft, m = i % nfft;
-    const float win = static_cast<float>(0.5 - 0.5 * cos(2.0 * M_PI * static_cast<double>(m) / nfft));
-    const double ang = 2.0 * M_PI * static_cast<double>((k * m) % nfft) / static_cast<double>(nfft);
-    tabRe[i] = static_cast<float>(win * cos(ang));
-    tabIm[i] = static_cast<float>(-win * sin(ang));
+// The DFT table for nfft = NF, built on the host (double cos / sin, rounded to f32) and passed by value.
+template <int NF>
+struct StftTable {
+  float re[(NF / 2 + 1) * NF], im[(NF / 2 + 1) * NF];
+};
+
+// n_fft = 20 (the model's): one thread per (frame t, bin k), k fastest. An interior frame reads its 20 samples at
+// immediate offsets from one base (only the first and last frames reflect); the bin's sums use the host-built
+// table in LDS, accumulated over m in order as below; the thread writes the bin's magnitude (column k), phase
+// (column 11 + k) and, for k < ldo - 22, the zero column 22 + k. 32-bit index math (s < 2^31).
+__global__ __launch_bounds__(256) void stft20Kernel(const float* __restrict__ x, float* __restrict__ out, int s,
+                                                   int frames, int hop, int ldo, StftTable<20> host) {
+  constexpr int NF = 20, B = 11, PAD = 10;
+  __shared__ float tabRe[B * NF], tabIm[B * NF];
+  for (int i = threadIdx.x; i < B * NF; i += blockDim.x) {
+    tabRe[i] = host.re[i];
+    tabIm[i] = host.im[i];
   }
   __syncthreads();
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= frames) return;
-  float fr[kStftMaxN];
-  for (int m = 0; m < nfft; ++m) {
-    int64_t q = t * hop + m - pad;
-    if (q < 0) q = -q;
-    if (q >= s) q = 2 * (s - 1) - q;
-    fr[m] = x[q];
-  }
-  float* o = out + t * ldo;
-  for (int k = 0; k < bins; ++k) {
+  const int total = frames * B;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const int t = i / B, k = i - t * B;
+    const int base = t * hop - PAD;
+    float fr[NF];
+    if (base >= 0 && base + NF <= s) {
+      const float* xb = x + base;
+#pragma unroll
+      for (int m = 0; m < NF; ++m) fr[m] = xb[m];
+    } else {
+#pragma unroll
+      for (int m = 0; m < NF; ++m) {
+        int q = base + m;
+        if (q < 0) q = -q;
+        if (q >= s) q = 2 * (s - 1) - q;
+        fr[m] = x[q];
+      }
+    }
     float re = 0.0f, im = 0.0f;
-    for (int m = 0; m < nfft; ++m) {
-      re += tabRe[k * nfft + m] * fr[m];
-      im += tabIm[k * nfft + m] * fr[m];
+#pragma unroll
+    for (int m = 0; m < NF; ++m) {
+      re += tabRe[k * NF + m] * fr[m];
+      im += tabIm[k * NF + m] * fr[m];
     }
     // Real-input DFT: the DC and Nyquist bins are exactly real. So is every bin of frame 0: with center = True
     // and reflect padding that frame is even about its centre (as is the periodic Hann window), and its exact
     // imaginary parts are 0 rather than rounding noise whose sign would flip the phase between +pi and -pi.
-    if (k == 0 || 2 * k == nfft || t == 0) im = 0.0f;
+    if (k == 0 || 2 * k == NF || t == 0) im = 0.0f;
+    float* o = out + static_cast<int64_t>(t) * ldo;
     o[k] = sqrtf(__builtin_fmaf(re, re, im * im));
-    o[bins + k] = atan2f(im, re);
+    o[B + k] = atan2f(im, re);
+    for (int c = 2 * B + k; c < ldo; c += B) o[c] = 0.0f;
   }
-  for (int64_t c = 2 * bins; c < ldo; ++c) o[c] = 0.0f;
+}
+
+// One thread per output element (frame t, column c; c fastest, so a wave's stores are contiguous): columns < bins
+// hold the magnitude of bin c, bins .. 2 bins - 1 the phase of bin c - bins, the rest 0. A bin is the windowed DFT of
+// the reflect-padded frame (center = True) by a table built like the reference's (double cos / sin, rounded to f32),
+// accumulated over m in order; the magnitude and phase threads of a bin compute the same sums. Grid-stride, so the
+// per-workgroup table build is amortized. (One thread per frame ran 114 us at 293281 samples: 230 workgroups and
+// 32 strided stores per thread; most of it was the load latency below.)
+// NF > 0: nfft == NF at compile time, so a frame's NF sample loads are independent and in flight together (a
+// runtime-length loop issues one load per iteration and waits for it: 110 us at 293281 samples).
+constexpr int kStftMaxN = 64;
+template <int NF>
+__global__ __launch_bounds__(256) void stftKernel(const float* __restrict__ x, float* __restrict__ out, int64_t s,
+                                                 int64_t frames, int nfftArg, int hop, int64_t ldo,
+                                                 StftTable<NF> host) {
+  __shared__ float tabRe[33 * kStftMaxN], tabIm[33 * kStftMaxN];
+  const int nfft = NF > 0 ? NF : nfftArg;
+  const int bins = nfft / 2 + 1, pad = nfft / 2;
+  for (int i = threadIdx.x; i < bins * nfft; i += blockDim.x) {
+    if constexpr (NF > 0) {
+      tabRe[i] = host.re[i];
+      tabIm[i] = host.im[i];
+    } else {
+      const int k = i / nfft, m = i % nfft;
+      const float win = static_cast<float>(0.5 - 0.5 * cos(2.0 * M_PI * static_cast<double>(m) / nfft));
+      const double ang = 2.0 * M_PI * static_cast<double>((k * m) % nfft) / static_cast<double>(nfft);
+      tabRe[i] = static_cast<float>(win * cos(ang));
+      tabIm[i] = static_cast<float>(-win * sin(ang));
+    }
+  }
+  __syncthreads();
+  const int64_t total = frames * ldo;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = i / ldo;
+    const int c = static_cast<int>(i - t * ldo);
+    float v = 0.0f;
+    if (c < 2 * bins) {
+      const int k = c < bins ? c : c - bins;
+      float re = 0.0f, im = 0.0f;
+      if constexpr (NF > 0) {
+        float fr[NF];
+#pragma unroll
+        for (int m = 0; m < NF; ++m) {
+          int64_t q = t * hop + m - pad;
+          if (q < 0) q = -q;
+          if (q >= s) q = 2 * (s - 1) - q;
+          fr[m] = x[q];
+        }
+#pragma unroll
+        for (int m = 0; m < NF; ++m) {
+          re += tabRe[k * NF + m] * fr[m];
+          im += tabIm[k * NF + m] * fr[m];
+        }
+      } else {
+        for (int m = 0; m < nfft; ++m) {
+          int64_t q = t * hop + m - pad;
+          if (q < 0) q = -q;
+          if (q >= s) q = 2 * (s - 1) - q;
+          const float xv = x[q];
+          re += tabRe[k * nfft + m] * xv;
+          im += tabIm[k * nfft + m] * xv;
+        }
+      }
+      // Real-input DFT: the DC and Nyquist bins are exactly real. So is every bin of frame 0: with center = True
+      // and reflect padding that frame is even about its centre (as is the periodic Hann window), and its exact
+      // imaginary parts are 0 rather than rounding noise whose sign would flip the phase between +pi and -pi.
+      if (k == 0 || 2 * k == nfft || t == 0) im = 0.0f;
+      v = c < bins ? sqrtf(__builtin_fmaf(re, re, im * im)) : atan2f(im, re);
+    }
+    out[i] = v;
+  }
 }
 
 __global__ void conv1chKernel(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
@@ -155,7 +279,11 @@ int lk_hip_harmonic_source_f32(const float* f0, const float* noise, const float*
   if (!workspace || workspaceBytes < n * lkd::kHarm * 4) return 3;
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* p300 = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(lkd::harmonicPhaseKernel, dim3(1), dim3(64 * lkd::kHarm), 0, st, f0, p300, n);
+  if (n <= lkd::kHarmLds)
+    hipLaunchKernelGGL(lkd::harmonicPhaseLdsKernel, dim3(lkd::kHarm), dim3(256), 0, st, f0, p300,
+                       static_cast<int>(n));
+  else
+    hipLaunchKernelGGL(lkd::harmonicPhaseKernel, dim3(1), dim3(64 * lkd::kHarm), 0, st, f0, p300, n);
   const int64_t s = n * 300;
   const int64_t blocks = std::min<int64_t>((s + 255) / 256, 65536);
   hipLaunchKernelGGL(lkd::harmonicSourceKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, f0, p300,
@@ -167,8 +295,31 @@ int lk_hip_harmonic_source_f32(const float* f0, const float* noise, const float*
 int lk_hip_stft_magphase_lc_f32(const float* x, float* out, int64_t s, int nfft, int hop, int64_t ldo, void* stream) {
   if (nfft < 2 || nfft % 2 || nfft > lkd::kStftMaxN || hop < 1 || s <= nfft / 2 || ldo < nfft + 2) return 1;
   const int64_t frames = s / hop + 1;
-  hipLaunchKernelGGL(lkd::stftKernel, dim3(lkh::ceilDiv(frames, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     x, out, s, frames, nfft, hop, ldo);
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(lkh::ceilDiv(frames * ldo, 256), 2048));
+  if (nfft == 20) {  // the model's n_fft: the table built once on the host, as the kernel builds it otherwise
+    static const lkd::StftTable<20> tab = [] {
+      lkd::StftTable<20> t{};
+      for (int i = 0; i < 11 * 20; ++i) {
+        const int k = i / 20, m = i % 20;
+        const float win = static_cast<float>(0.5 - 0.5 * std::cos(2.0 * M_PI * static_cast<double>(m) / 20));
+        const double ang = 2.0 * M_PI * static_cast<double>((k * m) % 20) / 20.0;
+        t.re[i] = static_cast<float>(win * std::cos(ang));
+        t.im[i] = static_cast<float>(-win * std::sin(ang));
+      }
+      return t;
+    }();
+    if (s < (int64_t{1} << 30) && frames * 11 < (int64_t{1} << 30)) {
+      const unsigned b20 = static_cast<unsigned>(std::min<int64_t>(lkh::ceilDiv(frames * 11, 256), 4096));
+      hipLaunchKernelGGL(lkd::stft20Kernel, dim3(b20), dim3(256), 0, static_cast<hipStream_t>(stream), x, out,
+                         static_cast<int>(s), static_cast<int>(frames), hop, static_cast<int>(ldo), tab);
+    } else {
+      hipLaunchKernelGGL(lkd::stftKernel<20>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, out, s,
+                         frames, nfft, hop, ldo, tab);
+    }
+  } else {
+    hipLaunchKernelGGL(lkd::stftKernel<0>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, out, s,
+                       frames, nfft, hop, ldo, lkd::StftTable<0>{});
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

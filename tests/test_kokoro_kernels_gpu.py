@@ -91,10 +91,10 @@ def test_repeat_interleave_adaln_concat(gpu):
     assert np.array_equal(out, np.concatenate([y, np.broadcast_to(v, (t, 128))], 1))
 
 
-@pytest.mark.parametrize("voiced", [True, False])
-def test_harmonic_source_matches_f32_restatement(gpu, voiced):
+# 4888: the 487-token forward's frames; 16500: past the LDS-staged phase scan's 16384 frames (the global-memory scan)
+@pytest.mark.parametrize("n,voiced", [(574, True), (574, False), (4888, True), (16500, True)])
+def test_harmonic_source_matches_f32_restatement(gpu, n, voiced):
     lk = gpu
-    n = 574
     f0 = (150 + 20 * rng.standard_normal(n) if voiced else rng.standard_normal(n)).astype(np.float32)
     f0[:7] = 0.0  # unvoiced frames inside a voiced curve
     noise = rng.standard_normal((300 * n, 9)).astype(np.float32)
