@@ -74,6 +74,7 @@ __device__ __forceinline__ h16 rmsElem(h16 x, h16 g, float r) {
 }
 
 // ---- RMSNorm over groups of `width` values (rows, or heads), one wave per group ----------------------------
+template <int W>  // W > 0: width == W, the lane's W / 512 chunks of x and g loaded once, in rowSumSq's order
 __global__ __launch_bounds__(256) void rmsGroupsKernel(const h16* __restrict__ x, const h16* __restrict__ g,
                                                        h16* __restrict__ out, int64_t groups, int64_t width,
                                                        float eps) {
@@ -81,14 +82,37 @@ __global__ __launch_bounds__(256) void rmsGroupsKernel(const h16* __restrict__ x
   const int64_t grp = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (grp >= groups) return;
   const h16* xr = x + grp * width;
-  const float r = rmsFactor(rowSumSq(xr, width, lane), width, eps);
   h16* o = out + grp * width;
-  for (int64_t c = lane; c < width / 8; c += 64) {
-    const half8 v = ld8(xr + 8 * c), gv = ld8(g + 8 * c);
-    half8 y;
+  if constexpr (W > 0) {
+    constexpr int C = W / 512;
+    half8 v[C], gv[C];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = rmsElem(v[e], gv[e], r);
-    st8(o + 8 * c, y);
+    for (int i = 0; i < C; ++i) {
+      v[i] = ld8(xr + 8 * (lane + 64 * i));
+      gv[i] = ld8(g + 8 * (lane + 64 * i));
+    }
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq = fmaf(static_cast<float>(v[i][e]), static_cast<float>(v[i][e]), sq);
+    const float r = rmsFactor(waveSum(sq), W, eps);
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      half8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = rmsElem(v[i][e], gv[i][e], r);
+      st8(o + 8 * (lane + 64 * i), y);
+    }
+  } else {
+    const float r = rmsFactor(rowSumSq(xr, width, lane), width, eps);
+    for (int64_t c = lane; c < width / 8; c += 64) {
+      const half8 v = ld8(xr + 8 * c), gv = ld8(g + 8 * c);
+      half8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = rmsElem(v[e], gv[e], r);
+      st8(o + 8 * c, y);
+    }
   }
 }
 
@@ -1419,7 +1443,8 @@ int lk_hip_f16_rms_gemm(const void* x, const void* g, const void* wt, void* out,
     return launched();
   }
   if (!aligned16(ws)) return 1;
-  hipLaunchKernelGGL(rmsGroupsKernel, dim3(static_cast<unsigned>((m + 3) / 4)), dim3(256), 0, s,
+  hipLaunchKernelGGL(k == 2048 ? rmsGroupsKernel<2048> : rmsGroupsKernel<0>, dim3(static_cast<unsigned>((m + 3) / 4)),
+                     dim3(256), 0, s,
                      static_cast<const h16*>(x), static_cast<const h16*>(g), static_cast<h16*>(ws), m, k, eps);
   if (launched()) return 2;
   return lk_hip_f16_gemm(ws, wt, nullptr, nullptr, out, m, n, k, swiglu, workspace, workspace_bytes, stream);
@@ -1452,7 +1477,8 @@ int lk_hip_f16_rmsnorm(const void* x, const void* g, void* out, int64_t rows, in
     return 1;
   const int64_t groups = rows * (c / width);
   if (groups == 0) return 0;
-  hipLaunchKernelGGL(rmsGroupsKernel, dim3(static_cast<unsigned>((groups + 3) / 4)), dim3(256), 0,
+  hipLaunchKernelGGL(width == 2048 ? rmsGroupsKernel<2048> : rmsGroupsKernel<0>,
+                     dim3(static_cast<unsigned>((groups + 3) / 4)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const h16*>(x), static_cast<const h16*>(g),
                      static_cast<h16*>(out), groups, width, eps);
   return launched();
