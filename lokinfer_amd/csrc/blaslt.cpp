@@ -11,14 +11,18 @@
 // unchanged as the column-major operands (B first), and the per-column bias becomes hipBLASLt's per-row bias of D.
 // A residual R [M, N] is the library's C operand with beta = 1 (D = A B + R + bias, one rounding at the output).
 // f32 compute (HIPBLAS_COMPUTE_32F, no reduced-precision inner products) for both storage types. One handle per
-// device and one plan (descriptors + the heuristic's first algorithm) per shape, cached for the process.
+// device and one plan per shape, cached for the process: its descriptors and the fastest of the heuristic's first
+// eight algorithms, timed on the shape's first (eager) call; LK_BLASLT_NOTUNE=1 keeps the heuristic's first.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <utility>
+#include <vector>
 
 namespace lkh {
 
@@ -30,6 +34,8 @@ struct Plan {
   hipblasLtMatmulAlgo_t algo{};
   size_t ws = 0;
   bool ok = false;
+  bool tuned = false;  // the algorithm is final: chosen on the shape's first call and never changed after
+  std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>> cands;  // the heuristic's candidates (algorithm, workspace)
 };
 
 using Key = std::tuple<int, int64_t, int64_t, int64_t, bool, bool, int, bool, bool, size_t>;
@@ -74,14 +80,20 @@ Plan makePlan(hipblasLtHandle_t h, int64_t m, int64_t n, int64_t k, bool nt, boo
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
   const uint64_t wsBytes = wsMax;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsBytes, sizeof(wsBytes));
-  hipblasLtMatmulHeuristicResult_t res[1];
+  constexpr int kCands = 8;
+  hipblasLtMatmulHeuristicResult_t res[kCands];
   int got = 0;
-  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &got);
+  const hipblasStatus_t st =
+      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCands, res, &got);
   hipblasLtMatmulPreferenceDestroy(pref);
-  if (st != HIPBLAS_STATUS_SUCCESS || got < 1 || res[0].state != HIPBLAS_STATUS_SUCCESS) return p;
-  p.algo = res[0].algo;
-  p.ws = res[0].workspaceSize;
-  p.ok = p.ws <= wsMax;
+  if (st != HIPBLAS_STATUS_SUCCESS) return p;
+  for (int i = 0; i < got; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= wsMax)
+      p.cands.emplace_back(res[i].algo, res[i].workspaceSize);
+  if (p.cands.empty()) return p;
+  p.algo = p.cands[0].first;  // the heuristic's first choice until tuned
+  p.ws = p.cands[0].second;
+  p.ok = true;
   return p;
 }
 
@@ -104,14 +116,49 @@ bool bltGemm(const void* a, const void* b, const void* bias, const void* res, vo
   const Key key{dev, m, n, k, nt, bias != nullptr, act, f16, f32out && f16, wsb};
   auto it = gPlans.find(key);
   if (it == gPlans.end()) it = gPlans.emplace(key, makePlan(h, m, n, k, nt, bias != nullptr, act, f16, f32out && f16, wsb)).first;
-  const Plan& plan = it->second;
+  Plan& plan = it->second;
   if (!plan.ok) return false;
   if (bias && hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=
                   HIPBLAS_STATUS_SUCCESS)
     return false;
   const float alpha = 1.0f, beta = res ? 1.0f : 0.0f;
-  return hipblasLtMatmul(h, plan.desc, &alpha, b, plan.la, a, plan.lb, &beta, res ? res : c, plan.lc, c, plan.lc,
-                         &plan.algo, plan.ws ? ws : nullptr, plan.ws, s) == HIPBLAS_STATUS_SUCCESS;
+  auto run = [&](const hipblasLtMatmulAlgo_t& algo, size_t wsz) {
+    return hipblasLtMatmul(h, plan.desc, &alpha, b, plan.la, a, plan.lb, &beta, res ? res : c, plan.lc, c, plan.lc,
+                           &algo, wsz ? ws : nullptr, wsz, s) == HIPBLAS_STATUS_SUCCESS;
+  };
+  if (!plan.tuned) {
+    plan.tuned = true;
+    // the shape's first call times the heuristic's candidates on these operands and keeps the fastest. Not while
+    // the stream is being captured (the first choice then stays), nor when the residual is the output (each trial
+    // run would add it again); the trial runs' outputs are overwritten by the call's own run below.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
+    if (plan.cands.size() > 1 && !capturing && !(res && res == c) && !getenv("LK_BLASLT_NOTUNE")) {
+      hipEvent_t e0 = nullptr, e1 = nullptr;
+      if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        float best = -1.0f;
+        for (const auto& cand : plan.cands) {
+          if (!run(cand.first, cand.second)) continue;  // warm-up; an algorithm that fails here is skipped
+          hipEventRecord(e0, s);
+          bool okRun = true;
+          for (int r = 0; r < 3 && okRun; ++r) okRun = run(cand.first, cand.second);
+          hipEventRecord(e1, s);
+          float ms = 0.0f;
+          if (!okRun || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+            continue;
+          if (best < 0.0f || ms < best) {
+            best = ms;
+            plan.algo = cand.first;
+            plan.ws = cand.second;
+          }
+        }
+      }
+      if (e0) hipEventDestroy(e0);
+      if (e1) hipEventDestroy(e1);
+      (void)hipGetLastError();  // a failed trial leaves no error for the caller's launch check
+    }
+  }
+  return run(plan.algo, plan.ws);
 }
 
 }  // namespace lkh
