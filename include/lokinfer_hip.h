@@ -63,7 +63,8 @@ const char* lk_device_error_message(int code);
  * partial tiles (split * M * N floats past the first 64 KiB) a second kernel sums; calls sharing a workspace
  * must be stream-ordered. With scale 1 (and no res when act != 0) the product runs as hipBLASLt's f32 GEMM (bias /
  * relu / gelu epilogues, res as its C operand, its workspace past the first 64 KiB); the first call per shape builds its
- * plan */
+ * plan and, outside graph capture, times the library's candidate algorithms on that call's operands (it synchronizes
+ * the stream once) */
 int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
                     int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
                     void* stream);
