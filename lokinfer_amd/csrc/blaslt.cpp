@@ -1,11 +1,12 @@
-// Plain GEMMs (f32, or f16 storage with f32 accumulation; optional per-column bias, ReLU / tanh-GELU, or a
-// residual) through hipBLASLt, the vendor library GEMM.
+// GEMMs through hipBLASLt, the vendor library GEMM: f32, or f16 storage with f32 accumulation (and f32 output
+// when asked, for the SwiGLU epilogue pass), with an optional per-column bias and either ReLU / tanh-GELU or a
+// residual.
 //
-// The hand-written MFMA kernels (gemm.hip) keep every fused form: activations, residuals, output scales, split-K
-// partials for a consumer, the conv loaders. For a plain row-major A [M, K] times B ([K, N], or [N, K] with nt) at
-// the few-hundred-row sizes of ALBERT and the GPT-2 prefill, the library's f32 kernels measured 1.3-1.5x faster
-// than the few-tile kernel; lk_hip_gemm_f32 routes those calls here (lkh::bltGemmF32) and falls back to its own
-// kernels when the library has no algorithm for a shape.
+// The hand-written MFMA kernels (gemm.hip, f16.hip) keep the forms the library cannot express: output scales,
+// activation plus residual, split-K partials for a consumer, the conv loaders, the fused SwiGLU without a
+// workspace. lk_hip_gemm_f32, lk_hip_f16_gemm and the one-tap convs call bltGemm and fall back to their own kernels
+// when the library has no algorithm for a shape. At the few-hundred-row sizes of ALBERT, the GPT-2 prefill and the
+// Qwen3 prefill the library's kernels measured 1.1-1.5x faster than the hand-written ones.
 //
 // Row-major C = A B is the column-major product C^T [N, M] = B^T [N, K] A^T [K, M]: the row-major buffers are passed
 // unchanged as the column-major operands (B first), and the per-column bias becomes hipBLASLt's per-row bias of D.
