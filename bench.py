@@ -33,18 +33,6 @@ GPT2_STEP_BYTES = 4 * (12 * (768 * 2304 + 768 * 768 + 2 * 768 * 3072 + 2304 + 76
 F32_MFMA_PEAK_TFLOPS = 157.3
 
 
-def mfma_probe():
-    """The bench-only MFMA-ceiling probe library (lokinfer_amd/bench/libmfma_probe.so, built by build())."""
-    from lokinfer_amd.build import PROBE_LIB
-
-    if not PROBE_LIB.exists():
-        raise RuntimeError(f"{PROBE_LIB} is not built: python -m lokinfer_amd.build")
-    lib = C.CDLL(str(PROBE_LIB))
-    lib.lk_hip_mfma_f32_probe.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
-    lib.lk_hip_mfma_f32_probe.restype = C.c_int
-    return lib
-
-
 def event_times(fn, n: int) -> list[float]:
     """Per-call milliseconds of fn() measured with events on the current stream."""
     s = torch.cuda.current_stream()
@@ -324,19 +312,6 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
         for _ in range(5):
             lk.ops.add_f32_gpu(p1, p2)
         torch.cuda.synchronize()
-    # the register-only f32 MFMA rate of this GPU under a chip-wide load (what the clock allows)
-    pit, pwg = 512, 1024
-    probe = mfma_probe()
-    probe_out = torch.empty(pwg * 256, device="cuda")
-
-    def run_probe():
-        rc = probe.lk_hip_mfma_f32_probe(C.c_void_p(probe_out.data_ptr()), pit, pwg,
-                                         C.c_void_p(torch.cuda.current_stream().cuda_stream))
-        assert rc == 0
-
-    run_probe()
-    probe_ms = statistics.median(event_times(run_probe, 5))
-    ceiling = pwg * 4 * pit * 8 * 4096 / (probe_ms * 1e-3) / 1e12
     a = W.alpha_of(k)
     flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c
     direct = 2.0 * l * c * c * k
@@ -344,8 +319,7 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
             "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
             "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops,
-            "conv_ms": conv_ms, "conv_direct_equiv_tflops": direct / (conv_ms * 1e-3) / 1e12,
-            "mfma_ceiling_tflops": ceiling}
+            "conv_ms": conv_ms, "conv_direct_equiv_tflops": direct / (conv_ms * 1e-3) / 1e12}
 
 
 def cpu_kokoro(sd, inputs, budget_s: float = 30.0) -> dict:
@@ -482,7 +456,6 @@ def main():
                    "global_batch": 1, "seq_len": tokens, "parallelism": "none"},
         "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": roof["kernel"], "roofline_avg_launch_ms": roof["avg_launch_ms"],
-        "roofline_mfma_ceiling_tflops": round(roof["mfma_ceiling_tflops"], 1),
         "roofline_conv_ms": roof["conv_ms"], "roofline_conv_direct_equiv_tflops": roof["conv_direct_equiv_tflops"],
         "forward_algorithmic_tflops": round(r["flops"] / (r["median_ms"] * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,

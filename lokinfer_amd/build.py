@@ -18,8 +18,6 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "liblokinfer_hip.so"
-PROBE_SRC = PKG / "bench" / "mfma_probe.hip"
-PROBE_LIB = PKG / "bench" / "libmfma_probe.so"  # bench-only measurement kernel, not part of the product library
 ARCH = "gfx950"
 
 
@@ -64,14 +62,6 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
-    # the bench's MFMA-ceiling probe: its own library
-    pobj = _compile(PROBE_SRC)
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    r = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(pobj)],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed (probe)\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
     return LIB
