@@ -61,10 +61,7 @@ const char* lk_device_error_message(int code);
 /* out[M, N] = (act(A[M, K] . B + bias) + res) * scale; nt: B given as B^T [N, K]; act 0 none, 1 relu, 2 gelu.
  * workspace (optional, may be NULL): with few output tiles and a long K, K is split across workgroups whose
  * partial tiles (split * M * N floats past the first 64 KiB) a second kernel sums; calls sharing a workspace
- * must be stream-ordered. With scale 1 (and no res when act != 0) the product runs as hipBLASLt's f32 GEMM (bias /
- * relu / gelu epilogues, res as its C operand, its workspace past the first 64 KiB); the first call per shape builds its
- * plan and, outside graph capture, times the library's candidate algorithms on that call's operands (it synchronizes
- * the stream once) */
+ * must be stream-ordered. Every form runs on this library's MFMA kernels; results depend only on the shape. */
 int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const float* res, float* out, int64_t m,
                     int64_t n, int64_t k, int nt, int act, float scale, void* workspace, int64_t workspace_bytes,
                     void* stream);
@@ -246,9 +243,8 @@ int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* 
  *      (lk_hip_f16_transpose); the reference fixes only the math and leaves the layout to the kernel. ---- */
 /* out f16[M, N] = x f16[M, K] @ W (+ bias f16[N]) (+ res f16[M, N]), or silu(x @ Wg) * (x @ Wu) with swiglu = 1
  * (W^T rows [gate | up], N' = 2N): gemm[_bias]_f16_gpu, gemm[_bias|_add|_swiglu]_opt_f16_gpu. K % 8 == 0, 16-byte
- * aligned x and W^T. M = 1 runs a GEMV; M > 1 runs as hipBLASLt's f16 GEMM (f32 accumulation; with swiglu its f32
- * [gate | up] goes to the workspace and one pass applies silu(gate) * up). workspace (optional): that plane, the
- * library's workspace, or split-K partials when the grid is small. */
+ * aligned x and W^T. M = 1 runs a GEMV; M > 1 the f16 MFMA tile kernels (f32 accumulation, the epilogue fused).
+ * workspace (optional): split-K partials when the grid is small. */
 int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void* res, void* out, int64_t m, int64_t n,
                     int64_t k, int swiglu, void* workspace, int64_t workspace_bytes, void* stream);
 int64_t lk_hip_f16_gemm_workspace_bytes(int64_t m, int64_t n, int swiglu);

@@ -1334,11 +1334,6 @@ int launched() { return hipGetLastError() == hipSuccess ? 0 : 2; }
 
 }  // namespace
 
-namespace lkh {
-bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, int act, bool f16, bool f32out, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
-}  // namespace lkh
-
 extern "C" {
 
 int lk_hip_f16_rms_lm_head(const void* x, const void* g, const void* table, float* out, int64_t t, int64_t d, int64_t v,
@@ -1367,24 +1362,8 @@ int lk_hip_f16_gemm(const void* x, const void* wt, const void* bias, const void*
     else launchGemvF16<EPI_PLAIN, false>(g, blocks, s);
     return launched();
   }
-  static const bool libOff = getenv("LK_BLASLT_OFF") != nullptr;  // A/B switch: hand-written kernels only
-  if (!swiglu && !libOff &&
-      lkh::bltGemm(x, wt, bias, res, out, m, n, k, true, 0, true, false, workspace,
-                   workspace ? static_cast<size_t>(workspace_bytes) : 0, s))
-    return launched();  // plain GEMM (bias, residual): the library's f16 GEMM with f32 accumulation
   GemmF16Params p{static_cast<const h16*>(x), static_cast<const h16*>(wt), static_cast<const h16*>(bias),
                   static_cast<const h16*>(res), static_cast<h16*>(out), nullptr, m, n, k, k, k, 1};
-  // SwiGLU: [gate | up] as the library's f32 accumulations into the workspace (one partial plane [M, 2N]), then the
-  // split-K reduction's epilogue with one plane, silu(gate) * up rounded once, as the fused kernels do
-  const int64_t dBytes = (m * 2 * n * 4 + 255) / 256 * 256;
-  if (swiglu && !libOff && workspace && workspace_bytes > dBytes &&
-      lkh::bltGemm(x, wt, nullptr, nullptr, workspace, m, 2 * n, k, true, 0, true, true,
-                   static_cast<char*>(workspace) + dBytes, static_cast<size_t>(workspace_bytes - dBytes), s)) {
-    p.part = static_cast<float*>(workspace);
-    const unsigned rb = static_cast<unsigned>(std::min<int64_t>((m * n + 255) / 256, 4096));
-    hipLaunchKernelGGL((gemmF16ReduceKernel<true>), dim3(rb), dim3(256), 0, s, p);
-    return launched();
-  }
   // the wide tile where it measured faster: SwiGLU at M >= 256 (Qwen3's 416-row gate/up: 57 -> 49 us) and any
   // M >= 1024 (4096^3: 471 -> 706 TFLOP/s); at M = 416 the plain shapes fill the chip better with 64-row tiles
   const bool wide = swiglu ? m >= 256 : m >= 1024;

@@ -877,10 +877,6 @@ static GemmParams baseParams() {
 
 }  // namespace lkh
 
-namespace lkh {
-bool bltGemm(const void* a, const void* b, const void* bias, const void* res, void* c, int64_t m, int64_t n, int64_t k,
-             bool nt, int act, bool f16, bool f32out, void* ws, size_t wsBytes, hipStream_t s);  // blaslt.cpp
-}  // namespace lkh
 
 // ---- typed C-ABI launchers ---------------------------------------------------------------------------------
 extern "C" {
@@ -906,14 +902,6 @@ int lk_hip_gemm_f32(const float* a, const float* b, const float* bias, const flo
   p.act = act;
   p.scale = scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  static const bool libOff = getenv("LK_BLASLT_OFF") != nullptr;  // A/B switch: hand-written kernels only
-  if (scale == 1.0f && (act == lkd::ACT_NONE || !res) && !libOff) {
-    // bias, then relu / gelu or a residual: the library's GEMM, its workspace past the 64 KiB counter area
-    void* ws = workspace && workspace_bytes > 65536 ? static_cast<char*>(workspace) + 65536 : nullptr;
-    const size_t wsb = ws ? static_cast<size_t>(workspace_bytes - 65536) : 0;
-    if (lkh::bltGemm(a, b, bias, res, out, m, n, k, nt != 0, act, false, false, ws, wsb, s))
-      return hipGetLastError() == hipSuccess ? 0 : 2;
-  }
   if (nt) lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NT>(p, s, workspace, workspace_bytes);
   else lkh::launchGemm<lkd::A_ROWMAJOR, lkd::B_NN>(p, s, workspace, workspace_bytes);
   return hipGetLastError() == hipSuccess ? 0 : 2;

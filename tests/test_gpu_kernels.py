@@ -316,10 +316,10 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(e1b, e1)
 
 
-def test_library_gemms_replay_in_graphs(gpu):
-    """The plain / bias / relu / gelu / residual f32 GEMMs and the f16 bias / residual GEMMs run as the vendor
-    library's GEMM; captured together in one graph at the models' shapes and at skinny large-K shapes (where a
-    library may split K), every replay, with eager library GEMMs between replays, equals the eager results."""
+def test_gemms_replay_in_graphs(gpu):
+    """The plain / bias / relu / gelu / residual f32 GEMMs and the f16 bias / residual GEMMs, captured together in
+    one graph at the models' shapes and at skinny large-K shapes (split K across workgroups, partials in the
+    workspace), equal the eager results on every replay, with eager GEMMs between the replays."""
     lk = gpu
     F = lk.ops.f16_gpu
     f32 = [(59, 2048, 768, "none", True), (487, 768, 2304, "none", False), (487, 768, 2048, "gelu", False),
@@ -348,7 +348,7 @@ def test_library_gemms_replay_in_graphs(gpu):
         torch.cuda.synchronize()
         for i, (g, e) in enumerate(zip(got, eager)):
             assert np.array_equal(g.view(np.uint8), e.view(np.uint8)), i
-        again = [t.numpy() for t in fn()]  # eager library work between replays
+        again = [t.numpy() for t in fn()]  # eager work between replays
         for i, (g, e) in enumerate(zip(again, eager)):
             assert np.array_equal(g.view(np.uint8), e.view(np.uint8)), i
 
