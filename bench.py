@@ -227,15 +227,18 @@ def kokoro_conv_flops(tokens: int, frames: int) -> float:
     return 2.0 * mac
 
 
-def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
+def bench_kokoro(tokens: int, steps: int, warmup: int, runtime: str = "compiled", sd=None) -> dict:
+    """Median ms of one Kokoro forward. runtime "compiled": lk.compile's C++ executable (one model arena, weights
+    uploaded once, the call replayed from its captured hipGraph with the independent branches on 4 lanes);
+    "capture": the torch stream capture of the same function."""
     import lokinfer_amd as lk
     from lokinfer_amd import kokoro_weights as KW
     from lokinfer_amd.kokoro import KokoroGpu
 
-    sd = KW.random_weights()
+    sd = KW.random_weights() if sd is None else sd
     ids, ref_s, dur, noise = KW.inputs(tokens)
     frames = int(dur.sum())
-    m = KokoroGpu(sd)
+    m = KokoroGpu(sd, runtime=runtime, lanes=4)
     args = [lk.from_numpy(a, device="gpu", copy=True) for a in (ids, ref_s, dur, noise)]
     for _ in range(max(warmup, 1)):
         m.forward(*args, inplace=True)
@@ -245,9 +248,10 @@ def bench_kokoro(tokens: int, steps: int, warmup: int) -> dict:
         m.forward(*args, inplace=True)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    per = event_times(lambda: m.model.run_inplace(*args), steps)
+    model = m.model if runtime == "capture" else m.compiled(args)
+    per = event_times(lambda: model.run_inplace(*args), steps)
     # A persistent kernel that stops on its bounded wait writes NaN; a timed run with such a launch is void.
-    outs = m.model.run_inplace(*args)
+    outs = model.run_inplace(*args)
     for o in (outs if isinstance(outs, tuple) else (outs,)):
         if not bool(torch.isfinite(o.t).all()):
             raise RuntimeError("kokoro forward produced non-finite outputs; timing discarded")
@@ -378,6 +382,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all", choices=["all", "kokoro487", "kokoro59", "gpt2", "qwen3", "decode_attn"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--runtime", default="compiled", choices=["compiled", "capture"],
+                    help="Kokoro: the lk.compile C++ executable (default) or the torch stream capture")
     ap.add_argument("--roofline-only", action="store_true",
                     help="launch only the roofline kernel (and the copy-calibration kernel), for rocprofv3 runs")
     a = ap.parse_args()
@@ -430,19 +436,21 @@ def main():
         print(json.dumps({"decode_attention_roofline": bench_decode_attention()}))
         return
     tokens = 59 if wl == "kokoro59" else 487
-    r = bench_kokoro(tokens, a.steps, a.warmup)
-    extra = {}
+    r = bench_kokoro(tokens, a.steps, a.warmup, runtime=a.runtime)
+    extra = {"runtime": a.runtime}
     if wl == "all":
-        r59 = bench_kokoro(59, a.steps, a.warmup)
+        other = "capture" if a.runtime == "compiled" else "compiled"
+        extra[f"kokoro{tokens}_{other}_ms"] = round(bench_kokoro(tokens, a.steps, a.warmup, other, r["sd"])["median_ms"], 3)
+        r59 = bench_kokoro(59, a.steps, a.warmup, a.runtime, r["sd"])
         g = bench_gpt2(max(a.steps, 20), a.warmup, cpu=not a.no_cpu)
-        extra = {"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
+        extra.update({"kokoro59_median_ms": round(r59["median_ms"], 3), "kokoro59_frames": r59["frames"],
                  "kokoro59_cpu_baseline": None if a.no_cpu else cpu_kokoro(r59["sd"], r59["inputs"], budget_s=10.0),
                  "gpt2_decode_median_ms": round(g["median_ms"], 4), "gpt2_decode_cpu_baseline": g.get("cpu_baseline"),
                  "gpt2_step_hbm_frac": round(GPT2_STEP_BYTES / (g["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                  "gpt2_lm_head_roofline": g["roofline"],
                  "gpt2_prefill512_ms": round(g["prefill512_ms"], 4),
                  "gpt2_prefill512_tflops": round(g["prefill512_tflops"], 2),
-                 "decode_attention_roofline": bench_decode_attention()}
+                 "decode_attention_roofline": bench_decode_attention()})
     roof = roofline_wino()
     cpu = None if a.no_cpu else cpu_kokoro(r["sd"], r["inputs"])
     line = {

@@ -45,7 +45,9 @@ const char* lk_last_error(void);
  * Kernels that find invalid data mid-graph (a position outside the cache, an id out of range, a persistent kernel
  * whose exchange timed out) write a neutral value and record the first error per GPU. lk_take_device_error waits
  * for the current device (hipDeviceSynchronize), returns the recorded code (0: none, -1: the read failed) with its
- * detail (the offending position / id / step), and clears the record. */
+ * detail (the offending position / id / step), and clears the record. The record belongs to the GPU, not to a call:
+ * an error is reported by whichever reader comes next (a synchronised executable call, a host read-back), which may
+ * be unrelated to the work that recorded it; creating an executable clears an unread record before its init. */
 enum {
   LK_DEVERR_EXCHANGE_TIMEOUT = 1,
   LK_DEVERR_POSITION = 2,

@@ -251,7 +251,7 @@ def _input_type(x, i: int, dynamic: bool):
 
 
 def compile(fn, inputs=None, *, dynamic: bool = False, input_types=None, pipeline=None,
-            graphs: bool = True, streams: int = 1) -> CompiledModel:
+            graphs: bool = True, lanes: int = 1) -> CompiledModel:
     """Traces `fn` on symbolic values and compiles it (reference lk.compile).
 
     inputs       example tensors / arrays / scalars (static shapes unless dynamic=True)
@@ -259,9 +259,9 @@ def compile(fn, inputs=None, *, dynamic: bool = False, input_types=None, pipelin
     input_types  explicit TensorType / BufferType (mutable) / ScalarType list, e.g. [TensorType(f32, [Sym("N"), 4])]
     pipeline     the compiler passes (default: dce, bufferize, plan-memory, hoist-init)
     graphs       capture statically shaped calls into hipGraphs
-    streams      the most HIP streams a statically shaped call may use (kernels are assigned from their dependencies);
-                 more than 1 is off by default: its first GPU run (the Kokoro forward) crashed the host process
-                 inside the call, and the cause is not yet found
+    lanes        the most concurrent lanes of a statically shaped call's graph (kernels are assigned to lanes from their
+                 data dependencies, and the captured graph's edges follow the lanes, so independent branches run
+                 concurrently on replay; every call still enqueues on torch's current stream)
     """
     from .rt import Executable, Model
 
@@ -279,17 +279,17 @@ def compile(fn, inputs=None, *, dynamic: bool = False, input_types=None, pipelin
         raise TypeError("the traced function must return traced values")
     text = g.to_text(outs)
     model = Model.parse(text).run_passes(pipeline if pipeline is not None else "pipeline")
-    exe = Executable(model, g.externals, graphs=graphs, streams=streams)
+    exe = Executable(model, g.externals, graphs=graphs, lanes=lanes)
     return CompiledModel(exe, model, text, input_types, single, g.externals)
 
 
-def load(path: str, graphs: bool = True, streams: int = 1) -> CompiledModel:
+def load(path: str, graphs: bool = True, lanes: int = 1) -> CompiledModel:
     """Loads a .lkm written by CompiledModel.save (or by the reference's writeModelFile): mmapped, constants
     uploaded once."""
     from .rt import Executable, Model
 
     model = Model.load(path)
-    exe = Executable(model, {}, graphs=graphs, streams=streams)
+    exe = Executable(model, {}, graphs=graphs, lanes=lanes)
     return CompiledModel(exe, model, model.text(), [], model.num_outputs == 1)
 
 

@@ -229,7 +229,7 @@ int lk_exe_run(lk_exe* e, int n_in, const lk_tensor* inputs, int max_out, lk_ten
 
 int lk_exe_stats(const lk_exe* e, uint64_t* model_bytes, uint64_t* call_bytes, int* graphs, int* streams) {
   if (!e) return fail(lkrt::Status::error("null executable"));
-  if (streams) *streams = e->e->streamsUsed();
+  if (streams) *streams = e->e->lanesUsed();
   if (model_bytes) *model_bytes = e->e->modelArenaBytes();
   if (call_bytes) *call_bytes = e->e->callArenaBytes();
   if (graphs) *graphs = e->e->graphsCaptured();

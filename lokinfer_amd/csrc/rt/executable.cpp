@@ -7,6 +7,8 @@
 #include <algorithm>
 #include <array>
 #include <climits>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "lokinfer_hip.h"
@@ -18,6 +20,7 @@ namespace {
 constexpr int64_t kUnbound = INT64_MIN;
 constexpr size_t kAlign = 256;
 constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+constexpr size_t kMaxInts = 256, kMaxFloats = 32;  // the registry's argument maxima (lk_run_kernel)
 
 size_t alignUp(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -46,11 +49,17 @@ struct Executable::Instr {
   std::vector<int64_t> ints;  // static ints; dynInts patch the symbolic ones per call
   std::vector<std::pair<uint32_t, Dim>> dynInts;
   std::vector<double> floats;
+  std::vector<double> floatBuf;  // floats, zero-padded to kMaxFloats
   mutable std::vector<void*> ptrBuf;
-  mutable std::vector<int64_t> intBuf;
-  int stream = 0;          // 0: the call's stream, k: side stream k
-  std::vector<int> waits;  // instructions on other streams this one waits for (their events)
-  int event = -1;          // recorded after this kernel when another stream waits for it
+  mutable std::vector<int64_t> intBuf;  // ints (symbolic ones patched per call), zero-padded to kMaxInts
+  int lane = 0;            // concurrency lane of a captured call (its workspace; kernels of a lane are ordered)
+  std::vector<int> waits;  // kernels of other lanes this one depends on (not already implied by its lane's order)
+};
+
+// One kernel instruction's nodes in a graph captured on one stream: a chain from `first` to `tail` (both null when
+// the kernel enqueued nothing); `before` is the capture's tail node before the kernel.
+struct Executable::Segment {
+  hipGraphNode_t before = nullptr, first = nullptr, tail = nullptr;
 };
 
 Executable::Memory::~Memory() {
@@ -63,8 +72,6 @@ Executable::~Executable() {
     if (g->graph) (void)hipGraphDestroy(g->graph);
   }
   if (captureStream_) (void)hipStreamDestroy(captureStream_);
-  for (hipStream_t h : side_) (void)hipStreamDestroy(h);
-  for (hipEvent_t e : events_) (void)hipEventDestroy(e);
   if (pinned_) (void)hipHostFree(pinned_);
 }
 
@@ -152,10 +159,16 @@ Status Executable::lower(const Region& r, std::vector<Instr>& out) {
           default: addDim(std::get<Dim>(a.value));
         }
       }
-      if (in.ints.size() > 256 || in.floats.size() > 32)
+      if (in.ints.size() > kMaxInts || in.floats.size() > kMaxFloats)
         return Status::error("kernel '" + op.name + "': too many int / float arguments");
       in.ptrBuf.resize(in.args.size());
+      // Runners index ints and floats by position: the arrays a call passes are zero-padded to the registry's
+      // maxima (as lk_run_kernel pads a caller's arrays), so a dim or attribute the op does not carry reads as 0,
+      // which every runner's shape checks reject, instead of reading past the array.
       in.intBuf = in.ints;
+      in.intBuf.resize(kMaxInts, 0);
+      in.floatBuf = in.floats;
+      in.floatBuf.resize(kMaxFloats, 0.0);
     } else if (op.kind == OpKind::MemPlan && r.args.empty() && &r == &model_->init) {
       return Status::error("mem.plan in init is not supported");
     }
@@ -253,16 +266,19 @@ Status Executable::bindInputs(const std::vector<TensorIn>& in, std::vector<int64
 }
 
 Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv,
-                             Bump& mem, hipStream_t s, std::vector<TensorOut>* outs) {
+                             Bump& mem, hipStream_t s, std::vector<TensorOut>* outs, std::vector<Segment>* segs) {
   const Model& m = *model_;
   const DimPool& dp = m.dims();
-  // streams: 0 is the call's; a side stream first waits for the call's work so far (fork) and the call's stream
-  // waits for every side stream at the end (join); events_[0] is the fork, events_[1 .. S-1] the joins
-  const bool multi = &code == &exec_ && numStreams_ > 1;
-  std::vector<uint8_t> forked(static_cast<size_t>(numStreams_), 0);
-  if (multi) LKRT_TRY(hipStatus(hipEventRecord(events_[0], s), "fork"));
-  auto streamOf = [&](const Instr& in) -> hipStream_t {
-    return in.stream == 0 || !multi ? s : side_[static_cast<size_t>(in.stream - 1)];
+  // A captured call records the graph nodes each kernel instruction enqueued (the capture runs on one stream, so
+  // they form a chain); the graph's edges are re-wired from the lanes afterwards (rewire).
+  auto captureTail = [&](hipGraphNode_t& tail) -> Status {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipGraphNode_t* deps = nullptr;
+    size_t nd = 0;
+    LKRT_TRY(hipStatus(hipStreamGetCaptureInfo_v2(s, &cs, nullptr, nullptr, &deps, &nd), "capture info"));
+    if (cs != hipStreamCaptureStatusActive || nd > 1) return Status::error("capture: not a single-stream capture");
+    tail = nd ? deps[0] : nullptr;
+    return Status();
   };
   auto eval = [&](Dim d, int64_t& v) -> bool {
     auto r = dp.eval(d, sv, kUnbound);
@@ -294,23 +310,36 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
         }
         for (const auto& [idx, d] : in.dynInts)
           if (!eval(d, in.intBuf[idx])) return Status::error("kernel '" + op.name + "': unbound symbol in its shapes");
-        lkh::KernelArgs a{in.ptrBuf.data(), nullptr, in.intBuf.data(), in.floats.data(), nullptr,
-                          static_cast<uint32_t>(in.ptrBuf.size()), static_cast<uint32_t>(in.intBuf.size()),
+        lkh::KernelArgs a{in.ptrBuf.data(), nullptr, in.intBuf.data(), in.floatBuf.data(), nullptr,
+                          static_cast<uint32_t>(in.ptrBuf.size()), static_cast<uint32_t>(in.ints.size()),
                           static_cast<uint32_t>(in.floats.size())};
-        hipStream_t ks = streamOf(in);
-        if (multi && in.stream > 0 && !forked[static_cast<size_t>(in.stream)]) {
-          LKRT_TRY(hipStatus(hipStreamWaitEvent(ks, events_[0], 0), "fork"));
-          forked[static_cast<size_t>(in.stream)] = 1;
-        }
-        if (multi)
-          for (int w : in.waits) LKRT_TRY(hipStatus(hipStreamWaitEvent(ks, events_[exec_[w].event], 0), "wait"));
+        Segment* seg = segs ? &(*segs)[static_cast<size_t>(&in - code.data())] : nullptr;
+        if (seg) LKRT_TRY(captureTail(seg->before));
         lkh::ExecCtx ctx;
-        ctx.stream = ks;
-        ctx.workspace = workspace_[multi ? static_cast<size_t>(in.stream) : 0];
+        ctx.stream = s;
+        ctx.workspace = workspace_[&code == &exec_ ? static_cast<size_t>(in.lane) : 0];
         ctx.workspaceBytes = workspaceBytes_;
         in.kernel->run(ctx, a);
         if (ctx.error) return Status::error("kernel '" + op.name + "': " + ctx.error);
-        if (multi && in.event >= 0) LKRT_TRY(hipStatus(hipEventRecord(events_[in.event], ks), "record"));
+        if (seg) {
+          LKRT_TRY(captureTail(seg->tail));
+          if (seg->tail == seg->before) {
+            seg->tail = nullptr;  // enqueued nothing
+          } else {  // walk the chain back to the kernel's first node
+            hipGraphNode_t n = seg->tail;
+            for (;;) {
+              size_t nd = 0;
+              LKRT_TRY(hipStatus(hipGraphNodeGetDependencies(n, nullptr, &nd), "graph node"));
+              if (nd > 1) return Status::error("capture: a kernel's nodes are not a chain");
+              hipGraphNode_t dep = nullptr;
+              if (nd) LKRT_TRY(hipStatus(hipGraphNodeGetDependencies(n, &dep, &nd), "graph node"));
+              if (dep == seg->before) break;
+              if (!dep) return Status::error("capture: a kernel's nodes do not follow the previous kernel's");
+              n = dep;
+            }
+            seg->first = n;
+          }
+        }
         break;
       }
       case OpKind::View: {
@@ -386,12 +415,6 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
       case OpKind::BufferFree:
         break;
       case OpKind::Return:
-        if (multi)
-          for (int k = 1; k < numStreams_; ++k)
-            if (forked[static_cast<size_t>(k)]) {
-              LKRT_TRY(hipStatus(hipEventRecord(events_[static_cast<size_t>(k)], side_[static_cast<size_t>(k - 1)]), "join"));
-              LKRT_TRY(hipStatus(hipStreamWaitEvent(s, events_[static_cast<size_t>(k)], 0), "join"));
-            }
         if (outs) {
           outs->clear();
           for (ValueId v : op.operands) {
@@ -442,24 +465,25 @@ Status Executable::callBytes(std::vector<int64_t> sv, size_t& bytes) const {
   return Status();
 }
 
-// Stream schedule of a statically shaped exec region, and the re-placement of its per-call temporaries.
+// Lane schedule of a statically shaped exec region, and the re-placement of its per-call temporaries.
 //
 // Dependencies are per memory root (a value, seen through views and syncs): a kernel depends on the last writer of
 // every root it reads or writes and, for the roots it writes, on their readers since that write. In program order,
-// a kernel continues the stream whose last kernel is its latest predecessor; if no predecessor ends a stream it
-// takes an unused stream, else the stream whose last kernel is oldest. A dependency on another stream becomes an
-// event wait unless the vector clock of the waiting stream already covers it; the vector clocks then give
-// happens-before between any two kernels.
+// a kernel continues the lane whose last kernel is its latest predecessor; if no predecessor ends a lane it takes
+// an unused lane, else the lane whose last kernel is oldest. Kernels of one lane are ordered (they share the lane's
+// workspace); a dependency on another lane is kept as a wait unless the vector clock of the waiting lane already
+// covers it; the vector clocks then give happens-before between any two kernels. The lanes become edges of the
+// call's captured graph (rewire), so concurrent branches run concurrently on replay without side streams.
 //
 // The temporaries plan-memory put in a static arena (hoisted to init, reaching exec as state) were placed for one
-// stream. They are placed again here, largest first at the lowest fitting offset, where two of them conflict unless
+// lane. They are placed again here, largest first at the lowest fitting offset, where two of them conflict unless
 // every kernel touching one happens before the first kernel touching the other: concurrent branches never share
 // bytes, and the schedule needs no extra edges.
-Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
+Status Executable::schedule(int maxLanes) {
   const Model& m = *model_;
   const Region& ex = m.exec;
   const size_t nv = m.numValues();
-  const int S = std::max(1, std::min(maxStreams, 8));
+  const int S = std::max(1, std::min(maxLanes, 8));
   relocOffset_.assign(nv, -1);
   skipAlloc_.assign(nv, 0);
 
@@ -477,14 +501,62 @@ Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
       for (const auto* vs : {&op.operands, &op.outs})
         for (ValueId v : *vs) arena[irootOf(v)] = 0;
   const Op& initRet = m.init.ops.back();
-  std::vector<uint8_t> reloc(nv, 0);
+  // Exec state can alias other exec state: init may return a view and a view of that view (a slice of a style-bank
+  // projection), which exec receives as two values. Each state value is resolved to its outermost state ancestor
+  // (`outer`, at byte offset `outerOff`): only those are re-placed, a nested one keeps its offset inside its
+  // ancestor, and in exec every access to it is an access to the ancestor.
+  std::vector<ValueId> iparent(nv, kNoValue);
+  std::vector<int64_t> ioff(nv, 0);
+  bool staticViews = true;
+  for (const Op& op : m.init.ops)
+    if ((op.kind == OpKind::View || op.kind == OpKind::Sync) && !op.results.empty()) {
+      iparent[op.results[0]] = op.operands[0];
+      if (op.kind == OpKind::View) {
+        if (!op.dims[0]->isConst()) staticViews = false;
+        ioff[op.results[0]] = op.dims[0]->value * static_cast<int64_t>(dtypeSize(m.typeOf(op.results[0])->dtype));
+      }
+    }
+  std::vector<ValueId> stateOfInit(nv, kNoValue);  // init value -> the first exec state value it becomes
   for (size_t i = 0; i < ex.state.size(); ++i)
-    if (arena[irootOf(initRet.operands[i])]) reloc[ex.state[i]] = 1;
+    if (stateOfInit[initRet.operands[i]] == kNoValue) stateOfInit[initRet.operands[i]] = ex.state[i];
+  std::vector<ValueId> outer(nv, kNoValue);
+  std::vector<int64_t> outerOff(nv, 0);
+  for (size_t i = 0; i < ex.state.size(); ++i) {
+    const ValueId sv = ex.state[i];
+    ValueId best = sv;
+    int64_t off = 0, acc = 0;
+    for (ValueId iv = initRet.operands[i]; iv != kNoValue; iv = iparent[iv]) {
+      const ValueId s = stateOfInit[iv];
+      if (s != kNoValue && s != sv) {
+        best = s;
+        off = acc;
+      }
+      acc += ioff[iv];
+    }
+    outer[sv] = best;
+    outerOff[sv] = off;
+  }
+  // a state value that is its own outermost ancestor is re-placed when it lives in a relocatable arena and every
+  // dim is static
+  bool relocOk = staticViews;
+  std::vector<uint8_t> reloc(nv, 0);
+  for (size_t i = 0; i < ex.state.size(); ++i) {
+    const ValueId sv = ex.state[i];
+    if (!arena[irootOf(initRet.operands[i])]) continue;
+    for (Dim d : m.typeOf(sv)->shape) relocOk = relocOk && d->isConst();
+    if (outer[sv] == sv) reloc[sv] = 1;
+  }
+  if (!relocOk) {  // symbolic temporaries: keep one lane and the compiler's placement
+    numLanes_ = 1;
+    return Status();
+  }
   for (const Op& op : m.init.ops)
     if (op.kind == OpKind::BufferAlloc && arena[op.results[0]]) skipAlloc_[op.results[0]] = 1;
 
   // dependencies between exec kernels
   std::vector<ValueId> root(nv, kNoValue);
+  for (ValueId sv : ex.state)
+    if (outer[sv] != sv) root[sv] = outer[sv];
   auto rootOf = [&](ValueId v) { return root[v] == kNoValue ? v : root[v]; };
   std::vector<int> lastWriter(nv, -1);
   std::vector<std::vector<int>> readers(nv);
@@ -532,17 +604,16 @@ Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
   // streams and vector clocks
   std::vector<std::array<int, 8>> vc(exec_.size());
   std::vector<int> pos(exec_.size(), 0), tail(static_cast<size_t>(S), -1), count(static_cast<size_t>(S), 0);
-  int nextEvent = S;  // events 0 .. S-1: fork and joins
   for (size_t j = 0; j < exec_.size(); ++j) {
     Instr& in = exec_[j];
     if (in.kind != OpKind::Kernel) continue;
     const std::vector<int>& P = preds[j];
     int best = -1;
     for (int p : P)
-      if (tail[static_cast<size_t>(exec_[p].stream)] == p && p > best) best = p;
+      if (tail[static_cast<size_t>(exec_[p].lane)] == p && p > best) best = p;
     int st = 0;
     if (best >= 0) {
-      st = exec_[best].stream;
+      st = exec_[best].lane;
     } else {
       int unused = -1, oldest = 0;
       for (int k = 0; k < S; ++k) {
@@ -557,23 +628,22 @@ Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
     std::array<int, 8> cur{};
     if (tail[static_cast<size_t>(st)] >= 0) cur = vc[static_cast<size_t>(tail[static_cast<size_t>(st)])];
     for (auto it = P.rbegin(); it != P.rend(); ++it) {  // latest first: its clock may cover the older ones
-      const int p = *it, sp = exec_[p].stream;
+      const int p = *it, sp = exec_[p].lane;
       if (sp == st || cur[static_cast<size_t>(sp)] >= pos[static_cast<size_t>(p)]) continue;
       in.waits.push_back(p);
-      if (exec_[p].event < 0) exec_[p].event = nextEvent++;
       for (int k = 0; k < 8; ++k) cur[static_cast<size_t>(k)] = std::max(cur[static_cast<size_t>(k)], vc[static_cast<size_t>(p)][static_cast<size_t>(k)]);
     }
-    in.stream = st;
+    in.lane = st;
     pos[j] = ++count[static_cast<size_t>(st)];
     cur[static_cast<size_t>(st)] = pos[j];
     vc[j] = cur;
     tail[static_cast<size_t>(st)] = static_cast<int>(j);
   }
-  numStreams_ = 1;
+  numLanes_ = 1;
   for (int k = 0; k < S; ++k)
-    if (count[static_cast<size_t>(k)] > 0) numStreams_ = std::max(numStreams_, k + 1);
+    if (count[static_cast<size_t>(k)] > 0) numLanes_ = std::max(numLanes_, k + 1);
   auto hb = [&](int a, int b) {  // kernel a happens before kernel b
-    return a == b || vc[static_cast<size_t>(b)][static_cast<size_t>(exec_[a].stream)] >= pos[static_cast<size_t>(a)];
+    return a == b || vc[static_cast<size_t>(b)][static_cast<size_t>(exec_[a].lane)] >= pos[static_cast<size_t>(a)];
   };
 
   // re-place the temporaries
@@ -624,12 +694,38 @@ Status Executable::schedule(int maxStreams, hipStream_t /*stream*/) {
                   np);
   }
   tempsBytes_ = total;
-  events_.assign(static_cast<size_t>(nextEvent), nullptr);
-  for (hipEvent_t& e : events_) LKRT_TRY(hipStatus(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate"));
-  for (int k = 1; k < numStreams_; ++k) {
-    hipStream_t h = nullptr;
-    LKRT_TRY(hipStatus(hipStreamCreateWithFlags(&h, hipStreamNonBlocking), "hipStreamCreate"));
-    side_.push_back(h);
+  for (ValueId sv : ex.state)
+    if (outer[sv] != sv && relocOffset_[outer[sv]] >= 0) relocOffset_[sv] = relocOffset_[outer[sv]] + outerOff[sv];
+  return Status();
+}
+
+// Turns a call captured on one stream (a chain of the kernels' node segments in program order) into the lanes'
+// graph: each kernel's first node depends on the tail of the previous kernel of its lane and on the tails of the
+// kernels it waits for, instead of on the kernel just before it. A kernel that enqueued nothing stands for its own
+// dependencies. Every node still completes before the graph does.
+Status Executable::rewire(hipGraph_t graph, const std::vector<Segment>& segs) const {
+  std::vector<std::vector<hipGraphNode_t>> eff(exec_.size());  // what depending on kernel j means
+  std::vector<int> laneLast(static_cast<size_t>(numLanes_), -1);
+  for (size_t j = 0; j < exec_.size(); ++j) {
+    const Instr& in = exec_[j];
+    if (in.kind != OpKind::Kernel) continue;
+    std::vector<hipGraphNode_t> deps;
+    auto add = [&](int p) {
+      if (p >= 0) deps.insert(deps.end(), eff[static_cast<size_t>(p)].begin(), eff[static_cast<size_t>(p)].end());
+    };
+    add(laneLast[static_cast<size_t>(in.lane)]);
+    for (int w : in.waits) add(w);
+    std::sort(deps.begin(), deps.end());
+    deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
+    laneLast[static_cast<size_t>(in.lane)] = static_cast<int>(j);
+    const Segment& sg = segs[j];
+    if (!sg.tail) {
+      eff[j] = deps;
+      continue;
+    }
+    eff[j] = {sg.tail};
+    if (sg.before) LKRT_TRY(hipStatus(hipGraphRemoveDependencies(graph, &sg.before, &sg.first, 1), "rewire"));
+    for (hipGraphNode_t d : deps) LKRT_TRY(hipStatus(hipGraphAddDependencies(graph, &d, &sg.first, 1), "rewire"));
   }
   return Status();
 }
@@ -657,8 +753,8 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
   bool planned = false;
   for (const Op& op : m.exec.ops)
     planned = planned || op.kind == OpKind::MemPlan || (op.kind == OpKind::BufferAlloc && op.flag("arena"));
-  if (!x->dynamic_ && !planned && maxStreams > 1)
-    if (Status s = x->schedule(maxStreams, stream); !s) return fail(s);
+  if (!x->dynamic_ && !planned && useGraphs && maxStreams > 1)
+    if (Status s = x->schedule(maxStreams); !s) return fail(s);
 
   // Model arena: every constant, init allocation, persistent buffer, then the workspace.
   const size_t nv = m.numValues();
@@ -736,14 +832,14 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
     }
   }
   const size_t wsOff = off;
-  off += kWorkspaceBytes * static_cast<size_t>(x->numStreams_);
+  off += kWorkspaceBytes * static_cast<size_t>(x->numLanes_);
   x->modelArena_ = std::make_unique<Memory>();
   x->modelArena_->n = off;
   if (Status s = hipStatus(hipMalloc(&x->modelArena_->p, off), "hipMalloc (model arena)"); !s) return fail(s);
   x->modelBytes_ = off;
   char* base = static_cast<char*>(x->modelArena_->p);
   if (Status s = hipStatus(hipMemsetAsync(base, 0, off, stream), "hipMemsetAsync"); !s) return fail(s);
-  for (int k = 0; k < x->numStreams_; ++k) x->workspace_.push_back(base + wsOff + kWorkspaceBytes * static_cast<size_t>(k));
+  for (int k = 0; k < x->numLanes_; ++k) x->workspace_.push_back(base + wsOff + kWorkspaceBytes * static_cast<size_t>(k));
   x->workspaceBytes_ = kWorkspaceBytes;
   x->fixed_.assign(nv, nullptr);
   for (ValueId v = 0; v < nv; ++v)
@@ -760,6 +856,10 @@ std::unique_ptr<Executable> Executable::create(std::shared_ptr<const Model> mode
   if (Status s = hipStatus(hipStreamCreateWithFlags(&x->captureStream_, hipStreamNonBlocking), "hipStreamCreate"); !s)
     return fail(s);
 
+  // The device error record is one per GPU, not per call: an error some earlier work recorded and nobody read is
+  // cleared here (after that work has finished), so that it is not reported as a failure of this init.
+  if (Status s = hipStatus(hipStreamSynchronize(stream), "init"); !s) return fail(s);
+  (void)deviceErrors();
   // init: model-lifetime results become the exec state
   std::vector<char*> slot(x->fixed_);
   std::vector<int64_t> sv(m.dims().numSymbols(), kUnbound);
@@ -856,10 +956,12 @@ Status Executable::run(const std::vector<TensorIn>& inputs, std::vector<TensorOu
         std::vector<char*> capSlot(slot);
         std::vector<int64_t> capSv(sv);
         std::vector<TensorOut> capOut;
+        std::vector<Segment> segs(numLanes_ > 1 ? exec_.size() : 0);
         LKRT_TRY(hipStatus(hipStreamBeginCapture(captureStream_, hipStreamCaptureModeThreadLocal), "capture"));
-        Status cs = interpret(exec_, capSlot, capSv, view, captureStream_, &capOut);
+        Status cs = interpret(exec_, capSlot, capSv, view, captureStream_, &capOut, numLanes_ > 1 ? &segs : nullptr);
         hipGraph_t graph = nullptr;
         const hipError_t ee = hipStreamEndCapture(captureStream_, &graph);
+        if (cs && ee == hipSuccess && numLanes_ > 1) cs = rewire(graph, segs);
         if (cs && ee == hipSuccess) {
           g->graph = graph;
           LKRT_TRY(hipStatus(hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate"));

@@ -9,11 +9,13 @@
 //    its first (eager) run is captured into a hipGraph that later calls replay after copying the inputs into the
 //    block's input buffers;
 //  - kernels are the registry's (lkh::findKernel), called with the reference's argument convention;
-//  - statically shaped exec regions run on up to kStreams HIP streams: kernels are assigned to streams from their
-//    data dependencies (a kernel continues the stream of its latest predecessor when it can, else takes an idle
-//    one), cross-stream dependencies become event waits, and the per-call temporaries the compiler placed in a
-//    static arena are re-placed so that two buffers share bytes only when every use of one happens before the
-//    other is written under that schedule;
+//  - a statically shaped exec region's captured graph can run its independent branches concurrently: kernels are
+//    assigned to up to 8 lanes from their data dependencies (a kernel continues the lane of its latest predecessor
+//    when it can, else takes an idle one), the call is captured on one stream and its graph's edges are re-wired
+//    from the lanes (each kernel after its lane's previous kernel and the kernels of other lanes it depends on),
+//    and the per-call temporaries the compiler placed in a static arena are re-placed so that two buffers share
+//    bytes only when every use of one happens before the other is written under that schedule. Every call still
+//    enqueues on the caller's one stream;
 //  - a kernel's ExecCtx::error becomes the call's Status, and so does a data error a kernel recorded on the device
 //    (read at the call's synchronisation, the reference's takeGpuError).
 #pragma once
@@ -64,10 +66,11 @@ class Executable {
   int graphsCaptured() const { return static_cast<int>(graphs_.size()); }
   // Address of init's i-th result (the exec state), in the model arena or an external's memory.
   const void* stateData(size_t i) const { return i < state_.size() ? state_[i] : nullptr; }
-  int streamsUsed() const { return numStreams_; }
+  int lanesUsed() const { return numLanes_; }
   std::string strategy() const;
 
   struct Instr;
+  struct Segment;
 
  private:
   Executable() = default;
@@ -94,11 +97,13 @@ class Executable {
   };
 
   Status lower(const Region& r, std::vector<Instr>& out);
-  // stream assignment + temporaries re-placement for a statically shaped exec region
-  Status schedule(int maxStreams, hipStream_t stream);
+  // lane assignment + temporaries re-placement for a statically shaped exec region
+  Status schedule(int maxLanes);
+  // the lanes as the edges of a graph captured on one stream
+  Status rewire(hipGraph_t graph, const std::vector<Segment>& segs) const;
   Status bindInputs(const std::vector<TensorIn>& in, std::vector<int64_t>& sv) const;
   Status interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv, Bump& mem,
-                   hipStream_t s, std::vector<TensorOut>* outs);
+                   hipStream_t s, std::vector<TensorOut>* outs, std::vector<Segment>* segs = nullptr);
   // bytes the exec region allocates for a binding (statically shaped calls only)
   Status callBytes(std::vector<int64_t> sv, size_t& bytes) const;
 
@@ -106,11 +111,9 @@ class Executable {
   std::vector<Instr> init_, exec_;
   std::unique_ptr<Memory> modelArena_;
   size_t modelBytes_ = 0;
-  std::vector<void*> workspace_;  // one per stream
+  std::vector<void*> workspace_;  // one per lane
   size_t workspaceBytes_ = 0;
-  int numStreams_ = 1;
-  std::vector<hipStream_t> side_;   // streams 1 .. numStreams_ - 1 (stream 0 is the caller's)
-  std::vector<hipEvent_t> events_;  // one per kernel another stream waits on, plus the call's fork / join events
+  int numLanes_ = 1;
   std::unique_ptr<Memory> temps_;   // re-placed per-call temporaries
   size_t tempsBytes_ = 0;
   std::vector<int64_t> relocOffset_;  // exec state value -> offset in temps_ (-1: not re-placed)

@@ -66,13 +66,15 @@ def _vec_pad(a: np.ndarray, n: int) -> np.ndarray:
 class KokoroGpu:
     """The Kokoro forward on the GPU. runtime="capture" replays a torch stream capture of the function with its
     concurrent side-stream branches; runtime="compiled" traces it into the runtime's IR (lk.compile) per (T, F)
-    signature and runs it from the C++ executable on one stream (save() writes that model as a .lkm). The conv
-    dispatch (Winograd or tap conv) depends on the lengths, so the traced model is specialized per signature."""
+    signature and runs it from the C++ executable (save() writes that model as a .lkm), its graph's independent
+    branches on up to `lanes` concurrent lanes. The conv dispatch (Winograd or tap conv) depends on the lengths,
+    so the traced model is specialized per signature."""
 
-    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, runtime: str = "capture"):
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, runtime: str = "capture", lanes: int = 4):
         if runtime not in ("capture", "compiled"):
             raise ValueError("runtime must be 'capture' or 'compiled'")
         self.runtime = runtime
+        self.lanes = lanes
         self._compiled: dict[tuple, object] = {}
         self.sd = sd
         self._g: dict[str, Tensor] = {}
@@ -396,7 +398,7 @@ class KokoroGpu:
         key = tuple(tuple(a.shape) for a in args)
         m = self._compiled.get(key)
         if m is None:
-            m = lk_compile(self._forward, inputs=list(args))
+            m = lk_compile(self._forward, inputs=list(args), lanes=self.lanes)
             self._compiled[key] = m
         return m
 

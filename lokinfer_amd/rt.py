@@ -208,13 +208,13 @@ class Executable:
     init run, calls replayed from captured hipGraphs for statically shaped calls. `externals` maps
     const.external names to lk.Tensors bound by reference (device) or uploaded (host)."""
 
-    def __init__(self, model: Model, externals: dict | None = None, graphs: bool = True, streams: int = 1):
+    def __init__(self, model: Model, externals: dict | None = None, graphs: bool = True, lanes: int = 1):
         L = _rt()
         externals = externals or {}
         self.model = model
         self._ext = dict(externals)  # keeps the bound tensors alive
         arrs, self._ts = _ext_arrays(externals)
-        flags = (1 if graphs else 0) | (max(1, min(int(streams), 8)) << 8)
+        flags = (1 if graphs else 0) | (max(1, min(int(lanes), 8)) << 8)
         self._h = L.lk_exe_create(model._h, *arrs, _stream(), flags)
         if not self._h:
             raise LokinferError(L.lk_last_error().decode())
@@ -255,16 +255,17 @@ class Executable:
         outs = (LkTensor * 16)()
         n_out = C.c_int(0)
         _check(L.lk_exe_run(self._h, len(inputs), arr, 16, outs, C.byref(n_out), _stream(), 1 if sync else 0))
-        return [_wrap_out(outs[k]) for k in range(n_out.value)]
+        return [_wrap_out(outs[k], self) for k in range(n_out.value)]
 
     def stats(self) -> dict:
         m, c, g, s = C.c_uint64(), C.c_uint64(), C.c_int(), C.c_int()
         _check(_rt().lk_exe_stats(self._h, C.byref(m), C.byref(c), C.byref(g), C.byref(s)))
-        return {"model_arena_bytes": m.value, "call_arena_bytes": c.value, "graphs": g.value, "streams": s.value}
+        return {"model_arena_bytes": m.value, "call_arena_bytes": c.value, "graphs": g.value, "lanes": s.value}
 
 
-def _wrap_out(o: LkTensor) -> Tensor:
-    """A torch tensor over executable-owned device memory (no copy)."""
+def _wrap_out(o: LkTensor, owner) -> Tensor:
+    """A torch tensor over executable-owned device memory (no copy). The tensor keeps `owner` (the executable)
+    alive, so its memory outlives every view; the values are overwritten by the executable's next call."""
     dt: DType = _BY_CODE[o.dtype]
     shape = [o.shape[j] for j in range(o.rank)]
     n = 1
@@ -273,7 +274,7 @@ def _wrap_out(o: LkTensor) -> Tensor:
     if n == 0:
         return Tensor(torch.empty(shape, dtype=dt.torch, device="cuda"))
     # wrap the raw device pointer through the CUDA array interface (torch-ROCm maps it to HIP)
-    holder = _DevPtr(o.data, shape, dt)
+    holder = _DevPtr(o.data, shape, dt, owner)
     return Tensor(torch.as_tensor(holder, device="cuda"))
 
 
@@ -282,6 +283,7 @@ class _DevPtr:
 
     _TYPESTR = {"f32": "<f4", "f16": "<f2", "i64": "<i8", "i32": "<i4", "u8": "|u1"}
 
-    def __init__(self, ptr: int, shape, dt: DType):
+    def __init__(self, ptr: int, shape, dt: DType, owner=None):
+        self.owner = owner
         self.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": self._TYPESTR[dt.name],
                                          "data": (ptr, False), "version": 3, "strides": None}

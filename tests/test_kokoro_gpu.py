@@ -92,22 +92,26 @@ def test_duration_mismatch_is_an_error(model):
         m.forward(ids, ref_s, dur + 1, noise)
 
 
-def test_compiled_runtime_equals_capture(model, tmp_path):
-    """The forward traced into the runtime's IR and run by the C++ executable (one stream, one arena) gives the
-    capture path's outputs bit for bit (the same kernels in a different interleaving); its .lkm loads and runs
-    to the same bits."""
+@pytest.mark.parametrize("lanes", [1, 4])
+def test_compiled_runtime_equals_capture(model, tmp_path, lanes):
+    """The forward traced into the runtime's IR and run by the C++ executable (one arena; its graph's branches on
+    1 or 4 concurrent lanes) gives the capture path's outputs bit for bit (the same kernels in a different
+    interleaving), on the eager first call and on every replay, with eager work between the replays; its .lkm
+    loads and runs to the same bits."""
     lk, KW, sd, m = model
     from lokinfer_amd.kokoro import KokoroGpu
 
     ids, ref_s, dur, noise = KW.inputs(59)
     want = [t.numpy() for t in m.forward(ids, ref_s, dur, noise)]
-    c = KokoroGpu(sd, runtime="compiled")
-    for _ in range(2):  # the first call runs eagerly in the call block, the second replays its hipGraph
+    c = KokoroGpu(sd, runtime="compiled", lanes=lanes)
+    for _ in range(4):  # the first call runs eagerly in the call block, the others replay its hipGraph
         got = [t.numpy() for t in c.forward(ids, ref_s, dur, noise)]
         for g, w in zip(got, want):
             assert np.array_equal(g, w)
+        m.forward(ids, ref_s, dur, noise)  # other work on the GPU between replays
     cm = next(iter(c._compiled.values()))
     assert cm.stats()["graphs"] == 1
+    assert (cm.stats()["lanes"] > 1) == (lanes > 1)
     path = tmp_path / "kokoro59.lkm"
     cm.save(path)
     loaded = lk.load(path)

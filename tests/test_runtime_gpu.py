@@ -162,6 +162,10 @@ def test_device_error_surfaces_at_a_synchronised_call(gpu):
     with pytest.raises(LokinferError, match="device error 2.*detail 16"):
         exe.run([q, G(lk, [cap], np.int64)], sync=True)
     exe.run([q, G(lk, [4], np.int64)], sync=True)  # the record was cleared
+    # the record is per GPU: an error left unread by earlier work is not blamed on a new executable's init
+    exe.run([q, G(lk, [cap], np.int64)], sync=False)
+    m2 = lk.compile(step, input_types=[lk.TensorType(lk.f32, [1, 3 * D]), lk.TensorType(lk.i64, [1])])
+    m2._exe.run([q, G(lk, [5], np.int64)], sync=True)
 
 
 # ---- bake-init (reference tests/unit/test_compiler.cpp:240-290, tests/python/test_call_api.py:195-220) ---------
