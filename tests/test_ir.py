@@ -117,3 +117,51 @@ def test_verifier_rejects(body, msg):
 def test_parse_errors_name_the_line():
     with pytest.raises(LokinferError, match="line 3"):
         Model.parse("model {\n  init {\n    bogus\n  }\n}\n")
+
+
+# ---- the reference's lit-test models (tests/golden/ir/lit, written by tests/golden/make_ir_lit_golden.py) ----------
+
+LIT = GOLD / "lit"
+LIT_CASES = sorted(p.stem for p in LIT.glob("*.lkir"))
+
+
+def test_lit_corpus_present():
+    assert len(LIT_CASES) >= 25
+
+
+@pytest.mark.parametrize("case", LIT_CASES)
+def test_lit_stage_matches_reference(case):
+    """The passes the reference's lit test runs (or none) give the reference library's text, or both reject."""
+    src = (LIT / f"{case}.lkir").read_text()
+    passes = (LIT / f"{case}.stage").read_text().strip()
+    want = (LIT / f"{case}.stage.txt").read_text()
+
+    def go():
+        m = Model.parse(src)
+        if passes != "-":
+            m.run_passes(passes)
+        return m.text()
+
+    if want == "rejected\n":
+        with pytest.raises(LokinferError):
+            go()
+    else:
+        assert go() == want
+
+
+@pytest.mark.parametrize("case", [c for c in LIT_CASES if (LIT / f"{c}.pipeline.txt").exists()])
+def test_lit_pipeline_and_lkm_match_reference(case, tmp_path):
+    src = (LIT / f"{case}.lkir").read_text()
+    m = Model.parse(src)
+    m.run_passes("pipeline")
+    assert m.text() == (LIT / f"{case}.pipeline.txt").read_text()
+    lkm = LIT / f"{case}.lkm"
+    if not lkm.exists():
+        return
+    for name, n in internal_constants(src):
+        m.set_constant(name, fixture_bytes(name, n))
+    gold = lkm.read_bytes()
+    assert m.to_bytes() == gold
+    back = Model.from_bytes(gold)
+    assert back.text() == (LIT / f"{case}.lkm.txt").read_text()
+    assert back.to_bytes() == gold
