@@ -165,3 +165,26 @@ def test_lit_pipeline_and_lkm_match_reference(case, tmp_path):
     back = Model.from_bytes(gold)
     assert back.text() == (LIT / f"{case}.lkm.txt").read_text()
     assert back.to_bytes() == gold
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_const_inline_half_rounding(dt):
+    """const.inline f16 / bf16 data rounds to nearest even like numpy's float16 / torch's bfloat16 casts, including
+    subnormals, exact ties, overflow to infinity and the largest finite values; printing gives the rounded value."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(400) * 10.0 ** rng.integers(-9, 6, 400),
+                        [0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -25,
+                         1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 3.0e38, 1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8]]).astype(np.float32)
+    text = ("model {\n init {\n return\n }\n exec() {\n %c = const.inline dense<["
+            + ", ".join(repr(float(v)) for v in x) + f"]> : tensor<{dt}[{len(x)}]>\n return %c\n }}\n}}\n")
+    printed = Model.parse(text).text()
+    # the text has 9 significant digits: enough to name a float32 (so every f16 / bf16 value) exactly
+    got = np.array([float(v) for v in re.search(r"dense<\[(.*?)\]>", printed).group(1).split(", ")], np.float32)
+    with np.errstate(over="ignore"):
+        if dt == "f16":
+            assert np.array_equal(got.astype(np.float16).view(np.uint16), x.astype(np.float16).view(np.uint16))
+        else:
+            b = lambda a: torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy()  # noqa: E731
+            assert np.array_equal(b(got), b(x))
