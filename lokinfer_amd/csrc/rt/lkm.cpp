@@ -1,9 +1,13 @@
-// .lkm v2 model files (the reference's binary format, lariaus/lokinfer include/lokinfer/ir/binary.h:1-45 and
-// docs/impl-notes/design-ir.md §8): a 64-byte header {"LKM\0", u32 version, u64 meta offset / size, u64 data
-// offset / size, 24 reserved bytes}, one metadata blob of LEB128 varints (zigzag for signed values), then the
-// constants' bytes, each 16 KiB-aligned within the data section. Metadata order: symbols, dims (operands first),
-// types, values, constants, then the init and exec regions. Dims and types are numbered in first-use order.
-// Reading maps the file and points every constant into the mapping (no copy).
+// .lkm v2 model files: the reference's binary format (lariaus/lokinfer include/lokinfer/ir/binary.h:1-45,
+// docs/impl-notes/design-ir.md §8). A 64-byte header {"LKM\0", u32 version, u64 meta offset / size, u64 data offset
+// / size, reserved}, one metadata blob of LEB128 varints (zigzag for signed values), then the constants' bytes, each
+// at a 16 KiB-aligned offset of the data section. Metadata order: symbols, dims (operands before the dims that use
+// them), types, values, constants, then the init and exec regions; dims and types are numbered in first-use order.
+//
+// The codec is table-driven: a model is first flattened into plain tables (rows of numbers and strings that index
+// each other), and ONE description of the table layout, `transfer`, is instantiated for a writing and a reading
+// stream, so the two directions cannot drift apart. Reading then builds the model from the tables, rebuilding dims
+// through the canonicalizing constructors and checking every cross-reference; constants point into the mapped file.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -20,231 +24,491 @@ namespace lkrt {
 
 namespace {
 
-constexpr uint32_t kLkmVersion = 2;  // version 2 added the exec mutable-argument flags (version 1 is still read)
-constexpr size_t kHeader = 64;
-constexpr uint64_t kDataAlign = 16384;
+constexpr uint32_t kVersion = 2;  // version 2 added the exec mutable-argument flags; version 1 files still load
+constexpr uint64_t kHeaderBytes = 64;
+constexpr uint64_t kConstAlign = 16384;
+constexpr uint64_t kMaxCount = 1ull << 26;  // no table of a corrupt file may ask for more rows than this
 
-uint64_t roundUp(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+uint64_t alignTo(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
-// ---- encoding --------------------------------------------------------------------------------------------------
-struct Sink {
-  std::vector<uint8_t> b;
-  void byte(uint8_t v) { b.push_back(v); }
-  void u(uint64_t v) {
-    for (; v >= 0x80; v >>= 7) b.push_back(static_cast<uint8_t>(v | 0x80));
-    b.push_back(static_cast<uint8_t>(v));
+// ---- tables ------------------------------------------------------------------------------------------------------
+struct DimRow {
+  uint8_t kind = 0;
+  int64_t value = 0;
+  std::vector<uint64_t> args;
+};
+struct TypeRow {
+  uint8_t kind = 0, dtype = 0;
+  std::vector<uint64_t> shape;
+};
+struct ValueRow {
+  uint64_t type = 0;
+  std::string name;
+};
+struct ConstRow {
+  std::string name;
+  uint64_t type = 0, offset = 0, size = 0;
+};
+struct AttrRow {
+  std::string name;
+  uint8_t tag = 0;  // the AttrValue alternative
+  uint8_t flag = 0;
+  int64_t i = 0;
+  double f = 0;
+  std::string s;
+  std::vector<int64_t> ints;
+  std::vector<double> floats;
+  uint64_t dim = 0;
+};
+struct OpRow {
+  uint8_t kind = 0;
+  std::string name;
+  std::vector<uint64_t> operands, outs, results;
+  std::vector<AttrRow> attrs;
+  std::vector<uint8_t> data;
+  std::vector<uint64_t> dims;
+  std::vector<int64_t> ints;
+  std::vector<uint64_t> symbols;
+};
+struct RegionRow {
+  std::vector<uint64_t> args;
+  std::vector<uint8_t> mutableFlags;
+  std::vector<uint64_t> state;
+  std::vector<OpRow> ops;
+};
+struct Tables {
+  std::vector<std::string> symbols;
+  std::vector<DimRow> dims;
+  std::vector<TypeRow> types;
+  std::vector<ValueRow> values;
+  std::vector<ConstRow> consts;
+  RegionRow regions[2];  // init, exec
+};
+
+// ---- streams -------------------------------------------------------------------------------------------------------
+// Both have the same primitives; `transfer` below uses nothing else.
+struct Put {
+  static constexpr bool kReading = false;
+  std::vector<uint8_t> out;
+  bool ok() const { return true; }
+  void var(uint64_t v) {
+    do {
+      out.push_back(static_cast<uint8_t>((v & 0x7f) | (v > 0x7f ? 0x80 : 0)));
+      v >>= 7;
+    } while (v);
   }
-  void s(int64_t v) { u((static_cast<uint64_t>(v) << 1) ^ static_cast<uint64_t>(v >> 63)); }
-  void f(double d) {
+  void u(uint64_t& v) { var(v); }
+  void i(int64_t& v) { var(static_cast<uint64_t>(v) << 1 ^ static_cast<uint64_t>(v >> 63)); }
+  void b(uint8_t& v) { out.push_back(v); }
+  void f(double& d) {
     uint64_t x;
     std::memcpy(&x, &d, 8);
-    for (int i = 0; i < 8; ++i) b.push_back(static_cast<uint8_t>(x >> (8 * i)));
+    for (int k = 0; k < 64; k += 8) out.push_back(static_cast<uint8_t>(x >> k));
   }
-  void str(const std::string& v) {
-    u(v.size());
-    b.insert(b.end(), v.begin(), v.end());
+  void s(std::string& v) {
+    var(v.size());
+    out.insert(out.end(), v.begin(), v.end());
   }
-  void ids(const std::vector<ValueId>& v) {
-    u(v.size());
-    for (ValueId x : v) u(x);
+  void bytes(std::vector<uint8_t>& v) {
+    var(v.size());
+    out.insert(out.end(), v.begin(), v.end());
+  }
+  template <class T, class F>
+  void list(std::vector<T>& v, F&& each) {
+    var(v.size());
+    for (T& x : v) each(x);
   }
 };
 
-class Encoder {
- public:
-  explicit Encoder(const Model& m) : m_(m) {}
+struct Get {
+  static constexpr bool kReading = true;
+  const uint8_t* p;
+  const uint8_t* end;
+  bool good = true;
+  bool ok() const { return good; }
+  void fail() {
+    good = false;
+    p = end;
+  }
+  uint64_t var() {
+    uint64_t v = 0;
+    for (int shift = 0; shift < 64 && p < end; shift += 7) {
+      const uint8_t c = *p++;
+      v |= static_cast<uint64_t>(c & 0x7f) << shift;
+      if (!(c & 0x80)) return v;
+    }
+    fail();
+    return 0;
+  }
+  void u(uint64_t& v) { v = var(); }
+  void i(int64_t& v) {
+    const uint64_t z = var();
+    v = static_cast<int64_t>(z >> 1) ^ -static_cast<int64_t>(z & 1);
+  }
+  void b(uint8_t& v) {
+    if (p < end) v = *p++;
+    else fail();
+  }
+  void f(double& d) {
+    uint64_t x = 0;
+    if (end - p < 8) return fail();
+    for (int k = 0; k < 8; ++k) x |= static_cast<uint64_t>(*p++) << (8 * k);
+    std::memcpy(&d, &x, 8);
+  }
+  void s(std::string& v) {
+    const uint64_t n = var();
+    if (static_cast<uint64_t>(end - p) < n) return fail();
+    v.assign(reinterpret_cast<const char*>(p), n);
+    p += n;
+  }
+  void bytes(std::vector<uint8_t>& v) {
+    const uint64_t n = var();
+    if (static_cast<uint64_t>(end - p) < n) return fail();
+    v.assign(p, p + n);
+    p += n;
+  }
+  template <class T, class F>
+  void list(std::vector<T>& v, F&& each) {
+    const uint64_t n = var();
+    if (n > kMaxCount) return fail();
+    v.clear();
+    for (uint64_t k = 0; k < n && good; ++k) each(v.emplace_back());
+  }
+};
 
-  // Appends the metadata to `out`; `offsets` receives each constant's offset within the data section.
-  Status run(Sink& out, std::vector<uint64_t>& offsets) {
-    for (ValueId v = 0; v < m_.numValues(); ++v) typeNo(m_.typeOf(v));
-    for (const Constant& c : m_.constants) typeNo(c.type);
+// ---- the layout (one description for both directions) ----------------------------------------------------------------
+template <class IO>
+void transferAttr(IO& io, AttrRow& a) {
+  io.s(a.name);
+  io.b(a.tag);
+  switch (a.tag) {
+    case 0: io.b(a.flag); break;
+    case 1: io.i(a.i); break;
+    case 2: io.f(a.f); break;
+    case 3: io.s(a.s); break;
+    case 4: io.list(a.ints, [&](int64_t& x) { io.i(x); }); break;
+    case 5: io.list(a.floats, [&](double& x) { io.f(x); }); break;
+    case 6: io.u(a.dim); break;
+    default:
+      if constexpr (IO::kReading) io.fail();
+  }
+}
+
+template <class IO>
+void transferRegion(IO& io, RegionRow& r, uint32_t version) {
+  auto ids = [&](std::vector<uint64_t>& v) { io.list(v, [&](uint64_t& x) { io.u(x); }); };
+  ids(r.args);
+  if (version >= 2) io.list(r.mutableFlags, [&](uint8_t& x) { io.b(x); });
+  ids(r.state);
+  io.list(r.ops, [&](OpRow& op) {
+    io.b(op.kind);
+    io.s(op.name);
+    ids(op.operands);
+    ids(op.outs);
+    ids(op.results);
+    io.list(op.attrs, [&](AttrRow& a) { transferAttr(io, a); });
+    io.bytes(op.data);
+    ids(op.dims);
+    io.list(op.ints, [&](int64_t& x) { io.i(x); });
+    ids(op.symbols);
+  });
+}
+
+template <class IO>
+void transfer(IO& io, Tables& t, uint32_t version) {
+  io.list(t.symbols, [&](std::string& s) { io.s(s); });
+  io.list(t.dims, [&](DimRow& d) {
+    io.b(d.kind);
+    io.i(d.value);
+    io.list(d.args, [&](uint64_t& x) { io.u(x); });
+  });
+  io.list(t.types, [&](TypeRow& ty) {
+    io.b(ty.kind);
+    io.b(ty.dtype);
+    io.list(ty.shape, [&](uint64_t& x) { io.u(x); });
+  });
+  io.list(t.values, [&](ValueRow& v) {
+    io.u(v.type);
+    io.s(v.name);
+  });
+  io.list(t.consts, [&](ConstRow& c) {
+    io.s(c.name);
+    io.u(c.type);
+    io.u(c.offset);
+    io.u(c.size);
+  });
+  for (RegionRow& r : t.regions) transferRegion(io, r, version);
+}
+
+// ---- model -> tables ---------------------------------------------------------------------------------------------------
+class Flattener {
+ public:
+  explicit Flattener(const Model& m) : m_(m) {}
+
+  Status run(Tables& t) {
+    // numbering: value types (with their dims), constant types, then the dims ops and dim attributes carry
+    for (ValueId v = 0; v < m_.numValues(); ++v) typeIndex(m_.typeOf(v));
+    for (const Constant& c : m_.constants) typeIndex(c.type);
     for (const Region* r : {&m_.init, &m_.exec})
       for (const Op& op : r->ops) {
-        for (Dim d : op.dims) dimNo(d);
+        for (Dim d : op.dims) dimIndex(d);
         for (const NamedAttr& a : op.attrs)
-          if (a.value.index() == 6) dimNo(std::get<Dim>(a.value));
+          if (const Dim* d = std::get_if<Dim>(&a.value)) dimIndex(*d);
       }
     const DimPool& dp = m_.dims();
-    out.u(dp.numSymbols());
-    for (size_t i = 0; i < dp.numSymbols(); ++i) out.str(dp.symbolName(static_cast<int64_t>(i)));
-    out.u(dimList_.size());
-    for (Dim d : dimList_) {
-      out.byte(static_cast<uint8_t>(d->kind));
-      out.s(d->value);
-      out.u(d->args.size());
-      for (Dim a : d->args) out.u(dimIdx_.at(a));
+    for (size_t k = 0; k < dp.numSymbols(); ++k) t.symbols.push_back(dp.symbolName(static_cast<int64_t>(k)));
+    for (Dim d : dimOrder_) {
+      DimRow row{static_cast<uint8_t>(d->kind), d->value, {}};
+      for (Dim a : d->args) row.args.push_back(dimNo_.at(a));
+      t.dims.push_back(std::move(row));
     }
-    out.u(typeList_.size());
-    for (Type t : typeList_) {
-      out.byte(static_cast<uint8_t>(t->kind));
-      out.byte(static_cast<uint8_t>(t->dtype));
-      out.u(t->shape.size());
-      for (Dim d : t->shape) out.u(dimIdx_.at(d));
+    for (Type ty : typeOrder_) {
+      TypeRow row{static_cast<uint8_t>(ty->kind), static_cast<uint8_t>(ty->dtype), {}};
+      for (Dim d : ty->shape) row.shape.push_back(dimNo_.at(d));
+      t.types.push_back(std::move(row));
     }
-    out.u(m_.numValues());
-    for (ValueId v = 0; v < m_.numValues(); ++v) {
-      out.u(typeIdx_.at(m_.typeOf(v)));
-      out.str(m_.nameOf(v));
-    }
-    uint64_t off = 0;
-    out.u(m_.constants.size());
+    for (ValueId v = 0; v < m_.numValues(); ++v) t.values.push_back({typeNo_.at(m_.typeOf(v)), m_.nameOf(v)});
+    uint64_t at = 0;
     for (const Constant& c : m_.constants) {
       if (!c.bytes && c.size) return Status::error("constant '" + c.name + "' has no data");
-      out.str(c.name);
-      out.u(typeIdx_.at(c.type));
-      out.u(off);
-      out.u(c.size);
-      offsets.push_back(off);
-      off = roundUp(off + c.size, kDataAlign);
+      t.consts.push_back({c.name, typeNo_.at(c.type), at, c.size});
+      at = alignTo(at + c.size, kConstAlign);
     }
-    for (const Region* r : {&m_.init, &m_.exec}) region(out, *r);
+    flattenRegion(m_.init, t.regions[0]);
+    flattenRegion(m_.exec, t.regions[1]);
     return Status();
   }
 
  private:
-  size_t dimNo(Dim d) {
-    auto it = dimIdx_.find(d);
-    if (it != dimIdx_.end()) return it->second;
-    for (Dim a : d->args) dimNo(a);
-    dimIdx_[d] = dimList_.size();
-    dimList_.push_back(d);
-    return dimList_.size() - 1;
+  uint64_t dimIndex(Dim d) {
+    if (auto it = dimNo_.find(d); it != dimNo_.end()) return it->second;
+    for (Dim a : d->args) dimIndex(a);
+    dimOrder_.push_back(d);
+    return dimNo_[d] = dimOrder_.size() - 1;
   }
-  size_t typeNo(Type t) {
-    auto it = typeIdx_.find(t);
-    if (it != typeIdx_.end()) return it->second;
-    for (Dim d : t->shape) dimNo(d);
-    typeIdx_[t] = typeList_.size();
-    typeList_.push_back(t);
-    return typeList_.size() - 1;
+  uint64_t typeIndex(Type t) {
+    if (auto it = typeNo_.find(t); it != typeNo_.end()) return it->second;
+    for (Dim d : t->shape) dimIndex(d);
+    typeOrder_.push_back(t);
+    return typeNo_[t] = typeOrder_.size() - 1;
   }
-  void region(Sink& out, const Region& r) {
-    out.ids(r.args);
-    out.u(r.mutableArgs.size());
-    for (uint8_t f : r.mutableArgs) out.byte(f);
-    out.ids(r.state);
-    out.u(r.ops.size());
+  static std::vector<uint64_t> widen(const std::vector<ValueId>& v) { return {v.begin(), v.end()}; }
+  void flattenRegion(const Region& r, RegionRow& out) {
+    out.args = widen(r.args);
+    out.mutableFlags = r.mutableArgs;
+    out.state = widen(r.state);
     for (const Op& op : r.ops) {
-      out.byte(static_cast<uint8_t>(op.kind));
-      out.str(op.name);
-      out.ids(op.operands);
-      out.ids(op.outs);
-      out.ids(op.results);
-      out.u(op.attrs.size());
+      OpRow row;
+      row.kind = static_cast<uint8_t>(op.kind);
+      row.name = op.name;
+      row.operands = widen(op.operands);
+      row.outs = widen(op.outs);
+      row.results = widen(op.results);
       for (const NamedAttr& a : op.attrs) {
-        out.str(a.name);
-        out.byte(static_cast<uint8_t>(a.value.index()));
-        switch (a.value.index()) {
-          case 0: out.byte(std::get<bool>(a.value) ? 1 : 0); break;
-          case 1: out.s(std::get<int64_t>(a.value)); break;
-          case 2: out.f(std::get<double>(a.value)); break;
-          case 3: out.str(std::get<std::string>(a.value)); break;
-          case 4:
-            out.u(std::get<Ints>(a.value).size());
-            for (int64_t x : std::get<Ints>(a.value)) out.s(x);
-            break;
-          case 5:
-            out.u(std::get<Floats>(a.value).size());
-            for (double x : std::get<Floats>(a.value)) out.f(x);
-            break;
-          default: out.u(dimIdx_.at(std::get<Dim>(a.value)));
-        }
+        AttrRow ar;
+        ar.name = a.name;
+        ar.tag = static_cast<uint8_t>(a.value.index());
+        std::visit(
+            [&](const auto& x) {
+              using T = std::decay_t<decltype(x)>;
+              if constexpr (std::is_same_v<T, bool>) ar.flag = x ? 1 : 0;
+              else if constexpr (std::is_same_v<T, int64_t>) ar.i = x;
+              else if constexpr (std::is_same_v<T, double>) ar.f = x;
+              else if constexpr (std::is_same_v<T, std::string>) ar.s = x;
+              else if constexpr (std::is_same_v<T, Ints>) ar.ints = x;
+              else if constexpr (std::is_same_v<T, Floats>) ar.floats = x;
+              else ar.dim = dimNo_.at(x);
+            },
+            a.value);
+        row.attrs.push_back(std::move(ar));
       }
-      out.u(op.data.size());
-      out.b.insert(out.b.end(), op.data.begin(), op.data.end());
-      out.u(op.dims.size());
-      for (Dim d : op.dims) out.u(dimIdx_.at(d));
-      out.u(op.ints.size());
-      for (int64_t x : op.ints) out.s(x);
-      out.u(op.symbols.size());
-      for (int64_t x : op.symbols) out.u(static_cast<uint64_t>(x));
+      row.data = op.data;
+      for (Dim d : op.dims) row.dims.push_back(dimNo_.at(d));
+      row.ints = op.ints;
+      for (int64_t s : op.symbols) row.symbols.push_back(static_cast<uint64_t>(s));
+      out.ops.push_back(std::move(row));
     }
   }
 
   const Model& m_;
-  std::vector<Dim> dimList_;
-  std::unordered_map<Dim, size_t> dimIdx_;
-  std::vector<Type> typeList_;
-  std::unordered_map<Type, size_t> typeIdx_;
+  std::vector<Dim> dimOrder_;
+  std::unordered_map<Dim, uint64_t> dimNo_;
+  std::vector<Type> typeOrder_;
+  std::unordered_map<Type, uint64_t> typeNo_;
 };
 
-void putU32(uint8_t* p, uint32_t v) {
-  for (int i = 0; i < 4; ++i) p[i] = static_cast<uint8_t>(v >> (8 * i));
-}
-void putU64(uint8_t* p, uint64_t v) {
-  for (int i = 0; i < 8; ++i) p[i] = static_cast<uint8_t>(v >> (8 * i));
-}
-uint32_t getU32(const uint8_t* p) {
-  uint32_t v = 0;
-  for (int i = 0; i < 4; ++i) v |= static_cast<uint32_t>(p[i]) << (8 * i);
-  return v;
-}
-uint64_t getU64(const uint8_t* p) {
-  uint64_t v = 0;
-  for (int i = 0; i < 8; ++i) v |= static_cast<uint64_t>(p[i]) << (8 * i);
-  return v;
-}
-
-// ---- decoding --------------------------------------------------------------------------------------------------
-class Source {
+// ---- tables -> model ---------------------------------------------------------------------------------------------------
+class Builder {
  public:
-  Source(const uint8_t* p, size_t n) : p_(p), end_(p + n) {}
-  bool ok() const { return ok_; }
-  uint8_t byte() {
-    if (p_ >= end_) return bad();
-    return *p_++;
-  }
-  uint64_t u() {
-    uint64_t v = 0;
-    for (int sh = 0; sh < 64; sh += 7) {
-      if (p_ >= end_) return bad();
-      const uint8_t b = *p_++;
-      v |= static_cast<uint64_t>(b & 0x7f) << sh;
-      if (!(b & 0x80)) return v;
+  Builder(const Tables& t, const uint8_t* data, uint64_t dataSize, std::shared_ptr<const void> owner)
+      : t_(t), data_(data), dataSize_(dataSize), owner_(std::move(owner)), m_(std::make_unique<Model>()) {}
+
+  std::unique_ptr<Model> run(std::string& err) {
+    if (!symbols() || !dims() || !types() || !values() || !constants() || !region(t_.regions[0], m_->init) ||
+        !region(t_.regions[1], m_->exec)) {
+      err = err_;
+      return nullptr;
     }
-    return bad();
-  }
-  int64_t s() {
-    const uint64_t x = u();
-    return static_cast<int64_t>(x >> 1) ^ -static_cast<int64_t>(x & 1);
-  }
-  double f() {
-    if (end_ - p_ < 8) return bad();
-    uint64_t x = getU64(p_);
-    p_ += 8;
-    double d;
-    std::memcpy(&d, &x, 8);
-    return d;
-  }
-  std::string str() {
-    const uint64_t n = u();
-    if (static_cast<uint64_t>(end_ - p_) < n) return bad(), std::string();
-    std::string v(reinterpret_cast<const char*>(p_), n);
-    p_ += n;
-    return v;
-  }
-  std::vector<uint8_t> bytes() {
-    const uint64_t n = u();
-    if (static_cast<uint64_t>(end_ - p_) < n) return bad(), std::vector<uint8_t>();
-    std::vector<uint8_t> v(p_, p_ + n);
-    p_ += n;
-    return v;
-  }
-  uint64_t count(uint64_t max = 1ull << 26) {  // bounded: a corrupt file must not allocate without limit
-    const uint64_t n = u();
-    return n > max ? bad() : n;
+    return std::move(m_);
   }
 
  private:
-  uint8_t bad() {
-    ok_ = false;
-    p_ = end_;
-    return 0;
+  bool bad(std::string msg) {
+    err_ = std::move(msg);
+    return false;
   }
-  const uint8_t* p_;
-  const uint8_t* end_;
-  bool ok_ = true;
+  bool symbols() {
+    for (const std::string& s : t_.symbols) sym_.push_back(m_->dims().sym(s)->value);
+    return true;
+  }
+  bool dims() {
+    DimPool& dp = m_->dims();
+    for (const DimRow& r : t_.dims) {
+      std::vector<Dim> a;
+      for (uint64_t j : r.args) {
+        if (j >= dim_.size()) return bad("bad dim reference");
+        a.push_back(dim_[j]);
+      }
+      if (r.kind > static_cast<uint8_t>(DimKind::Max)) return bad("bad dim kind");
+      const DimKind k = static_cast<DimKind>(r.kind);
+      Dim d = nullptr;  // stored nodes are canonical; rebuilding them through the constructors returns the same form
+      if (k == DimKind::Const) {
+        d = dp.constant(r.value);
+      } else if (k == DimKind::Sym) {
+        if (r.value < 0 || static_cast<uint64_t>(r.value) >= sym_.size()) return bad("bad symbol");
+        d = dp.sym(dp.symbolName(sym_[static_cast<size_t>(r.value)]));
+      } else if (k == DimKind::Add || k == DimKind::Mul) {
+        if (a.empty()) return bad("empty n-ary dim");
+        d = a[0];
+        for (size_t q = 1; q < a.size(); ++q) d = k == DimKind::Add ? dp.add(d, a[q]) : dp.mul(d, a[q]);
+      } else {
+        if (a.size() != 2) return bad("binary dim needs 2 operands");
+        const bool divides = k == DimKind::FloorDiv || k == DimKind::CeilDiv || k == DimKind::Mod;
+        if (divides && a[1]->isConst(0)) return bad("division by zero in a dim");
+        switch (k) {
+          case DimKind::FloorDiv: d = dp.floorDiv(a[0], a[1]); break;
+          case DimKind::CeilDiv: d = dp.ceilDiv(a[0], a[1]); break;
+          case DimKind::Mod: d = dp.mod(a[0], a[1]); break;
+          case DimKind::Min: d = dp.min(a[0], a[1]); break;
+          default: d = dp.max(a[0], a[1]);
+        }
+      }
+      dim_.push_back(d);
+    }
+    return true;
+  }
+  bool types() {
+    for (const TypeRow& r : t_.types) {
+      if (r.kind > static_cast<uint8_t>(TypeKind::Buffer) || r.dtype > static_cast<uint8_t>(DType::Bool) ||
+          r.shape.size() > 64)
+        return bad("bad type");
+      std::vector<Dim> shape;
+      for (uint64_t j : r.shape) {
+        if (j >= dim_.size()) return bad("bad dim reference in type");
+        shape.push_back(dim_[j]);
+      }
+      type_.push_back(m_->types().get(static_cast<TypeKind>(r.kind), static_cast<DType>(r.dtype), shape));
+    }
+    return true;
+  }
+  bool values() {
+    for (const ValueRow& v : t_.values) {
+      if (v.type >= type_.size()) return bad("bad type reference");
+      m_->newValue(type_[v.type], v.name);
+    }
+    return true;
+  }
+  bool constants() {
+    for (const ConstRow& r : t_.consts) {
+      if (r.type >= type_.size() || r.offset > dataSize_ || r.size > dataSize_ - r.offset)
+        return bad("bad constant '" + r.name + "'");
+      Constant c;
+      c.name = r.name;
+      c.type = type_[r.type];
+      c.size = r.size;
+      // a statically shaped constant's byte count must be its type's
+      uint64_t want = dtypeSize(c.type->dtype);
+      bool known = true;
+      for (Dim d : c.type->shape) {
+        known = known && d->isConst() && d->value >= 0 && (d->value == 0 || want <= UINT64_MAX / d->value);
+        if (known) want *= static_cast<uint64_t>(d->value);
+      }
+      if (known && want != c.size) return bad("constant '" + c.name + "' size doesn't match its type");
+      c.bytes = data_ + r.offset;
+      c.owner = owner_;
+      m_->addConstant(std::move(c));
+    }
+    return true;
+  }
+  bool ids(const std::vector<uint64_t>& in, std::vector<ValueId>& out) {
+    for (uint64_t v : in) {
+      if (v >= m_->numValues()) return bad("bad value reference");
+      out.push_back(static_cast<ValueId>(v));
+    }
+    return true;
+  }
+  bool region(const RegionRow& r, Region& reg) {
+    if (!ids(r.args, reg.args) || !ids(r.state, reg.state)) return false;
+    if (!r.mutableFlags.empty() && r.mutableFlags.size() != r.args.size()) return bad("bad mutable-arg flags");
+    for (uint8_t f : r.mutableFlags) reg.mutableArgs.push_back(f != 0);
+    for (const OpRow& o : r.ops) {
+      if (o.kind > static_cast<uint8_t>(OpKind::Return)) return bad("bad op kind");
+      Op op;
+      op.kind = static_cast<OpKind>(o.kind);
+      op.name = o.name;
+      if (!ids(o.operands, op.operands) || !ids(o.outs, op.outs) || !ids(o.results, op.results)) return false;
+      for (const AttrRow& a : o.attrs) {
+        NamedAttr na{a.name, false};
+        switch (a.tag) {
+          case 0: na.value = a.flag != 0; break;
+          case 1: na.value = a.i; break;
+          case 2: na.value = a.f; break;
+          case 3: na.value = a.s; break;
+          case 4: na.value = a.ints; break;
+          case 5: na.value = a.floats; break;
+          default:
+            if (a.dim >= dim_.size()) return bad("bad dim attribute");
+            na.value = dim_[a.dim];
+        }
+        op.attrs.push_back(std::move(na));
+      }
+      op.data = o.data;
+      for (uint64_t j : o.dims) {
+        if (j >= dim_.size()) return bad("bad dim reference in op");
+        op.dims.push_back(dim_[j]);
+      }
+      op.ints = o.ints;
+      for (uint64_t s : o.symbols) {
+        if (s >= sym_.size()) return bad("bad symbol reference");
+        op.symbols.push_back(sym_[s]);
+      }
+      reg.ops.push_back(std::move(op));
+    }
+    return true;
+  }
+
+  const Tables& t_;
+  const uint8_t* data_;
+  uint64_t dataSize_;
+  std::shared_ptr<const void> owner_;
+  std::unique_ptr<Model> m_;
+  std::vector<int64_t> sym_;
+  std::vector<Dim> dim_;
+  std::vector<Type> type_;
+  std::string err_;
 };
+
+// little-endian header fields
+template <class T>
+void storeLe(uint8_t* p, T v) {
+  for (size_t k = 0; k < sizeof(T); ++k) p[k] = static_cast<uint8_t>(v >> (8 * k));
+}
+template <class T>
+T loadLe(const uint8_t* p) {
+  T v = 0;
+  for (size_t k = 0; k < sizeof(T); ++k) v |= static_cast<T>(p[k]) << (8 * k);
+  return v;
+}
 
 }  // namespace
 
@@ -255,210 +519,58 @@ std::vector<uint8_t> writeLkm(const Model& m, Status& st) {
         st = Status::error("lkm: external constant '" + op.name + "' must be internalized before export");
         return {};
       }
-  Sink meta;
-  std::vector<uint64_t> offsets;
-  st = Encoder(m).run(meta, offsets);
-  if (!st) return {};
-  const uint64_t dataOffset = roundUp(kHeader + meta.b.size(), kDataAlign);
+  Tables t;
+  if (st = Flattener(m).run(t); !st) return {};
+  Put meta;
+  transfer(meta, t, kVersion);
+  const uint64_t dataOff = alignTo(kHeaderBytes + meta.out.size(), kConstAlign);
   uint64_t dataSize = 0;
-  for (size_t i = 0; i < offsets.size(); ++i) dataSize = std::max<uint64_t>(dataSize, offsets[i] + m.constants[i].size);
-  std::vector<uint8_t> out(dataOffset + dataSize, 0);
-  std::memcpy(out.data(), "LKM\0", 4);
-  putU32(out.data() + 4, kLkmVersion);
-  putU64(out.data() + 8, kHeader);
-  putU64(out.data() + 16, meta.b.size());
-  putU64(out.data() + 24, dataOffset);
-  putU64(out.data() + 32, dataSize);
-  std::memcpy(out.data() + kHeader, meta.b.data(), meta.b.size());
-  for (size_t i = 0; i < offsets.size(); ++i)
-    if (m.constants[i].size) std::memcpy(out.data() + dataOffset + offsets[i], m.constants[i].bytes, m.constants[i].size);
-  return out;
+  for (const ConstRow& c : t.consts) dataSize = std::max(dataSize, c.offset + c.size);
+  std::vector<uint8_t> file(dataOff + dataSize, 0);
+  std::memcpy(file.data(), "LKM\0", 4);
+  storeLe<uint32_t>(file.data() + 4, kVersion);
+  storeLe<uint64_t>(file.data() + 8, kHeaderBytes);
+  storeLe<uint64_t>(file.data() + 16, meta.out.size());
+  storeLe<uint64_t>(file.data() + 24, dataOff);
+  storeLe<uint64_t>(file.data() + 32, dataSize);
+  std::copy(meta.out.begin(), meta.out.end(), file.begin() + kHeaderBytes);
+  for (size_t k = 0; k < t.consts.size(); ++k)
+    if (t.consts[k].size) std::memcpy(file.data() + dataOff + t.consts[k].offset, m.constants[k].bytes, t.consts[k].size);
+  return file;
 }
 
 std::unique_ptr<Model> readLkm(const uint8_t* base, size_t size, std::shared_ptr<const void> owner, Status& st) {
-  auto fail = [&](const std::string& msg) {
+  auto fail = [&](const std::string& msg) -> std::unique_ptr<Model> {
     st = Status::error("lkm: " + msg);
     return nullptr;
   };
-  if (size < kHeader) return fail("file too small");
+  if (size < kHeaderBytes) return fail("file too small");
   if (std::memcmp(base, "LKM\0", 4) != 0) return fail("bad magic");
-  const uint32_t version = getU32(base + 4);
-  if (version != 1 && version != kLkmVersion) return fail("unsupported version " + std::to_string(version));
-  const uint64_t metaOff = getU64(base + 8), metaSize = getU64(base + 16);
-  const uint64_t dataOff = getU64(base + 24), dataSize = getU64(base + 32);
+  const uint32_t version = loadLe<uint32_t>(base + 4);
+  if (version != 1 && version != kVersion) return fail("unsupported version " + std::to_string(version));
+  const uint64_t metaOff = loadLe<uint64_t>(base + 8), metaSize = loadLe<uint64_t>(base + 16);
+  const uint64_t dataOff = loadLe<uint64_t>(base + 24), dataSize = loadLe<uint64_t>(base + 32);
   if (metaOff > size || metaSize > size - metaOff || dataOff > size || dataSize > size - dataOff)
     return fail("truncated file");
-  Source r(base + metaOff, metaSize);
-  auto m = std::make_unique<Model>();
-  DimPool& dp = m->dims();
-  std::vector<int64_t> symOf;  // file symbol index -> pool symbol id
-  for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) symOf.push_back(dp.sym(r.str())->value);
-  std::vector<Dim> dimOf;
-  for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) {
-    const uint8_t kindByte = r.byte();
-    const int64_t value = r.s();
-    std::vector<Dim> args;
-    for (uint64_t k = 0, na = r.count(); k < na && r.ok(); ++k) {
-      const uint64_t j = r.u();
-      if (j >= dimOf.size()) return fail("bad dim reference");
-      args.push_back(dimOf[j]);
-    }
-    if (!r.ok()) break;
-    if (kindByte > static_cast<uint8_t>(DimKind::Max)) return fail("bad dim kind");
-    const DimKind kind = static_cast<DimKind>(kindByte);
-    Dim d = nullptr;  // rebuilt through the canonicalizing constructors (stored nodes are canonical)
-    switch (kind) {
-      case DimKind::Const: d = dp.constant(value); break;
-      case DimKind::Sym:
-        if (value < 0 || static_cast<size_t>(value) >= symOf.size()) return fail("bad symbol");
-        d = dp.sym(dp.symbolName(symOf[static_cast<size_t>(value)]));
-        break;
-      case DimKind::Add:
-      case DimKind::Mul:
-        if (args.empty()) return fail("empty n-ary dim");
-        d = args[0];
-        for (size_t k = 1; k < args.size(); ++k) d = kind == DimKind::Add ? dp.add(d, args[k]) : dp.mul(d, args[k]);
-        break;
-      default:
-        if (args.size() != 2) return fail("binary dim needs 2 operands");
-        if ((kind == DimKind::FloorDiv || kind == DimKind::CeilDiv || kind == DimKind::Mod) && args[1]->isConst(0))
-          return fail("division by zero in a dim");
-        d = kind == DimKind::FloorDiv ? dp.floorDiv(args[0], args[1])
-            : kind == DimKind::CeilDiv ? dp.ceilDiv(args[0], args[1])
-            : kind == DimKind::Mod     ? dp.mod(args[0], args[1])
-            : kind == DimKind::Min     ? dp.min(args[0], args[1])
-                                       : dp.max(args[0], args[1]);
-    }
-    dimOf.push_back(d);
-  }
-  std::vector<Type> typeOf;
-  for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) {
-    const uint8_t kb = r.byte(), db = r.byte();
-    if (kb > static_cast<uint8_t>(TypeKind::Buffer) || db > static_cast<uint8_t>(DType::Bool)) return fail("bad type");
-    std::vector<Dim> shape;
-    for (uint64_t k = 0, rank = r.count(64); k < rank && r.ok(); ++k) {
-      const uint64_t j = r.u();
-      if (j >= dimOf.size()) return fail("bad dim reference in type");
-      shape.push_back(dimOf[j]);
-    }
-    typeOf.push_back(m->types().get(static_cast<TypeKind>(kb), static_cast<DType>(db), shape));
-  }
-  for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) {
-    const uint64_t t = r.u();
-    std::string name = r.str();
-    if (t >= typeOf.size()) return fail("bad type reference");
-    m->newValue(typeOf[t], std::move(name));
-  }
-  for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) {
-    Constant c;
-    c.name = r.str();
-    const uint64_t t = r.u(), off = r.u();
-    c.size = r.u();
-    if (!r.ok()) break;
-    if (t >= typeOf.size() || off > dataSize || c.size > dataSize - off) return fail("bad constant '" + c.name + "'");
-    c.type = typeOf[t];
-    uint64_t bytes = dtypeSize(c.type->dtype);
-    bool known = true;
-    for (Dim d : c.type->shape) {
-      if (!d->isConst() || d->value < 0 || (d->value && bytes > UINT64_MAX / static_cast<uint64_t>(d->value))) {
-        known = false;
-        break;
-      }
-      bytes *= static_cast<uint64_t>(d->value);
-    }
-    if (known && bytes != c.size) return fail("constant '" + c.name + "' size doesn't match its type");
-    c.bytes = base + dataOff + off;
-    c.owner = owner;
-    m->addConstant(std::move(c));
-  }
-  auto ids = [&](std::vector<ValueId>& v) {
-    for (uint64_t k = 0, n = r.count(); k < n && r.ok(); ++k) v.push_back(static_cast<ValueId>(r.u()));
-  };
-  for (Region* reg : {&m->init, &m->exec}) {
-    ids(reg->args);
-    if (version >= 2) {
-      const uint64_t n = r.count();
-      if (n != 0 && n != reg->args.size()) return fail("bad mutable-arg flags");
-      for (uint64_t k = 0; k < n && r.ok(); ++k) reg->mutableArgs.push_back(r.byte() != 0);
-    }
-    ids(reg->state);
-    for (uint64_t i = 0, n = r.count(); i < n && r.ok(); ++i) {
-      Op op;
-      const uint8_t kb = r.byte();
-      if (kb > static_cast<uint8_t>(OpKind::Return)) return fail("bad op kind");
-      op.kind = static_cast<OpKind>(kb);
-      op.name = r.str();
-      ids(op.operands);
-      ids(op.outs);
-      ids(op.results);
-      for (uint64_t k = 0, na = r.count(); k < na && r.ok(); ++k) {
-        NamedAttr a;
-        a.name = r.str();
-        switch (r.byte()) {
-          case 0: a.value = r.byte() != 0; break;
-          case 1: a.value = r.s(); break;
-          case 2: a.value = r.f(); break;
-          case 3: a.value = r.str(); break;
-          case 4: {
-            Ints v;
-            for (uint64_t j = 0, nv = r.count(); j < nv && r.ok(); ++j) v.push_back(r.s());
-            a.value = std::move(v);
-            break;
-          }
-          case 5: {
-            Floats v;
-            for (uint64_t j = 0, nv = r.count(); j < nv && r.ok(); ++j) v.push_back(r.f());
-            a.value = std::move(v);
-            break;
-          }
-          case 6: {
-            const uint64_t j = r.u();
-            if (j >= dimOf.size()) return fail("bad dim attribute");
-            a.value = dimOf[j];
-            break;
-          }
-          default:
-            if (r.ok()) return fail("bad attribute tag");
-        }
-        op.attrs.push_back(std::move(a));
-      }
-      op.data = r.bytes();
-      for (uint64_t k = 0, nd = r.count(); k < nd && r.ok(); ++k) {
-        const uint64_t j = r.u();
-        if (j >= dimOf.size()) return fail("bad dim reference in op");
-        op.dims.push_back(dimOf[j]);
-      }
-      for (uint64_t k = 0, ni = r.count(); k < ni && r.ok(); ++k) op.ints.push_back(r.s());
-      for (uint64_t k = 0, ns = r.count(); k < ns && r.ok(); ++k) {
-        const uint64_t s = r.u();
-        if (s >= symOf.size()) return fail("bad symbol reference");
-        op.symbols.push_back(symOf[s]);
-      }
-      reg->ops.push_back(std::move(op));
-    }
-  }
-  if (!r.ok()) return fail("corrupt metadata");
-  auto badIds = [&](const std::vector<ValueId>& vs) {
-    return std::any_of(vs.begin(), vs.end(), [&](ValueId v) { return v >= m->numValues(); });
-  };
-  for (const Region* reg : {&m->init, &m->exec}) {
-    if (badIds(reg->args) || badIds(reg->state)) return fail("bad value reference");
-    for (const Op& op : reg->ops)
-      if (badIds(op.operands) || badIds(op.outs) || badIds(op.results)) return fail("bad value reference");
-  }
+  Tables t;
+  Get in{base + metaOff, base + metaOff + metaSize};
+  transfer(in, t, version);
+  if (!in.ok()) return fail("corrupt metadata");
+  std::string err;
+  auto m = Builder(t, base + dataOff, dataSize, std::move(owner)).run(err);
+  if (!m) return fail(err);
   st = Status();
   return m;
 }
 
 Status writeLkmFile(const Model& m, const std::string& path) {
   Status st;
-  std::vector<uint8_t> bytes = writeLkm(m, st);
+  const std::vector<uint8_t> bytes = writeLkm(m, st);
   if (!st) return st;
   std::FILE* f = std::fopen(path.c_str(), "wb");
   if (!f) return Status::error("cannot open " + path + " for writing");
-  const size_t n = std::fwrite(bytes.data(), 1, bytes.size(), f);
-  const bool closed = std::fclose(f) == 0;
-  if (n != bytes.size() || !closed) return Status::error("failed writing " + path);
+  const bool wrote = std::fwrite(bytes.data(), 1, bytes.size(), f) == bytes.size();
+  if (std::fclose(f) != 0 || !wrote) return Status::error("failed writing " + path);
   return Status();
 }
 
@@ -468,21 +580,22 @@ std::unique_ptr<Model> readLkmFile(const std::string& path, Status& st) {
     st = Status::error("cannot open " + path);
     return nullptr;
   }
-  struct stat sb;
-  if (::fstat(fd, &sb) != 0 || sb.st_size <= 0) {
+  struct stat info {};
+  const bool statOk = ::fstat(fd, &info) == 0;
+  if (!statOk || info.st_size <= 0) {
     ::close(fd);
-    st = Status::error(sb.st_size <= 0 ? "lkm: file too small" : "cannot stat " + path);
+    st = Status::error(statOk ? "lkm: file too small" : "cannot stat " + path);
     return nullptr;
   }
-  const size_t size = static_cast<size_t>(sb.st_size);
-  void* p = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+  const size_t size = static_cast<size_t>(info.st_size);
+  void* map = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
   ::close(fd);
-  if (p == MAP_FAILED) {
+  if (map == MAP_FAILED) {
     st = Status::error("cannot mmap " + path);
     return nullptr;
   }
-  std::shared_ptr<const void> owner(p, [size](const void* q) { ::munmap(const_cast<void*>(q), size); });
-  return readLkm(static_cast<const uint8_t*>(p), size, owner, st);
+  std::shared_ptr<const void> owner(map, [size](const void* q) { ::munmap(const_cast<void*>(q), size); });
+  return readLkm(static_cast<const uint8_t*>(map), size, owner, st);
 }
 
 }  // namespace lkrt
