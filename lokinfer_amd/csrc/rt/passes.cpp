@@ -1,7 +1,6 @@
-// Compiler passes over the runtime IR: dce, bufferize, plan-memory, hoist-init (the reference's default pipeline,
-// in that order) and internalize. Their contracts are the reference's (lariaus/lokinfer src/compiler/*.cpp,
-// docs/impl-notes/design-compiler-passes.md), so a model compiled here prints and saves as the reference's
-// compiler would write it:
+// Compiler passes over the runtime IR: dce, bufferize, plan-memory, hoist-init (the default pipeline, in that order)
+// and internalize. The contracts are the reference's (lariaus/lokinfer docs/impl-notes/design-compiler-passes.md),
+// so a model compiled here prints and saves as the reference's compiler writes it:
 //   dce          drops ops whose results nothing live uses (kept: return, dim.read, inout / result-less kernels)
 //   bufferize    tensor values become buffers: each kernel result gets a buffer.alloc before the kernel and moves
 //                to `outs` (or reuses a dying operand named by `inplace = [out, in, ...]`); a buffer.free follows
@@ -13,6 +12,11 @@
 //                an arena with the others
 //   hoist-init   moves what does not depend on exec inputs (constants, static allocs, kernels over constants) into
 //                init; the values exec still uses become state
+//
+// Structure: the passes share a few analyses over a region's op list (value origins through views and syncs, last
+// touch per origin, device touches, the init-able subset as a greatest fixpoint), and none edits its op list in
+// place: each fills an EditList (ops to insert before / after an op, ops to drop, a prologue) that one routine
+// applies.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -25,485 +29,521 @@ namespace lkrt {
 
 namespace {
 
-constexpr size_t kNone = ~size_t(0);
+constexpr size_t kNever = ~size_t(0);
 constexpr int64_t kArenaAlign = 256;
 
-bool staticType(Type t) {
-  return std::all_of(t->shape.begin(), t->shape.end(), [](Dim d) { return d->isConst(); });
+bool shapeIsStatic(Type t) {
+  for (Dim d : t->shape)
+    if (!d->isConst()) return false;
+  return true;
+}
+bool isCopyOf(const Op& op) { return (op.kind == OpKind::View || op.kind == OpKind::Sync) && !op.results.empty(); }
+
+// ---- analyses ------------------------------------------------------------------------------------------------------
+
+// origin[v]: the value whose memory v is (through views and syncs); itself for everything else
+std::vector<ValueId> originsOf(const std::vector<Op>& ops, size_t nv) {
+  std::vector<ValueId> o(nv);
+  std::iota(o.begin(), o.end(), ValueId{0});
+  for (const Op& op : ops)
+    if (isCopyOf(op)) o[op.results[0]] = o[op.operands[0]];
+  return o;
 }
 
-// view / sync result -> the value whose memory it is
-struct Roots {
-  std::vector<ValueId> up;
-  explicit Roots(size_t n) : up(n, kNoValue) {}
-  ValueId of(ValueId v) const { return up[v] == kNoValue ? v : up[v]; }
-  void scan(const std::vector<Op>& ops) {
-    for (const Op& op : ops)
-      if ((op.kind == OpKind::View || op.kind == OpKind::Sync) && !op.results.empty())
-        up[op.results[0]] = of(op.operands[0]);
-  }
+// calls f(value) for every operand and out of op
+template <class F>
+void forTouched(const Op& op, F&& f) {
+  for (ValueId v : op.operands) f(v);
+  for (ValueId v : op.outs) f(v);
+}
+
+// last op index touching each origin (kNever: untouched)
+std::vector<size_t> lastTouchOf(const std::vector<Op>& ops, const std::vector<ValueId>& origin) {
+  std::vector<size_t> last(origin.size(), kNever);
+  for (size_t i = 0; i < ops.size(); ++i) forTouched(ops[i], [&](ValueId v) { last[origin[v]] = i; });
+  return last;
+}
+
+// The part of a buffer-form region that can run once, in init (shared by plan-memory and hoist-init):
+//  - memory: constants, static non-output allocs, constant-offset static views of that memory;
+//  - kernels: the greatest set of candidates (not `nohoist`, with outs, static results and dim attrs, every out
+//    init-able memory) in which each member reads only constant contents (a constant, or init-able memory whose
+//    every writer is a member) and writes only memory whose every writer is a member.
+struct InitPart {
+  std::vector<uint8_t> op;           // per op index
+  std::vector<uint8_t> value;        // per value: available in init
+  std::vector<uint8_t> initWritten;  // per origin: written by init kernels only
 };
 
-// Which ops of a buffer-form region can run once, in init:
-//  - memory: constants, static non-output allocs, constant-offset static views of those;
-//  - kernels (fixpoint): not `nohoist`, with outs, static results and dim attrs, every operand's contents constant
-//    (a constant, or a buffer all of whose writers are hoisted) and every out hoistable memory no per-call kernel
-//    writes.
-struct Hoist {
-  std::vector<uint8_t> op, value, initWritten;
-};
-
-Hoist hoistable(const Model& m, const Region& r) {
-  const size_t nv = m.numValues(), no = r.ops.size();
-  Roots roots(nv);
-  roots.scan(r.ops);
-  Hoist h{std::vector<uint8_t>(no, 0), std::vector<uint8_t>(nv, 0), std::vector<uint8_t>(nv, 0)};
-  std::vector<uint8_t> isConst(nv, 0);
-  for (size_t i = 0; i < no; ++i) {
+InitPart initPart(const Model& m, const Region& r) {
+  const size_t nv = m.numValues(), n = r.ops.size();
+  const std::vector<ValueId> origin = originsOf(r.ops, nv);
+  InitPart part{std::vector<uint8_t>(n, 0), std::vector<uint8_t>(nv, 0), std::vector<uint8_t>(nv, 0)};
+  std::vector<uint8_t> constant(nv, 0);
+  for (size_t i = 0; i < n; ++i) {
     const Op& op = r.ops[i];
-    bool ok = false;
-    if (op.kind == OpKind::ConstInline || op.kind == OpKind::ConstInternal || op.kind == OpKind::ConstExternal) {
-      ok = true;
-      isConst[op.results[0]] = 1;
-    } else if (op.kind == OpKind::BufferAlloc) {
-      ok = !op.flag("output") && staticType(m.typeOf(op.results[0]));
-    } else if (op.kind == OpKind::View) {
-      ok = h.value[op.operands[0]] && op.dims[0]->isConst() && staticType(m.typeOf(op.results[0]));
+    bool movable = false;
+    switch (op.kind) {
+      case OpKind::ConstInline:
+      case OpKind::ConstInternal:
+      case OpKind::ConstExternal:
+        movable = true;
+        constant[op.results[0]] = 1;
+        break;
+      case OpKind::BufferAlloc: movable = !op.flag("output") && shapeIsStatic(m.typeOf(op.results[0])); break;
+      case OpKind::View:
+        movable = part.value[op.operands[0]] && op.dims[0]->isConst() && shapeIsStatic(m.typeOf(op.results[0]));
+        break;
+      default: break;
     }
-    h.op[i] = ok;
-    if (ok) h.value[op.results[0]] = 1;
+    if (movable) {
+      part.op[i] = 1;
+      part.value[op.results[0]] = 1;
+    }
   }
-  std::vector<uint8_t> cand(no, 0);
-  for (size_t i = 0; i < no; ++i) {
+  // candidate kernels
+  std::vector<uint8_t> member(n, 0);
+  for (size_t i = 0; i < n; ++i) {
     const Op& op = r.ops[i];
-    if (op.kind != OpKind::Kernel) continue;
-    bool ok = !op.flag("nohoist") && !op.outs.empty();
+    if (op.kind != OpKind::Kernel || op.flag("nohoist") || op.outs.empty()) continue;
+    bool ok = true;
     for (const NamedAttr& a : op.attrs)
-      if (a.value.index() == 6) ok = ok && std::get<Dim>(a.value)->isConst();
-    for (ValueId v : op.results) ok = ok && staticType(m.typeOf(v));
-    for (ValueId v : op.outs) ok = ok && h.value[v];
-    cand[i] = ok;
+      if (const Dim* d = std::get_if<Dim>(&a.value)) ok = ok && (*d)->isConst();
+    for (ValueId v : op.results) ok = ok && shapeIsStatic(m.typeOf(v));
+    for (ValueId v : op.outs) ok = ok && part.value[v];
+    member[i] = ok;
   }
-  std::vector<int8_t> writersOk(nv);  // per root: -1 unwritten, 0 a writer stays per-call, 1 all writers hoisted
-  while (true) {
-    std::fill(writersOk.begin(), writersOk.end(), int8_t(-1));
-    for (size_t i = 0; i < no; ++i) {
-      if (r.ops[i].kind != OpKind::Kernel) continue;
-      for (ValueId v : r.ops[i].outs) {
-        int8_t& w = writersOk[roots.of(v)];
-        w = (w != 0 && cand[i]) ? 1 : 0;
-      }
-    }
-    auto constContents = [&](ValueId v) {
-      const ValueId root = roots.of(v);
-      return isConst[root] || (writersOk[root] == 1 && h.value[root]);
-    };
-    bool changed = false;
-    for (size_t i = 0; i < no; ++i) {
-      if (!cand[i]) continue;
+  // shrink to the greatest fixpoint (the condition is monotone in the member set, so any removal order ends there)
+  std::vector<uint8_t> allWritersIn(nv);
+  auto recount = [&] {
+    std::vector<uint8_t> written(nv, 0), outsider(nv, 0);
+    for (size_t i = 0; i < n; ++i)
+      if (r.ops[i].kind == OpKind::Kernel)
+        for (ValueId v : r.ops[i].outs) {
+          written[origin[v]] = 1;
+          if (!member[i]) outsider[origin[v]] = 1;
+        }
+    for (size_t v = 0; v < nv; ++v) allWritersIn[v] = written[v] && !outsider[v];
+  };
+  for (bool changed = true; changed;) {
+    recount();
+    changed = false;
+    for (size_t i = 0; i < n; ++i) {
+      if (!member[i]) continue;
       const Op& op = r.ops[i];
-      bool ok = std::all_of(op.operands.begin(), op.operands.end(), constContents);
-      for (ValueId v : op.outs) ok = ok && writersOk[roots.of(v)] == 1;
-      if (!ok) {
-        cand[i] = 0;
+      bool keep = true;
+      for (ValueId v : op.operands) {
+        const ValueId o = origin[v];
+        keep = keep && (constant[o] || (allWritersIn[o] && part.value[o]));
+      }
+      for (ValueId v : op.outs) keep = keep && allWritersIn[origin[v]];
+      if (!keep) {
+        member[i] = 0;
         changed = true;
-        for (ValueId v : op.outs) writersOk[roots.of(v)] = 0;
       }
     }
-    if (!changed) break;
   }
-  for (size_t v = 0; v < nv; ++v) h.initWritten[v] = writersOk[v] == 1;
-  for (size_t i = 0; i < no; ++i)
-    if (cand[i]) {
-      h.op[i] = 1;
-      for (ValueId v : r.ops[i].results) h.value[v] = 1;
+  recount();
+  part.initWritten = allWritersIn;
+  for (size_t i = 0; i < n; ++i)
+    if (member[i]) {
+      part.op[i] = 1;
+      for (ValueId v : r.ops[i].results) part.value[v] = 1;
     }
-  return h;
+  return part;
 }
 
-// ---- dce -------------------------------------------------------------------------------------------------------
-Status dce(Model& m) {
+// ---- edits ---------------------------------------------------------------------------------------------------------
+struct EditList {
+  explicit EditList(size_t n) : before(n), after(n), drop(n, 0) {}
+  std::vector<Op> prologue;
+  std::vector<std::vector<Op>> before, after;
+  std::vector<uint8_t> drop;
+};
+
+void applyEdits(Region& r, EditList& e) {
+  std::vector<Op> out;
+  for (Op& p : e.prologue) out.push_back(std::move(p));
+  for (size_t i = 0; i < r.ops.size(); ++i) {
+    for (Op& b : e.before[i]) out.push_back(std::move(b));
+    if (!e.drop[i]) out.push_back(std::move(r.ops[i]));
+    for (Op& a : e.after[i]) out.push_back(std::move(a));
+  }
+  r.ops = std::move(out);
+}
+
+Op allocOp(ValueId v) {
+  Op op;
+  op.kind = OpKind::BufferAlloc;
+  op.results.push_back(v);
+  return op;
+}
+Op freeOp(ValueId v) {
+  Op op;
+  op.kind = OpKind::BufferFree;
+  op.operands.push_back(v);
+  return op;
+}
+
+// ---- dce -----------------------------------------------------------------------------------------------------------
+Status deadCode(Model& m) {
   Region& r = m.exec;
-  std::vector<uint8_t> live(m.numValues(), 0);
-  std::vector<uint8_t> keep(r.ops.size(), 0);
+  std::vector<uint8_t> needed(m.numValues(), 0);
+  EditList e(r.ops.size());
   for (size_t i = r.ops.size(); i-- > 0;) {
     const Op& op = r.ops[i];
-    bool k = op.kind == OpKind::Return || op.kind == OpKind::DimRead ||
-             (op.kind == OpKind::Kernel && (op.attr("inout") || (op.results.empty() && op.outs.empty())));
-    for (ValueId v : op.results) k = k || live[v];
-    for (ValueId v : op.outs) k = k || live[v];
-    if (!k) continue;
-    keep[i] = 1;
-    for (ValueId v : op.operands) live[v] = 1;
-    for (ValueId v : op.outs) live[v] = 1;
+    const bool effect = op.kind == OpKind::Return || op.kind == OpKind::DimRead ||
+                        (op.kind == OpKind::Kernel && (op.attr("inout") || (op.results.empty() && op.outs.empty())));
+    bool live = effect;
+    for (ValueId v : op.results) live = live || needed[v];
+    for (ValueId v : op.outs) live = live || needed[v];
+    if (!live) {
+      e.drop[i] = 1;
+      continue;
+    }
+    forTouched(op, [&](ValueId v) { needed[v] = 1; });
   }
-  std::vector<Op> out;
-  for (size_t i = 0; i < r.ops.size(); ++i)
-    if (keep[i]) out.push_back(std::move(r.ops[i]));
-  r.ops = std::move(out);
+  applyEdits(r, e);
   return Status();
 }
 
-// ---- bufferize -------------------------------------------------------------------------------------------------
-Status bufferizeRegion(Model& m, Region& r, bool exec, const std::vector<uint8_t>& wasTensor) {
-  const size_t nv = m.numValues();
-  // Liveness before rewriting: a tensor kernel result is its own (future alloc) root.
-  Roots pre(nv);
-  pre.scan(r.ops);
-  std::vector<uint8_t> allocRoot(nv, 0);
-  for (const Op& op : r.ops) {
-    if (op.kind == OpKind::BufferAlloc) allocRoot[op.results[0]] = 1;
-    if (op.kind == OpKind::Kernel)
-      for (ValueId v : op.results)
-        if (wasTensor[v]) allocRoot[v] = 1;
-  }
-  auto lastUse = [&](const std::vector<Op>& ops, const Roots& roots) {
-    std::vector<size_t> last(nv, kNone);
-    for (size_t i = 0; i < ops.size(); ++i) {
-      for (ValueId v : ops[i].operands) last[roots.of(v)] = i;
-      for (ValueId v : ops[i].outs) last[roots.of(v)] = i;
-    }
-    return last;
-  };
-  std::vector<size_t> preLast = lastUse(r.ops, pre);
-  std::vector<uint8_t> persistent(nv, 0);
-  for (const Op& op : r.ops)
-    if (op.kind == OpKind::BufferAlloc && op.flag("persistent")) persistent[op.results[0]] = 1;
+// ---- bufferize -----------------------------------------------------------------------------------------------------
+class Bufferizer {
+ public:
+  Bufferizer(Model& m, Region& r, bool isExec, const std::vector<uint8_t>& wasTensor)
+      : m_(m), r_(r), exec_(isExec), wasTensor_(wasTensor), nv_(m.numValues()) {}
 
-  std::vector<ValueId> renamed(nv, kNoValue);
-  auto ren = [&](ValueId v) { return renamed[v] == kNoValue ? v : renamed[v]; };
-  std::vector<std::pair<size_t, ValueId>> newAllocs;  // (before op index, value)
-  for (size_t i = 0; i < r.ops.size(); ++i) {
-    Op& op = r.ops[i];
-    for (ValueId& v : op.operands) v = ren(v);
-    for (ValueId& v : op.outs) v = ren(v);
-    if (op.kind != OpKind::Kernel) continue;
-    std::vector<std::pair<size_t, size_t>> inplace;  // (result k, operand j)
-    if (const AttrValue* a = op.attr("inplace")) {
-      const Ints* v = std::get_if<Ints>(a);
-      if (!v) return Status::error("bufferize: inplace must be an int list");
-      for (size_t k = 0; k + 1 < v->size(); k += 2)
-        inplace.emplace_back(static_cast<size_t>((*v)[k]), static_cast<size_t>((*v)[k + 1]));
-    }
-    std::vector<ValueId> reusedHere;
-    std::vector<ValueId> scalarResults;
-    for (size_t k = 0; k < op.results.size(); ++k) {
-      const ValueId res = op.results[k];
-      if (!wasTensor[res]) {
-        scalarResults.push_back(res);
-        continue;
-      }
-      bool reused = false;
-      for (auto [outK, inJ] : inplace) {
-        if (outK != k || inJ >= op.operands.size()) continue;
-        const ValueId in = op.operands[inJ];
-        const ValueId inRoot = pre.of(in);
-        // the operand must be an in-region alloc root that dies at this kernel, used once by it
-        if (!allocRoot[inRoot] || inRoot != in || persistent[inRoot] || preLast[inRoot] != i) continue;
-        if (std::find(reusedHere.begin(), reusedHere.end(), inRoot) != reusedHere.end()) continue;
-        if (m.typeOf(in) != m.typeOf(res)) continue;
-        size_t uses = 0;
-        for (ValueId o : op.operands) uses += pre.of(o) == inRoot;
-        if (uses != 1) continue;
-        renamed[res] = in;
-        if (preLast[res] != kNone) preLast[inRoot] = preLast[res];  // the buffer now lives as long as the result
-        reusedHere.push_back(inRoot);
-        op.outs.push_back(in);
-        reused = true;
-        break;
-      }
-      if (reused) continue;
-      newAllocs.emplace_back(i, res);
-      op.outs.push_back(res);
-    }
-    op.results = scalarResults;
+  Status run() {
+    EditList e(r_.ops.size());
+    LKRT_TRY(assignStorage(e));
+    return placeFrees(e);
   }
-  std::vector<Op>& ops = r.ops;
 
-  Roots post(nv);
-  post.scan(ops);
-  std::vector<uint8_t> postAlloc(nv, 0);
-  for (const Op& op : ops)
-    if (op.kind == OpKind::BufferAlloc) postAlloc[op.results[0]] = 1;
-  for (const auto& a : newAllocs) postAlloc[a.second] = 1;
-  const std::vector<size_t> last = lastUse(ops, post);
-  std::vector<uint8_t> returned(nv, 0);
-  for (ValueId v : ops.back().operands) returned[post.of(v)] = 1;
-  if (exec)
-    for (ValueId v : ops.back().operands)
-      if (persistent[post.of(v)])
+ private:
+  // Every tensor result of a kernel becomes an out: a fresh alloc just before the kernel, or the operand an
+  // `inplace` pair names when that operand is an alloc of this region, used once by the kernel and dead after it.
+  Status assignStorage(EditList& e) {
+    const std::vector<ValueId> origin = originsOf(r_.ops, nv_);
+    std::vector<uint8_t> ownsMemory(nv_, 0);  // allocs, and tensor kernel results (future allocs)
+    persistent_.assign(nv_, 0);
+    for (const Op& op : r_.ops) {
+      if (op.kind == OpKind::BufferAlloc) {
+        ownsMemory[op.results[0]] = 1;
+        if (op.flag("persistent")) persistent_[op.results[0]] = 1;
+      }
+      if (op.kind == OpKind::Kernel)
+        for (ValueId v : op.results)
+          if (wasTensor_[v]) ownsMemory[v] = 1;
+    }
+    std::vector<size_t> dies = lastTouchOf(r_.ops, origin);
+    std::vector<ValueId> alias(nv_);  // a result renamed to the operand it reuses
+    std::iota(alias.begin(), alias.end(), ValueId{0});
+    fresh_.assign(nv_, 0);
+    for (size_t i = 0; i < r_.ops.size(); ++i) {
+      Op& op = r_.ops[i];
+      for (ValueId& v : op.operands) v = alias[v];
+      for (ValueId& v : op.outs) v = alias[v];
+      if (op.kind != OpKind::Kernel) continue;
+      std::vector<std::pair<size_t, size_t>> pairs;  // (result k, operand j)
+      if (const AttrValue* a = op.attr("inplace")) {
+        const Ints* list = std::get_if<Ints>(a);
+        if (!list) return Status::error("bufferize: inplace must be an int list");
+        for (size_t q = 0; q + 1 < list->size(); q += 2)
+          pairs.emplace_back(static_cast<size_t>((*list)[q]), static_cast<size_t>((*list)[q + 1]));
+      }
+      std::vector<ValueId> keptResults, taken;
+      for (size_t k = 0; k < op.results.size(); ++k) {
+        const ValueId res = op.results[k];
+        if (!wasTensor_[res]) {
+          keptResults.push_back(res);
+          continue;
+        }
+        ValueId reuse = kNoValue;
+        for (auto [outK, inJ] : pairs) {
+          if (outK != k || inJ >= op.operands.size()) continue;
+          const ValueId in = op.operands[inJ];
+          const ValueId o = origin[in];
+          const bool dying = ownsMemory[o] && o == in && !persistent_[o] && dies[o] == i;
+          if (!dying || std::count(taken.begin(), taken.end(), o) || m_.typeOf(in) != m_.typeOf(res)) continue;
+          const auto once = std::count_if(op.operands.begin(), op.operands.end(), [&](ValueId x) { return origin[x] == o; });
+          if (once != 1) continue;
+          reuse = in;
+          break;
+        }
+        if (reuse != kNoValue) {
+          alias[res] = reuse;
+          if (dies[res] != kNever) dies[origin[reuse]] = dies[res];  // the buffer now lives as long as the result
+          taken.push_back(origin[reuse]);
+          op.outs.push_back(reuse);
+        } else {
+          e.before[i].push_back(allocOp(res));
+          fresh_[res] = 1;
+          op.outs.push_back(res);
+        }
+      }
+      op.results = keptResults;
+    }
+    return Status();
+  }
+
+  // Frees after last uses, and the output / gpu_only marks, from the rewritten ops.
+  Status placeFrees(EditList& e) {
+    const std::vector<Op>& ops = r_.ops;
+    const size_t n = ops.size();
+    const std::vector<ValueId> origin = originsOf(ops, nv_);
+    const std::vector<size_t> last = lastTouchOf(ops, origin);
+    std::vector<uint8_t> isAlloc(fresh_), returned(nv_, 0);
+    for (const Op& op : ops)
+      if (op.kind == OpKind::BufferAlloc) isAlloc[op.results[0]] = 1;
+    for (ValueId v : ops.back().operands) {
+      returned[origin[v]] = 1;
+      if (exec_ && persistent_[origin[v]])
         return Status::error("exec returns persistent state %" + std::to_string(v) +
                              " (or a view of it); persistent buffers can't be graph outputs: return a copy");
-  // A buffer both a GPU kernel and a CPU op touch is freed no earlier than the next gpu_to_cpu sync after its last
-  // GPU use (else the end of the region): until then the GPU may still read it.
-  std::vector<size_t> lastGpu(nv, kNone);
-  std::vector<uint8_t> cpuTouched(nv, 0);
-  for (size_t i = 0; i < ops.size(); ++i) {
-    const Op& o = ops[i];
-    if (o.kind == OpKind::Kernel && isGpuKernelName(o.name)) {
-      for (ValueId v : o.operands) lastGpu[post.of(v)] = i;
-      for (ValueId v : o.outs) lastGpu[post.of(v)] = i;
-    } else if (o.kind == OpKind::Kernel || o.kind == OpKind::DimRead || o.kind == OpKind::Return) {
-      for (ValueId v : o.operands) cpuTouched[post.of(v)] = 1;
-      for (ValueId v : o.outs) cpuTouched[post.of(v)] = 1;
     }
-  }
-  std::vector<size_t> nextSync(ops.size() + 1, ops.size() - 1);
-  for (size_t i = ops.size(); i-- > 0;) {
-    nextSync[i] = nextSync[i + 1];
-    if (ops[i].kind == OpKind::Sync && ops[i].ints[0] == kGpuToCpu) nextSync[i] = i;
-  }
-  std::vector<std::pair<size_t, ValueId>> frees;
-  for (ValueId root = 0; root < nv; ++root) {
-    if (!postAlloc[root] || post.of(root) != root || returned[root] || persistent[root] || last[root] == kNone)
-      continue;
-    size_t at = last[root];
-    if (lastGpu[root] != kNone && cpuTouched[root]) {
-      const size_t s = nextSync[lastGpu[root]];
-      at = std::max(at, s >= ops.size() - 1 ? ops.size() - 2 : s);
+    // device touches: the last GPU kernel use; any host use (CPU kernel, dim.read, return)
+    std::vector<size_t> lastGpu(nv_, kNever);
+    std::vector<uint8_t> host(nv_, 0);
+    for (size_t i = 0; i < n; ++i) {
+      const Op& op = ops[i];
+      const bool gpu = op.kind == OpKind::Kernel && isGpuKernelName(op.name);
+      const bool cpu = !gpu && (op.kind == OpKind::Kernel || op.kind == OpKind::DimRead || op.kind == OpKind::Return);
+      if (gpu) forTouched(op, [&](ValueId v) { lastGpu[origin[v]] = i; });
+      if (cpu) forTouched(op, [&](ValueId v) { host[origin[v]] = 1; });
     }
-    frees.emplace_back(at, root);
-  }
-  std::sort(frees.begin(), frees.end());
-  auto mark = [&](Op& alloc) {
-    const ValueId v = alloc.results[0];
-    if (exec && returned[v]) alloc.setAttr("output", true);
-    if (lastGpu[v] != kNone && !cpuTouched[v] && !persistent[v]) alloc.setAttr("gpu_only", true);
-  };
-  std::vector<Op> out;
-  out.reserve(ops.size() + newAllocs.size() + frees.size());
-  size_t f = 0, a = 0;
-  for (size_t i = 0; i < ops.size(); ++i) {
-    for (; a < newAllocs.size() && newAllocs[a].first == i; ++a) {
-      Op alloc;
-      alloc.kind = OpKind::BufferAlloc;
-      alloc.results.push_back(newAllocs[a].second);
-      mark(alloc);
-      out.push_back(std::move(alloc));
+    // first gpu_to_cpu sync at or after each index (the return when none)
+    std::vector<size_t> syncFrom(n + 1, n - 1);
+    for (size_t i = n; i-- > 0;)
+      syncFrom[i] = ops[i].kind == OpKind::Sync && ops[i].ints[0] == kGpuToCpu ? i : syncFrom[i + 1];
+    // A buffer both devices touch is freed no earlier than the first gpu_to_cpu sync after its last GPU use (the
+    // op before the return when there is none): until then the GPU may still read it.
+    std::vector<std::pair<size_t, ValueId>> frees;
+    for (ValueId v = 0; v < nv_; ++v) {
+      if (!isAlloc[v] || origin[v] != v || returned[v] || persistent_[v] || last[v] == kNever) continue;
+      size_t at = last[v];
+      if (lastGpu[v] != kNever && host[v]) {
+        const size_t s = syncFrom[lastGpu[v]];
+        at = std::max(at, s >= n - 1 ? n - 2 : s);
+      }
+      frees.emplace_back(at, v);
     }
-    if (ops[i].kind == OpKind::BufferAlloc) mark(ops[i]);
-    out.push_back(std::move(ops[i]));
-    for (; f < frees.size() && frees[f].first == i; ++f) {
-      Op fr;
-      fr.kind = OpKind::BufferFree;
-      fr.operands.push_back(frees[f].second);
-      out.push_back(std::move(fr));
-    }
+    std::sort(frees.begin(), frees.end());
+    for (auto [at, v] : frees) e.after[at].push_back(freeOp(v));
+    auto mark = [&](Op& alloc) {
+      const ValueId v = alloc.results[0];
+      if (exec_ && returned[v]) alloc.setAttr("output", true);
+      if (lastGpu[v] != kNever && !host[v] && !persistent_[v]) alloc.setAttr("gpu_only", true);
+    };
+    for (auto& list : e.before)
+      for (Op& a : list) mark(a);
+    for (Op& op : r_.ops)
+      if (op.kind == OpKind::BufferAlloc) mark(op);
+    applyEdits(r_, e);
+    return Status();
   }
-  r.ops = std::move(out);
-  return Status();
-}
+
+  Model& m_;
+  Region& r_;
+  bool exec_;
+  const std::vector<uint8_t>& wasTensor_;
+  size_t nv_;
+  std::vector<uint8_t> persistent_, fresh_;
+};
 
 Status bufferize(Model& m) {
   std::vector<uint8_t> wasTensor(m.numValues(), 0);
-  for (ValueId v = 0; v < m.numValues(); ++v) {
-    Type t = m.typeOf(v);
-    if (t->isTensor()) {
+  for (ValueId v = 0; v < m.numValues(); ++v)
+    if (const Type t = m.typeOf(v); t->isTensor()) {
       wasTensor[v] = 1;
       m.setType(v, m.types().withKind(t, TypeKind::Buffer));
     }
-  }
-  LKRT_TRY(bufferizeRegion(m, m.init, false, wasTensor));
-  return bufferizeRegion(m, m.exec, true, wasTensor);
+  LKRT_TRY(Bufferizer(m, m.init, false, wasTensor).run());
+  return Bufferizer(m, m.exec, true, wasTensor).run();
 }
 
-// ---- plan-memory -----------------------------------------------------------------------------------------------
+// ---- plan-memory ---------------------------------------------------------------------------------------------------
 Status planMemory(Model& m) {
   Region& r = m.exec;
-  const Hoist hoist = hoistable(m, r);
-  DimPool& dp = m.dims();
-  std::vector<int64_t> readAt(dp.numSymbols(), -1);  // symbol -> index of the dim.read defining it
-  bool anyRead = false;
-  for (size_t i = 0; i < r.ops.size(); ++i)
-    if (r.ops[i].kind == OpKind::DimRead) {
-      readAt[static_cast<size_t>(r.ops[i].symbols[0])] = static_cast<int64_t>(i);
-      anyRead = true;
+  DimPool& dims = m.dims();
+  const InitPart init = initPart(m, r);
+  const size_t n = r.ops.size();
+  // where each dim.read symbol is defined, and where each buffer is freed
+  std::vector<int64_t> definedAt(dims.numSymbols(), -1);
+  bool reads = false;
+  std::vector<size_t> freedAt(m.numValues(), kNever);
+  for (size_t i = 0; i < n; ++i) {
+    const Op& op = r.ops[i];
+    if (op.kind == OpKind::DimRead) {
+      definedAt[static_cast<size_t>(op.symbols[0])] = static_cast<int64_t>(i);
+      reads = true;
     }
-  std::vector<size_t> freeAt(m.numValues(), kNone);
-  for (size_t i = 0; i < r.ops.size(); ++i)
-    if (r.ops[i].kind == OpKind::BufferFree) freeAt[r.ops[i].operands[0]] = i;
-
-  struct Cand {
+    if (op.kind == OpKind::BufferFree) freedAt[op.operands[0]] = i;
+  }
+  // candidates: per-call allocs with a free (not outputs, not arenas, not written by init)
+  struct Slot {
     size_t alloc, free;
     ValueId v;
     Dim bytes;
-    int64_t group;
-    bool gpuOnly;
   };
-  std::vector<Cand> cands;
-  std::unordered_map<Type, Dim> bytesOf;
-  for (size_t i = 0; i < r.ops.size(); ++i) {
+  // (the dim.read after which the sizes are known, or -1; gpu_only) -> slots, in op order
+  std::map<std::pair<int64_t, bool>, std::vector<Slot>> pools;
+  for (size_t i = 0; i < n; ++i) {
     const Op& op = r.ops[i];
     if (op.kind != OpKind::BufferAlloc) continue;
     const ValueId v = op.results[0];
-    if (hoist.initWritten[v] || freeAt[v] == kNone || op.flag("output") || op.flag("arena")) continue;
-    Type t = m.typeOf(v);
-    auto it = bytesOf.find(t);
-    Dim bytes = it != bytesOf.end() ? it->second : (bytesOf[t] = m.types().numBytes(t));
-    Cand c{i, freeAt[v], v, bytes, -1, op.flag("gpu_only")};
-    if (anyRead && !bytes->isConst()) {
+    if (init.initWritten[v] || freedAt[v] == kNever || op.flag("output") || op.flag("arena")) continue;
+    const Dim bytes = m.types().numBytes(m.typeOf(v));
+    int64_t after = -1;
+    if (reads && !bytes->isConst()) {
       std::vector<int64_t> syms;
       collectSymbols(bytes, syms);
-      for (int64_t s : syms)
-        if (readAt[static_cast<size_t>(s)] >= 0) c.group = std::max(c.group, readAt[static_cast<size_t>(s)]);
+      for (int64_t s : syms) after = std::max(after, definedAt[static_cast<size_t>(s)]);
     }
-    cands.push_back(c);
+    pools[{after, op.flag("gpu_only")}].push_back({i, freedAt[v], v, bytes});
   }
-  if (cands.empty()) return Status();
-  std::map<std::pair<int64_t, bool>, std::vector<size_t>> groups;
-  for (size_t i = 0; i < cands.size(); ++i) groups[{cands[i].group, cands[i].gpuOnly}].push_back(i);
+  if (pools.empty()) return Status();
 
-  std::vector<uint8_t> drop(r.ops.size(), 0);
-  std::vector<Op> prologue;
-  std::vector<std::pair<size_t, Op>> after;
-  auto elemBytes = [&](ValueId v) { return static_cast<int64_t>(dtypeSize(m.typeOf(v)->dtype)); };
+  EditList e(n);
+  auto elemSize = [&](ValueId v) { return static_cast<int64_t>(dtypeSize(m.typeOf(v)->dtype)); };
   int planNo = 0;
-  for (auto& [key, idx] : groups) {
-    const int64_t group = key.first;
-    const bool allStatic = std::all_of(idx.begin(), idx.end(), [&](size_t i) { return cands[i].bytes->isConst(); });
-    Op plan;
+  for (auto& [key, slots] : pools) {
+    const int64_t after = key.first;
+    const bool sizesKnown = std::all_of(slots.begin(), slots.end(), [](const Slot& s) { return s.bytes->isConst(); });
+    Op arenaOp;
     ValueId arena;
-    std::vector<Dim> offsets;
-    if (allStatic && group < 0) {
+    std::vector<Dim> where;  // each slot's offset in its own elements
+    if (sizesKnown && after < 0) {
       std::vector<PlanItem> items;
-      for (size_t i : idx)
-        items.push_back({cands[i].bytes->value, static_cast<int64_t>(cands[i].alloc), static_cast<int64_t>(cands[i].free)});
-      std::vector<int64_t> offs;
-      const int64_t total = planOffsets(items, kArenaAlign, offs);
-      arena = m.newValue(m.types().buffer(DType::U8, {dp.constant(total)}), "arena");
-      plan.kind = OpKind::BufferAlloc;
-      plan.setAttr("arena", true);
-      plan.results.push_back(arena);
-      for (size_t k = 0; k < idx.size(); ++k) offsets.push_back(dp.constant(offs[k] / elemBytes(cands[idx[k]].v)));
+      for (const Slot& s : slots)
+        items.push_back({s.bytes->value, static_cast<int64_t>(s.alloc), static_cast<int64_t>(s.free)});
+      std::vector<int64_t> byteOff;
+      const int64_t total = planOffsets(items, kArenaAlign, byteOff);
+      arena = m.newValue(m.types().buffer(DType::U8, {dims.constant(total)}), "arena");
+      arenaOp = allocOp(arena);
+      arenaOp.setAttr("arena", true);
+      for (size_t k = 0; k < slots.size(); ++k) where.push_back(dims.constant(byteOff[k] / elemSize(slots[k].v)));
     } else {
-      while (dp.findSymbol("M" + std::to_string(planNo) + "_size") >= 0) ++planNo;
+      while (dims.findSymbol("M" + std::to_string(planNo) + "_size") >= 0) ++planNo;
       const std::string base = "M" + std::to_string(planNo++);
-      plan.kind = OpKind::MemPlan;
-      plan.symbols.push_back(dp.sym(base + "_size")->value);
-      Ints elems;
-      for (size_t k = 0; k < idx.size(); ++k) {
-        const Cand& c = cands[idx[k]];
-        Dim off = dp.sym(base + "_o" + std::to_string(k));  // in elements of buffer k (attr `elem`)
-        plan.dims.push_back(c.bytes);
-        plan.ints.push_back(static_cast<int64_t>(c.alloc));
-        plan.ints.push_back(static_cast<int64_t>(c.free));
-        plan.symbols.push_back(off->value);
-        elems.push_back(elemBytes(c.v));
-        offsets.push_back(off);
+      arenaOp.kind = OpKind::MemPlan;
+      const Dim size = dims.sym(base + "_size");
+      arenaOp.symbols.push_back(size->value);
+      Ints elem;
+      for (size_t k = 0; k < slots.size(); ++k) {
+        const Dim off = dims.sym(base + "_o" + std::to_string(k));
+        arenaOp.dims.push_back(slots[k].bytes);
+        arenaOp.ints.push_back(static_cast<int64_t>(slots[k].alloc));
+        arenaOp.ints.push_back(static_cast<int64_t>(slots[k].free));
+        arenaOp.symbols.push_back(off->value);
+        elem.push_back(elemSize(slots[k].v));
+        where.push_back(off);
       }
-      plan.ints.push_back(kArenaAlign);
-      plan.setAttr("elem", elems);
-      if (key.second) plan.setAttr("gpu_only", true);
-      arena = m.newValue(m.types().buffer(DType::U8, {dp.sym(base + "_size")}), "arena");
-      plan.results.push_back(arena);
+      arenaOp.ints.push_back(kArenaAlign);
+      arenaOp.setAttr("elem", elem);
+      if (key.second) arenaOp.setAttr("gpu_only", true);
+      arena = m.newValue(m.types().buffer(DType::U8, {size}), "arena");
+      arenaOp.results.push_back(arena);
     }
-    for (size_t k = 0; k < idx.size(); ++k) {
-      const Cand& c = cands[idx[k]];
-      Op& view = r.ops[c.alloc];  // the alloc becomes a view of the arena, same result
-      view.kind = OpKind::View;
-      view.attrs.clear();
-      view.operands.assign(1, arena);
-      view.dims.assign(1, offsets[k]);
-      drop[c.free] = 1;
+    for (size_t k = 0; k < slots.size(); ++k) {  // the alloc becomes a view of the arena (same result value)
+      Op& op = r.ops[slots[k].alloc];
+      op.kind = OpKind::View;
+      op.attrs.clear();
+      op.operands = {arena};
+      op.dims = {where[k]};
+      e.drop[slots[k].free] = 1;
     }
-    if (group < 0) prologue.push_back(std::move(plan));
-    else after.emplace_back(static_cast<size_t>(group), std::move(plan));
+    if (after < 0) e.prologue.push_back(std::move(arenaOp));
+    else e.after[static_cast<size_t>(after)].push_back(std::move(arenaOp));
   }
-  std::stable_sort(after.begin(), after.end(), [](const auto& a, const auto& b) { return a.first < b.first; });
-  std::vector<Op> out;
-  out.reserve(r.ops.size() + prologue.size() + after.size());
-  for (Op& p : prologue) out.push_back(std::move(p));
-  size_t a = 0;
-  for (size_t i = 0; i < r.ops.size(); ++i) {
-    if (!drop[i]) out.push_back(std::move(r.ops[i]));
-    for (; a < after.size() && after[a].first == i; ++a) out.push_back(std::move(after[a].second));
-  }
-  r.ops = std::move(out);
+  applyEdits(r, e);
   return Status();
 }
 
-// ---- hoist-init ------------------------------------------------------------------------------------------------
+// ---- hoist-init ----------------------------------------------------------------------------------------------------
 Status hoistInit(Model& m) {
   Region& ex = m.exec;
-  const Hoist h = hoistable(m, ex);
-  std::vector<uint8_t> usedByExec(m.numValues(), 0);
-  for (size_t i = 0; i < ex.ops.size(); ++i) {
-    const Op& op = ex.ops[i];
-    if (h.op[i] || op.kind == OpKind::BufferFree) continue;
-    for (ValueId v : op.operands) usedByExec[v] = 1;
-    for (ValueId v : op.outs) usedByExec[v] = 1;
-  }
-  Op initReturn = std::move(m.init.ops.back());
+  const InitPart part = initPart(m, ex);
+  const size_t n = ex.ops.size();
+  std::vector<uint8_t> execUses(m.numValues(), 0);  // touched by an op that stays per call
+  for (size_t i = 0; i < n; ++i)
+    if (!part.op[i] && ex.ops[i].kind != OpKind::BufferFree) forTouched(ex.ops[i], [&](ValueId v) { execUses[v] = 1; });
+  Op initRet = std::move(m.init.ops.back());
   m.init.ops.pop_back();
-  std::vector<Op> stay;
-  for (size_t i = 0; i < ex.ops.size(); ++i) {
+  EditList stays(n);
+  for (size_t i = 0; i < n; ++i) {
     Op& op = ex.ops[i];
-    if (h.op[i]) {
+    const bool freesInitMemory = op.kind == OpKind::BufferFree && part.value[op.operands[0]];
+    if (part.op[i]) {
       m.init.ops.push_back(std::move(op));
-    } else if (op.kind == OpKind::BufferFree && h.value[op.operands[0]]) {
-      if (!usedByExec[op.operands[0]]) m.init.ops.push_back(std::move(op));  // an init-only temporary
-      // else dropped: the buffer lives as long as the model
-    } else {
-      stay.push_back(std::move(op));
+      stays.drop[i] = 1;
+    } else if (freesInitMemory) {
+      // an init-only temporary is freed in init; memory exec still uses lives as long as the model
+      if (!execUses[op.operands[0]]) m.init.ops.push_back(std::move(op));
+      stays.drop[i] = 1;
     }
   }
-  ex.ops = std::move(stay);
-  std::vector<ValueId> stateOf(m.numValues(), kNoValue);
-  auto toState = [&](ValueId& v) {
-    if (v >= h.value.size() || !h.value[v]) return;
-    if (stateOf[v] == kNoValue) {
-      stateOf[v] = m.newValue(m.typeOf(v), m.nameOf(v));
-      initReturn.operands.push_back(v);
-      ex.state.push_back(stateOf[v]);
+  applyEdits(ex, stays);
+  // init values exec still refers to become state, in order of first reference
+  std::vector<ValueId> asState(m.numValues(), kNoValue);
+  auto stateFor = [&](ValueId& v) {
+    if (v >= part.value.size() || !part.value[v]) return;
+    if (asState[v] == kNoValue) {
+      asState[v] = m.newValue(m.typeOf(v), m.nameOf(v));
+      initRet.operands.push_back(v);
+      ex.state.push_back(asState[v]);
     }
-    v = stateOf[v];
+    v = asState[v];
   };
   for (Op& op : ex.ops) {
-    for (ValueId& v : op.operands) toState(v);
-    for (ValueId& v : op.outs) toState(v);
+    for (ValueId& v : op.operands) stateFor(v);
+    for (ValueId& v : op.outs) stateFor(v);
   }
-  m.init.ops.push_back(std::move(initReturn));
+  m.init.ops.push_back(std::move(initRet));
   return Status();
 }
+
+// ---- pass table ----------------------------------------------------------------------------------------------------
+struct PassEntry {
+  const char* name;
+  Status (*run)(Model&);
+};
+const PassEntry kPasses[] = {
+    {"dce", deadCode}, {"bufferize", bufferize}, {"plan-memory", planMemory}, {"hoist-init", hoistInit}};
 
 }  // namespace
 
+// Greedy by size (largest first, ties by index); each buffer goes to the smallest gap between the placed buffers
+// whose [start, end] lifetimes overlap its own that holds it, else past all of them.
 int64_t planOffsets(const std::vector<PlanItem>& items, int64_t align, std::vector<int64_t>& offsets) {
-  const size_t n = items.size();
-  offsets.assign(n, 0);
-  std::vector<size_t> order(n);
-  std::iota(order.begin(), order.end(), 0);
-  std::sort(order.begin(), order.end(), [&](size_t a, size_t b) {
-    return items[a].bytes != items[b].bytes ? items[a].bytes > items[b].bytes : a < b;
-  });
-  struct Placed {
-    int64_t off, size, start, end;
+  offsets.assign(items.size(), 0);
+  std::vector<size_t> order(items.size());
+  std::iota(order.begin(), order.end(), size_t{0});
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return items[a].bytes > items[b].bytes; });
+  struct Span {
+    int64_t lo, hi;  // [lo, hi) bytes
+    size_t item;
   };
-  std::vector<Placed> placed;  // by offset
+  std::vector<Span> spans;  // by lo
   int64_t total = 0;
   for (size_t i : order) {
-    const PlanItem& b = items[i];
-    const int64_t size = (std::max<int64_t>(b.bytes, 1) + align - 1) / align * align;
-    // best fit: the smallest gap between lifetime-overlapping placed buffers that holds it, else past them all
-    int64_t best = -1, bestGap = INT64_MAX, cursor = 0;
-    for (const Placed& p : placed) {
-      if (p.end < b.start || b.end < p.start) continue;
-      if (p.off >= cursor) {
-        const int64_t gap = p.off - cursor;
-        if (gap >= size && gap < bestGap) {
-          best = cursor;
-          bestGap = gap;
-        }
+    const PlanItem& it = items[i];
+    const int64_t size = (std::max<int64_t>(it.bytes, 1) + align - 1) / align * align;
+    int64_t at = -1, tightest = INT64_MAX, frontier = 0;
+    for (const Span& s : spans) {
+      const PlanItem& other = items[s.item];
+      if (other.end < it.start || it.end < other.start) continue;  // never live together
+      if (s.lo >= frontier && s.lo - frontier >= size && s.lo - frontier < tightest) {
+        at = frontier;
+        tightest = s.lo - frontier;
       }
-      cursor = std::max(cursor, p.off + p.size);
+      frontier = std::max(frontier, s.hi);
     }
-    if (best < 0) best = cursor;
-    offsets[i] = best;
-    total = std::max(total, best + size);
-    const Placed np{best, size, b.start, b.end};
-    placed.insert(std::upper_bound(placed.begin(), placed.end(), np,
-                                   [](const Placed& x, const Placed& y) { return x.off < y.off; }),
-                  np);
+    if (at < 0) at = frontier;
+    offsets[i] = at;
+    total = std::max(total, at + size);
+    const Span mine{at, at + size, i};
+    spans.insert(std::upper_bound(spans.begin(), spans.end(), mine, [](const Span& a, const Span& b) { return a.lo < b.lo; }),
+                 mine);
   }
   return total;
 }
@@ -514,44 +554,48 @@ const std::vector<std::string>& defaultPipeline() {
 }
 
 Status runPass(Model& m, std::string_view name) {
-  Status s;
-  if (name == "dce") s = dce(m);
-  else if (name == "bufferize") s = bufferize(m);
-  else if (name == "plan-memory") s = planMemory(m);
-  else if (name == "hoist-init") s = hoistInit(m);
-  else return Status::error("unknown pass '" + std::string(name) + "'");
-  if (!s) return Status::error(std::string(name) + ": " + s.message());
+  const PassEntry* pass = nullptr;
+  for (const PassEntry& p : kPasses)
+    if (name == p.name) pass = &p;
+  if (!pass) return Status::error("unknown pass '" + std::string(name) + "'");
+  if (Status s = pass->run(m); !s) return Status::error(std::string(name) + ": " + s.message());
   if (Status v = verifyModel(m); !v) return Status::error("IR invalid after pass '" + std::string(name) + "': " + v.message());
   return Status();
 }
 
+// const.external -> const.internal for every external whose bytes are given; with `copy` the model keeps its own
+// page-aligned copy, else it refers to the caller's bytes (kept alive through `owner`).
 Status internalize(Model& m, const std::vector<ExternalBytes>& data, bool copy) {
+  auto bytesFor = [&](const std::string& name) -> const ExternalBytes* {
+    for (const ExternalBytes& e : data)
+      if (e.name == name) return &e;
+    return nullptr;
+  };
   for (Region* r : {&m.init, &m.exec})
     for (Op& op : r->ops) {
       if (op.kind != OpKind::ConstExternal) continue;
-      const ExternalBytes* d = nullptr;
-      for (const ExternalBytes& e : data)
-        if (e.name == op.name) d = &e;
+      const ExternalBytes* d = bytesFor(op.name);
       if (!d) return Status::error("internalize: no data for external constant '" + op.name + "'");
       if (!m.findConstant(op.name)) {
-        Type t = m.typeOf(op.results[0]);
-        size_t bytes = dtypeSize(t->dtype);
+        const Type t = m.typeOf(op.results[0]);
+        size_t need = dtypeSize(t->dtype);
         for (Dim dim : t->shape) {
           if (!dim->isConst() || dim->value < 0)
             return Status::error("internalize: external constant '" + op.name + "' has a symbolic shape");
-          bytes *= static_cast<size_t>(dim->value);
+          need *= static_cast<size_t>(dim->value);
         }
-        if (d->size != bytes)
+        if (d->size != need)
           return Status::error("internalize: '" + op.name + "' has " + std::to_string(d->size) + " bytes, its type " +
-                               std::to_string(bytes));
-        Constant c{op.name, t, d->owner, d->bytes, bytes};
+                               std::to_string(need));
+        Constant c{op.name, t, d->owner, d->bytes, need};
         if (copy) {
           constexpr size_t kPage = 16384;
-          void* p = std::aligned_alloc(kPage, (std::max<size_t>(bytes, 1) + kPage - 1) / kPage * kPage);
-          if (!p) return Status::error("internalize: out of memory");
-          if (bytes) std::memcpy(p, d->bytes, bytes);
-          c.owner = std::shared_ptr<const void>(p, [](const void* q) { std::free(const_cast<void*>(q)); });
-          c.bytes = static_cast<const uint8_t*>(p);
+          const size_t cap = (std::max<size_t>(need, 1) + kPage - 1) / kPage * kPage;
+          void* mem = std::aligned_alloc(kPage, cap);
+          if (!mem) return Status::error("internalize: out of memory");
+          if (need) std::memcpy(mem, d->bytes, need);
+          c.owner = std::shared_ptr<const void>(mem, [](const void* q) { std::free(const_cast<void*>(q)); });
+          c.bytes = static_cast<const uint8_t*>(mem);
         }
         m.addConstant(std::move(c));
       }
