@@ -229,7 +229,7 @@ def kokoro_conv_flops(tokens: int, frames: int) -> float:
 
 def bench_kokoro(tokens: int, steps: int, warmup: int, runtime: str = "compiled", sd=None) -> dict:
     """Median ms of one Kokoro forward. runtime "compiled": lk.compile's C++ executable (one model arena, weights
-    uploaded once, the call replayed from its captured hipGraph with the independent branches on 4 lanes);
+    uploaded once, the call replayed from its captured hipGraph with the independent branches on 6 lanes);
     "capture": the torch stream capture of the same function."""
     import lokinfer_amd as lk
     from lokinfer_amd import kokoro_weights as KW
@@ -238,7 +238,7 @@ def bench_kokoro(tokens: int, steps: int, warmup: int, runtime: str = "compiled"
     sd = KW.random_weights() if sd is None else sd
     ids, ref_s, dur, noise = KW.inputs(tokens)
     frames = int(dur.sum())
-    m = KokoroGpu(sd, runtime=runtime, lanes=4)
+    m = KokoroGpu(sd, runtime=runtime, lanes=6)
     args = [lk.from_numpy(a, device="gpu", copy=True) for a in (ids, ref_s, dur, noise)]
     for _ in range(max(warmup, 1)):
         m.forward(*args, inplace=True)

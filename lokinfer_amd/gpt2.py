@@ -217,3 +217,36 @@ def generate(model: Gpt2Generator, prompt: list[int], n_new: int) -> list[int]:
         _, am = model.run(Tensor(out[i:i + 1]), pos)
         pos += 1
     return [int(v) for v in out.cpu()]
+
+
+def build_decode(sd: dict[str, np.ndarray]):
+    """The reference's `build_decode(sd, device="gpu")` (models/gpt2.py:161-249) through lk.compile: one decode step
+    whose per-layer K / V caches are `lk.persistent_buffer`s (model state that persists across calls; the step
+    writes row `pos` in place and attends over rows 0..pos). Inputs tok i64[1], pos i64[1] (device tensors) ->
+    logits f32[1, 50257]. The reference's op sequence (gemv4, attention_decode_split, add_bias_layernorm2, the tied
+    LM head); its CPU embedding lookups are one device kernel here. Returns the lk.CompiledModel."""
+    import lokinfer_amd as lk
+
+    w = {k: from_numpy(v, device="gpu", copy=True) for k, v in sd.items()}
+    P = "transformer."
+
+    def fn(tok, pos):
+        caches = [(lk.persistent_buffer(lk.f32, [N_POS, D]), lk.persistent_buffer(lk.f32, [N_POS, D]))
+                  for _ in range(N_LAYER)]
+        h = ops.embedding2_add_f32_gpu(w[P + "wte.weight"], tok, w[P + "wpe.weight"], pos)
+        ln = ops.layernorm_f32_gpu(h, w[P + "h.0.ln_1.weight"], w[P + "h.0.ln_1.bias"], eps=LN_EPS)
+        for i, (kc, vc) in enumerate(caches):
+            L = f"{P}h.{i}."
+            nxt = f"{P}h.{i + 1}.ln_1." if i + 1 < N_LAYER else P + "ln_f."
+            qkv = ops.gemv4_f32_gpu(ln, w[L + "attn.c_attn.weight"])
+            att = ops.attention_decode_split_f32_gpu(qkv, kc, vc, pos, w[L + "attn.c_attn.bias"], heads=HEADS)
+            o = ops.gemv4_f32_gpu(att, w[L + "attn.c_proj.weight"])
+            h, ln = ops.add_bias_layernorm2_f32_gpu(o, w[L + "attn.c_proj.bias"], h, w[L + "ln_2.weight"],
+                                                    w[L + "ln_2.bias"], eps=LN_EPS)
+            f = ops.gemv4_f32_gpu(ln, w[L + "mlp.c_fc.weight"], w[L + "mlp.c_fc.bias"], act="gelu")
+            o = ops.gemv4_f32_gpu(f, w[L + "mlp.c_proj.weight"])
+            h, ln = ops.add_bias_layernorm2_f32_gpu(o, w[L + "mlp.c_proj.bias"], h, w[nxt + "weight"], w[nxt + "bias"],
+                                                    eps=LN_EPS)
+        return ops.gemm_nt_f32_gpu_mps(ln, w[P + "wte.weight"])
+
+    return lk.compile(fn, input_types=[lk.TensorType(lk.i64, [1]), lk.TensorType(lk.i64, [1])])

@@ -221,6 +221,10 @@ class Graph:
         self._n += 1
         return f"{hint}{self._n}"
 
+    def fresh_symbol(self, hint: str) -> str:
+        """A symbol name no dim of this graph uses yet."""
+        return self._fresh(hint)
+
     def arg(self, type_, hint: str = "in") -> Value:
         v = Value(self, self._fresh(hint), type_)
         self.args.append(v)

@@ -70,7 +70,7 @@ class KokoroGpu:
     branches on up to `lanes` concurrent lanes. The conv dispatch (Winograd or tap conv) depends on the lengths,
     so the traced model is specialized per signature."""
 
-    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, runtime: str = "capture", lanes: int = 4):
+    def __init__(self, sd: dict[str, np.ndarray], graph: bool = True, runtime: str = "capture", lanes: int = 6):
         if runtime not in ("capture", "compiled"):
             raise ValueError("runtime must be 'capture' or 'compiled'")
         self.runtime = runtime

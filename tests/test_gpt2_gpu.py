@@ -63,3 +63,22 @@ def test_fused_matches_reference_op_sequence(setup):
         x, y = la.numpy()[0], lb.numpy()[0]
         assert np.abs(x - y).max() <= 1e-5 * np.abs(y).max(), p
         assert int(aa.numpy()[0]) == int(ab.numpy()[0])
+
+
+def test_build_decode_with_persistent_buffers(setup):
+    """The reference's build_decode restated (lk.persistent_buffer caches, traced through lk.compile, run by the C++
+    executable): stepping the 512-token prompt then the next token at pos 512 matches the oracle (1e-4, argmax
+    equal), and each step equals the captured reference-op-sequence decoder bit for bit."""
+    lk, G, sd, ids, nxt, ref = setup
+    m = G.build_decode(sd)
+    b = G.Gpt2Decoder(sd, fused=False)
+    for p, t in enumerate(ids):
+        got = m(_dev(lk, int(t)), _dev(lk, p))
+        want, _ = b.step(_dev(lk, int(t)), _dev(lk, p))
+        if p < 8 or p % 97 == 0:
+            assert np.array_equal(got.numpy(), want.numpy()), p
+    got = m(_dev(lk, nxt), _dev(lk, 512)).numpy()[0]
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= 1e-4, err
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+    assert m.stats()["graphs"] == 1  # one captured step replayed with new tok / pos
