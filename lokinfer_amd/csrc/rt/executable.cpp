@@ -388,6 +388,10 @@ Status Executable::interpret(const std::vector<Instr>& code, std::vector<char*>&
       case OpKind::DimRead: {
         const ValueId v = op.operands[0];
         const size_t es = dtypeSize(m.typeOf(v)->dtype);
+        int64_t have;  // the index against the operand's extent (the verifier checks it only for static shapes)
+        if (!bytesOf(m.typeOf(v), have) || op.ints[0] < 0 || (op.ints[0] + 1) * static_cast<int64_t>(es) > have)
+          return Status::error("dim.read: index " + std::to_string(op.ints[0]) + " is outside its operand");
+        if (!slot[v]) return Status::error("dim.read: its operand has no memory");
         LKRT_TRY(hipStatus(hipMemcpyAsync(pinned_, slot[v] + op.ints[0] * static_cast<int64_t>(es), es,
                                           hipMemcpyDeviceToHost, s),
                            "dim.read"));

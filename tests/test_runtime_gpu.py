@@ -80,7 +80,7 @@ def test_data_dependent_shape_dim_read(gpu):
 
     def f(scores, rows):
         idx = lk.ops.argmax_f32_gpu(scores)  # i64[1]
-        F = lk.graph.current_graph().dim_read(lk.ops.to_cpu(idx), 0, "F")
+        F = lk.dim_read(lk.ops.to_cpu(idx), 0, "F")
         head = lk.ops.view(rows, [F, 64], 0)
         return lk.ops.gemm_f32_gpu_mps(head, w)
 
@@ -94,6 +94,28 @@ def test_data_dependent_shape_dim_read(gpu):
         assert got.shape == (k, 32)
         assert np.array_equal(got, lk.ops.gemm_f32_gpu_mps(G(lk, rows[:k]), w).numpy())
     assert m.stats()["graphs"] == 0
+
+
+def test_dim_read_index_checked_against_a_symbolic_extent(gpu):
+    """dim.read's index is checked at run time when its operand's extent is symbolic (the verifier can only check
+    static ones): element 5 of an i64[N] input reads fine at N = 8 and is an error at N = 3."""
+    lk = gpu
+    ir = """model {
+  init {
+    return
+  }
+  exec(%x: tensor<i64[N]>, %a: tensor<f32[N]>) {
+    dim.read %x[5] -> F
+    %b = kernel "add_f32_gpu"(%a, %a) : tensor<f32[N]>
+    return %b
+  }
+}
+"""
+    m = lk.compile_ir(ir)
+    got = m(G(lk, np.arange(8), np.int64), G(lk, np.ones(8))).numpy()
+    assert np.array_equal(got, np.full(8, 2.0, np.float32))
+    with pytest.raises(LokinferError, match="outside its operand"):
+        m(G(lk, np.arange(3), np.int64), G(lk, np.ones(3)))
 
 
 def test_persistent_kv_cache_written_in_place(gpu):

@@ -45,6 +45,61 @@ def _call_pair(L, heads, cap, pos, seed):
         assert np.array_equal(a, b)
 
 
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    """Collected first in this file, so in a fresh process the entry point's first call (which resolves the device
+    array's address and the error record) happens while a graph is being captured. The graph is replayed with
+    three positions written in place, eager work between the replays, and every replay equals the workspace entry
+    point run eagerly on the same inputs."""
+    from lokinfer_amd import _lib
+
+    L = _lib.lib()
+    L.lk_hip_attention_decode_workspace_bytes.restype = C.c_int64
+    dev = torch.device("cuda", 0)
+    heads, cap = 12, 1024
+    d = 64 * heads
+    g = torch.Generator().manual_seed(9)
+    qkv = torch.randn(1, 3 * d, generator=g).to(dev)
+    bias = (0.1 * torch.randn(3 * d, generator=g)).to(dev)
+    kc0 = torch.randn(cap, d, generator=g).to(dev)
+    vc0 = torch.randn(cap, d, generator=g).to(dev)
+    kc, vc = kc0.clone(), vc0.clone()
+    pos = torch.zeros(1, dtype=torch.int64, device=dev)
+    out = torch.zeros(1, d, device=dev)
+    vp = C.c_void_p
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = L.lk_hip_attention_decode_f32_noalloc(
+                vp(qkv.data_ptr()), vp(kc.data_ptr()), vp(vc.data_ptr()), vp(pos.data_ptr()), vp(bias.data_ptr()),
+                vp(out.data_ptr()), C.c_int64(cap), C.c_int(heads), C.c_int64(cap), C.c_int(1),
+                vp(side.cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    for p in (700, 3, 1023):
+        kc.copy_(kc0)
+        vc.copy_(vc0)
+        pos.fill_(p)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (out.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy())
+        # the workspace entry point, eagerly, on the same inputs
+        kw, vw = kc0.clone(), vc0.clone()
+        ow = torch.zeros(1, d, device=dev)
+        nbytes = L.lk_hip_attention_decode_workspace_bytes(heads, C.c_int64(cap))
+        ws = torch.empty(nbytes // 4, device=dev)
+        rc = L.lk_hip_attention_decode_f32(vp(qkv.data_ptr()), vp(kw.data_ptr()), vp(vw.data_ptr()),
+                                           vp(pos.data_ptr()), vp(bias.data_ptr()), vp(ow.data_ptr()),
+                                           C.c_int64(cap), C.c_int(heads), C.c_int64(cap), C.c_int(1),
+                                           vp(ws.data_ptr()), C.c_int64(nbytes),
+                                           vp(torch.cuda.current_stream(dev).cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert np.isfinite(got[0]).all()
+        for a, b in zip(got, (ow.cpu().numpy(), kw.cpu().numpy(), vw.cpu().numpy())):
+            assert np.array_equal(a, b), p
+
+
 def test_noalloc_decode_attention_matches_workspace_entry_point(gpu):
     from lokinfer_amd import _lib
 
