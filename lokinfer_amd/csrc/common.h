@@ -214,6 +214,16 @@ __device__ __forceinline__ GridItem xcdOrder() {
   const unsigned w = xcd * per + min(xcd, rem) + k;
   return GridItem{static_cast<int>(w % gx), static_cast<int>((w / gx) % gy), static_cast<int>(w / (gx * gy))};
 }
+// The same with y fastest (w = y + gy (x + gx z)): neighbouring row blocks, which read the same B columns, share
+// one L2. The better order for a GEMM whose B is larger than its A.
+__device__ __forceinline__ GridItem xcdOrderYFast() {
+  const unsigned gx = gridDim.x, gy = gridDim.y;
+  const unsigned total = gx * gy * gridDim.z;
+  const unsigned l = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const unsigned per = total / 8, rem = total % 8, xcd = l % 8, k = l / 8;
+  const unsigned w = xcd * per + min(xcd, rem) + k;
+  return GridItem{static_cast<int>((w / gy) % gx), static_cast<int>(w % gy), static_cast<int>(w / (gx * gy))};
+}
 
 // AdaIN affine af [3, C] = (mean, (1 + g) / sqrt(var + eps), b) from per-chunk (mean, M2) statistics st [S, C, 2]
 // of an L-row tensor; gb [2 creal]; channels >= creal get 0. Chunk i = (rho, y) = (i / chunks, i % chunks) holds

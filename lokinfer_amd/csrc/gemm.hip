@@ -55,6 +55,9 @@ struct GemmParams {
   float* part;
   int64_t kSplit;
   int splitk;
+  // work order: row blocks fastest within an XCD's range (B larger than A: an XCD then reads a slice of B and all
+  // of A through its L2), else column blocks fastest
+  int yFast;
 };
 
 constexpr int BK = 16;
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(NT, 2) void gemmSplitKKernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, lk = lane >> 5;
-  const GridItem gi = xcdOrder();  // column blocks of one row block share an XCD's L2
+  const GridItem gi = p.yFast ? xcdOrderYFast() : xcdOrder();
   const int64_t m0 = static_cast<int64_t>(gi.y) * BM, n0 = static_cast<int64_t>(gi.x) * BN;
   const int64_t lastRow = p.m - 1, lastCol = p.n - 1;
   // this workgroup's K range (the whole K without a split)
@@ -826,6 +829,7 @@ static void launchGemm(GemmParams p, hipStream_t s, void* ws = nullptr, int64_t 
     else
       hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
   } else if (AM == lkd::A_ROWMAJOR && aligned) {
+    { const char* e = getenv("LK_YFAST"); p.yFast = e && *e == '1' ? 1 : (e && *e == 'a' ? (p.n > p.m) : 0); }
     // few output tiles: K split over the waves of a workgroup; 32-column tiles unless the 64-column grid alone
     // already gives every CU two workgroups (at M ~ 500, N = 2304 / 3072, 288-384 wide tiles left the last round
     // of workgroups a fraction of the chip: 40.9 -> 32.7 us and 42.8 -> 34.2 us with 32 columns)
