@@ -708,29 +708,39 @@ Status Executable::schedule(int maxLanes) {
 // kernels it waits for, instead of on the kernel just before it. A kernel that enqueued nothing stands for its own
 // dependencies. Every node still completes before the graph does.
 Status Executable::rewire(hipGraph_t graph, const std::vector<Segment>& segs) const {
-  std::vector<std::vector<hipGraphNode_t>> eff(exec_.size());  // what depending on kernel j means
+  // what depending on kernel j means: its tail node, or (a kernel that enqueued nothing) its own dependencies
+  std::vector<std::vector<hipGraphNode_t>> eff(exec_.size());
+  std::vector<std::vector<hipGraphNode_t>> laneDeps(exec_.size()), waitDeps(exec_.size());
   std::vector<int> laneLast(static_cast<size_t>(numLanes_), -1);
   for (size_t j = 0; j < exec_.size(); ++j) {
     const Instr& in = exec_[j];
     if (in.kind != OpKind::Kernel) continue;
-    std::vector<hipGraphNode_t> deps;
-    auto add = [&](int p) {
-      if (p >= 0) deps.insert(deps.end(), eff[static_cast<size_t>(p)].begin(), eff[static_cast<size_t>(p)].end());
-    };
-    add(laneLast[static_cast<size_t>(in.lane)]);
-    for (int w : in.waits) add(w);
-    std::sort(deps.begin(), deps.end());
-    deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
+    const int prev = laneLast[static_cast<size_t>(in.lane)];
+    if (prev >= 0) laneDeps[j] = eff[static_cast<size_t>(prev)];
+    for (int w : in.waits)
+      for (hipGraphNode_t d : eff[static_cast<size_t>(w)])
+        if (std::find(laneDeps[j].begin(), laneDeps[j].end(), d) == laneDeps[j].end() &&
+            std::find(waitDeps[j].begin(), waitDeps[j].end(), d) == waitDeps[j].end())
+          waitDeps[j].push_back(d);
     laneLast[static_cast<size_t>(in.lane)] = static_cast<int>(j);
-    const Segment& sg = segs[j];
-    if (!sg.tail) {
-      eff[j] = deps;
-      continue;
+    if (segs[j].tail) {
+      eff[j] = {segs[j].tail};
+    } else {
+      eff[j] = laneDeps[j];
+      eff[j].insert(eff[j].end(), waitDeps[j].begin(), waitDeps[j].end());
     }
-    eff[j] = {sg.tail};
-    if (sg.before) LKRT_TRY(hipStatus(hipGraphRemoveDependencies(graph, &sg.before, &sg.first, 1), "rewire"));
-    for (hipGraphNode_t d : deps) LKRT_TRY(hipStatus(hipGraphAddDependencies(graph, &d, &sg.first, 1), "rewire"));
   }
+  // the capture's chain edges go first, then every lane's own chain, then the waits across lanes: a node's first
+  // successor is then the next kernel of its lane, so a runtime that follows first successors to form its
+  // streams follows the lanes
+  for (size_t j = 0; j < exec_.size(); ++j)
+    if (exec_[j].kind == OpKind::Kernel && segs[j].tail && segs[j].before)
+      LKRT_TRY(hipStatus(hipGraphRemoveDependencies(graph, &segs[j].before, &segs[j].first, 1), "rewire"));
+  for (const auto* deps : {&laneDeps, &waitDeps})
+    for (size_t j = 0; j < exec_.size(); ++j)
+      if (exec_[j].kind == OpKind::Kernel && segs[j].tail)
+        for (hipGraphNode_t d : (*deps)[j])
+          LKRT_TRY(hipStatus(hipGraphAddDependencies(graph, &d, &segs[j].first, 1), "rewire"));
   return Status();
 }
 
