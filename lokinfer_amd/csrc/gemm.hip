@@ -829,7 +829,7 @@ static void launchGemm(GemmParams p, hipStream_t s, void* ws = nullptr, int64_t 
     else
       hipLaunchKernelGGL((lkd::gemmMfmaKernel<128, 128, AM, BMODE>), grid, dim3(lkd::NT), 0, s, p);
   } else if (AM == lkd::A_ROWMAJOR && aligned) {
-    { const char* e = getenv("LK_YFAST"); p.yFast = e && *e == '1' ? 1 : (e && *e == 'a' ? (p.n > p.m) : 0); }
+    p.yFast = p.n > p.m ? 1 : 0;  // consecutive workgroups on one XCD walk the longer output dimension
     // few output tiles: K split over the waves of a workgroup; 32-column tiles unless the 64-column grid alone
     // already gives every CU two workgroups (at M ~ 500, N = 2304 / 3072, 288-384 wide tiles left the last round
     // of workgroups a fraction of the chip: 40.9 -> 32.7 us and 42.8 -> 34.2 us with 32 columns)
