@@ -11,6 +11,10 @@ from ._lib import LokinferError, registered_kernels  # noqa: F401
 from .compiler import CapturedModel, CompiledModel, Pending, capture, compile, compile_ir, load  # noqa: F401
 from .graph import BufferType, Dim, ScalarType, Sym, TensorType, ceildiv  # noqa: F401
 
+ops.f16_gpu = _f16_gpu  # lk.ops.f16_gpu.<name>_f16_gpu, as in the reference
+
+__version__ = "0.1.0"
+
 # A mutable input type: the caller's buffer (a KV cache) written in place, never an output, bound without a copy
 # (reference python/lokinfer/types.py: MutableType = BufferType).
 MutableType = BufferType

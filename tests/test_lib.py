@@ -163,3 +163,12 @@ def test_decode_step_ops_reject_bad_shapes_before_any_launch():
     assert rc == 1 and "gemv_partial_embed_ln" in msg
     rc, msg = run("gemv_partial_embed_ln_f32_gpu", [V, K, 2] + good[3:])
     assert rc == 1 and "gemv_partial_embed_ln" in msg
+
+
+def test_front_end_names():
+    """The reference's lk.* names resolve (python/lokinfer/__init__.py in lariaus/lokinfer): the f16 family under
+    lk.ops.f16_gpu, the state / mutability names, and a version string."""
+    assert lk.ops.f16_gpu.gemm_f16_gpu is not None
+    for name in ("persistent_buffer", "MutableType", "Pending", "dim_read", "compile", "load", "ceildiv"):
+        assert hasattr(lk, name), name
+    assert isinstance(lk.__version__, str)
