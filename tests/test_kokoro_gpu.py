@@ -121,3 +121,4 @@ def test_compiled_runtime_equals_capture(model, tmp_path, tokens, lanes):
     got = [t.numpy() for t in loaded(*args)]
     for g, w in zip(got, want):
         assert np.array_equal(g, w)
+
