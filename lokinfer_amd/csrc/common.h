@@ -227,78 +227,79 @@ __device__ __forceinline__ GridItem xcdOrderYFast() {
 
 // AdaIN affine af [3, C] = (mean, (1 + g) / sqrt(var + eps), b) from per-chunk (mean, M2) statistics st [S, C, 2]
 // of an L-row tensor; gb [2 creal]; channels >= creal get 0. Chunk i = (rho, y) = (i / chunks, i % chunks) holds
-// the rows of residue class rho of the dilation d from 128 y on: clamp(ceil((L - rho) / d) - 128 y, 0, 128) rows
-// (d = 1: the plain 128-row chunks; chunks with no rows are never read). Two passes in double, as instance norm
-// with a biased variance: mean = sum n_i m_i / L, then M2 = sum (M2_i + n_i (m_i - mean)^2), var = M2 / L.
-// Workgroup of 256 = CH channels x (256 / CH) chunk slices; the slices' partial sums merge through LDS in a fixed
-// order. Many short slices rather than few long ones: the chunk loads are independent, so a slice's time is its
-// number of load round trips, and the kernel sits on the dependency chain between two convs (a generator tensor
-// has ~2300 chunks per channel). Small workgroups, so it still schedules while long conv kernels hold most of the
-// chip on other streams.
-template <int CH>
+// the rows of residue class rho of the dilation d from 128 y on: n_i = clamp(ceil((L - rho) / d) - 128 y, 0, 128)
+// rows (d = 1: the plain 128-row chunks; chunks with no rows are never read). Instance norm with a biased
+// variance, combined in one pass in double around a shift K (the channel's first chunk mean, so the sums carry
+// deviations, not the mean's magnitude): S1 = sum n_i (m_i - K), S2 = sum (M2_i + n_i (m_i - K)^2);
+// mean = K + S1 / L, M2 = S2 - S1^2 / L, var = M2 / L.
+// Workgroup of 256 = 4 channels x 64 chunk slices. The workgroup is kept small on purpose: the kernel sits on the
+// dependency chain between two convs while long conv kernels of other branches hold most of the chip, and a
+// workgroup only starts once a CU has its resources free; 256 threads fit in the slot a retiring conv workgroup
+// leaves (a 1024-thread form waited for up to 0.9 ms there). A slice's chunk loads are independent and issued in
+// batches of 12, so a slice takes a few load round trips even at the generator's ~2300 chunks per channel. The 64
+// slices combine by wave shuffles (16 per wave), then the 4 wave partials in LDS, in a fixed order.
+constexpr int kAffineCh = 4;
+constexpr int kAffineThreads = 256;
 __device__ __forceinline__ void adainAffineSlices(const float* __restrict__ st, const float* __restrict__ gb,
                                                   float* __restrict__ af, int64_t l, int64_t c, int d,
                                                   int64_t chunks, int64_t creal, float eps) {
-  constexpr int SL = 256 / CH;
-  __shared__ double red[SL][CH];
-  const int cl = threadIdx.x % CH, sl = threadIdx.x / CH;
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * CH + cl;
+  constexpr int SL = kAffineThreads / kAffineCh;  // 64 slices
+  constexpr int B = 12;                           // loads in flight per thread
+  __shared__ double red[2][kAffineThreads / 64][kAffineCh];
+  const int cl = threadIdx.x % kAffineCh, sl = threadIdx.x / kAffineCh, wave = threadIdx.x >> 6;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * kAffineCh + cl;
   const bool live = ch < creal && ch < c;
-  const int64_t total = static_cast<int64_t>(d) * chunks;
-  const float2* sp = reinterpret_cast<const float2*>(st);
-  // rows of chunk (rho, yy)
-  auto rows = [&](int64_t rho, int64_t yy) -> double {
-    const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
-    return static_cast<double>(min<int64_t>(max<int64_t>(lr - yy * 128, 0), 128));
-  };
-  double s = 0.0;
+  const int total = static_cast<int>(static_cast<int64_t>(d) * chunks);
+  const int ichunks = static_cast<int>(chunks);
+  const float2* sp = reinterpret_cast<const float2*>(st) + (live ? ch : 0);
+  const double shift = live ? static_cast<double>(sp[0].x) : 0.0;
+  double s1 = 0.0, s2 = 0.0;
   if (live) {
-    int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
-#pragma unroll 4
-    for (int64_t i = sl; i < total; i += SL) {
-      const double n = rows(rho, yy);
-      if (n > 0.0) s += static_cast<double>(sp[i * c + ch].x) * n;
-      yy += SL;
-      while (yy >= chunks) {
-        yy -= chunks;
-        ++rho;
+    for (int i0 = sl; i0 < total; i0 += SL * B) {
+      float2 v[B];
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * SL;
+        v[b] = i < total ? sp[static_cast<int64_t>(i) * c] : make_float2(0.0f, 0.0f);
+      }
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * SL;
+        const int rho = i / ichunks, yy = i - rho * ichunks;
+        const int64_t lr = rho < l ? (l - rho + d - 1) / d : 0;
+        const int64_t n = min<int64_t>(max<int64_t>(lr - static_cast<int64_t>(yy) * 128, 0), 128);
+        if (i < total && n > 0) {
+          const double dn = static_cast<double>(n), dm = static_cast<double>(v[b].x) - shift;
+          s1 += dn * dm;
+          s2 += static_cast<double>(v[b].y) + dn * dm * dm;
+        }
       }
     }
   }
-  red[sl][cl] = s;
-  __syncthreads();
-  double tot = 0.0;
-  for (int w = 0; w < SL; ++w) tot += red[w][cl];
-  const double mean = tot / static_cast<double>(l);
-  __syncthreads();
-  double m2 = 0.0;
-  if (live) {
-    int64_t rho = sl / chunks, yy = sl - (sl / chunks) * chunks;
-#pragma unroll 4
-    for (int64_t i = sl; i < total; i += SL) {
-      const double n = rows(rho, yy);
-      if (n > 0.0) {
-        const float2 v = sp[i * c + ch];
-        const double dm = static_cast<double>(v.x) - mean;
-        m2 += static_cast<double>(v.y) + n * dm * dm;
-      }
-      yy += SL;
-      while (yy >= chunks) {
-        yy -= chunks;
-        ++rho;
-      }
-    }
+  // the wave's 16 slices of each channel: lanes cl + 4 k
+#pragma unroll
+  for (int off = kAffineCh; off < 64; off <<= 1) {
+    s1 += __shfl_xor(s1, off, 64);
+    s2 += __shfl_xor(s2, off, 64);
   }
-  red[sl][cl] = m2;
+  if ((threadIdx.x & 63) < kAffineCh) {
+    red[0][wave][cl] = s1;
+    red[1][wave][cl] = s2;
+  }
   __syncthreads();
-  if (sl == 0 && ch < c) {
+  if (threadIdx.x < kAffineCh && ch < c) {
     if (!live) {
       af[ch] = af[c + ch] = af[2 * c + ch] = 0.0f;
     } else {
-      double M2 = 0.0;
-      for (int w = 0; w < SL; ++w) M2 += red[w][cl];
-      const float var = static_cast<float>(M2 / static_cast<double>(l));
-      af[ch] = static_cast<float>(mean);
+      double t1 = 0.0, t2 = 0.0;
+      for (int w = 0; w < kAffineThreads / 64; ++w) {
+        t1 += red[0][w][cl];
+        t2 += red[1][w][cl];
+      }
+      const double dl = static_cast<double>(l);
+      const double m2 = t2 - t1 * t1 / dl;
+      const float var = static_cast<float>(max(m2, 0.0) / dl);
+      af[ch] = static_cast<float>(shift + t1 / dl);
       af[c + ch] = (1.0f + gb[ch]) / sqrtf(var + eps);
       af[2 * c + ch] = gb[creal + ch];
     }

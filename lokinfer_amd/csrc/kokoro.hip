@@ -68,10 +68,10 @@ __global__ __launch_bounds__(256) void statsKernel(const float* __restrict__ x, 
 }
 
 // AdaIN affine from channel_stats_lc statistics (128-row chunks), 4 channels x 64 chunk slices per workgroup.
-__global__ __launch_bounds__(256) void adainAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
-                                                         float* __restrict__ af, int64_t l, int64_t c, int64_t creal,
-                                                         float eps) {
-  adainAffineSlices<4>(st, gb, af, l, c, 1, (l + kStatChunk - 1) / kStatChunk, creal, eps);
+__global__ __launch_bounds__(kAffineThreads) void adainAffineKernel(const float* __restrict__ st,
+                                                                   const float* __restrict__ gb, float* __restrict__ af,
+                                                                   int64_t l, int64_t c, int64_t creal, float eps) {
+  adainAffineSlices(st, gb, af, l, c, 1, (l + kStatChunk - 1) / kStatChunk, creal, eps);
 }
 
 // act: 1 snake, 2 leaky (0: affine only).
@@ -380,7 +380,7 @@ int lk_hip_channel_stats_lc_f32(const float* x, float* st, int64_t l, int64_t c,
 int lk_hip_adain_affine_lc_f32(const float* st, const float* gb, float* af, int64_t l, int64_t c, int64_t creal,
                                float eps, void* stream) {
   if (l <= 0 || c <= 0 || creal > c) return 1;
-  hipLaunchKernelGGL(lkd::adainAffineKernel, dim3(lkh::ceilDiv(c, 4)), dim3(256), 0,
+  hipLaunchKernelGGL(lkd::adainAffineKernel, dim3(lkh::ceilDiv(c, lkd::kAffineCh)), dim3(lkd::kAffineThreads), 0,
                      static_cast<hipStream_t>(stream), st, gb, af, l, c, creal, eps);
   LK_RET;
 }

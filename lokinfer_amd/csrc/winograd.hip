@@ -347,10 +347,11 @@ __global__ __launch_bounds__(256) void winoSplitReduceKernel(const float* __rest
 
 // AdaIN affine from wino_mm statistics (chunks per residue class of the dilation), 4 channels x 64 chunk slices
 // per workgroup.
-__global__ __launch_bounds__(256) void winoAffineKernel(const float* __restrict__ st, const float* __restrict__ gb,
-                                                       float* __restrict__ af, int64_t l, int64_t c, int d,
-                                                       int64_t chunks, int64_t creal, float eps) {
-  adainAffineSlices<4>(st, gb, af, l, c, d, chunks, creal, eps);
+__global__ __launch_bounds__(kAffineThreads) void winoAffineKernel(const float* __restrict__ st,
+                                                                  const float* __restrict__ gb,
+                                                                  float* __restrict__ af, int64_t l, int64_t c, int d,
+                                                                  int64_t chunks, int64_t creal, float eps) {
+  adainAffineSlices(st, gb, af, l, c, d, chunks, creal, eps);
 }
 
 }  // namespace lkd
@@ -439,7 +440,8 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
                                     int64_t creal, int dilation, int64_t length, float eps, void* stream) {
   if (dilation < 1 || s % dilation != 0 || length < 1 || creal > c) return 1;
-  hipLaunchKernelGGL(lkd::winoAffineKernel, dim3(lkh::ceilDiv(c, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(lkd::winoAffineKernel, dim3(lkh::ceilDiv(c, lkd::kAffineCh)), dim3(lkd::kAffineThreads), 0,
+                     static_cast<hipStream_t>(stream),
                      stats, gb, af, length, c, dilation, s / dilation, creal, eps);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
