@@ -124,15 +124,21 @@ struct WinoMmArgs {
 // and in the epilogue): on grids of more than two workgroups per CU a third wave per SIMD keeps the matrix pipe fed
 // through the other waves' barriers and LDS stores (K = 11 roofline launch 0.574 -> 0.599 of peak); smaller grids
 // leave the third slot empty and run the unconstrained OCC = 2 form (176 VGPRs), which is 0.5% faster there.
-template <int M, int A, int N, int OCC = 2>
+//
+// S: 16-channel sub-chunks per step (one tap group only). A step of one tap group and 16 channels is 8 MFMAs per
+// wave, too few to cover the step's fixed costs (barrier, staging, the first operand reads); S sub-chunks make it
+// 8 S MFMAs. Sub-chunk s of the step's 16 S channels has its own A plane, laid out as a 16-channel step's.
+template <int M, int A, int N, int OCC = 2, int S = 1>
 __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
+  static_assert(S == 1 || N == 1, "sub-chunks only for one tap group");
   constexpr int TT = 64;              // tiles per workgroup
   constexpr int ROWS = TT + N - 1;    // staged V rows (group shift)
   constexpr int LDB = 64 + 8;         // k-major U rows: the two lane halves read 4 rows = 32 banks apart
   constexpr int AQ = ROWS * 4;
-  constexpr int AS = (AQ + 255) / 256;
+  constexpr int AS1 = (AQ + 255) / 256;  // staging float4s per thread and sub-chunk
+  constexpr int AS = S * AS1;
   __shared__ v4w As[2][AS * 256];  // rows past ROWS: every thread stores, so no store sits behind a branch
-  __shared__ float Bs[2][N * 16 * LDB];
+  __shared__ float Bs[2][N * S * 16 * LDB];
   __shared__ float red[2][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
@@ -143,7 +149,7 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   const int64_t t0 = static_cast<int64_t>(wk.y) * TT;
   if (t0 * M >= lor) return;
   const int64_t c0 = static_cast<int64_t>(wk.x) * 64;
-  const int chunks = static_cast<int>(p.ci / 16);
+  const int chunks = static_cast<int>(p.ci / (16 * S));
   const int steps = A * chunks;
   // split-K: this workgroup runs steps [sb, se) of the point-major step sequence; a point cut by the range is
   // folded with AT at the range's end, and AT is linear, so the splits' outputs sum to the full one
@@ -152,35 +158,37 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   const int nsteps = se - sb;
   const int64_t nci = static_cast<int64_t>(N) * p.ci;
 
-  // staging: A rows (ROWS x 4 slots) over 256 threads, U (N x 16 rows x 16 float4) over 256 threads
-  constexpr int BQ = N * 16 * 16;
+  // staging: A rows (S planes of ROWS x 4 slots) over 256 threads, U (N S 16 rows x 16 float4) over 256 threads
+  constexpr int BQ = N * S * 16 * 16;
   constexpr int BSL = BQ / 256;
   // two register sets: step t's operands live in set t & 1, loaded two steps ahead of their LDS store
   v4w ra0[AS], rb0[BSL], ra1[AS], rb1[BSL];
   auto gload = [&](int s, v4w(&ra)[AS], v4w(&rb)[BSL]) {
     const int xi = s / chunks, ch = s - xi * chunks;
-    const float* vx = p.v + (static_cast<int64_t>(rho) * A + xi) * p.rmax * p.ci + static_cast<int64_t>(ch) * 16;
+    const float* vx =
+        p.v + (static_cast<int64_t>(rho) * A + xi) * p.rmax * p.ci + static_cast<int64_t>(ch) * 16 * S;
 #pragma unroll
     for (int i = 0; i < AS; ++i) {
-      const int idx = tid + 256 * i;
+      const int idx = tid + 256 * (i % AS1);
       const int row = min(idx >> 2, ROWS - 1), slot = idx & 3;
       const int64_t t = min<int64_t>(t0 + row, p.rmax - 1);  // rows past rmax only feed tiles never stored
-      ra[i] = *reinterpret_cast<const v4w*>(vx + t * p.ci + 4 * slot);
+      ra[i] = *reinterpret_cast<const v4w*>(vx + t * p.ci + 16 * (i / AS1) + 4 * slot);
     }
     const float* ux = p.u + static_cast<int64_t>(xi) * nci * p.co + c0;
 #pragma unroll
     for (int i = 0; i < BSL; ++i) {
       const int idx = tid + 256 * i;
-      const int c4 = idx & 15, gk = idx >> 4, g = gk >> 4, k = gk & 15;
-      rb[i] = *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 + k) * p.co + 4 * c4);
+      const int c4 = idx & 15, gk = idx >> 4, g = gk / (16 * S), k = gk % (16 * S);
+      rb[i] =
+          *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 * S + k) * p.co + 4 * c4);
     }
   };
   auto sstore = [&](int buf, const v4w(&ra)[AS], const v4w(&rb)[BSL]) {
 #pragma unroll
     for (int i = 0; i < AS; ++i) {
-      const int idx = tid + 256 * i;
+      const int idx = tid + 256 * (i % AS1);
       const int row = idx >> 2, slot = idx & 3;
-      As[buf][row * 4 + (slot ^ ((row >> 2) & 3))] = ra[i];
+      As[buf][(i / AS1) * AS1 * 256 + row * 4 + (slot ^ ((row >> 2) & 3))] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < BSL; ++i) {
@@ -204,27 +212,29 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   auto step = [&](int sl, v4w(&lra)[AS], v4w(&lrb)[BSL], const v4w(&sra)[AS], const v4w(&srb)[BSL]) {
     const int buf = sl & 1, s = sb + sl;
     const int xi = s / chunks, ch = s - xi * chunks;
-    v4w af[N][2];
-    float bq[N][2][4];
+    // operand sets (tap group g, sub-chunk s) = e = g S + s
+    v4w af[N * S][2];
+    float bq[N * S][2][4];
 #pragma unroll
-    for (int g = 0; g < N; ++g) {
-      const int row = arow + g;
+    for (int e = 0; e < N * S; ++e) {
+      const int row = arow + e / S;
+      const int plane = (e % S) * AS1 * 256;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) af[g][h] = As[buf][row * 4 + ((2 * h + lk) ^ ((row >> 2) & 3))];
+      for (int h = 0; h < 2; ++h) af[e][h] = As[buf][plane + row * 4 + ((2 * h + lk) ^ ((row >> 2) & 3))];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bq[g][h][q] = Bs[buf][(g * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
+        for (int q = 0; q < 4; ++q) bq[e][h][q] = Bs[buf][(e * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
     }
     // unconditional (the last two steps reload the final step), so the wait before each LDS store counts only
     // the loads of the set it stores and never the ones just issued
     gload(min(s + 2, se - 1), lra, lrb);
 #pragma unroll
-    for (int g = 0; g < N; ++g)
+    for (int e = 0; e < N * S; ++e)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][h][q], bq[g][h][q], acc, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[e][h][q], bq[e][h][q], acc, 0, 0, 0);
     if (ch == chunks - 1 || s == se - 1) {  // the point (or this split's part of it) is complete: fold it
 #pragma unroll
       for (int j = 0; j < M; ++j) {
@@ -399,7 +409,9 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
   // workgroups; so did splits up to three workgroups per CU at 16 steps), partials in the workspace past its 64 KiB
   // counter area
   const int64_t base = (co / 64) * ((tiles + 63) / 64) * dilation;
-  const int steps = a * static_cast<int>(ci / 16);
+  const int steps = a * static_cast<int>(ci / 16);  // in 16-channel units
+  // one tap group: 48 or 32 channels per pipeline step where they divide Ci
+  const int sub = groups == 1 && tile == 4 ? ((ci / 16) % 3 == 0 ? 3 : (ci / 16) % 2 == 0 ? 2 : 1) : 1;
   int split = 1;
   if (workspace && base < 512) {
     split = static_cast<int>(std::min<int64_t>({8, 512 / base, steps / 32}));
@@ -415,8 +427,16 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
   const bool occ3 = static_cast<int64_t>(grid.x) * grid.y * grid.z > 2 * 256;  // more than two per CU
   if (a == 4)
     hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1>), grid, dim3(256), 0, s, p);
+  else if (a == 6 && occ3 && sub == 3)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 3>), grid, dim3(256), 0, s, p);
+  else if (a == 6 && occ3 && sub == 2)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 2>), grid, dim3(256), 0, s, p);
   else if (a == 6 && occ3)
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3>), grid, dim3(256), 0, s, p);
+  else if (a == 6 && sub == 3)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 3>), grid, dim3(256), 0, s, p);
+  else if (a == 6 && sub == 2)
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 2>), grid, dim3(256), 0, s, p);
   else if (a == 6)
     hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1>), grid, dim3(256), 0, s, p);
   else if (groups == 2 && occ3)

@@ -45,7 +45,9 @@ def _direct(h, w, b, pad, d, res=None, scale=1.0):
 CONVS = [(128, 128, 1000, 11, 5), (128, 128, 777, 7, 3), (256, 256, 300, 3, 1), (128, 128, 1001, 3, 5),
          (256, 256, 513, 7, 1), (128, 128, 37, 11, 3), (16, 64, 5, 3, 1), (128, 64, 1001, 7, 1),
          (32, 128, 70, 5, 2), (64, 64, 9, 12, 1), (16, 64, 40, 4, 1), (128, 128, 2, 3, 1),
-         (256, 256, 1770, 3, 3), (128, 128, 10621, 11, 5)]
+         (256, 256, 1770, 3, 3), (128, 128, 10621, 11, 5),
+         # one tap group with 48- and 32-channel pipeline steps (Ci / 16 divisible by 3, by 2)
+         (144, 64, 500, 3, 1), (48, 128, 301, 3, 2), (96, 64, 257, 3, 1)]
 
 
 @pytest.mark.parametrize("ci,co,l,k,d", CONVS)
