@@ -45,7 +45,7 @@ __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   const float4 bv = *reinterpret_cast<const float4*>(p.bias + 2 * D + c4);
   const int64_t pos = *p.pos;
   DecodeChunk ch;
-  ch.load(p.kc, p.vc, pos, p.cap, s * p.sub, D, c4);
+  ch.load<true>(p.kc, p.vc, pos, p.cap, s * p.sub, D, c4);
   // an out-of-range position writes no cache row and NaN partials, and is recorded; the merge writes NaN
   if (ch.badPos && h == 0 && s == 0 && lane == 0) raiseDeviceError(p.err, LK_DEVERR_POSITION, pos);
   const decF4 q = decF4{q4.x + bq.x, q4.y + bq.y, q4.z + bq.z, q4.w + bq.w} * (0.125f * kLog2e);
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(64) void decodeChunkKernel(DecodeParams p) {
   // a long cache: this wave also takes the next sub - 1 64-key chunks, combined online (stops at pos)
   for (int j = 1; j < p.sub && !ch.badPos && static_cast<int64_t>(s * p.sub + j) * kChunk <= pos; ++j) {
     DecodeChunk nx;
-    nx.load(p.kc, p.vc, pos, p.cap, s * p.sub + j, D, c4);
+    nx.load<true>(p.kc, p.vc, pos, p.cap, s * p.sub + j, D, c4);
     if (p.writeKv && nx.writesRow()) {
       *reinterpret_cast<decF4*>(p.kc + pos * D + c4) = knew;
       *reinterpret_cast<decF4*>(p.vc + pos * D + c4) = vnew;

@@ -24,7 +24,9 @@ struct DecodeChunk {
   bool badPos, dead;
   int g, d4;
 
-  // pos: this step's row; cap: cache rows. Issues the 32 row loads of the chunk.
+  // pos: this step's row; cap: cache rows. Issues the 32 row loads of the chunk; NT: non-temporal loads (a cache
+  // read once, not again in the next step)
+  template <bool NT = false>
   __device__ __forceinline__ void load(const float* kc, const float* vc, int64_t pos, int64_t cap, int chunk,
                                        int64_t D, int64_t c4) {
     const int lane = threadIdx.x & 63;
@@ -39,8 +41,13 @@ struct DecodeChunk {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t row = min<int64_t>(kb + g + 4 * i, ke - 1);
-      kr[i] = *reinterpret_cast<const decF4*>(kc + row * D + c4);
-      vr[i] = *reinterpret_cast<const decF4*>(vc + row * D + c4);
+      if constexpr (NT) {
+        kr[i] = __builtin_nontemporal_load(reinterpret_cast<const decF4*>(kc + row * D + c4));
+        vr[i] = __builtin_nontemporal_load(reinterpret_cast<const decF4*>(vc + row * D + c4));
+      } else {
+        kr[i] = *reinterpret_cast<const decF4*>(kc + row * D + c4);
+        vr[i] = *reinterpret_cast<const decF4*>(vc + row * D + c4);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // all 32 row loads issued here, not spread into the reduction
   }

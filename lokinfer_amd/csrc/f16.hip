@@ -885,6 +885,8 @@ struct GqaChunk {
   int64_t kb, nk;
   int g, d8;
 
+  // NT: non-temporal loads (a cache streamed once, as by the split kernel)
+  template <bool NT = false>
   __device__ __forceinline__ void load(const h16* kc, const h16* vc, int64_t nkeys, int ch, int64_t dk,
                                        int64_t kvOff) {
     const int lane = threadIdx.x & 63;
@@ -896,8 +898,13 @@ struct GqaChunk {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t row = min<int64_t>(kb + g + 4 * i, last);
-      kr[i] = ld8(kc + row * dk + kvOff + 8 * d8);
-      vr[i] = ld8(vc + row * dk + kvOff + 8 * d8);
+      if constexpr (NT) {
+        kr[i] = __builtin_nontemporal_load(reinterpret_cast<const half8*>(kc + row * dk + kvOff + 8 * d8));
+        vr[i] = __builtin_nontemporal_load(reinterpret_cast<const half8*>(vc + row * dk + kvOff + 8 * d8));
+      } else {
+        kr[i] = ld8(kc + row * dk + kvOff + 8 * d8);
+        vr[i] = ld8(vc + row * dk + kvOff + 8 * d8);
+      }
     }
     // all 32 row loads in flight before the first use (left alone, the scheduler spreads them through the dots
     // to save registers, and the chunk then waits on memory several times)
@@ -1009,7 +1016,7 @@ __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
 #pragma unroll
   for (int k = 0; k < H; ++k) qh8[k] = ld8(p.q + (h0 + k) * QHD + 8 * (lane & 15));
   GqaChunk c;
-  c.load(p.kc, p.vc, nk, ch0, dk, kvOff);
+  c.load<true>(p.kc, p.vc, nk, ch0, dk, kvOff);
   float q8[H][8];
 #pragma unroll
   for (int k = 0; k < H; ++k)
@@ -1020,7 +1027,7 @@ __global__ __launch_bounds__(64) void gqaDecodeChunkKernel(GqaParams p) {
 #pragma unroll
   for (int k = 0; k < H; ++k) r[k] = c.compute(q8[k], -1, none, none, p.scale);
   for (int j = 1; j < p.sub; ++j) {
-    c.load(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
+    c.load<true>(p.kc, p.vc, nk, ch0 + j, dk, kvOff);
 #pragma unroll
     for (int k = 0; k < H; ++k) r[k] = GqaChunk::combine(r[k], c.compute(q8[k], -1, none, none, p.scale));
   }
