@@ -50,6 +50,10 @@ __device__ __forceinline__ h16 toH16(float v) {
 }
 
 __device__ __forceinline__ half8 ld8(const h16* p) { return *reinterpret_cast<const half8*>(p); }
+// weight rows streamed once per call (decode GEMVs: gigabytes per token, far above the last-level cache)
+__device__ __forceinline__ half8 ldStream8(const h16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const half8*>(p));
+}
 __device__ __forceinline__ void st8(h16* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
 
 // Sum of squares of a row of k values (k % 8 == 0, 16-byte aligned) over one wave.
@@ -262,8 +266,8 @@ __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
     for (int j = 0; j < CH; ++j) xs[j] = ld8(p.x + 8 * (lane + 64 * j));
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      u[j] = ld8(w0 + 8 * (lane + 64 * j));
-      v[j] = ld8(w1 + 8 * (lane + 64 * j));
+      u[j] = ldStream8(w0 + 8 * (lane + 64 * j));
+      v[j] = ldStream8(w1 + 8 * (lane + 64 * j));
     }
     float r = 1.0f;
     if constexpr (RMS) {
@@ -283,11 +287,11 @@ __global__ __launch_bounds__(256) void gemvF16Kernel(GemvF16Params p) {
 #pragma unroll 4
     for (int64_t i = 0; i < full; ++i) {
       const int64_t c = lane + 64 * i;
-      dot(ld8(p.x + 8 * c), ld8(w0 + 8 * c), ld8(w1 + 8 * c), c, r);
+      dot(ld8(p.x + 8 * c), ldStream8(w0 + 8 * c), ldStream8(w1 + 8 * c), c, r);
     }
     if (lane + 64 * full < chunks) {
       const int64_t c = lane + 64 * full;
-      dot(ld8(p.x + 8 * c), ld8(w0 + 8 * c), ld8(w1 + 8 * c), c, r);
+      dot(ld8(p.x + 8 * c), ldStream8(w0 + 8 * c), ldStream8(w1 + 8 * c), c, r);
     }
   }
   a0 = waveSum(a0);
