@@ -234,6 +234,14 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
                           const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
                           int dilation, int groups, int kernel, int tile, float scale, void* workspace,
                           int64_t workspace_bytes, void* stream);
+/* The same with U given tiled (MI355X backend; the wino_mm ops' u_layout = 1), ut [A, Co / 64, (Ci / 16) N 4 64 4]:
+ * ut[x, cb, (((c N + g) 4 + k4) 64 + j) 4 + q] = U[x, g Ci + 16 c + 4 k4 + q, 64 cb + j] (lokinfer_amd/winograd.py
+ * wino_weights_t), each pipeline step's slab of U contiguous in the order the kernel stages it; identical
+ * arithmetic, so the same bits as lk_hip_wino_mm_lc_f32. */
+int lk_hip_wino_mm_ut_lc_f32(const float* v, const float* ut, const float* bias, const float* res, float* out,
+                             const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
+                             int dilation, int groups, int kernel, int tile, float scale, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 /* stats [s, c, 2] of a length-row output -> af [3, c] = (mean, (1 + g) / sqrt(var + eps), b), gb [2 creal];
  * channels >= creal get 0 */
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,

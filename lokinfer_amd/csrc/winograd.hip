@@ -128,7 +128,15 @@ struct WinoMmArgs {
 // S: 16-channel sub-chunks per step (one tap group only). A step of one tap group and 16 channels is 8 MFMAs per
 // wave, too few to cover the step's fixed costs (barrier, staging, the first operand reads); S sub-chunks make it
 // 8 S MFMAs. Sub-chunk s of the step's 16 S channels has its own A plane, laid out as a 16-channel step's.
-template <int M, int A, int N, int OCC = 2, int S = 1>
+//
+// UT: U given tiled (ops u_layout = 1), Ut [A, Co / 64, (Ci / 16) N 4 64 4]: per point and 64-column block, for
+// each 16-channel chunk and tap group the 16 x 64 slab stored k-quad-major, [k4][col][4] (U row g Ci + 16 c + 4 k4 + q,
+// column 64 cb + col). A step's U is then one contiguous run, staged with coalesced 16-byte loads straight into
+// the LDS order Bs[e * 4 + k4][col] (e = g S + s), and a wave fetches an operand set's B fragments for eight MFMAs
+// with two 16-byte reads: 4 N S reads per step in all, few enough for the LDS counter to wait on each read
+// separately (with U k-major, the 16 N S + 2 N S reads of a step exceed it). The same MFMAs in the same order, so
+// the same bits.
+template <int M, int A, int N, int OCC = 2, int S = 1, bool UT = false>
 __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   static_assert(S == 1 || N == 1, "sub-chunks only for one tap group");
   constexpr int TT = 64;              // tiles per workgroup
@@ -138,7 +146,7 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
   constexpr int AS1 = (AQ + 255) / 256;  // staging float4s per thread and sub-chunk
   constexpr int AS = S * AS1;
   __shared__ v4w As[2][AS * 256];  // rows past ROWS: every thread stores, so no store sits behind a branch
-  __shared__ float Bs[2][N * S * 16 * LDB];
+  __shared__ float Bs[2][UT ? N * S * 16 * 64 : N * S * 16 * LDB];
   __shared__ float red[2][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
@@ -174,13 +182,19 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
       const int64_t t = min<int64_t>(t0 + row, p.rmax - 1);  // rows past rmax only feed tiles never stored
       ra[i] = *reinterpret_cast<const v4w*>(vx + t * p.ci + 16 * (i / AS1) + 4 * slot);
     }
-    const float* ux = p.u + static_cast<int64_t>(xi) * nci * p.co + c0;
+    const float* ux = UT ? p.u + (static_cast<int64_t>(xi) * (p.co / 64) + c0 / 64) * nci * 64 +
+                               static_cast<int64_t>(ch) * (N * S * 1024)
+                         : p.u + static_cast<int64_t>(xi) * nci * p.co + c0;
 #pragma unroll
     for (int i = 0; i < BSL; ++i) {
       const int idx = tid + 256 * i;
-      const int c4 = idx & 15, gk = idx >> 4, g = gk / (16 * S), k = gk % (16 * S);
-      rb[i] =
-          *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 * S + k) * p.co + 4 * c4);
+      if constexpr (UT) {  // the step's slab, in the LDS order
+        rb[i] = *reinterpret_cast<const v4w*>(ux + 4 * idx);
+      } else {
+        const int c4 = idx & 15, gk = idx >> 4, g = gk / (16 * S), k = gk % (16 * S);
+        rb[i] =
+            *reinterpret_cast<const v4w*>(ux + (static_cast<int64_t>(g) * p.ci + ch * 16 * S + k) * p.co + 4 * c4);
+      }
     }
   };
   auto sstore = [&](int buf, const v4w(&ra)[AS], const v4w(&rb)[BSL]) {
@@ -193,8 +207,12 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
     for (int i = 0; i < BSL; ++i) {
       const int idx = tid + 256 * i;
-      const int c4 = idx & 15, gk = idx >> 4;
-      *reinterpret_cast<v4w*>(&Bs[buf][gk * LDB + 4 * c4]) = rb[i];
+      if constexpr (UT) {
+        *reinterpret_cast<v4w*>(&Bs[buf][4 * idx]) = rb[i];
+      } else {
+        const int c4 = idx & 15, gk = idx >> 4;
+        *reinterpret_cast<v4w*>(&Bs[buf][gk * LDB + 4 * c4]) = rb[i];
+      }
     }
   };
 
@@ -222,9 +240,16 @@ __global__ __launch_bounds__(256, OCC) void winoMmKernel(WinoMmArgs p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) af[e][h] = As[buf][plane + row * 4 + ((2 * h + lk) ^ ((row >> 2) & 3))];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (UT) {
+          const v4w b4 = *reinterpret_cast<const v4w*>(&Bs[buf][((e * 4 + 2 * h + lk) * 64 + bcol) * 4]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bq[e][h][q] = Bs[buf][(e * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
+          for (int q = 0; q < 4; ++q) bq[e][h][q] = b4[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bq[e][h][q] = Bs[buf][(e * 16 + 8 * h + 4 * lk + q) * LDB + bcol];
+        }
+      }
     }
     // unconditional (the last two steps reload the final step), so the wait before each LDS store counts only
     // the loads of the set it stores and never the ones just issued
@@ -392,10 +417,14 @@ int lk_hip_wino_tf_lc_f32(const float* x, const float* tr, const float* affine, 
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
-                          const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
-                          int dilation, int groups, int kernel, int tile, float scale, void* workspace,
-                          int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+template <bool UT>
+int winoMm(const float* v, const float* u, const float* bias, const float* res, float* out, const float* tr,
+           float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo, int dilation, int groups, int kernel,
+           int tile, float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   const int a = tile == 2 ? 4 : kernel == 3 ? 6 : 7;
   if (ci % 16 != 0 || co % 64 != 0 || dilation < 1 || groups < 1 || groups > 3 || lo < 1) return 1;
   if (v_rows % (static_cast<int64_t>(dilation) * a) != 0) return 1;  // V holds whole (residue, point) row blocks
@@ -426,27 +455,27 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool occ3 = static_cast<int64_t>(grid.x) * grid.y * grid.z > 2 * 256;  // more than two per CU
   if (a == 4)
-    hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<2, 4, 1, 2, 1, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6 && occ3 && sub == 3)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 3, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6 && occ3 && sub == 2)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 2>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 2, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6 && occ3)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 3, 1, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6 && sub == 3)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 3, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6 && sub == 2)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 2>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 2, UT>), grid, dim3(256), 0, s, p);
   else if (a == 6)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 6, 1, 2, 1, UT>), grid, dim3(256), 0, s, p);
   else if (groups == 2 && occ3)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2, 3, 1, UT>), grid, dim3(256), 0, s, p);
   else if (groups == 2)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 2, 2, 1, UT>), grid, dim3(256), 0, s, p);
   else if (occ3)
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3, 3, 1, UT>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((lkd::winoMmKernel<4, 7, 3, 2, 1, UT>), grid, dim3(256), 0, s, p);
   if (split > 1) {
     hipLaunchKernelGGL(lkd::winoSplitReduceKernel,
                        dim3(static_cast<unsigned>(std::min<int64_t>((lo * co / 4 + 255) / 256, 8192))), dim3(256), 0,
@@ -455,6 +484,26 @@ int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, con
     if (stats && lkh::residueStats(out, stats, lo, co, dilation, p.chunks, s)) return 2;
   }
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lk_hip_wino_mm_lc_f32(const float* v, const float* u, const float* bias, const float* res, float* out,
+                          const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
+                          int dilation, int groups, int kernel, int tile, float scale, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+  return winoMm<false>(v, u, bias, res, out, tr, stats, v_rows, ci, co, lo, dilation, groups, kernel, tile, scale,
+                       workspace, workspace_bytes, stream);
+}
+
+int lk_hip_wino_mm_ut_lc_f32(const float* v, const float* ut, const float* bias, const float* res, float* out,
+                             const float* tr, float* stats, int64_t v_rows, int64_t ci, int64_t co, int64_t lo,
+                             int dilation, int groups, int kernel, int tile, float scale, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  return winoMm<true>(v, ut, bias, res, out, tr, stats, v_rows, ci, co, lo, dilation, groups, kernel, tile, scale,
+                      workspace, workspace_bytes, stream);
 }
 
 int lk_hip_wino_adain_affine_lc_f32(const float* stats, const float* gb, float* af, int64_t s, int64_t c,
@@ -492,26 +541,31 @@ void runWinoTf(ExecCtx& ctx, const KernelArgs& a) {
 
 // wino_mm[_res][_stats]_lc_f32_gpu. ptrs: v, u, b, tr, x, [res], out, [stats]. ints: v(R, Ci), u(A, N Ci, Co),
 // b(Co), tr(T), x(L, Ci), [res(Lo, Co)], out(Lo, Co), [stats(d chunks, Co, 2)], dilation, groups, kernel,
-// padding, tile; floats: [oscale].
+// padding, tile, [u_layout]; floats: [oscale]. u_layout 1 (this backend's addition; absent = 0, the reference's
+// layout): u is U tiled, Ut(A, Co / 64, N Ci 64) (winoMmKernel's UT layout).
 template <bool RES, bool STATS>
 void runWinoMm(ExecCtx& ctx, const KernelArgs& a) {
-  const int64_t vr = a.ints[0], ci = a.ints[1], co = a.ints[4];
+  const int64_t vr = a.ints[0], ci = a.ints[1];
   const int o = RES ? 11 : 9;
   const int at = o + 2 + (STATS ? 3 : 0);
-  const int64_t lo = a.ints[o];
+  const int64_t co = a.ints[o + 1], lo = a.ints[o];
   const int d = static_cast<int>(a.ints[at]), groups = static_cast<int>(a.ints[at + 1]);
   const int k = static_cast<int>(a.ints[at + 2]), tile = static_cast<int>(a.ints[at + 4]);
-  LK_REQUIRE(ctx, a.ints[o + 1] == co && a.ints[3] == groups * ci, "wino_mm: u must be f32[A, N Ci, Co]");
+  const bool ut = a.numInts > static_cast<uint32_t>(at + 5) && a.ints[at + 5] == 1;
+  LK_REQUIRE(ctx,
+             ut ? (a.ints[3] * 64 == co && a.ints[4] == groups * ci * 64)
+                : (a.ints[4] == co && a.ints[3] == groups * ci),
+             "wino_mm: u must be f32[A, N Ci, Co] (u_layout 1: f32[A, Co / 64, N Ci 64])");
   const int64_t alpha = tile == 2 ? 4 : k == 3 ? 6 : 7;  // transform points of this kernel size and tile
   LK_REQUIRE(ctx, a.ints[2] == alpha, "wino_mm: u's leading dim must be the transform's point count");
   LK_REQUIRE(ctx, d >= 1 && vr % (static_cast<int64_t>(d) * alpha) == 0,
              "wino_mm: v rows must be a multiple of dilation * points");
   const int outp = RES ? 6 : 5;
   const float scale = RES && a.numFloats > 0 ? static_cast<float>(a.floats[0]) : 1.0f;
-  if (lk_hip_wino_mm_lc_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), RES ? P<float>(a, 5) : nullptr,
-                            P<float>(a, outp), P<float>(a, 3), STATS ? P<float>(a, outp + 1) : nullptr, vr, ci, co, lo,
-                            d, groups, k, tile, scale, ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes),
-                            ctx.stream))
+  const auto mm = ut ? lk_hip_wino_mm_ut_lc_f32 : lk_hip_wino_mm_lc_f32;
+  if (mm(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), RES ? P<float>(a, 5) : nullptr, P<float>(a, outp),
+         P<float>(a, 3), STATS ? P<float>(a, outp + 1) : nullptr, vr, ci, co, lo, d, groups, k, tile, scale,
+         ctx.workspace, static_cast<int64_t>(ctx.workspaceBytes), ctx.stream))
     ctx.error = "wino_mm: invalid configuration";
 }
 

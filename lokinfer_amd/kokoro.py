@@ -172,14 +172,14 @@ class KokoroGpu:
         return self.conv(h, p + ".conv2", af2, 3, act="leaky", slope=0.2, residual=sc, out_scale=SQRT1_2)[0]
 
     def wino(self, key: str, ci_pad: int, co_pad: int):
-        """(U, tr) of conv weight `key` for the Winograd ops, input channels zero-padded to ci_pad and output
-        channels to co_pad, transformed once on the host."""
+        """(Ut, tr) of conv weight `key` for the Winograd ops (U transposed, the ops' u_layout 1), input channels
+        zero-padded to ci_pad and output channels to co_pad, transformed once on the host."""
         k = f"{key}#wino{ci_pad}x{co_pad}"
         if k not in self._g:
             w = self.sd[key]
             wp = np.zeros((co_pad, ci_pad, w.shape[2]), np.float32)
             wp[: w.shape[0], : w.shape[1]] = w
-            u, tr = winograd.wino_weights(wp)
+            u, tr = winograd.wino_weights_t(wp)
             self._g[k] = (from_numpy(u, device="gpu", copy=True), from_numpy(tr, device="gpu", copy=True))
         return self._g[k]
 
@@ -201,7 +201,7 @@ class KokoroGpu:
             kw = {"alpha": alpha} if act == "snake" else {"slope": slope} if act == "leaky" else {}
             y = ops.conv1d_wino_lc_f32_gpu(x, u, bias, tr, k, residual=residual, out_scale=out_scale,
                                            padding=pad, dilation=d, affine=af if act != "none" else None,
-                                           stats=stats, **kw)
+                                           stats=stats, u_layout=1, **kw)
             return (y + (d,)) if stats else (y, None, 1)
         w = self.g(p + ".weight", _w_lc) if cop == co else self.const(
             f"{p}#lc{cop}", lambda: _w_lc(np.concatenate([self.sd[p + ".weight"],

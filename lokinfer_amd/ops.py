@@ -339,16 +339,19 @@ def wino_tf_lc_f32_gpu(x, tr, dilation, groups, kernel, padding, tile, affine=No
 
 
 def wino_mm_lc_f32_gpu(v, u, b, tr, x, dilation, groups, kernel, padding, tile, residual=None, out_scale=1.0,
-                       stats=False):
+                       stats=False, u_layout=0):
     """Per-point GEMM + AT output transform + bias [+ residual * out_scale] [+ per-128-row channel (mean, M2)],
-    out [Lo, Co], stats [d * chunks, Co, 2]. Reference winograd.py:157-202."""
+    out [Lo, Co], stats [d * chunks, Co, 2]. Reference winograd.py:157-202. u_layout = 1 (MI355X backend): u is
+    U tiled, f32[A, Co / 64, groups * Ci * 64] (winograd.wino_weights_t), the same result."""
     _wino_attrs_ok(x, dilation, groups, kernel, padding, tile)
     _f32(v, rank=2)
     _f32(u, rank=3)
     _f32(b, tr, rank=1)
-    a, nci, co = u.shape
+    check(u_layout in (0, 1), "u_layout must be 0 or 1")
+    a, nci, co = (u.shape[0], u.shape[2] // 64, u.shape[1] * 64) if u_layout else u.shape
     check(a == _wino.alpha_of(kernel, tile), "u must come from wino_weights for this kernel size")
-    check(nci == groups * x.shape[1], "u must be f32[A, groups * Ci, Co]")
+    check(nci == groups * x.shape[1] and (not u_layout or u.shape[2] % 64 == 0),
+          "u must be f32[A, groups * Ci, Co] (u_layout 1: [A, Co / 64, groups * Ci * 64])")
     check(co % 64 == 0, "Co must be a multiple of 64")
     check(b.shape[0] == co, "bias must be f32[Co]")
     check(tr.shape[0] == a * (a + tile), "bad transform table")
@@ -358,6 +361,8 @@ def wino_mm_lc_f32_gpu(v, u, b, tr, x, dilation, groups, kernel, padding, tile, 
     if stats:
         shapes.append((_wino.stats_chunks(lo, dilation) * dilation, co, 2))
     attrs = dict(dilation=int(dilation), groups=int(groups), kernel=int(kernel), padding=int(padding), tile=int(tile))
+    if u_layout:
+        attrs["u_layout"] = 1
     sfx = "_stats" if stats else ""
     if residual is None:
         check(out_scale == 1.0, "out_scale needs a residual")
@@ -382,7 +387,7 @@ def wino_adain_affine_lc_f32_gpu(stats, gb, length, dilation=1, eps=1e-5):
 
 
 def conv1d_wino_lc_f32_gpu(x, u, b, tr, kernel, residual=None, out_scale=1.0, padding=0, dilation=1, affine=None,
-                           alpha=None, slope=None, stats=False):
+                           alpha=None, slope=None, stats=False, u_layout=0):
     """(conv1d(h, w) + b [+ residual]) * out_scale with (u, tr) = winograd.wino_weights(w), h = x, or
     snake(affine(x), alpha), or leaky(affine(x), slope); stats=True also returns the output's channel statistics
     for wino_adain_affine_lc_f32_gpu. Two launches: transform, GEMM. Reference winograd.py:221-247."""
@@ -393,7 +398,8 @@ def conv1d_wino_lc_f32_gpu(x, u, b, tr, kernel, residual=None, out_scale=1.0, pa
     if affine is None:
         check(alpha is None and slope is None, "alpha / slope need an affine")
     v = wino_tf_lc_f32_gpu(x, tr, affine=affine, alpha=alpha, slope=slope, **attrs)
-    return wino_mm_lc_f32_gpu(v, u, b, tr, x, residual=residual, out_scale=out_scale, stats=stats, **attrs)
+    return wino_mm_lc_f32_gpu(v, u, b, tr, x, residual=residual, out_scale=out_scale, stats=stats, u_layout=u_layout,
+                              **attrs)
 
 
 # ---- transformer --------------------------------------------------------------------------------------------

@@ -122,6 +122,23 @@ def wino_weights(w: np.ndarray, tile: int = TILE) -> tuple[np.ndarray, np.ndarra
     return np.ascontiguousarray(u, dtype=np.float32), tr.astype(np.float32)
 
 
+def tile_u(u: np.ndarray, groups: int) -> np.ndarray:
+    """U f32[A, n Ci, Co] -> the wino_mm ops' tiled form (u_layout = 1) f32[A, Co / 64, n Ci 64]:
+    ut[x, cb, (((c n + g) 4 + k4) 64 + j) 4 + q] = U[x, g Ci + 16 c + 4 k4 + q, 64 cb + j] (Ci % 16 == 0,
+    Co % 64 == 0): per point, 64-column block, 16-channel chunk and tap group, a k-quad-major 16 x 64 slab."""
+    a, nci, co = u.shape
+    ci = nci // groups
+    t = u.reshape(a, groups, ci // 16, 4, 4, co // 64, 64)  # x, g, c, k4, q, cb, j
+    t = t.transpose(0, 5, 2, 1, 3, 6, 4)  # x, cb, c, g, k4, j, q
+    return np.ascontiguousarray(t.reshape(a, co // 64, nci * 64))
+
+
+def wino_weights_t(w: np.ndarray, tile: int = TILE) -> tuple[np.ndarray, np.ndarray]:
+    """(Ut, tr): wino_weights' U in the wino_mm ops' tiled form (u_layout = 1, tile_u)."""
+    u, tr = wino_weights(w, tile)
+    return tile_u(u, variant(w.shape[2])[1]), tr
+
+
 def tiles_rows(lo: int, dilation: int, groups: int, tile: int, kernel: int) -> int:
     """Rows of V: d * A * rmax, rmax = ceil(ceil(Lo / d) / 128) * (128 / tile) + groups - 1."""
     per_class = (lo + dilation - 1) // dilation

@@ -226,3 +226,26 @@ def test_wino_large_grid_instantiations(gpu, ci, co, l, k, d):
     gb = (r.standard_normal(2 * co) * 0.3).astype(np.float32)
     af2 = lk.ops.wino_adain_affine_lc_f32_gpu(st, G(lk, gb), l, dilation=d).numpy()
     _check_affine(af2, yn, gb, co)
+
+
+@pytest.mark.parametrize("ci,co,l,k,d", CONVS[:10] + [(1104, 1024, 300, 3, 1), (144, 64, 500, 3, 1)] + LARGE[:2])
+def test_wino_u_layouts_agree(gpu, ci, co, l, k, d):
+    """u_layout 1 (U transposed, the Kokoro graph's form) runs the same MFMAs in the same order as the reference
+    layout: the outputs and statistics are the same bits (small grids through the split-K path too)."""
+    lk = gpu
+    r, x, w, b = _case(ci + 2 * l + k, l, ci, co, k)
+    pad = _pad(k, d)
+    u, tr = W.wino_weights(w)
+    ut, tr2 = W.wino_weights_t(w)
+    n = W.variant(k)[1]
+    # the tiled element (x, cb, c, g, k4, j, q) is U[x, g Ci + 16 c + 4 k4 + q, 64 cb + j]
+    t = ut.reshape(u.shape[0], co // 64, ci // 16, n, 4, 64, 4)
+    x_, cb, c, g, k4, j, q = 1, co // 64 - 1, ci // 16 - 1, n - 1, 2, 37, 3
+    assert t[x_, cb, c, g, k4, j, q] == u[x_, g * ci + 16 * c + 4 * k4 + q, 64 * cb + j]
+    assert np.array_equal(tr, tr2) and np.array_equal(np.sort(ut.ravel()), np.sort(u.ravel()))
+    args = (G(lk, x), None, G(lk, b), G(lk, tr), k)
+    y0, s0 = lk.ops.conv1d_wino_lc_f32_gpu(args[0], G(lk, u), *args[2:], padding=pad, dilation=d, stats=True)
+    y1, s1 = lk.ops.conv1d_wino_lc_f32_gpu(args[0], G(lk, ut), *args[2:], padding=pad, dilation=d, stats=True,
+                                           u_layout=1)
+    assert np.array_equal(y0.numpy(), y1.numpy())
+    assert np.array_equal(s0.numpy(), s1.numpy())
