@@ -282,8 +282,8 @@ def wino_tiles(lo: int, d: int, m: int = 4) -> int:
 
 
 def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
-    """The dominant kernel of the Kokoro forward: the Winograd GEMM (winoMmKernel<4,7,3,3>, wino_mm_lc_f32_gpu) of a
-    generator stage-1 resblock conv (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11 as 3 nested
+    """The dominant kernel of the Kokoro forward: the Winograd GEMM (winoMmKernel<4,7,3,3>, wino_mm_lc_f32_gpu with
+    U tiled, u_layout 1, as the Kokoro graph runs it) of a generator stage-1 resblock conv (L = 120 F + 1 rows at 487 tokens, 128 -> 128 channels, K = 11 as 3 nested
     F(4,4) tap groups, d = 5). Its algorithm is A = 7 point GEMMs over (group, channel): 2 A T (N Ci) Co FLOPs
     per launch for T output tiles of 4 rows. The whole conv (input transform + GEMM, snake prologue) is timed
     beside it and reported against the direct conv's 2 L Ci Co K FLOPs. With calibrate, also launches add_f32_gpu
@@ -295,16 +295,16 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
     l, c, k, d = ROOFLINE_SHAPE
     pad = d * (k - 1) // 2
     G = lambda a: lk.from_numpy(np.ascontiguousarray(a, np.float32), device="gpu", copy=True)  # noqa: E731
-    u, tr = W.wino_weights(rng.standard_normal((c, c, k)) / np.sqrt(c * k))
+    u, tr = W.wino_weights_t(rng.standard_normal((c, c, k)) / np.sqrt(c * k))
     x, u, tr, b = G(rng.standard_normal((l, c))), G(u), G(tr), G(rng.standard_normal(c))
     af = G(np.stack([np.zeros(c), np.ones(c), np.zeros(c)]))
     alpha = G(np.ones(c))
     _, n = W.variant(k)
     attrs = dict(dilation=d, groups=n, kernel=k, padding=pad, tile=4)
     v = lk.ops.wino_tf_lc_f32_gpu(x, tr, affine=af, alpha=alpha, **attrs)
-    mm = lambda: lk.ops.wino_mm_lc_f32_gpu(v, u, b, tr, x, **attrs)  # noqa: E731
+    mm = lambda: lk.ops.wino_mm_lc_f32_gpu(v, u, b, tr, x, u_layout=1, **attrs)  # noqa: E731
     conv = lambda: lk.ops.conv1d_wino_lc_f32_gpu(x, u, b, tr, k, padding=pad, dilation=d, affine=af,  # noqa: E731
-                                                 alpha=alpha)
+                                                 alpha=alpha, u_layout=1)
     mm()
     ms = statistics.mean(event_times(mm, launches))
     conv()
@@ -319,7 +319,8 @@ def roofline_wino(launches: int = 20, calibrate: bool = False) -> dict:
     a = W.alpha_of(k)
     flops = 2.0 * a * wino_tiles(l, d) * (n * c) * c
     direct = 2.0 * l * c * c * k
-    return {"kernel": "winoMmKernel<4,7,3,3> (wino_mm_lc_f32_gpu: K = 11 Winograd GEMM, generator stage 1)",
+    return {"kernel": "winoMmKernel<4,7,3,3,1,true> (wino_mm_lc_f32_gpu, tiled U: K = 11 Winograd GEMM, "
+                      "generator stage 1)",
             "bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": F32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS,
             "traffic": measured_traffic(), "avg_launch_ms": ms, "flops_per_launch": flops,
