@@ -57,6 +57,11 @@ def _w_convt(a: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(a.transpose(0, 2, 1).reshape(ci, k * co))
 
 
+def _w_convt_nt(a: np.ndarray) -> np.ndarray:
+    """ConvTranspose1d weight [Ci, Co, K] -> [K * Co, Ci], the NT GEMM's form of _w_convt (its transpose)."""
+    return np.ascontiguousarray(_w_convt(a).T)
+
+
 def _vec_pad(a: np.ndarray, n: int) -> np.ndarray:
     out = np.zeros(n, np.float32)
     out[: a.shape[0]] = a
@@ -252,18 +257,20 @@ class KokoroGpu:
         M = "bert.encoder.embedding_hidden_mapping_in"
         h = ops.gemm_bias_f32_gpu(e, self.g(M + ".weight", _t), self.g(M + ".bias"))
         L = "bert.encoder.albert_layer_groups.0.albert_layers.0."
-        wqkv = self.const("albert#wqkv", lambda: np.concatenate(
-            [self.sd[L + f"attention.{n}.weight"].T for n in ("query", "key", "value")], axis=1))
+        # the plain projections run as NT GEMMs on the [out, in] weights (the GEMM's B fragments are then 16-byte
+        # runs of K); the result is the reference's x . W^T
+        wqkv = self.const("albert#wqkv_nt", lambda: np.concatenate(
+            [self.sd[L + f"attention.{n}.weight"] for n in ("query", "key", "value")], axis=0))
         bqkv = self.const("albert#bqkv", lambda: np.concatenate(
             [self.sd[L + f"attention.{n}.bias"] for n in ("query", "key", "value")]))
         for _ in range(12):
-            a = ops.attention_qkv_sg_f32_gpu(ops.gemm_f32_gpu_mps(h, wqkv), bqkv, heads=12)
-            a = ops.gemm_f32_gpu_mps(a, self.g(L + "attention.dense.weight", _t))
+            a = ops.attention_qkv_sg_f32_gpu(ops.gemm_nt_f32_gpu_mps(h, wqkv), bqkv, heads=12)
+            a = ops.gemm_nt_f32_gpu_mps(a, self.g(L + "attention.dense.weight"))
             h = ops.add_bias_layernorm_f32_gpu(a, self.g(L + "attention.dense.bias"), h,
                                                self.g(L + "attention.LayerNorm.weight"),
                                                self.g(L + "attention.LayerNorm.bias"), eps=1e-12)
             f = ops.gemm_steel_f32_gpu(h, self.g(L + "ffn.weight", _t), self.g(L + "ffn.bias"), act="gelu")
-            f = ops.gemm_f32_gpu_mps(f, self.g(L + "ffn_output.weight", _t))
+            f = ops.gemm_nt_f32_gpu_mps(f, self.g(L + "ffn_output.weight"))
             h = ops.add_bias_layernorm_f32_gpu(f, self.g(L + "ffn_output.bias"), h,
                                                self.g(L + "full_layer_layer_norm.weight"),
                                                self.g(L + "full_layer_layer_norm.bias"), eps=1e-12)
@@ -355,7 +362,7 @@ class KokoroGpu:
         # generator
         for i, (k_up, u) in enumerate(((20, 10), (12, 6))):
             x = ops.leaky_lc_f32_gpu(x, 0.1)
-            y = ops.gemm_f32_gpu_mps(x, self.g(G + f"ups.{i}.weight", _w_convt))  # [Lin, K * Co]
+            y = ops.gemm_nt_f32_gpu_mps(x, self.g(G + f"ups.{i}.weight", _w_convt_nt))  # [Lin, K * Co]
             ctx.join(self.streams[2 + i])
             x = ops.convt_gather_lc_f32_gpu(y, self.g(G + f"ups.{i}.bias"), k_up, u, (k_up - u) // 2,
                                             add=xs_stage[i], reflect_left=(i == 1))
