@@ -200,6 +200,13 @@ int lk_hip_argmax_f32(const float* x, int64_t* out, int64_t rows, int64_t n, voi
 /* x [T, I], w_ih [8H, I], w_hh_t [H, 8H] (W_hh^T), b [8H] = b_ih + b_hh -> out [T, 2H]; workspace >= T * 8H floats */
 int lk_hip_lstm_bidir_f32(const float* x, const float* w_ih, const float* w_hh_t, const float* b, float* out,
                           int64_t t, int64_t in, int64_t h, void* workspace, int64_t workspace_bytes, void* stream);
+/* Two lk_hip_lstm_bidir_f32 of the same length T (H = 256) in one recurrence launch (MI355X backend; no reference
+ * counterpart: the Kokoro graph runs its text encoder's BiLSTM beside the duration encoder's first). Workspace:
+ * 2 (ceil256(T 8H 4) + 8384) bytes. */
+int lk_hip_lstm_bidir2_f32(const float* x1, const float* wih1, const float* whhT1, const float* b1, float* out1,
+                           int64_t in1, const float* x2, const float* wih2, const float* whhT2, const float* b2,
+                           float* out2, int64_t in2, int64_t t, int64_t h, void* workspace, int64_t workspaceBytes,
+                           void* stream);
 int lk_hip_repeat_interleave_f32(const float* x, const int64_t* dur, float* out, int64_t t, int64_t c, int64_t frames,
                                  void* stream);
 int lk_hip_adalayernorm_f32(const float* x, const float* gb, float* out, int64_t r, int64_t c, float eps,

@@ -16,6 +16,8 @@
 #include "lokinfer_hip.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 namespace lkd {
 
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(1024) void lstmRecurrenceKernel(const float* __rest
 // KW values of h(t-1) that its own lanes polled: they pass through a wave-private LDS slice (no workgroup barrier
 // before the dot products). The waves' partial sums meet at one barrier; then wave 0 applies one activation per
 // lane (its gate row), gathers the four gates of each unit into row 0 with permlane swaps, updates the cell and
-// publishes h(t) as 64-bit words {tag = step + 1, value} with agent-scope atomic stores. Every wave then polls its
+// publishes h(t) as 64-bit words {tag = step + 1, value} (single 8-byte stores, see storeWord). Every wave then polls its
 // KW words of h(t) until the tags match. No fences, no counters: the tag orders each value on its own. The gate
 // pre-activations of the next step are loaded while wave 0 polls.
 // The words are double-buffered by step parity: a writer can be one step ahead of a reader (it only needs the
@@ -114,18 +116,97 @@ __device__ __forceinline__ void gatherGates(float v, float& i, float& f, float& 
   o = __uint_as_float(p3[1]);
 }
 
-__global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float* __restrict__ g,
-                                                                    const float* __restrict__ whhT,
-                                                                    float* __restrict__ out,
-                                                                    unsigned long long* xbuf,
-                                                                    unsigned long long* err, int64_t t) {
+// Up to two independent LSTMs of the same length in one launch (2 kLstmWgs workgroups each): the Kokoro text
+// encoder's BiLSTM runs beside the duration encoder's first one instead of as a launch of its own.
+struct LstmJobs {
+  const float* g[2];
+  const float* whhT[2];
+  float* out[2];
+  unsigned long long* xbuf[2];
+};
+
+// Exchange word I/O. kXcd: every workgroup of a direction runs on one XCD, so the words meet in that XCD's L2.
+// A non-temporal (nt) load does not allocate in, or hit, the CU's vector cache and is served by the L2 that the
+// writer's store wrote through to; a plain or sc0 load can keep returning a stale vector-cache line. Measured
+// round trip between two workgroups of one XCD: 0.55 us with nt words against 1.06 us with the agent-scope (sc1)
+// accesses of kXcd = false, which stay coherent across XCDs (1.42 us between two XCDs; nt words are not).
+template <bool kXcd>
+__device__ __forceinline__ unsigned long long loadWord(const unsigned long long* p) {
+  if constexpr (kXcd) {
+    unsigned long long w;
+    asm volatile("global_load_dwordx2 %0, %1, off nt\n\ts_waitcnt vmcnt(0)" : "=v"(w) : "v"(p) : "memory");
+    return w;
+  } else {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+template <bool kXcd>
+__device__ __forceinline__ void storeWord(unsigned long long* p, unsigned long long w) {
+  if constexpr (kXcd) asm volatile("global_store_dwordx2 %0, %1, off nt" : : "v"(p), "v"(w) : "memory");
+  else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kXcds = 8;              // XCDs of an MI355X
+constexpr int kLstmXcdSlots = 32;     // workgroups launched per XCD and direction team (16 claim a unit slice)
+constexpr int kLstmXbufWords = 4 * 256 + 24;  // [direction][parity][256] exchange words + team formation words
+
+// kXcd = false: workgroup bid = blockIdx.x % (2 kLstmWgs) of job blockIdx.x / (2 kLstmWgs); the words live
+// wherever the workgroups run. kXcd = true: a direction team is kLstmWgs workgroups of one XCD (read from the
+// XCC_ID hardware register). Dispatch deals workgroups to the XCDs round robin from wherever the previous
+// dispatch stopped, so the mapping is formed at run time: the first workgroup to arrive on an XCD takes the next
+// team ticket (job = ticket / 2, direction = ticket % 2) and publishes it, the next kLstmWgs - 1 read it and take
+// unit slices 1.., and every later arrival (or one whose XCD drew a ticket beyond the teams) exits. The grid
+// launches kLstmXcdSlots workgroups per XCD, so every XCD that draws a ticket also receives its kLstmWgs members.
+template <bool kXcd>
+__global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(LstmJobs jobs, unsigned long long* err,
+                                                                    int64_t t, int teams) {
   constexpr int H = 256;
   constexpr int KW = H / kLstmWaves;  // k per wave
   __shared__ float4 hsw[kLstmWaves][KW / 4];  // wave w: h(t-1)[KW w .. KW w + KW - 1]
   // wave w's partial dot product of each gate row, double-buffered by step parity: a wave w >= 1 may finish step
   // s (it polls other workgroups' words only) and write step s + 1's partials before wave 0 has read step s's
   __shared__ float part[2][kLstmWaves][64];
-  const int dir = blockIdx.x / kLstmWgs, b = blockIdx.x % kLstmWgs;
+  int job, dir, b;
+  if constexpr (kXcd) {
+    __shared__ int claim[2];
+    unsigned long long* ctl = jobs.xbuf[0] + 4 * H;  // [0, 8): per-XCD arrivals, [8]: tickets, [16, 24): team + 1
+    if (threadIdx.x == 0) {
+      const int xcc = static_cast<int>(__builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11))) & 7;
+      const int slot = static_cast<int>(
+          __hip_atomic_fetch_add(ctl + xcc, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      int team = teams;  // none
+      if (slot == 0) {
+        team = static_cast<int>(__hip_atomic_fetch_add(ctl + 8, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        __hip_atomic_store(ctl + 16 + xcc, static_cast<unsigned long long>(team) + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      } else if (slot < kLstmWgs) {
+        unsigned long long v = 0;
+        for (long long spins = 0; (v = __hip_atomic_load(ctl + 16 + xcc, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)) == 0;)
+          if (++spins > kLstmSpinLimit) {
+            lkd::raiseDeviceError(err, LK_DEVERR_EXCHANGE_TIMEOUT, -1);
+            break;
+          }
+        if (v) team = static_cast<int>(v - 1);
+      }
+      claim[0] = slot;
+      claim[1] = team;
+    }
+    __syncthreads();
+    if (claim[0] >= kLstmWgs || claim[1] >= teams) return;
+    job = claim[1] / 2;
+    dir = claim[1] % 2;
+    b = claim[0];
+  } else {
+    job = blockIdx.x / (2 * kLstmWgs);
+    const int bid = blockIdx.x % (2 * kLstmWgs);
+    dir = bid / kLstmWgs;
+    b = bid % kLstmWgs;
+  }
+  const float* __restrict__ g = jobs.g[job];
+  const float* __restrict__ whhT = jobs.whhT[job];
+  float* __restrict__ out = jobs.out[job];
+  unsigned long long* xbuf = jobs.xbuf[job];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ld = 8 * H;
   const int gate = lane >> 4, unit = lane & 15;
@@ -181,7 +262,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
         c = fg * c + ig * gg;
         const float hv = ok ? og * tanhHw(c) : __builtin_nanf("");
         const unsigned long long word = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(hv);
-        __hip_atomic_store(xb + b * kLstmUnits + lane, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        storeWord<kXcd>(xb + b * kLstmUnits + lane, word);
         out[tt * 2 * H + dir * H + b * kLstmUnits + lane] = hv;
       }
       if (step + 1 < t) gv = g[(dir == 0 ? step + 1 : t - 2 - step) * ld + col];
@@ -192,7 +273,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
       unsigned long long word = 0ull;
       long long spins = 0;
       while (ok) {
-        word = __hip_atomic_load(xb + KW * wave + lane % KW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        word = loadWord<kXcd>(xb + KW * wave + lane % KW);
         if (static_cast<unsigned>(word >> 32) == tag) break;
         if (++spins > kLstmSpinLimit) {
           ok = false;
@@ -205,6 +286,30 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(const float
           ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
   }
+}
+
+// The XCD-local exchange needs all eight XCDs of an MI355X in one device (256 CUs, SPX mode); LK_LSTM_EXCHANGE=agent
+// selects the agent-scope exchange anyway (the two give identical bits: only the words' cache path differs).
+inline bool lstmXcdLocal() {
+  const char* e = getenv("LK_LSTM_EXCHANGE");
+  if (e && strcmp(e, "agent") == 0) return false;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  static int cached[64] = {};  // 0 unknown, 1 XCD-local, 2 agent
+  if (dev >= 0 && dev < 64 && cached[dev]) return cached[dev] == 1;
+  const bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                  cus == kXcds * 32;
+  if (dev >= 0 && dev < 64) cached[dev] = ok ? 1 : 2;
+  return ok;
+}
+
+inline void launchLstm(const LstmJobs& jobs, int njobs, int64_t t, hipStream_t s) {
+  if (lstmXcdLocal())
+    hipLaunchKernelGGL(lstmPersistentKernel<true>, dim3(kXcds * kLstmXcdSlots), dim3(kLstmThreads), 0, s, jobs,
+                       lkh::deviceErrorRecord(), t, 2 * njobs);
+  else
+    hipLaunchKernelGGL(lstmPersistentKernel<false>, dim3(2 * njobs * kLstmWgs), dim3(kLstmThreads), 0, s, jobs,
+                       lkh::deviceErrorRecord(), t, 2 * njobs);
 }
 
 // Each workgroup scans dur (T <= 8192) into LDS, then gathers its rows: row f copies x[token(f)], token(f) =
@@ -299,16 +404,41 @@ int lk_hip_lstm_bidir_f32(const float* x, const float* wih, const float* whhT, c
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;
-  const int64_t xBytes = 4 * 256 * 8;  // [direction][parity][256] exchange words
+  const int64_t xBytes = lkd::kLstmXbufWords * 8;
   if (h == 256 && workspaceBytes >= gBytes + xBytes) {
     auto* xbuf = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + gBytes);
-    hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(4), dim3(256), 0, s, xbuf, 4 * 256);
-    hipLaunchKernelGGL(lkd::lstmPersistentKernel, dim3(2 * lkd::kLstmWgs), dim3(lkd::kLstmThreads), 0, s, g, whhT,
-                       out, xbuf, lkh::deviceErrorRecord(), t);
+    hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(5), dim3(256), 0, s, xbuf, lkd::kLstmXbufWords);
+    const lkd::LstmJobs jobs{{g, g}, {whhT, whhT}, {out, out}, {xbuf, xbuf}};
+    lkd::launchLstm(jobs, 1, t, s);
   } else {
     hipLaunchKernelGGL(lkd::lstmRecurrenceKernel, dim3(2), dim3(static_cast<unsigned>(4 * h)), 0, s, g, whhT, out,
                        t, static_cast<int>(h));
   }
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Two bidirectional LSTMs of the same length T and H = 256 in one recurrence launch (4 x 16 workgroups); each
+// one's arithmetic is lk_hip_lstm_bidir_f32's. Workspace: two gate planes and two exchange buffers.
+int lk_hip_lstm_bidir2_f32(const float* x1, const float* wih1, const float* whhT1, const float* b1, float* out1,
+                           int64_t in1, const float* x2, const float* wih2, const float* whhT2, const float* b2,
+                           float* out2, int64_t in2, int64_t t, int64_t h, void* workspace, int64_t workspaceBytes,
+                           void* stream) {
+  if (h != 256 || t < 1) return 1;
+  const int64_t gBytes = ((t * 8 * h * 4 + 255) / 256) * 256;
+  const int64_t xBytes = lkd::kLstmXbufWords * 8;
+  if (!workspace || workspaceBytes < 2 * gBytes + 2 * xBytes) return 3;
+  char* ws = static_cast<char*>(workspace);
+  float* g1 = reinterpret_cast<float*>(ws);
+  float* g2 = reinterpret_cast<float*>(ws + gBytes);
+  auto* xb1 = reinterpret_cast<unsigned long long*>(ws + 2 * gBytes);
+  auto* xb2 = reinterpret_cast<unsigned long long*>(ws + 2 * gBytes + xBytes);
+  int rc = lk_hip_gemm_f32(x1, wih1, b1, nullptr, g1, t, 8 * h, in1, 1, 0, 1.0f, nullptr, 0, stream);
+  if (!rc) rc = lk_hip_gemm_f32(x2, wih2, b2, nullptr, g2, t, 8 * h, in2, 1, 0, 1.0f, nullptr, 0, stream);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(lkd::lstmClearKernel, dim3(9), dim3(256), 0, s, xb1, 2 * lkd::kLstmXbufWords);  // adjacent
+  const lkd::LstmJobs jobs{{g1, g2}, {whhT1, whhT2}, {out1, out2}, {xb1, xb2}};
+  lkd::launchLstm(jobs, 2, t, s);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
@@ -345,6 +475,22 @@ int lk_hip_concat_bcast_f32(const float* x, const float* v, float* out, int64_t 
 namespace lkh {
 
 namespace {
+
+// lstm2_bidir_t_f32_gpu(x1[T, I1], w_ih1[8H, I1], w_hh_t1[H, 8H], b1[8H], x2[T, I2], w_ih2[8H, I2],
+//   w_hh_t2[H, 8H], b2[8H]) -> ([T, 2H], [T, 2H]) (MI355X backend: two lstm_bidir_t in one recurrence launch)
+void runLstm2(ExecCtx& ctx, const KernelArgs& a) {
+  const int64_t t = a.ints[0], in1 = a.ints[1], h = a.ints[4], in2 = a.ints[8];
+  LK_REQUIRE(ctx,
+             a.ints[2] == 8 * h && a.ints[3] == in1 && a.ints[5] == 8 * h && a.ints[6] == 8 * h && a.ints[7] == t &&
+                 a.ints[9] == 8 * h && a.ints[10] == in2 && a.ints[11] == h && a.ints[12] == 8 * h &&
+                 a.ints[13] == 8 * h,
+             "lstm2_bidir_t: expected two lstm_bidir_t operand sets of one length and hidden size");
+  const int rc = lk_hip_lstm_bidir2_f32(P<float>(a, 0), P<float>(a, 1), P<float>(a, 2), P<float>(a, 3), P<float>(a, 8),
+                                        in1, P<float>(a, 4), P<float>(a, 5), P<float>(a, 6), P<float>(a, 7),
+                                        P<float>(a, 9), in2, t, h, ctx.workspace,
+                                        static_cast<int64_t>(ctx.workspaceBytes), ctx.stream);
+  if (rc) ctx.error = rc == 3 ? "lstm2_bidir_t: workspace too small" : "lstm2_bidir_t: H must be 256, or launch failed";
+}
 
 // lstm_bidir_t_f32_gpu(x[T, I], w_ih[8H, I], w_hh_t[H, 8H], b[8H]) -> [T, 2H]
 void runLstm(ExecCtx& ctx, const KernelArgs& a) {
@@ -385,6 +531,7 @@ void runConcatBcast(ExecCtx& ctx, const KernelArgs& a) {
 void registerSequenceKernels() {
   const Device G = Device::Gpu;
   registerKernel({"lstm_bidir_t_f32_gpu", G, runLstm, 4, 1});
+  registerKernel({"lstm2_bidir_t_f32_gpu", G, runLstm2, 8, 2});
   registerKernel({"repeat_interleave_f32_gpu", G, runRepeatInterleave, 2, 1});
   registerKernel({"adalayernorm_f32_gpu", G, runAdaLn, 2, 1});
   registerKernel({"concat_bcast_f32_gpu", G, runConcatBcast, 2, 1});

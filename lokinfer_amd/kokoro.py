@@ -276,7 +276,8 @@ class KokoroGpu:
                                                self.g(L + "full_layer_layer_norm.bias"), eps=1e-12)
         return h
 
-    def text_encoder(self, ids: Tensor) -> Tensor:
+    def text_encoder_cnn(self, ids: Tensor) -> Tensor:
+        """The TextEncoder up to its BiLSTM: embedding, 3 x (conv k5, LayerNorm, leaky 0.2) -> [T, 512]."""
         x = ops.embedding_f32_gpu(self.g("text_encoder.embedding.weight"), ids)  # [T, 512]
         for i in range(3):
             x = ops.conv1d_lc_f32_gpu(x, self.g(f"text_encoder.cnn.{i}.0.weight", _w_lc),
@@ -284,7 +285,7 @@ class KokoroGpu:
             x = ops.layernorm_f32_gpu(x, self.g(f"text_encoder.cnn.{i}.1.gamma"), self.g(f"text_encoder.cnn.{i}.1.beta"),
                                       eps=1e-5)
             x = ops.leaky_lc_f32_gpu(x, 0.2)
-        return self.lstm(x, "text_encoder.lstm")  # [T, 512]
+        return x
 
     def _forward(self, ids: Tensor, ref_s: Tensor, dur: Tensor, noise: Tensor):
         frames = noise.shape[0] // 600
@@ -294,20 +295,34 @@ class KokoroGpu:
         bank_d = (ops.gemv4_f32_gpu(s_d, self.banks["decoder"][0], self.banks["decoder"][1]), self.banks["decoder"][2])
         sp_vec = ops.view(s_p, [128])
         ctx = GpuContext.shared()
-        # The TextEncoder (-> asr) depends only on the ids: it runs as a concurrent branch of the graph (the
-        # reference overlaps it with GPU work the same way, model.py:682-699). It is issued after ALBERT, which is on
-        # the critical path and then has the chip to itself; the text encoder overlaps the duration encoder instead
-        # (487 tokens: 28.05 -> 27.99 ms against issuing it first; issued before the frame-level LSTM: 28.11 ms).
+        # The TextEncoder (-> asr) depends only on the ids: it runs as a concurrent branch after ALBERT (which is on
+        # the critical path and has the chip to itself; the reference overlaps it with GPU work the same way,
+        # model.py:682-699). From 256 tokens on, its BiLSTM, of the same length as the duration encoder's first, runs
+        # in the same recurrence launch (lstm2_bidir_t), so asr is ready long before the F0 / N curves the decoder
+        # also needs, whatever order a graph runtime issues the branches in (487 tokens: 26.42 -> 26.25 ms). Below
+        # that, waiting for the text encoder's convs before the first recurrence costs more than the shared launch
+        # saves (59 tokens: 5.67 ms as a branch, 5.83 ms shared).
         bert = self.albert(ids)
         self._keep("bert", bert)
+        shared = ids.shape[0] >= 256
         with ctx.branch(self.streams[0], 1):
-            t_en = self.text_encoder(ids)
-            asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
-            self._keep("t_en", t_en)
+            t_x = self.text_encoder_cnn(ids)
+            if not shared:
+                t_en = self.lstm(t_x, "text_encoder.lstm")
+                asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)  # [F, 512] = asr^T
+                self._keep("t_en", t_en)
         d_en = ops.gemm_bias_f32_gpu(bert, self.g("bert_encoder.weight", _t), self.g("bert_encoder.bias"))
         x = ops.concat_bcast_f32_gpu(d_en, sp_vec)
+        if shared:
+            ctx.join(self.streams[0])
+            x, t_en = ops.lstm2_bidir_t_f32_gpu(x, *self.lstm_w("predictor.text_encoder.lstms.0"), t_x,
+                                                *self.lstm_w("text_encoder.lstm"))
+            with ctx.branch(self.streams[0], 1):
+                asr = ops.repeat_interleave_f32_gpu(t_en, dur, frames)
+                self._keep("t_en", t_en)
         for i in range(3):
-            x = self.lstm(x, f"predictor.text_encoder.lstms.{2 * i}")
+            if i > 0 or not shared:
+                x = self.lstm(x, f"predictor.text_encoder.lstms.{2 * i}")
             x = ops.adalayernorm_f32_gpu(x, self.style(bank_p, f"predictor.text_encoder.lstms.{2 * i + 1}.fc"))
             x = ops.concat_bcast_f32_gpu(x, sp_vec)
         self._keep("d", x)

@@ -869,6 +869,20 @@ def lstm_bidir_t_f32_gpu(x, w_ih, w_hh_t, b):
     return _launch("lstm_bidir_t_f32_gpu", [x, w_ih, w_hh_t, b], [(x.shape[0], 2 * h)])
 
 
+def lstm2_bidir_t_f32_gpu(x1, w_ih1, w_hh_t1, b1, x2, w_ih2, w_hh_t2, b2):
+    """(MI355X backend) Two lstm_bidir_t_f32_gpu of one length T and H = 256 in one recurrence launch:
+    (f32[T, 2H], f32[T, 2H]), each equal to its own lstm_bidir_t_f32_gpu."""
+    _f32(x1, w_ih1, w_hh_t1, x2, w_ih2, w_hh_t2, rank=2)
+    h = w_hh_t1.shape[0]
+    check(h == 256 and x1.shape[0] == x2.shape[0], "two LSTMs of one length with H = 256")
+    for x, wi, wh, b in ((x1, w_ih1, w_hh_t1, b1), (x2, w_ih2, w_hh_t2, b2)):
+        check(wi.shape == (8 * h, x.shape[1]) and tuple(wh.shape) == (h, 8 * h) and tuple(b.shape) == (8 * h,),
+              "expected w_ih [8H, I], w_hh_t [H, 8H], b [8H]")
+    t = x1.shape[0]
+    return _launch("lstm2_bidir_t_f32_gpu", [x1, w_ih1, w_hh_t1, b1, x2, w_ih2, w_hh_t2, b2],
+                   [(t, 2 * h), (t, 2 * h)])
+
+
 def repeat_interleave_f32_gpu(x, dur, frames):
     """x.repeat_interleave(dur, 0) -> f32[frames, C]; dur is a device i64[T]. `frames` must equal sum(dur): the
     caller checks it on the host (reference repeat_interleave_f32_cpu reports a mismatch as an error)."""

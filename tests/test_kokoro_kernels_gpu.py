@@ -45,6 +45,44 @@ def test_lstm_bidir(gpu, t, i):
     close(got, ref, 1e-4)
 
 
+@pytest.mark.parametrize("t", [1, 59, 487])
+def test_lstm2_bidir_equals_two_lstms(gpu, t):
+    """lstm2_bidir_t (two BiLSTMs of one length in one recurrence launch, the Kokoro text encoder beside the
+    duration encoder) gives each LSTM the bits of its own lstm_bidir_t launch; different input widths."""
+    lk = gpu
+    h = 256
+    sets = []
+    for i in (640, 512):
+        w_ih = (rng.standard_normal((8 * h, i)) / np.sqrt(i)).astype(np.float32)
+        w_hh_t = (rng.standard_normal((h, 8 * h)) / np.sqrt(h)).astype(np.float32)
+        b = (rng.standard_normal(8 * h) * 0.1).astype(np.float32)
+        x = rng.standard_normal((t, i)).astype(np.float32)
+        sets.append(tuple(G(lk, a) for a in (x, w_ih, w_hh_t, b)))
+    y1, y2 = lk.ops.lstm2_bidir_t_f32_gpu(*sets[0], *sets[1])
+    assert np.array_equal(y1.numpy(), lk.ops.lstm_bidir_t_f32_gpu(*sets[0]).numpy())
+    assert np.array_equal(y2.numpy(), lk.ops.lstm_bidir_t_f32_gpu(*sets[1]).numpy())
+
+
+@pytest.mark.parametrize("t", [1, 59, 2444])
+def test_lstm_exchange_paths_agree(gpu, t, monkeypatch):
+    """The XCD-local exchange (each direction's workgroups on one XCD, words through its L2) and the agent-scope
+    one (LK_LSTM_EXCHANGE=agent) run the same arithmetic: identical bits, for one LSTM and for two in one launch."""
+    lk = gpu
+    h, i = 256, 640
+    w_ih = (rng.standard_normal((8 * h, i)) / np.sqrt(i)).astype(np.float32)
+    w_hh_t = (rng.standard_normal((h, 8 * h)) / np.sqrt(h)).astype(np.float32)
+    b = (rng.standard_normal(8 * h) * 0.1).astype(np.float32)
+    x = rng.standard_normal((t, i)).astype(np.float32)
+    a = tuple(G(lk, v) for v in (x, w_ih, w_hh_t, b))
+    local = lk.ops.lstm_bidir_t_f32_gpu(*a).numpy()
+    local2 = [y.numpy() for y in lk.ops.lstm2_bidir_t_f32_gpu(*a, *a)]
+    monkeypatch.setenv("LK_LSTM_EXCHANGE", "agent")
+    agent = lk.ops.lstm_bidir_t_f32_gpu(*a).numpy()
+    assert np.isfinite(agent).all()
+    assert np.array_equal(local, agent)
+    assert all(np.array_equal(y, agent) for y in local2)
+
+
 def test_lstm_bidir_repeated_launches(gpu):
     """Back-to-back launches with alternating lengths, the second one concurrent with work on another stream:
     every result is finite and identical to the first (the cross-workgroup exchange words are reused by every
