@@ -226,6 +226,8 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(LstmJobs jo
   if (wave == 0) gv = g[(dir == 0 ? 0 : t - 1) * ld + col];
   for (int64_t step = 0; step < t; ++step) {
     const int64_t tt = dir == 0 ? step : t - 1 - step;
+    float gnx = 0.0f;  // wave 0: the next step's pre-activation, loaded a whole dot product before the poll
+    if (wave == 0 && step + 1 < t) gnx = g[(dir == 0 ? step + 1 : t - 2 - step) * ld + col];
     __builtin_amdgcn_wave_barrier();
     // all 16 broadcast reads in flight before the first product
     float4 hv[KW / 4];
@@ -265,7 +267,6 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(LstmJobs jo
         storeWord<kXcd>(xb + b * kLstmUnits + lane, word);
         out[tt * 2 * H + dir * H + b * kLstmUnits + lane] = hv;
       }
-      if (step + 1 < t) gv = g[(dir == 0 ? step + 1 : t - 2 - step) * ld + col];
     }
     // gather this wave's KW values of h(t): lane polls word KW w + lane % KW (with KW = 32 both wave halves poll
     // the same words and store the same values)
@@ -285,6 +286,7 @@ __global__ __launch_bounds__(kLstmThreads) void lstmPersistentKernel(LstmJobs jo
       reinterpret_cast<float*>(hsw[wave])[lane % KW] =
           ok ? __uint_as_float(static_cast<unsigned>(word & 0xffffffffull)) : __builtin_nanf("");
     }
+    gv = gnx;
   }
 }
 
