@@ -259,9 +259,12 @@ def compile(fn, inputs=None, *, dynamic: bool = False, input_types=None, pipelin
     input_types  explicit TensorType / BufferType (mutable) / ScalarType list, e.g. [TensorType(f32, [Sym("N"), 4])]
     pipeline     the compiler passes (default: dce, bufferize, plan-memory, hoist-init)
     graphs       capture statically shaped calls into hipGraphs
-    lanes        the most concurrent lanes of a statically shaped call's graph (kernels are assigned to lanes from their
-                 data dependencies, and the captured graph's edges follow the lanes, so independent branches run
-                 concurrently on replay; every call still enqueues on torch's current stream)
+    lanes        the most concurrent lanes of a statically shaped call's graph. A function that issues branches on side
+                 streams (GpuContext.branch / join / mark / wait_mark) keeps that structure: each stream is a lane,
+                 captured on a stream of its own with the function's waits plus the data dependencies. Otherwise
+                 kernels are assigned to lanes from their data dependencies and the captured graph's edges follow
+                 the lanes. Either way independent branches run concurrently on replay, and every call still
+                 enqueues on torch's current stream
     """
     from .rt import Executable, Model
 

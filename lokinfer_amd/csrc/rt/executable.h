@@ -103,7 +103,8 @@ class Executable {
   Status rewire(hipGraph_t graph, const std::vector<Segment>& segs) const;
   Status bindInputs(const std::vector<TensorIn>& in, std::vector<int64_t>& sv) const;
   Status interpret(const std::vector<Instr>& code, std::vector<char*>& slot, std::vector<int64_t>& sv, Bump& mem,
-                   hipStream_t s, std::vector<TensorOut>* outs, std::vector<Segment>* segs = nullptr);
+                   hipStream_t s, std::vector<TensorOut>* outs, std::vector<Segment>* segs = nullptr,
+                   bool laneStreams = false);
   // bytes the exec region allocates for a binding (statically shaped calls only)
   Status callBytes(std::vector<int64_t> sv, size_t& bytes) const;
 
@@ -114,6 +115,7 @@ class Executable {
   std::vector<void*> workspace_;  // one per lane
   size_t workspaceBytes_ = 0;
   int numLanes_ = 1;
+  bool tracedLanes_ = false;  // lanes taken from the trace's stream structure (lane / seq / after attributes)
   std::unique_ptr<Memory> temps_;   // re-placed per-call temporaries
   size_t tempsBytes_ = 0;
   std::vector<int64_t> relocOffset_;  // exec state value -> offset in temps_ (-1: not re-placed)
@@ -126,6 +128,10 @@ class Executable {
   Bump eager_;
   std::map<std::vector<int64_t>, std::unique_ptr<Graph>> graphs_;
   hipStream_t captureStream_ = nullptr;
+  // multi-stream capture: lane k's kernels are captured on laneStreams_[k] (0: captureStream_), a cross-lane wait
+  // as an event recorded after the waited kernel (laneEvents_[kernel]) and waited for on the waiting lane
+  std::vector<hipStream_t> laneStreams_;
+  std::vector<hipEvent_t> laneEvents_;  // per exec instruction (null: nothing waits for it), then fork / joins
   int64_t* pinned_ = nullptr;         // dim.read landing slot
 };
 

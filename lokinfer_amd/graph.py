@@ -13,6 +13,8 @@ import contextlib
 import re
 import threading
 
+import torch
+
 from .tensor import DType, Tensor
 
 _INT = re.compile(r"-?\d+")
@@ -216,6 +218,16 @@ class Graph:
         self.externals: dict[str, Tensor] = {}  # const.external name -> the captured tensor
         self._ext_of: dict[int, tuple] = {}      # id(tensor) -> (tensor, value)
         self._n = 0
+        # stream structure of the traced function (GpuContext.branch / join / wait): lane 0 is the stream tracing
+        # began on, other streams get lanes 1, 2, ... in first-use order; every kernel has a trace sequence number,
+        # and a stream's wait on another is kept as (lane, last sequence number issued there) for the next kernel
+        # the waiting stream issues
+        self.base_stream = None
+        self._lanes: dict[int, int] = {}
+        self._seq = 0
+        self._last_seq: dict[int, int] = {}       # lane -> sequence number of its last kernel
+        self._pending: dict[int, list] = {}       # lane -> [(lane, seq)] for its next kernel
+        self._kernels: list[list] = []           # [line index, lane, seq, after]
 
     def _fresh(self, hint: str) -> str:
         self._n += 1
@@ -250,18 +262,48 @@ class Graph:
             return v
         raise TypeError(f"expected a traced value or lk.Tensor, got {type(x).__name__}")
 
+    def lane_of(self, stream) -> int:
+        h = stream.cuda_stream
+        if self.base_stream is None or h == self.base_stream:
+            return 0
+        return self._lanes.setdefault(h, len(self._lanes) + 1)
+
+    def stream_wait(self, waiter, producer) -> None:
+        """`waiter` waits for the kernels issued on `producer` so far (a fork, a join or an event)."""
+        a, b = self.lane_of(waiter), self.lane_of(producer)
+        if a != b and b in self._last_seq:
+            self._pending.setdefault(a, []).append((b, self._last_seq[b]))
+
+    def mark(self, stream) -> tuple:
+        """An event recorded on `stream`: what a later wait_mark waits for."""
+        b = self.lane_of(stream)
+        return (b, self._last_seq.get(b, -1))
+
+    def wait_mark(self, waiter, mark: tuple) -> None:
+        a = self.lane_of(waiter)
+        if mark[0] != a and mark[1] >= 0:
+            self._pending.setdefault(a, []).append(mark)
+
     def kernel(self, name: str, operands: list, attrs: dict, result_types: list) -> list[Value]:
+        lane = self.lane_of(torch.cuda.current_stream()) if self.base_stream is not None else 0
         vals = [self.value_of(x) for x in operands]
         results = [Value(self, self._fresh("v"), t) for t in result_types]
+        self._kernels.append([len(self.lines), lane, self._seq, self._pending.pop(lane, []),
+                              (name, vals, dict(attrs), results, result_types)])
+        self._last_seq[lane] = self._seq
+        self._seq += 1
+        self.lines.append(self._kernel_line(name, vals, attrs, results, result_types))
+        return results
+
+    @staticmethod
+    def _kernel_line(name, vals, attrs, results, result_types) -> str:
         attr = ""
         if attrs:
             attr = " {" + ", ".join(f"{k} = {_attr_text(attrs[k])}" for k in sorted(attrs)) + "}"
         lhs = ", ".join(f"%{r.name}" for r in results)
         types = ", ".join(t.ir() for t in result_types)
         ops = ", ".join(f"%{v.name}" for v in vals)
-        self.lines.append((f"{lhs} = " if results else "") + f'kernel "{name}"({ops}){attr}' +
-                          (f" : {types}" if results else ""))
-        return results
+        return (f"{lhs} = " if results else "") + f'kernel "{name}"({ops}){attr}' + (f" : {types}" if results else "")
 
     def view(self, x, type_, offset=0) -> Value:
         src = self.value_of(x)
@@ -287,7 +329,19 @@ class Graph:
         self.lines.append(f"dim.read %{src.name}[{int(index)}] -> {symbol}")
         return Dim(symbol)
 
+    def _stream_attrs(self) -> None:
+        """Once any kernel ran on a side stream, every kernel line carries its lane, sequence number and waits as
+        string attributes (no kernel argument: the executable's lane schedule reads them)."""
+        if not any(k[1] for k in self._kernels):
+            return
+        for idx, lane, seq, after, (name, vals, attrs, results, types) in self._kernels:
+            extra = dict(attrs, lane=str(lane), seq=str(seq))
+            if after:
+                extra["after"] = ",".join(f"{l}:{q}" for l, q in after)
+            self.lines[idx] = self._kernel_line(name, vals, extra, results, types)
+
     def to_text(self, outputs: list[Value]) -> str:
+        self._stream_attrs()
         args = ", ".join(f"%{a.name}: {a.type.ir()}" + (" mutable" if isinstance(a.type, BufferType) else "")
                          for a in self.args)
         types = [o.type.ir() for o in outputs]
@@ -307,6 +361,8 @@ def current_graph() -> Graph | None:
 @contextlib.contextmanager
 def tracing(graph: Graph):
     prev = current_graph()
+    if graph.base_stream is None and torch.cuda.is_available():
+        graph.base_stream = torch.cuda.current_stream().cuda_stream
     _state.graph = graph
     try:
         yield graph

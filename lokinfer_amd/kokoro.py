@@ -345,12 +345,11 @@ class KokoroGpu:
         # stage 0's block runs beside the decoder on one side stream, stage 1's on another, issued after the decoder
         # (below), that waits for the STFT; the generator joins each just before adding it.
         G = "decoder.generator."
-        har_ready = torch.cuda.Event()
         with ctx.branch(self.streams[2], 3):
             har_src = ops.harmonic_source_f32_gpu(f0, noise, self.g(G + "m_source.l_linear.weight", _flat),
                                                   self.g(G + "m_source.l_linear.bias"))
             har = ops.stft_magphase_lc_f32_gpu(har_src, 20, 5, cpad=32)  # [120 F + 1, 32]
-            har_ready.record(self.streams[2])
+            har_ready = ctx.mark(self.streams[2])
             self._keep("har_source", har_src)
             self._keep("har", har)
             xs_stage = [self.noise_block(har, bank_d, 0)]
@@ -372,7 +371,7 @@ class KokoroGpu:
         # stage 1's noise block is issued after the decoder: beside it, its large stage-1-resolution convs slowed the
         # decoder's (the generator's stage 0 waits for the decoder, stage 1 only for this block): 28.11 -> 28.02 ms
         with ctx.branch(self.streams[3], 4):
-            self.streams[3].wait_event(har_ready)
+            ctx.wait_mark(self.streams[3], har_ready)
             xs_stage.append(self.noise_block(har, bank_d, 1))
         # generator
         for i, (k_up, u) in enumerate(((20, 10), (12, 6))):

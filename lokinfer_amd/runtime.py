@@ -12,6 +12,7 @@ import ctypes as C
 import torch
 
 from ._lib import LokinferError, check_device_errors, lib
+from .graph import current_graph
 
 WORKSPACE_BYTES = 64 << 20
 
@@ -49,7 +50,11 @@ class GpuContext:
 
         class _Branch:
             def __enter__(self):
-                stream.wait_stream(torch.cuda.current_stream(ctx.device))
+                cur = torch.cuda.current_stream(ctx.device)
+                stream.wait_stream(cur)
+                g = current_graph()
+                if g is not None:
+                    g.stream_wait(stream, cur)
                 self._prev = ctx.slot
                 self._sc = torch.cuda.stream(stream)
                 self._sc.__enter__()
@@ -64,7 +69,25 @@ class GpuContext:
         return _Branch()
 
     def join(self, stream: "torch.cuda.Stream") -> None:
-        torch.cuda.current_stream(self.device).wait_stream(stream)
+        cur = torch.cuda.current_stream(self.device)
+        cur.wait_stream(stream)
+        g = current_graph()
+        if g is not None:
+            g.stream_wait(cur, stream)
+
+    def mark(self, stream: "torch.cuda.Stream"):
+        """An event recorded on `stream` now; `wait_mark(other, m)` makes `other` wait for it. Traced functions
+        record the same structure for the compiled runtime's lane schedule."""
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        g = current_graph()
+        return (ev, g.mark(stream) if g is not None else None)
+
+    def wait_mark(self, stream: "torch.cuda.Stream", m) -> None:
+        stream.wait_event(m[0])
+        g = current_graph()
+        if g is not None and m[1] is not None:
+            g.wait_mark(stream, m[1])
 
     @classmethod
     def shared(cls) -> "GpuContext":

@@ -49,6 +49,44 @@ def test_mnist_mlp_compiled_equals_eager_and_oracle(gpu, tmp_path):
     assert 'const.internal @"ext0"' in m2.ir_text()
 
 
+def test_traced_stream_structure_replayed(gpu):
+    """A function that runs branches on side streams (GpuContext.branch / join / mark / wait_mark) leaves its stream
+    structure in the IR (lane, seq, after); the executable captures each lane on its own stream with those waits
+    plus the data dependencies. The replays equal the eager run bit for bit, with other work between them."""
+    from lokinfer_amd.runtime import GpuContext
+
+    lk = gpu
+    ctx = GpuContext.shared()
+    side = [torch.cuda.Stream() for _ in range(2)]
+    D = 256
+    w1, w2, w3 = (G(lk, rng.standard_normal((D, D)) / 16) for _ in range(3))
+    b = G(lk, 0.1 * rng.standard_normal(D))
+
+    def f(x):
+        h = lk.ops.gemm_bias_f32_gpu(x, w1, b)
+        with ctx.branch(side[0], 1):  # a branch of two dependent kernels, marked half way
+            u = lk.ops.gemm_f32_gpu_mps(h, w2)
+            m = ctx.mark(side[0])
+            u = lk.ops.leaky_lc_f32_gpu(u, 0.2)
+        with ctx.branch(side[1], 2):  # waits for the branch's first kernel only
+            ctx.wait_mark(side[1], m)
+            v = lk.ops.gemm_f32_gpu_mps(h, w3)
+        y = lk.ops.gemm_f32_gpu_mps(h, w1)
+        ctx.join(side[0])
+        ctx.join(side[1])
+        return lk.ops.add3_scale_f32_gpu(y, u, v, 0.5)
+
+    X = G(lk, rng.standard_normal((300, D)))
+    eager = f(X).numpy()
+    cm = lk.compile(f, inputs=[X], lanes=4)
+    ir = cm.source_ir
+    assert 'lane = "1"' in ir and 'lane = "2"' in ir and 'after = "' in ir
+    for _ in range(4):
+        assert np.array_equal(cm(X).numpy(), eager)
+        lk.ops.gemm_f32_gpu_mps(X, w2).numpy()  # eager work between the replays
+    assert cm.stats()["graphs"] == 1 and cm.stats()["lanes"] == 3
+
+
 def test_symbolic_rows_one_graph_per_binding(gpu):
     lk = gpu
     D = 256
