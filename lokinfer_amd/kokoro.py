@@ -263,17 +263,25 @@ class KokoroGpu:
             [self.sd[L + f"attention.{n}.weight"] for n in ("query", "key", "value")], axis=0))
         bqkv = self.const("albert#bqkv", lambda: np.concatenate(
             [self.sd[L + f"attention.{n}.bias"] for n in ("query", "key", "value")]))
+        # Below 64 output tiles (T <= 320) the projections feeding a LayerNorm split K over workgroups; their
+        # partial planes then go straight into the LayerNorm, which sums them (add_bias_layernorm2_sk), instead of
+        # through a reduction launch of their own (59 tokens: 24 launches fewer)
+        sk = ops.splitk_planes(t, 768, 3) > 1
+
+        def proj_ln(x, w, splits, b, g, beta):
+            if sk:
+                parts = ops.gemm_splitk_f32_gpu(x, self.g(w, _t), splits)
+                return ops.add_bias_layernorm2_sk_f32_gpu(parts, self.g(b), h, self.g(g), self.g(beta), eps=1e-12)[1]
+            return ops.add_bias_layernorm_f32_gpu(ops.gemm_nt_f32_gpu_mps(x, self.g(w)), self.g(b), h, self.g(g),
+                                                  self.g(beta), eps=1e-12)
+
         for _ in range(12):
             a = ops.attention_qkv_sg_f32_gpu(ops.gemm_nt_f32_gpu_mps(h, wqkv), bqkv, heads=12)
-            a = ops.gemm_nt_f32_gpu_mps(a, self.g(L + "attention.dense.weight"))
-            h = ops.add_bias_layernorm_f32_gpu(a, self.g(L + "attention.dense.bias"), h,
-                                               self.g(L + "attention.LayerNorm.weight"),
-                                               self.g(L + "attention.LayerNorm.bias"), eps=1e-12)
+            h = proj_ln(a, L + "attention.dense.weight", 3, L + "attention.dense.bias",
+                        L + "attention.LayerNorm.weight", L + "attention.LayerNorm.bias")
             f = ops.gemm_steel_f32_gpu(h, self.g(L + "ffn.weight", _t), self.g(L + "ffn.bias"), act="gelu")
-            f = ops.gemm_nt_f32_gpu_mps(f, self.g(L + "ffn_output.weight"))
-            h = ops.add_bias_layernorm_f32_gpu(f, self.g(L + "ffn_output.bias"), h,
-                                               self.g(L + "full_layer_layer_norm.weight"),
-                                               self.g(L + "full_layer_layer_norm.bias"), eps=1e-12)
+            h = proj_ln(f, L + "ffn_output.weight", 8, L + "ffn_output.bias", L + "full_layer_layer_norm.weight",
+                        L + "full_layer_layer_norm.bias")
         return h
 
     def text_encoder_cnn(self, ids: Tensor) -> Tensor:
