@@ -191,9 +191,10 @@ class KokoroGpu:
     def conv(self, x: Tensor, p: str, af: Tensor | None, k: int, d: int = 1, act: str = "none", alpha=None,
              slope: float = 0.0, residual=None, out_scale: float = 1.0, stats: bool = False, co_pad: int = 0):
         """conv(act(affine(x))) (+ residual) * out_scale, optionally with the output's channel statistics, on the
-        Winograd pair or the tap conv, whichever is faster at this shape (measured on MI355X: Winograd once its
-        GEMM grid of 64-tile x 64-channel workgroups reaches 256, or 64 with K >= 7 or Ci >= 512, or at any grid
-        with Ci >= 1024, where its split-K fills the chip). co_pad > Co: output channels past Co are zero (zero weights and bias). Returns (y, stats,
+        Winograd pair or the tap conv, whichever is faster at this shape. Measured on MI355X over every conv of the
+        59- and 487-token forwards: the pair (transform + GEMM) costs at least ~55-60 us, the K = 3 tap conv ~55-60
+        us per 1e9 multiply-adds, and K >= 7 favours Winograd once its grid of 64-tile x 64-channel workgroups
+        reaches 64. co_pad > Co: output channels past Co are zero (zero weights and bias). Returns (y, stats,
         stats_dilation): Winograd statistics come per residue class of the dilation."""
         co, ci = self.sd[p + ".weight"].shape[:2]
         cop = max(co, co_pad)
@@ -201,7 +202,8 @@ class KokoroGpu:
         pad = d * (k - 1) // 2
         bias = self.g(p + ".bias") if cop == co else self.const(f"{p}.bias#pad{cop}",
                                                                  lambda: _vec_pad(self.sd[p + ".bias"], cop))
-        if cop % 64 == 0 and (grid >= 256 or (grid >= 64 and (k >= 7 or ci >= 512)) or ci >= 1024):
+        macs = x.shape[0] * ci * cop * k
+        if cop % 64 == 0 and (macs >= 1_000_000_000 or (k >= 7 and grid >= 64)):
             u, tr = self.wino(p + ".weight", x.shape[1], cop)
             kw = {"alpha": alpha} if act == "snake" else {"slope": slope} if act == "leaky" else {}
             y = ops.conv1d_wino_lc_f32_gpu(x, u, bias, tr, k, residual=residual, out_scale=out_scale,
