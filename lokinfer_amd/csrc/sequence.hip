@@ -16,6 +16,7 @@
 #include "lokinfer_hip.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -297,11 +298,14 @@ inline bool lstmXcdLocal() {
   if (e && strcmp(e, "agent") == 0) return false;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
-  static int cached[64] = {};  // 0 unknown, 1 XCD-local, 2 agent
-  if (dev >= 0 && dev < 64 && cached[dev]) return cached[dev] == 1;
+  static std::atomic<int> cached[64] = {};  // per device: 0 unknown, 1 XCD-local, 2 agent
+  if (dev >= 0 && dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c) return c == 1;
+  }
   const bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
                   cus == kXcds * 32;
-  if (dev >= 0 && dev < 64) cached[dev] = ok ? 1 : 2;
+  if (dev >= 0 && dev < 64) cached[dev].store(ok ? 1 : 2, std::memory_order_relaxed);
   return ok;
 }
 
